@@ -1,0 +1,194 @@
+/*
+ * mslim_attn -- MI355X (gfx950) attention hot path of M-SLIM behind a C ABI.
+ *
+ * Drop-in boundary for the reference's native bridge (native_hip.rs:13-20,
+ * :84-134; native/hipblaslt_bridge.cpp:155-233) and for the device launches
+ * that gpu_backend.rs / gpu_llm/gpu_resources.rs / gpu_llm/prefill.rs /
+ * gpu_llm/tiled_attention.rs issue today through OpenCL.  Plain pointers and
+ * sizes only.
+ *
+ * Conventions (kept from hipblaslt_bridge.cpp:24-39):
+ *   * every int-returning entry point returns 0 on success, -1 for invalid
+ *     arguments, 100 + hipError_t for a HIP runtime failure and 400..409 for a
+ *     failed stage; pointer-returning ones return NULL on failure;
+ *   * the message of the last failure on the calling thread is returned by
+ *     mslim_attn_last_error();
+ *   * a context serialises its calls with its own mutex (hipblaslt_bridge.cpp
+ *     :61, :179) and issues all device work in order on one HIP stream, the
+ *     equivalent of the reference's single in-order OpenCL queue
+ *     (gpu_resources.rs:122-123);
+ *   * compute entry points are stream-ordered: they return after enqueueing.
+ *     mslim_attn_synchronize() is the queue.finish() equivalent; the buffer
+ *     read/write entry points block, like CL_BLOCKING transfers;
+ *   * all tensors are BF16 bit patterns (uint16 little-endian) unless stated,
+ *     device pointers, and the output must not alias any input
+ *     (tiled_attention.rs:204-207).
+ *
+ * Layouts:
+ *   Q        [batch][q_heads][head_dim]                 (decode)
+ *            [queries][q_heads][head_dim]               (prefill)
+ *   dense K/V token-major [tokens][kv_heads][head_dim] per sequence
+ *            (gpu_llm.cl:148-149); sequence b starts at b * seq_stride_tokens
+ *            tokens.
+ *   paged K/V pool of pages [page][kv_heads][page_tokens][head_dim]: the
+ *            head-major ColdStore page payload (cold_store.rs:480-483,
+ *            gpu_region_store.rs:386-390); page_table[b][i] is the pool page
+ *            holding tokens [i*page_tokens, (i+1)*page_tokens) of sequence b.
+ */
+#ifndef MSLIM_ATTN_H
+#define MSLIM_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MSLIM_ATTN_MAX_BATCH 64 /* sequences per decode launch */
+
+/* ---- Context and errors -------------------------------------------------- */
+
+/* Replaces tv_hip_last_error (hipblaslt_bridge.cpp:157-159, bound at
+ * native_hip.rs:13,101).  Thread-local, never NULL. */
+const char *mslim_attn_last_error(void);
+
+/* Replaces tv_hip_new (hipblaslt_bridge.cpp:160-169, native_hip.rs:102,111).
+ * Gate: device 0 must report gcnArchName "gfx950..." and
+ * HSA_OVERRIDE_GFX_VERSION must be unset (hipblaslt_bridge.cpp:69-87).
+ * NULL on failure. */
+void *mslim_attn_ctx_new(void);
+
+/* Replaces tv_hip_destroy (hipblaslt_bridge.cpp:170-172, native_hip.rs:103). */
+void mslim_attn_ctx_destroy(void *ctx);
+
+/* Route this context's work onto an existing HIP stream; NULL names the HIP
+ * null (legacy default) stream.  Until this is called the context uses a
+ * stream of its own.  No reference counterpart: the OpenCL engine owns its
+ * single queue (gpu_resources.rs:122-123); callers that share a stream with
+ * other libraries need to name it. */
+int mslim_attn_ctx_set_stream(void *ctx, void *hip_stream);
+
+/* queue.finish() equivalent (gpu_llm/mod.rs:1998-2001). */
+int mslim_attn_synchronize(void *ctx);
+
+/* ---- Device buffers ------------------------------------------------------- */
+
+/* GpuEngine::alloc_u8 (gpu_resources.rs) equivalent; NULL on failure. */
+void *mslim_attn_buf_alloc(void *ctx, size_t bytes);
+/* Replaces tv_hip_load_weight (hipblaslt_bridge.cpp:173-187,
+ * native_hip.rs:104,146): allocate and copy `bytes` host bytes. */
+void *mslim_attn_buf_upload(void *ctx, const uint8_t *bytes, size_t byte_length);
+/* Replaces tv_hip_free_weight (hipblaslt_bridge.cpp:188-193). */
+int mslim_attn_buf_free(void *ctx, void *buffer);
+/* Replaces tv_hip_read_weight (hipblaslt_bridge.cpp:194-202): blocking
+ * device->host copy of `size` bytes at `offset`. */
+int mslim_attn_buf_read(void *ctx, const void *buffer, size_t offset, uint8_t *out,
+                        size_t size);
+/* Blocking host->device copy (enqueue_write_buffer CL_BLOCKING,
+ * gpu_resources.rs:1010-1016, :1028-1033). */
+int mslim_attn_buf_write(void *ctx, void *buffer, size_t offset, const uint8_t *in,
+                         size_t size);
+
+/* ---- Attention ------------------------------------------------------------ */
+
+/* Single-token GQA decode over a dense token-major BF16 K/V cache for a
+ * ragged batch.  Replaces GpuEngine::attention (gpu_resources.rs:583-643:
+ * llm_attention_qk/softmax/pv, gpu_llm.cl:150-212), exact_hot_fused_attention
+ * (gpu_resources.rs:783-825, gpu_llm.cl:975-1025) and TiledAttention::run with
+ * queries = 1 (tiled_attention.rs:161-293).
+ *   seq_lens: host array of `batch` token counts (>= 1), batch <= 64.
+ *   scale: softmax scale applied to Q.K (reference: 1/sqrt(head_dim)).
+ *   split_tokens: tokens per split-KV partition, a multiple of 64, or 0 to let
+ *   the library pick from the shape.  Partitions are defined on logical token
+ *   indices only, so the paged entry point with the same split_tokens gives
+ *   bit-identical output. */
+int mslim_attn_decode_dense(void *ctx, const void *q, const void *k, const void *v,
+                            void *out, int batch, const int32_t *seq_lens,
+                            int64_t seq_stride_tokens, int q_heads, int kv_heads,
+                            int head_dim, float scale, int split_tokens);
+
+/* The same decode over the ColdStore-exact paged layout.  Replaces
+ * attention_gpu_region (gpu_resources.rs:883-1063: llm_attention_qk/softmax +
+ * llm_lod_pv_stage/finish, gpu_llm.cl:280-322) at epsilon = 0, with K and V
+ * both resident in the device page pool.
+ *   page_table: device int32 [batch][pages_per_seq].
+ *   page_tokens: tokens per page, a multiple of 16 (16 in the ColdStore-exact
+ *   configuration). */
+int mslim_attn_decode_paged(void *ctx, const void *q, const void *k_pool,
+                            const void *v_pool, void *out, int batch,
+                            const int32_t *seq_lens, const int32_t *page_table,
+                            int pages_per_seq, int page_tokens, int q_heads,
+                            int kv_heads, int head_dim, float scale, int split_tokens);
+
+/* Causal GQA attention for a chunk of `queries` new tokens after `prior`
+ * cached tokens: row i attends keys 0..prior+i.  K/V hold prior+queries
+ * tokens, token-major.  Replaces BatchKernels::attention (prefill.rs:363-435:
+ * llm_prefill_qk/softmax/pv, gpu_llm.cl:462-541) and TiledAttention::run
+ * (tiled_attention.rs:161-293) for queries >= 1, including batched
+ * multi-query decode. */
+int mslim_attn_prefill_causal(void *ctx, const void *q, const void *k, const void *v,
+                              void *out, int queries, int prior, int q_heads,
+                              int kv_heads, int head_dim, float scale);
+
+/* ---- Feeder kernels ------------------------------------------------------- */
+
+/* RMSNorm over `tokens` rows of `hidden` BF16 values: 128-lane strided FMA
+ * sum of squares, tree reduction, y = BF16(BF16(x*f)*w).  Replaces
+ * GpuEngine::norm (gpu_resources.rs:485-507, llm_rmsnorm gpu_llm.cl:72-98) and
+ * the prefill norm (prefill.rs:292-320, llm_prefill_norm gpu_llm.cl:378-408). */
+int mslim_attn_rmsnorm(void *ctx, const void *input, const void *weight, void *output,
+                       int tokens, int hidden, float epsilon);
+
+/* Rotate-half RoPE on [tokens][heads][head_dim], row t at position
+ * start_position + t, optional llama3 frequency scaling.  Replaces
+ * GpuEngine::rope (gpu_resources.rs:509-537, llm_rope gpu_llm.cl:102-146) and
+ * the prefill RoPE (prefill.rs:322-361, llm_prefill_rope gpu_llm.cl:412-456);
+ * arguments mirror RopeKernelConfig (gpu_llm/kernels.rs:15-23). */
+int mslim_attn_rope(void *ctx, const void *input, void *output, int tokens, int heads,
+                    int head_dim, int start_position, float theta, int llama3_scaling,
+                    float factor, float low_freq_factor, float high_freq_factor,
+                    float original_max_position);
+
+/* out = BF16(BF16(silu(gate)) * up) over n elements.  Replaces
+ * GpuEngine::swiglu (gpu_resources.rs:561-581, llm_swiglu gpu_llm.cl:225-237). */
+int mslim_attn_swiglu(void *ctx, const void *gate, const void *up, void *output, size_t n);
+
+/* ---- ColdStore-exact page pool --------------------------------------------- */
+
+/* Write `tokens` token-major rows of one sequence (K and V, [tokens][kv_heads]
+ * [head_dim]) into the page pool at logical positions first_token.. through
+ * the device page table row `page_table` (int32 [pages]).  The device
+ * counterpart of GpuRegionStore::append_batch's token-major -> head-major page
+ * conversion (gpu_region_store.rs:391-520). */
+int mslim_attn_pages_write(void *ctx, void *k_pool, void *v_pool, const int32_t *page_table,
+                           int page_tokens, int kv_heads, int head_dim, int64_t first_token,
+                           int64_t tokens, const void *k_rows, const void *v_rows);
+
+/* Gather `tokens` logical positions [first_token, first_token+tokens) of one
+ * sequence from a page pool into token-major rows [tokens][kv_heads][head_dim].
+ * The device counterpart of GpuRegionStore::read_keys / read_values
+ * (gpu_region_store.rs:828-927).  Apply it once to the K pool and once to the
+ * V pool. */
+int mslim_attn_pages_gather(void *ctx, const void *pool, const int32_t *page_table,
+                            int page_tokens, int kv_heads, int head_dim,
+                            int64_t first_token, int64_t tokens, void *rows_out);
+
+/* Logical K/V SHA-256 (hex, 65 bytes with NUL) of `layers` layers of one
+ * sequence of `tokens` tokens: "mslim-dense-kv-state-v1" || u64 LE tokens ||
+ * per layer K then V in [kv_heads][token][head_dim] order.  Replaces
+ * GpuLlm::logical_kv_sha256 (gpu_llm/mod.rs:1981-2028) and
+ * GpuRegionStore::logical_kv_sha256 (gpu_region_store.rs:341-371).
+ *   Dense: keys[l] / values[l] are token-major device buffers, page_tables
+ *   NULL.  Paged: keys[l] / values[l] are page pools and page_tables[l] the
+ *   device page-table row of layer l (page_tokens > 0).  Blocking. */
+int mslim_attn_logical_kv_sha256(void *ctx, int layers, int64_t tokens, int kv_heads,
+                                 int head_dim, const void *const *keys,
+                                 const void *const *values,
+                                 const int32_t *const *page_tables, int page_tokens,
+                                 char *hex_out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MSLIM_ATTN_H */

@@ -1,0 +1,49 @@
+"""Seeded synthetic inputs shared by the tests and bench.
+
+Values are numpy PCG64 standard normals (or the reference's own generators,
+restated where a test mirrors a reference test) rounded to BF16 with the
+reference's round-to-nearest-even rule (gpu_llm.cl:10-21).
+"""
+import numpy as np
+
+import oracle
+
+
+def normal_bf16(rng: np.random.Generator, shape, scale: float = 1.0) -> np.ndarray:
+    x = rng.standard_normal(size=shape, dtype=np.float32)
+    if scale != 1.0:
+        x = x * np.float32(scale)
+    return oracle.write_bf16(x).reshape(shape)
+
+
+def tiled_input(count: int, salt: int) -> np.ndarray:
+    """tiled_attention.rs:305-312: ((i*37 + salt*13) % 257 - 128) / 128 as BF16."""
+    i = np.arange(count, dtype=np.int64)
+    v = (((i * 37 + salt * 13) % 257) - 128).astype(np.float32) / np.float32(128.0)
+    return oracle.write_bf16(v)
+
+
+def bench_lcg(count: int, seed: int) -> tuple:
+    """mslim-attention-bench.rs:21-28 LCG: returns (values f32, final seed)."""
+    out = np.empty(count, np.float32)
+    s = seed & 0xFFFFFFFFFFFFFFFF
+    for j in range(count):
+        s = (s * 6364136223846793005 + 1442695040888963407) & 0xFFFFFFFFFFFFFFFF
+        u = s >> 40
+        out[j] = (np.float32(u) / np.float32(16777216.0) - np.float32(0.5)) * np.float32(0.75)
+    return out, s
+
+
+def to_torch(bits: np.ndarray, device="cuda"):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).to(device)
+
+
+def from_torch(t) -> np.ndarray:
+    return t.detach().cpu().contiguous().view(dtype=__import__("torch").int16).numpy().view(np.uint16)
+
+
+def max_abs_bf16(a_bits: np.ndarray, b) -> float:
+    a = oracle.read_bf16(a_bits).astype(np.float64).reshape(-1)
+    b = np.asarray(b, np.float64).reshape(-1)
+    return float(np.max(np.abs(a - b))) if a.size else 0.0

@@ -1,0 +1,220 @@
+"""GPU parity of single-token decode (dense and ColdStore-paged) against the
+CPU oracle, through the C ABI.
+
+Tolerance (north star): max abs <= 2e-2 on BF16 outputs against the
+reference CPU attention (`dense_attention_bf16`, native_cpu_adapter.rs:253-307)
+and against the f64 CpuReferenceBackend (portable.rs:575-646).  The paged
+path must equal the dense path bit for bit.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from _data import from_torch, max_abs_bf16, normal_bf16, tiled_input, to_torch
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-2
+
+
+def _decode(ctx, qb, kb, vb, lens, qh, kvh, d, split=0, stride=0):
+    q, k, v = to_torch(qb), to_torch(kb), to_torch(vb)
+    out = torch.empty_like(q)
+    ctx.decode_dense(q, k, v, out, lens, qh, kvh, d, seq_stride_tokens=stride, split_tokens=split)
+    torch.cuda.synchronize()
+    return from_torch(out)
+
+
+def _oracle_decode(qb, kb, vb, qh, kvh, d):
+    return oracle.dense_attention_bf16(oracle.read_bf16(qb), kb, vb, qh, kvh, d)
+
+
+def test_decode_cfg1_parity_repeatability_and_inputs_untouched(ctx):
+    # B=1, T=1024, 32/8/128, N(0,1) seeded -> BF16.
+    rng = np.random.default_rng(20261201)
+    qh, kvh, d, t = 32, 8, 128, 1024
+    qb = normal_bf16(rng, (1, qh, d))
+    kb = normal_bf16(rng, (t, kvh, d))
+    vb = normal_bf16(rng, (t, kvh, d))
+    q, k, v = to_torch(qb), to_torch(kb), to_torch(vb)
+    out = torch.empty_like(q)
+    ctx.decode_dense(q, k, v, out, [t], qh, kvh, d)
+    torch.cuda.synchronize()
+    got = from_torch(out)
+    ref = _oracle_decode(qb, kb, vb, qh, kvh, d)
+    assert max_abs_bf16(got, ref) <= TOL
+    rc, f64 = oracle.cpu_reference_decode(oracle.read_bf16(qb), kb, vb, 1, qh, kvh, d)
+    assert rc == 0 and max_abs_bf16(got, f64) <= TOL
+    # repeat: bit-identical (tiled_attention.rs:380-387); K/V unmodified (:388-397)
+    out2 = torch.empty_like(q)
+    ctx.decode_dense(q, k, v, out2, [t], qh, kvh, d)
+    torch.cuda.synchronize()
+    assert np.array_equal(from_torch(out2), got)
+    assert np.array_equal(from_torch(k), kb) and np.array_equal(from_torch(v), vb)
+
+
+GEOMS = [(32, 8, 128), (64, 8, 128), (8, 8, 128), (16, 8, 128), (8, 2, 64), (32, 4, 64),
+         (4, 2, 80), (4, 1, 256), (12, 4, 128)]
+HISTORIES = [1, 2, 15, 31, 33, 63, 65, 129, 375, 2049]
+
+
+@pytest.mark.parametrize("qh,kvh,d", GEOMS)
+def test_decode_histories_and_geometries(ctx, qh, kvh, d):
+    # tiled_attention.rs:408-434 histories and head dims; the reference's
+    # deterministic synthetic inputs (tiled_attention.rs:305-312).
+    for t in HISTORIES:
+        qb = tiled_input(qh * d, 3).reshape(1, qh, d)
+        kb = tiled_input(t * kvh * d, 7).reshape(t, kvh, d)
+        vb = tiled_input(t * kvh * d, 11).reshape(t, kvh, d)
+        ref = _oracle_decode(qb, kb, vb, qh, kvh, d)
+        for split in (0, 64):
+            got = _decode(ctx, qb, kb, vb, [t], qh, kvh, d, split=split)
+            err = max_abs_bf16(got, ref)
+            assert err <= TOL, (qh, kvh, d, t, split, err)
+
+
+def test_decode_ragged_batch_dense(ctx):
+    rng = np.random.default_rng(7)
+    qh, kvh, d, stride = 32, 8, 128, 1100
+    lens = [1, 100, 1000, 64, 513, 1100, 2]
+    qb = normal_bf16(rng, (len(lens), qh, d))
+    kb = normal_bf16(rng, (len(lens), stride, kvh, d))
+    vb = normal_bf16(rng, (len(lens), stride, kvh, d))
+    got = _decode(ctx, qb, kb, vb, lens, qh, kvh, d, stride=stride).reshape(len(lens), -1)
+    for b, t in enumerate(lens):
+        ref = _oracle_decode(qb[b], kb[b, :t], vb[b, :t], qh, kvh, d)
+        assert max_abs_bf16(got[b], ref) <= TOL, b
+
+
+def _paged_pool(ctx, k, v, lens, stride, page_tokens, seed):
+    """Scatter dense [B][stride][KVH][D] K/V into a randomly permuted page pool
+    with the product's page writer; returns (k_pool, v_pool, table, pages_per_seq)."""
+    b_count = len(lens)
+    kvh, d = k.shape[2], k.shape[3]
+    pages_per_seq = (max(lens) + page_tokens - 1) // page_tokens
+    needed = [(t + page_tokens - 1) // page_tokens for t in lens]
+    total = sum(needed)
+    perm = np.random.default_rng(seed).permutation(total).astype(np.int32)
+    table = np.zeros((b_count, pages_per_seq), np.int32)
+    cursor = 0
+    for b, n in enumerate(needed):
+        table[b, :n] = perm[cursor:cursor + n]
+        cursor += n
+    table_t = torch.from_numpy(table).cuda()
+    k_pool = torch.zeros((total, kvh, page_tokens, d), dtype=torch.int16, device="cuda")
+    v_pool = torch.zeros_like(k_pool)
+    for b, t in enumerate(lens):
+        ctx.pages_write(k_pool, v_pool, table_t[b], page_tokens, kvh, d, 0, t,
+                        k[b, :t].contiguous(), v[b, :t].contiguous())
+    torch.cuda.synchronize()
+    return k_pool, v_pool, table_t, pages_per_seq, table
+
+
+def test_paged_equals_dense_bitwise_cfg3(ctx):
+    # 32 sessions, T ~ U[512, 8192] seeded, 16-token pages,
+    # seeded random page table, epsilon = 0, 32/8/128.
+    rng = np.random.default_rng(3)
+    qh, kvh, d, pt = 32, 8, 128, 16
+    lens = [int(x) for x in rng.integers(512, 8193, size=32)]
+    stride = max(lens)
+    gen = torch.Generator(device="cuda").manual_seed(1234)
+    k = torch.randn((32, stride, kvh, d), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    v = torch.randn((32, stride, kvh, d), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    q = torch.randn((32, qh, d), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    k_pool, v_pool, table_t, pps, table = _paged_pool(ctx, k, v, lens, stride, pt, seed=99)
+    for split in (0, 64, 512):
+        dense = torch.empty_like(q)
+        paged = torch.empty_like(q)
+        ctx.decode_dense(q, k, v, dense, lens, qh, kvh, d, seq_stride_tokens=stride, split_tokens=split)
+        ctx.decode_paged(q, k_pool, v_pool, paged, lens, table_t, pps, pt, qh, kvh, d, split_tokens=split)
+        torch.cuda.synchronize()
+        assert torch.equal(dense, paged), split
+    # parity of a few sessions against the CPU oracle
+    dn = from_torch(dense).reshape(32, -1)
+    for b in (0, int(np.argmax(lens)), int(np.argmin(lens)), 17):
+        t = lens[b]
+        kb = from_torch(k[b, :t])
+        vb = from_torch(v[b, :t])
+        qb = from_torch(q[b])
+        assert max_abs_bf16(dn[b], _oracle_decode(qb, kb, vb, qh, kvh, d)) <= TOL, b
+    # the pool holds the dense bytes exactly: gather each session back
+    for b in (0, 5, 31):
+        t = lens[b]
+        rows = torch.empty((t, kvh, d), dtype=torch.int16, device="cuda")
+        ctx.pages_gather(k_pool, table_t[b], pt, kvh, d, 0, t, rows)
+        torch.cuda.synchronize()
+        assert torch.equal(rows, k[b, :t])
+
+
+def test_paged_parity_small_pages_and_tails(ctx):
+    rng = np.random.default_rng(21)
+    qh, kvh, d = 16, 4, 128
+    lens = [1, 15, 16, 17, 33, 300, 1023]
+    stride = 1024
+    for pt in (16, 32, 64):
+        kb = normal_bf16(rng, (len(lens), stride, kvh, d))
+        vb = normal_bf16(rng, (len(lens), stride, kvh, d))
+        qb = normal_bf16(rng, (len(lens), qh, d))
+        k, v, q = to_torch(kb), to_torch(vb), to_torch(qb)
+        k_pool, v_pool, table_t, pps, _ = _paged_pool(ctx, k, v, lens, stride, pt, seed=pt)
+        paged = torch.empty_like(q)
+        dense = torch.empty_like(q)
+        ctx.decode_paged(q, k_pool, v_pool, paged, lens, table_t, pps, pt, qh, kvh, d, split_tokens=64)
+        ctx.decode_dense(q, k, v, dense, lens, qh, kvh, d, seq_stride_tokens=stride, split_tokens=64)
+        torch.cuda.synchronize()
+        assert torch.equal(paged, dense), pt
+        got = from_torch(paged).reshape(len(lens), -1)
+        for b, t in enumerate(lens):
+            ref = _oracle_decode(qb[b], kb[b, :t], vb[b, :t], qh, kvh, d)
+            assert max_abs_bf16(got[b], ref) <= TOL, (pt, b)
+
+
+def test_decode_cfg4_shape_parity(ctx):
+    # BASELINE config 4 decode shape: B=4, T=32768, 64/8/128.  Two sequences
+    # are checked in full against the CPU oracle.
+    qh, kvh, d, t, batch = 64, 8, 128, 32768, 4
+    gen = torch.Generator(device="cuda").manual_seed(4)
+    k = torch.randn((batch, t, kvh, d), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    v = torch.randn((batch, t, kvh, d), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    q = torch.randn((batch, qh, d), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    out = torch.empty_like(q)
+    ctx.decode_dense(q, k, v, out, [t] * batch, qh, kvh, d, seq_stride_tokens=t)
+    torch.cuda.synchronize()
+    got = from_torch(out).reshape(batch, -1)
+    for b in (0, 3):
+        ref = _oracle_decode(from_torch(q[b]), from_torch(k[b]), from_torch(v[b]), qh, kvh, d)
+        assert max_abs_bf16(got[b], ref) <= TOL, b
+
+
+def test_extreme_scores_are_stable(ctx):
+    # portable.rs:712-726 analogue: one dominant key -> its V exactly.
+    qh, kvh, d, t = 8, 8, 128, 70
+    qb = oracle.write_bf16(np.full((1, qh, d), 8.0, np.float32))
+    k = np.zeros((t, kvh, d), np.float32)
+    k[37] = 8.0
+    k[5] = -8.0
+    v = np.tile(np.arange(t, dtype=np.float32)[:, None, None], (1, kvh, d))
+    got = oracle.read_bf16(_decode(ctx, qb, oracle.write_bf16(k), oracle.write_bf16(v), [t], qh, kvh, d))
+    assert np.all(got == 37.0)
+
+
+def test_decode_rejects_bad_arguments(ctx):
+    import mslim_attn
+    q = torch.zeros((1, 8, 128), dtype=torch.int16, device="cuda")
+    k = torch.zeros((64, 8, 128), dtype=torch.int16, device="cuda")
+    with pytest.raises(mslim_attn.MslimAttnError, match="alias"):
+        ctx.decode_dense(q, k, k, q, [64], 8, 8, 128)
+    out = torch.empty_like(q)
+    for kwargs, msg in [(dict(split_tokens=65), "split_tokens"), (dict(split_tokens=-64), "split_tokens")]:
+        with pytest.raises(mslim_attn.MslimAttnError, match=msg):
+            ctx.decode_dense(q, k, k, out, [64], 8, 8, 128, **kwargs)
+    with pytest.raises(mslim_attn.MslimAttnError, match="seq_lens"):
+        ctx.decode_dense(q, k, k, out, [0], 8, 8, 128)
+    with pytest.raises(mslim_attn.MslimAttnError, match="geometry"):
+        ctx.decode_dense(q, k, k, out, [64], 8, 3, 128)
+    table = torch.zeros((1, 4), dtype=torch.int32, device="cuda")
+    with pytest.raises(mslim_attn.MslimAttnError, match="page_tokens"):
+        ctx.decode_paged(q, k, k, out, [64], table, 4, 24, 8, 8, 128)
+    with pytest.raises(mslim_attn.MslimAttnError, match="shorter"):
+        ctx.decode_paged(q, k, k, out, [65], table, 4, 16, 8, 8, 128)

@@ -1,0 +1,144 @@
+"""GPU parity of causal prefill attention against the CPU oracle.
+
+Row i of a chunk attends keys 0..prior+i (llm_prefill_qk/softmax/pv,
+gpu_llm.cl:462-541; the CPU decoder processes prompts token by token,
+native_cpu_adapter.rs:486-534).  Tolerance: max abs <= 2e-2 on BF16 outputs.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from _data import from_torch, max_abs_bf16, normal_bf16, tiled_input, to_torch
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-2
+
+
+def _prefill(ctx, qb, kb, vb, queries, prior, qh, kvh, d):
+    q, k, v = to_torch(qb), to_torch(kb), to_torch(vb)
+    out = torch.empty_like(q)
+    ctx.prefill_causal(q, k, v, out, queries, prior, qh, kvh, d)
+    torch.cuda.synchronize()
+    return from_torch(out)
+
+
+@pytest.mark.parametrize("qh,kvh,d", [(32, 8, 128), (64, 8, 128), (8, 8, 128), (16, 8, 128),
+                                      (8, 2, 64), (4, 4, 64), (4, 2, 80), (12, 4, 128)])
+def test_prefill_small_shapes(ctx, qh, kvh, d):
+    rng = np.random.default_rng(qh * 7 + d)
+    for queries, prior in [(1, 0), (5, 0), (33, 7), (100, 0), (130, 60), (64, 64)]:
+        hist = prior + queries
+        qb = normal_bf16(rng, (queries, qh, d))
+        kb = normal_bf16(rng, (hist, kvh, d))
+        vb = normal_bf16(rng, (hist, kvh, d))
+        got = _prefill(ctx, qb, kb, vb, queries, prior, qh, kvh, d)
+        ref = oracle.prefill_causal_cpu(oracle.read_bf16(qb), kb, vb, qh, kvh, d, queries, prior)
+        err = max_abs_bf16(got, ref)
+        assert err <= TOL, (queries, prior, err)
+        gref = oracle.gpu_reference_attention(qb, kb, vb, qh, kvh, d, queries, prior)
+        assert max_abs_bf16(got, oracle.read_bf16(gref)) <= TOL
+
+
+def test_prefill_reference_inputs_multi_query(ctx):
+    # tiled_attention.rs:345-362: queries in {1, min(n,5)} at histories n.
+    qh, kvh, d = 8, 2, 128
+    for n in [1, 2, 31, 33, 63, 65, 129, 375]:
+        for queries in sorted({1, min(n, 5)}):
+            prior = n - queries
+            qb = tiled_input(queries * qh * d, 3).reshape(queries, qh, d)
+            kb = tiled_input(n * kvh * d, 7).reshape(n, kvh, d)
+            vb = tiled_input(n * kvh * d, 11).reshape(n, kvh, d)
+            got = _prefill(ctx, qb, kb, vb, queries, prior, qh, kvh, d)
+            ref = oracle.prefill_causal_cpu(oracle.read_bf16(qb), kb, vb, qh, kvh, d, queries, prior)
+            assert max_abs_bf16(got, ref) <= TOL, (n, queries)
+
+
+def _rows_reference(q_bits, k_bits, v_bits, rows, prior, qh, kvh, d):
+    out = {}
+    for r in rows:
+        n = prior + r + 1
+        out[r] = oracle.dense_attention_bf16(oracle.read_bf16(q_bits[r].reshape(-1)), k_bits[:n],
+                                             v_bits[:n], qh, kvh, d)
+    return out
+
+
+def test_prefill_cfg2_with_rope(ctx):
+    # S=2048, 32/8/128, RoPE theta=5e5 rotate-half applied
+    # to Q and K by the product's RoPE kernel, causal, fp32 accumulate.
+    s, qh, kvh, d = 2048, 32, 8, 128
+    rng = np.random.default_rng(2)
+    qb = normal_bf16(rng, (s, qh, d))
+    kb = normal_bf16(rng, (s, kvh, d))
+    vb = normal_bf16(rng, (s, kvh, d))
+    q_raw, k_raw, v = to_torch(qb), to_torch(kb), to_torch(vb)
+    q = torch.empty_like(q_raw)
+    k = torch.empty_like(k_raw)
+    ctx.rope(q_raw, q, s, qh, d, 0, 500000.0)
+    ctx.rope(k_raw, k, s, kvh, d, 0, 500000.0)
+    out = torch.empty_like(q)
+    ctx.prefill_causal(q, k, v, out, s, 0, qh, kvh, d)
+    torch.cuda.synchronize()
+    # the RoPE outputs are bit-exact against the oracle's restatement
+    q_rot = oracle.rope_gpu(qb, s, qh, d, 0, 500000.0).reshape(s, qh, d)
+    k_rot = oracle.rope_gpu(kb, s, kvh, d, 0, 500000.0).reshape(s, kvh, d)
+    assert np.array_equal(from_torch(q), q_rot)
+    assert np.array_equal(from_torch(k), k_rot)
+    got = from_torch(out)
+    rows = [0, 1, 31, 32, 63, 64, 127, 1000, 1023, 1024, 2046, 2047] + \
+        [int(x) for x in rng.integers(0, s, size=12)]
+    ref = _rows_reference(q_rot, k_rot, vb, rows, 0, qh, kvh, d)
+    for r in rows:
+        assert max_abs_bf16(got[r], ref[r]) <= TOL, r
+    # repeat is bit-identical and inputs are unmodified
+    out2 = torch.empty_like(q)
+    ctx.prefill_causal(q, k, v, out2, s, 0, qh, kvh, d)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2)
+    assert np.array_equal(from_torch(v), vb)
+
+
+def test_prefill_cfg4_shape_rows(ctx):
+    # BASELINE config 4 prefill shape: S=8192, 64/8/128.  Sampled rows.
+    s, qh, kvh, d = 8192, 64, 8, 128
+    gen = torch.Generator(device="cuda").manual_seed(8)
+    q = torch.randn((s, qh, d), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    k = torch.randn((s, kvh, d), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    v = torch.randn((s, kvh, d), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    out = torch.empty_like(q)
+    ctx.prefill_causal(q, k, v, out, s, 0, qh, kvh, d)
+    torch.cuda.synchronize()
+    got = from_torch(out)
+    qb, kb, vb = from_torch(q), from_torch(k), from_torch(v)
+    rows = [0, 8191, 4095, 4096, 127, 128, 5000, 7777]
+    ref = _rows_reference(qb, kb, vb, rows, 0, qh, kvh, d)
+    for r in rows:
+        assert max_abs_bf16(got[r], ref[r]) <= TOL, r
+
+
+def test_prefill_chunk_after_prior_matches_single_pass(ctx):
+    # a prompt processed as two chunks (prefill.rs chunking) equals one pass
+    qh, kvh, d, s = 16, 4, 128, 300
+    rng = np.random.default_rng(12)
+    qb = normal_bf16(rng, (s, qh, d))
+    kb = normal_bf16(rng, (s, kvh, d))
+    vb = normal_bf16(rng, (s, kvh, d))
+    whole = _prefill(ctx, qb, kb, vb, s, 0, qh, kvh, d)
+    second = _prefill(ctx, qb[200:], kb, vb, 100, 200, qh, kvh, d)
+    ref = oracle.prefill_causal_cpu(oracle.read_bf16(qb[200:]), kb, vb, qh, kvh, d, 100, 200)
+    assert max_abs_bf16(second, ref) <= TOL
+    assert max_abs_bf16(whole[200:], oracle.read_bf16(second)) <= TOL
+
+
+def test_prefill_rejects_bad_arguments(ctx):
+    import mslim_attn
+    q = torch.zeros((4, 8, 128), dtype=torch.int16, device="cuda")
+    k = torch.zeros((4, 8, 128), dtype=torch.int16, device="cuda")
+    with pytest.raises(mslim_attn.MslimAttnError, match="alias"):
+        ctx.prefill_causal(q, k, k, k, 4, 0, 8, 8, 128)
+    out = torch.empty_like(q)
+    with pytest.raises(mslim_attn.MslimAttnError):
+        ctx.prefill_causal(q, k, k, out, 0, 0, 8, 8, 128)
+    with pytest.raises(mslim_attn.MslimAttnError):
+        ctx.prefill_causal(q, k, k, out, 4, -1, 8, 8, 128)

@@ -1,0 +1,397 @@
+"""Pins the CPU oracle against the reference's own known answers, published
+vectors and closed forms (CPU only; no GPU).
+
+Each test names the reference test or fact it restates.  These checks are
+chosen so that a plausible mistake in the oracle (dropped term, wrong sign or
+index, transposed operand, wrong rounding) fails one of them.
+"""
+import hashlib
+import math
+import struct
+from concurrent.futures import ThreadPoolExecutor
+
+import numpy as np
+import pytest
+
+import oracle
+from _data import normal_bf16, tiled_input
+
+
+# ---- BF16 codec ---------------------------------------------------------
+def test_bf16_decode_every_encoding():
+    # tests/fixed_width_decode.rs:10-21: every 16-bit pattern decodes to the
+    # f32 whose high half it is.
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    dec = oracle.read_bf16(bits)
+    assert np.array_equal(dec.view(np.uint32), bits.astype(np.uint32) << 16)
+
+
+def test_bf16_encoders_agree_on_all_2_32_inputs():
+    # gpu_llm.cl:10-21 vs half 2.7.1's branch form vs an independent
+    # nearbyint()-based RNE, over every f32 bit pattern.
+    chunk = 1 << 29
+    with ThreadPoolExecutor(8) as pool:
+        bad = sum(pool.map(lambda s: oracle.bf16_encoder_mismatches(s, chunk),
+                           range(0, 1 << 32, chunk)))
+    assert bad == 0
+
+
+def test_bf16_encode_edge_cases():
+    lib = oracle.lib()
+    cases = {
+        1.0: 0x3F80, -0.0: 0x8000, float("inf"): 0x7F80, float("-inf"): 0xFF80,
+        # ties to even: 1 + 2^-8 is halfway between 1 and 1 + 2^-7
+        1.0 + 2.0 ** -8: 0x3F80, 1.0 + 3 * 2.0 ** -8: 0x3F82,
+        # largest finite rounds up to infinity past the midpoint
+        struct.unpack("<f", struct.pack("<I", 0x7F7FFFFF))[0]: 0x7F80,
+    }
+    for value, expected in cases.items():
+        assert lib.orc_write_bf16(value) == expected, value
+    # NaN keeps sign and upper payload, forces the quiet bit (gpu_llm.cl:16-17)
+    nan_small = struct.unpack("<f", struct.pack("<I", 0x7F800001))[0]
+    assert lib.orc_write_bf16(nan_small) == 0x7FC0
+    nan_neg = struct.unpack("<f", struct.pack("<I", 0xFFFFFFFF))[0]
+    assert lib.orc_write_bf16(nan_neg) == 0xFFFF
+
+
+# ---- Integrity primitives -------------------------------------------------
+def test_fnv1a64_published_vectors():
+    assert oracle.fnv1a64(b"") == 0xCBF29CE484222325
+    assert oracle.fnv1a64(b"a") == 0xAF63DC4C8601EC8C
+    assert oracle.fnv1a64(b"foobar") == 0x85944171F73967E8
+
+
+@pytest.mark.parametrize("msg", [b"", b"abc",
+                                 b"abcdbcdecdefdefgefghfghighijhijkijkljklmklmnlmnomnopnopq",
+                                 b"a" * 1000000])
+def test_sha256_fips_vectors(msg):
+    known = {
+        b"": "e3b0c44298fc1c149afbf4c8996fb92427ae41e4649b934ca495991b7852b855",
+        b"abc": "ba7816bf8f01cfea414140de5dae2223b00361a396177a9cb410ff61f20015ad",
+        b"abcdbcdecdefdefgefghfghighijhijkijkljklmklmnlmnomnopnopq":
+            "248d6a61d20638b8e5c026930c3e6039a33ce45964ff2167f6ecedd419db06c1",
+        b"a" * 1000000: "cdc76e5c9914fb9281a1c7e284d73e67f1809a48a497200e046d39ccc7112cd0",
+    }
+    assert oracle.sha256(msg).hex() == known[msg]
+    assert oracle.sha256(msg).hex() == hashlib.sha256(msg).hexdigest()
+
+
+# ---- ColdStore record -------------------------------------------------------
+def _geometry(page):
+    # cold_store.rs:975-984
+    return dict(layer=3, token_start=page * 4, tokens=4, heads=2, head_dim=4, tile=4)
+
+
+def _parse_record(rec: bytes):
+    hdr = rec[:104]
+    assert hdr[:8] == b"TSKVPG04"
+    version, header_len, page_id, layer, _, token_start, tokens, heads, head_dim, tile, \
+        key_len, value_len, kc, vc, khc, vhc = struct.unpack("<IIQIIQIIIIQQQQQQ", hdr[8:104])
+    return dict(version=version, header_len=header_len, page_id=page_id, layer=layer,
+                token_start=token_start, tokens=tokens, heads=heads, head_dim=head_dim,
+                tile=tile, key_len=key_len, value_len=value_len, kc=kc, vc=vc, khc=khc, vhc=vhc)
+
+
+def test_coldstore_record_committed_bytes():
+    # cold_store.rs:1118-1145: a 4-token, 2-head page with 32-byte K and V
+    # commits HEADER_LEN + 4*8*2 + 64 + FOOTER_LEN bytes.
+    g = _geometry(0)
+    rec = oracle.coldstore_record(0, g["layer"], g["token_start"], g["tokens"], g["heads"],
+                                  g["head_dim"], g["tile"], bytes([1] * 32), bytes([2] * 32))
+    assert len(rec) == 104 + 4 * 8 * 2 + 64 + 56
+
+
+def test_coldstore_record_layout_and_checksums():
+    # cold_store.rs:269-349 field by field, checked with independent Python
+    # FNV-1a and hashlib SHA-256 over the parsed parts.
+    def fnv(data, state=0xCBF29CE484222325):
+        for b in data:
+            state = ((state ^ b) * 0x100000001B3) & 0xFFFFFFFFFFFFFFFF
+        return state
+
+    key = bytes(range(32))
+    value = bytes(range(100, 132))
+    rec = oracle.coldstore_record(7, 3, 28, 4, 2, 4, 4, key, value)
+    h = _parse_record(rec)
+    assert (h["version"], h["header_len"], h["page_id"], h["layer"], h["token_start"]) == (3, 104, 7, 3, 28)
+    assert (h["tokens"], h["heads"], h["head_dim"], h["tile"]) == (4, 2, 4, 4)
+    assert (h["key_len"], h["value_len"]) == (32, 32)
+    kh = rec[104:136]
+    vh = rec[136:168]
+    assert rec[168:200] == key and rec[200:232] == value
+    # token hash covers all heads of the token, head-major payload
+    # (cold_store.rs:725-742): token t = bytes [h*16 + t*4, +4) for h = 0, 1
+    for t in range(4):
+        expected = fnv(key[t * 4:t * 4 + 4] + key[16 + t * 4:16 + t * 4 + 4])
+        assert struct.unpack("<Q", kh[8 * t:8 * t + 8])[0] == expected
+        expected_v = fnv(value[t * 4:t * 4 + 4] + value[16 + t * 4:16 + t * 4 + 4])
+        assert struct.unpack("<Q", vh[8 * t:8 * t + 8])[0] == expected_v
+    assert h["kc"] == fnv(key) and h["vc"] == fnv(value)
+    assert h["khc"] == fnv(kh) and h["vhc"] == fnv(vh)
+    footer = rec[-56:]
+    body = rec[:-56]
+    assert footer[:8] == b"TSKVCMIT"
+    assert struct.unpack("<Q", footer[8:16])[0] == fnv(body)
+    assert struct.unpack("<Q", footer[16:24])[0] == len(rec)
+    assert footer[24:] == hashlib.sha256(body).digest()
+
+
+def test_coldstore_rejects_invalid_geometry():
+    # cold_store.rs:702-723
+    with pytest.raises(ValueError):
+        oracle.coldstore_record(0, 0, 0, 0, 2, 4, 4, bytes(32), bytes(32))
+    with pytest.raises(ValueError):
+        oracle.coldstore_record(0, 0, 0, 4, 2, 6, 4, bytes(32), bytes(32))  # head_dim % tile
+    with pytest.raises(ValueError):
+        oracle.coldstore_record(0, 0, 0, 4, 3, 4, 4, bytes(32), bytes(32))  # not divisible
+
+
+def test_head_major_partial_layout_known_answer():
+    # cold_store.rs:1043-1072: value byte = head*10 + token, head-major;
+    # selecting tokens [1, 3] yields [1,3,11,13] rows.
+    value = bytes(b for head in range(2) for token in range(4) for b in [head * 10 + token] * 4)
+    pool = np.frombuffer(value, np.uint8)
+    page_of = np.zeros(4, np.uint32)
+    offset_of = np.arange(4, dtype=np.uint32)
+    out = oracle.gather_token_major(pool, 4, 2, 4, page_of, offset_of, np.array([1, 3], np.uint32))
+    # token-major: token 1 (head0, head1) then token 3
+    assert list(out) == [1] * 4 + [11] * 4 + [3] * 4 + [13] * 4
+
+
+def test_batched_pages_gather_known_answer():
+    # gpu_region_store.rs:991-1040: 37 tokens, 8 BF16 per token (2 kv heads x
+    # 4 dims), pages of 8 tokens -> 5 pages; dense and sparse reads return the
+    # original token-major bytes.
+    count, kvh, dim, page = 37, 2, 4, 8
+    keys = oracle.write_bf16(((np.arange(count * 8) % 59) - 29).astype(np.float32) * np.float32(0.03125))
+    values = oracle.write_bf16(((np.arange(count * 8) % 61) - 30).astype(np.float32) * np.float32(0.0625))
+    vb = values.view(np.uint8)
+    pages = []
+    page_of = np.zeros(count, np.uint32)
+    offset_of = np.zeros(count, np.uint32)
+    for start in range(0, count, page):
+        n = min(page, count - start)
+        hm = oracle.token_to_head_major(vb[start * 16:(start + n) * 16], n, kvh, dim * 2)
+        padded = np.zeros(page * 16, np.uint8)
+        # pool slots have room for `page` tokens: place each head's rows at stride page
+        for h in range(kvh):
+            padded[h * page * 8:(h * page + n) * 8] = hm[h * n * 8:(h + 1) * n * 8]
+        pages.append(padded)
+        page_of[start:start + n] = len(pages) - 1
+        offset_of[start:start + n] = np.arange(n)
+    assert len(pages) == 5
+    pool = np.concatenate(pages)
+    dense = oracle.gather_token_major(pool, page, kvh, dim * 2, page_of, offset_of,
+                                      np.arange(count, dtype=np.uint32))
+    assert dense.tobytes() == vb.tobytes()
+    sparse = np.array([0, 2, 4, 7, 8, 11, 23, 24, 36], np.uint32)
+    got = oracle.gather_token_major(pool, page, kvh, dim * 2, page_of, offset_of, sparse)
+    assert got.tobytes() == b"".join(vb[i * 16:(i + 1) * 16].tobytes() for i in sparse)
+
+
+def test_logical_kv_sha256_matches_independent_serialisation():
+    # gpu_region_store.rs:341-371: tag || u64 tokens || per layer K then V,
+    # [kvh][token][D].
+    rng = np.random.default_rng(5)
+    layers, tokens, kvh, d = 2, 5, 2, 4
+    ks = [normal_bf16(rng, (tokens, kvh, d)) for _ in range(layers)]
+    vs = [normal_bf16(rng, (tokens, kvh, d)) for _ in range(layers)]
+    h = hashlib.sha256(b"mslim-dense-kv-state-v1" + struct.pack("<Q", tokens))
+    for layer in range(layers):
+        for t in (ks[layer], vs[layer]):
+            h.update(np.ascontiguousarray(t.transpose(1, 0, 2)).tobytes())
+    assert oracle.logical_kv_sha256(ks, vs, tokens, kvh, d * 2) == h.hexdigest()
+    # a transposed serialisation must not collide
+    h2 = hashlib.sha256(b"mslim-dense-kv-state-v1" + struct.pack("<Q", tokens))
+    for layer in range(layers):
+        for t in (ks[layer], vs[layer]):
+            h2.update(t.tobytes())
+    assert oracle.logical_kv_sha256(ks, vs, tokens, kvh, d * 2) != h2.hexdigest()
+
+
+# ---- Attention oracles ----------------------------------------------------
+def _bits_f32(values):
+    return np.asarray(values, np.float32)
+
+
+def test_cpu_reference_zero_query_maps_kv_head():
+    # portable.rs:683-710 (MHA, GQA, MQA head maps): zero query -> uniform
+    # softmax over one token -> exactly the mapped kv head's V.
+    for qh, kvh in [(2, 2), (4, 2), (8, 1)]:
+        keys = np.zeros(kvh * 2, np.float32)
+        values = np.array([x for h in range(kvh) for x in (h + 1.0, -(h + 1.0))], np.float32)
+        rc, out = oracle.cpu_reference_decode(np.zeros(qh * 2), keys, values, 3, qh, kvh, 2)
+        assert rc == 0
+        for head in range(qh):
+            kv = head // (qh // kvh)
+            assert list(out[head * 2:head * 2 + 2]) == [values[kv * 2], values[kv * 2 + 1]]
+
+
+def test_cpu_reference_extreme_scores_exact():
+    # portable.rs:712-726: scores +/-1e8 -> output exactly 3.0
+    rc, out = oracle.cpu_reference_decode(np.array([10000.0]), np.array([10000.0, -10000.0], np.float32),
+                                          np.array([3.0, 9.0], np.float32), 3, 1, 1, 1)
+    assert rc == 0 and out.tolist() == [3.0]
+
+
+def test_cpu_reference_rejections():
+    # portable.rs:806-825
+    rc, _ = oracle.cpu_reference_decode(np.array([np.nan, 1.0]), np.array([1.0, 2.0], np.float32),
+                                        np.array([1.0, 2.0], np.float32), 3, 1, 1, 2)
+    assert rc == 2
+    rc, _ = oracle.cpu_reference_decode(np.zeros(3), np.zeros(2, np.float32), np.zeros(2, np.float32),
+                                        3, 3, 2, 1)
+    assert rc == 1
+
+
+def _brute_force(q, k, v, qh, kvh, d):
+    """Textbook softmax(QK^T / sqrt(D)) V in float64 with numpy."""
+    t = k.shape[0]
+    q = q.reshape(qh, d).astype(np.float64)
+    k = k.reshape(t, kvh, d).astype(np.float64)
+    v = v.reshape(t, kvh, d).astype(np.float64)
+    out = np.empty((qh, d))
+    for h in range(qh):
+        kh = h // (qh // kvh)
+        s = k[:, kh, :] @ q[h] / math.sqrt(d)
+        p = np.exp(s - s.max())
+        p /= p.sum()
+        out[h] = p @ v[:, kh, :]
+    return out.reshape(-1)
+
+
+@pytest.mark.parametrize("qh,kvh,d,t", [(4, 2, 8, 7), (8, 1, 16, 33), (4, 4, 32, 65), (32, 8, 128, 40)])
+def test_attention_oracles_match_brute_force(qh, kvh, d, t):
+    rng = np.random.default_rng(qh * 1000 + t)
+    qb = normal_bf16(rng, (qh * d,))
+    kb = normal_bf16(rng, (t, kvh, d))
+    vb = normal_bf16(rng, (t, kvh, d))
+    q = oracle.read_bf16(qb)
+    ref = _brute_force(q, oracle.read_bf16(kb), oracle.read_bf16(vb), qh, kvh, d)
+    rc, f64 = oracle.cpu_reference_decode(q, kb, vb, 1, qh, kvh, d)
+    assert rc == 0
+    assert np.max(np.abs(f64 - ref)) < 1e-6
+    dense = oracle.dense_attention_bf16(q, kb, vb, qh, kvh, d)
+    # BF16 output: half an ulp of |x| <= 4 is 2^-7
+    assert np.max(np.abs(dense - ref)) <= 2.0 ** -7
+    gpu_ref = oracle.gpu_reference_attention(qb, kb, vb, qh, kvh, d, 1, t - 1)
+    assert np.max(np.abs(oracle.read_bf16(gpu_ref) - ref)) <= 2.0 ** -7
+
+
+def test_gqa_head_map_is_not_interleaved():
+    # kvh = qh / group (portable.rs:443-448): with distinct V per kv head and a
+    # zero query, head h must return kv head h // group, never h % kv_heads.
+    qh, kvh, d, t = 8, 2, 4, 3
+    q = np.zeros(qh * d, np.float32)
+    kb = oracle.write_bf16(np.zeros((t, kvh, d), np.float32))
+    vals = np.zeros((t, kvh, d), np.float32)
+    vals[:, 0, :] = 1.0
+    vals[:, 1, :] = 2.0
+    out = oracle.dense_attention_bf16(q, kb, oracle.write_bf16(vals), qh, kvh, d).reshape(qh, d)
+    assert np.all(out[:4] == 1.0) and np.all(out[4:] == 2.0)
+
+
+def test_prefill_rows_are_causal():
+    # row i equals a decode over keys 0..prior+i and ignores later keys
+    rng = np.random.default_rng(11)
+    qh, kvh, d, prior, queries = 4, 2, 16, 3, 6
+    qb = normal_bf16(rng, (queries, qh, d))
+    kb = normal_bf16(rng, (prior + queries, kvh, d))
+    vb = normal_bf16(rng, (prior + queries, kvh, d))
+    q = oracle.read_bf16(qb)
+    out = oracle.prefill_causal_cpu(q, kb, vb, qh, kvh, d, queries, prior).reshape(queries, -1)
+    for i in range(queries):
+        n = prior + i + 1
+        ref = _brute_force(q[i].reshape(-1), oracle.read_bf16(kb[:n]), oracle.read_bf16(vb[:n]), qh, kvh, d)
+        assert np.max(np.abs(out[i] - ref)) <= 2.0 ** -7
+    # changing a future key leaves earlier rows untouched
+    kb2 = kb.copy()
+    kb2[-1] ^= 0x0100
+    out2 = oracle.prefill_causal_cpu(q, kb2, vb, qh, kvh, d, queries, prior).reshape(queries, -1)
+    assert np.array_equal(out[:-1], out2[:-1])
+
+
+def test_softmax_is_normalised():
+    # native_cpu_adapter.rs:1003-1008
+    p = oracle.softmax([1.0, 2.0, 3.0])
+    assert abs(float(p.sum()) - 1.0) < 1e-6
+    assert np.allclose(p, np.exp([1, 2, 3]) / np.exp([1, 2, 3]).sum(), rtol=1e-6)
+
+
+# ---- Feeders --------------------------------------------------------------
+def test_rms_norm_cpu_finite_and_bf16_rounded():
+    # native_cpu_adapter.rs:989-994
+    out = oracle.rms_norm_cpu([1.0, 2.0, 3.0, 4.0], [1.0] * 4, 1e-5)
+    assert np.all(np.isfinite(out))
+    assert np.array_equal(oracle.round_bf16(out), out)
+    # closed form: x / sqrt(mean(x^2) + eps), mean = 7.5
+    expected = np.array([1, 2, 3, 4]) / math.sqrt(7.5 + 1e-5)
+    assert np.max(np.abs(out - expected)) <= 2.0 ** -8 * 2
+
+
+def test_rmsnorm_gpu_form_matches_cpu_form():
+    rng = np.random.default_rng(3)
+    hidden = 4096
+    x = normal_bf16(rng, (2, hidden))
+    w = normal_bf16(rng, (hidden,), 0.5)
+    gpu = oracle.read_bf16(oracle.rmsnorm_gpu(x, w, 2, hidden, 1e-5)).reshape(2, hidden)
+    for t in range(2):
+        cpu = oracle.rms_norm_cpu(oracle.read_bf16(x[t]), oracle.read_bf16(w), 1e-5)
+        # only the sum-of-squares order differs: at most one BF16 ulp apart
+        ulp = np.abs(oracle.read_bf16(oracle.write_bf16(cpu)).view(np.int32) -
+                     gpu[t].view(np.int32))
+        assert ulp.max() <= 1 << 16
+
+
+LLAMA3_TABLE = [(0, 1.0), (20, 0.12868738), (40, 0.01656044), (60, 0.0013718937),
+                (80, 0.000034281024), (100, 0.0000044115345), (120, 0.0000005677088),
+                (126, 0.0000003068926)]
+
+
+@pytest.mark.parametrize("fd,expected", LLAMA3_TABLE)
+def test_llama3_rope_frequencies_match_transformers(fd, expected):
+    # gpu_llm/mod.rs:2849-2877 (transformers 4.51.3 _compute_llama3_parameters)
+    actual = oracle.rope_inverse_frequency(fd, 128, 500000.0, 1, 8.0, 1.0, 4.0, 8192.0)
+    assert abs(actual - expected) / expected <= 2.0e-6
+
+
+def test_rope_closed_form_and_identity():
+    rng = np.random.default_rng(9)
+    heads, d = 3, 8
+    x = normal_bf16(rng, (2, heads, d))
+    # position 0 is the identity (native_cpu_adapter.rs:996-1001), both forms
+    assert np.array_equal(oracle.rope_gpu(x[:1], 1, heads, d, 0, 10000.0), x[:1].reshape(-1))
+    assert np.array_equal(oracle.rope_cpu([1.0, 2.0, 3.0, 4.0], 1, 4, 0, 10000.0), [1.0, 2.0, 3.0, 4.0])
+    # rotate-half closed form at position p (GPU form, theta^(-2i/D))
+    p = 5
+    out = oracle.read_bf16(oracle.rope_gpu(x[1:], 1, heads, d, p, 10000.0)).reshape(heads, d)
+    xf = oracle.read_bf16(x[1]).astype(np.float64)
+    half = d // 2
+    for h in range(heads):
+        for i in range(d):
+            j = i % half
+            ang = p * 10000.0 ** (-2 * j / d)
+            c, s = math.cos(ang), math.sin(ang)
+            other = -xf[h, i + half] if i < half else xf[h, i - half]
+            assert abs(out[h, i] - (xf[h, i] * c + other * s)) <= 0.03 * (abs(xf[h]).max() + 1)
+    # the CPU form rotates the same way: both forms agree within one BF16 ulp
+    cpu = np.concatenate([oracle.rope_cpu(oracle.read_bf16(x[1, h]), 1, d, p, 10000.0) for h in range(heads)])
+    diff = np.abs(cpu.view(np.int32) - out.reshape(-1).view(np.int32))
+    assert diff.max() <= 1 << 16
+
+
+def test_swiglu_closed_form():
+    g = oracle.write_bf16(np.array([-4.0, -1.0, 0.0, 0.5, 1.0, 3.0, 20.0, -20.0], np.float32))
+    u = oracle.write_bf16(np.array([1.0, 2.0, -1.0, 4.0, 0.25, -3.0, 1.0, 1.0], np.float32))
+    out = oracle.read_bf16(oracle.swiglu(g, u))
+    gf = oracle.read_bf16(g).astype(np.float64)
+    uf = oracle.read_bf16(u).astype(np.float64)
+    expected = gf / (1 + np.exp(-gf)) * uf
+    assert np.all(np.abs(out - expected) <= np.abs(expected) * 2.0 ** -7 + 1e-30)
+    assert out[2] == 0.0  # silu(0) = 0
+
+
+def test_reference_tiled_input_generator():
+    # tiled_attention.rs:305-312 first values for salt 3: i=0 -> (39 % 257 - 128)/128
+    vals = oracle.read_bf16(tiled_input(3, 3))
+    assert vals.tolist() == [(39 - 128) / 128, (76 - 128) / 128, (113 - 128) / 128]

@@ -1,0 +1,476 @@
+// C ABI of libmslim_attn: context, buffers, argument checks and dispatch.
+// Declarations and reference citations live in include/mslim_attn.h.
+#include "../../include/mslim_attn.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <string>
+
+#include "kernels.hpp"
+#include "sha256.hpp"
+
+namespace {
+
+thread_local std::string g_error;
+
+// hipblaslt_bridge.cpp:26-34 conventions: -1 bad arguments, 100 + hipError_t.
+int fail(const std::string &message, int code = -1) {
+    g_error = message;
+    return code;
+}
+int check_hip(hipError_t code, const char *what) {
+    if (code == hipSuccess) return 0;
+    g_error = std::string(what) + ": " + hipGetErrorString(code);
+    return 100 + (int)code;
+}
+
+
+struct Context {
+    int device = 0;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    std::mutex mutex;
+    void *workspace = nullptr;
+    size_t workspace_bytes = 0;
+    void *staging = nullptr;       // device, digest serialisation
+    size_t staging_bytes = 0;
+    void *host_staging = nullptr;  // pinned host, digest readback
+    size_t host_staging_bytes = 0;
+
+    ~Context() {
+        if (stream) (void)hipStreamSynchronize(stream);
+        if (workspace) (void)hipFree(workspace);
+        if (staging) (void)hipFree(staging);
+        if (host_staging) (void)hipHostFree(host_staging);
+        if (own_stream) (void)hipStreamDestroy(own_stream);
+    }
+};
+
+Context *ctx_of(void *handle) { return static_cast<Context *>(handle); }
+
+// Grow a device scratch buffer; the stream is drained first so no queued
+// kernel still uses the old allocation.
+int grow_device(Context &c, void **mem, size_t *cap, size_t bytes, const char *what) {
+    if (*cap >= bytes) return 0;
+    if (*mem) {
+        if (int rc = check_hip(hipStreamSynchronize(c.stream), what)) return rc;
+        if (int rc = check_hip(hipFree(*mem), what)) return rc;
+    }
+    *mem = nullptr;
+    *cap = 0;
+    if (int rc = check_hip(hipMalloc(mem, bytes), what)) return rc;
+    *cap = bytes;
+    return 0;
+}
+
+int grow_host(void **mem, size_t *cap, size_t bytes, const char *what) {
+    if (*cap >= bytes) return 0;
+    if (*mem) (void)hipHostFree(*mem);
+    *mem = nullptr;
+    *cap = 0;
+    if (int rc = check_hip(hipHostMalloc(mem, bytes, hipHostMallocDefault), what)) return rc;
+    *cap = bytes;
+    return 0;
+}
+
+bool valid_geometry(int q_heads, int kv_heads, int head_dim) {
+    // portable.rs:420-441 plus the kernels' 16-byte row pieces and D <= 256
+    // (attention_kernel.rs:113-118 bounds the tiled kernel the same way).
+    return q_heads > 0 && kv_heads > 0 && q_heads % kv_heads == 0 && head_dim > 0 &&
+           head_dim <= 256 && head_dim % 8 == 0;
+}
+
+bool is_pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
+
+struct Lock {
+    explicit Lock(Context &c) : guard(c.mutex) { (void)hipSetDevice(c.device); }
+    std::lock_guard<std::mutex> guard;
+};
+
+int decode_common(Context &c, mslim::DecodeLaunch &l, const int32_t *seq_lens, int split_tokens) {
+    if (l.batch < 1 || l.batch > MSLIM_ATTN_MAX_BATCH || !seq_lens)
+        return fail("decode batch must be 1..64 with host seq_lens");
+    if (!valid_geometry(l.q_heads, l.kv_heads, l.head_dim))
+        return fail("decode geometry invalid (q_heads % kv_heads, head_dim multiple of 8 <= 256)");
+    if (!l.q || !l.k || !l.v || !l.out) return fail("decode needs non-null q, k, v, out");
+    if (l.out == l.q || l.out == l.k || l.out == l.v)
+        return fail("decode output must not alias read-only Q/K/V");
+    if (!(l.scale > 0.0f) || !std::isfinite(l.scale)) return fail("decode scale must be finite and > 0");
+    for (int i = 0; i < l.batch; ++i) {
+        if (seq_lens[i] < 1) return fail("decode seq_lens must be >= 1");
+        l.seq_len[i] = seq_lens[i];
+    }
+    if (split_tokens < 0 || split_tokens % 64)
+        return fail("split_tokens must be 0 or a positive multiple of 64");
+    l.split_tokens = split_tokens ? split_tokens
+                                  : mslim::decode_auto_split_tokens(seq_lens, l.batch, l.kv_heads);
+    int64_t splits = 0;
+    for (int i = 0; i < l.batch; ++i) splits += mslim::decode_splits(seq_lens[i], l.split_tokens);
+    const int group = l.q_heads / l.kv_heads;
+    const size_t ml_bytes = (size_t)splits * l.kv_heads * group * 2 * sizeof(float);
+    const size_t acc_bytes = (size_t)splits * l.kv_heads * group * l.head_dim * sizeof(float);
+    if (int rc = grow_device(c, &c.workspace, &c.workspace_bytes, ml_bytes + acc_bytes,
+                             "hipMalloc decode split workspace"))
+        return rc;
+    l.partial_ml = static_cast<float *>(c.workspace);
+    l.partial_acc = reinterpret_cast<float *>(static_cast<char *>(c.workspace) + ml_bytes);
+    return check_hip(mslim::launch_decode(l, c.stream), "decode attention launch");
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *mslim_attn_last_error(void) { return g_error.c_str(); }
+
+void *mslim_attn_ctx_new(void) {
+    g_error.clear();
+    if (const char *ov = std::getenv("HSA_OVERRIDE_GFX_VERSION")) {
+        g_error = std::string("HSA_OVERRIDE_GFX_VERSION=") + ov +
+                  " is refused: the kernels are built for native gfx950 only";
+        return nullptr;
+    }
+    int count = 0;
+    if (check_hip(hipGetDeviceCount(&count), "hipGetDeviceCount")) return nullptr;
+    if (count < 1) {
+        g_error = "No HIP GPU device";
+        return nullptr;
+    }
+    int device = 0;
+    if (check_hip(hipGetDevice(&device), "hipGetDevice")) return nullptr;
+    hipDeviceProp_t props{};
+    if (check_hip(hipGetDeviceProperties(&props, device), "hipGetDeviceProperties")) return nullptr;
+    if (std::strncmp(props.gcnArchName, "gfx950", 6) != 0) {
+        g_error = std::string("mslim_attn requires a gfx950 (MI355X) device, found ") + props.gcnArchName;
+        return nullptr;
+    }
+    auto *c = new (std::nothrow) Context;
+    if (!c) {
+        g_error = "Out of memory for mslim_attn context";
+        return nullptr;
+    }
+    c->device = device;
+    if (check_hip(hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking), "hipStreamCreate")) {
+        delete c;
+        return nullptr;
+    }
+    c->stream = c->own_stream;
+    return c;
+}
+
+void mslim_attn_ctx_destroy(void *ctx) { delete ctx_of(ctx); }
+
+int mslim_attn_ctx_set_stream(void *ctx, void *hip_stream) {
+    g_error.clear();
+    if (!ctx) return fail("null context");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    c.stream = static_cast<hipStream_t>(hip_stream);
+    return 0;
+}
+
+int mslim_attn_synchronize(void *ctx) {
+    g_error.clear();
+    if (!ctx) return fail("null context");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    return check_hip(hipStreamSynchronize(c.stream), "hipStreamSynchronize");
+}
+
+void *mslim_attn_buf_alloc(void *ctx, size_t bytes) {
+    g_error.clear();
+    if (!ctx || !bytes) {
+        g_error = "invalid buffer allocation";
+        return nullptr;
+    }
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    void *p = nullptr;
+    if (check_hip(hipMalloc(&p, bytes), "hipMalloc buffer")) return nullptr;
+    return p;
+}
+
+void *mslim_attn_buf_upload(void *ctx, const uint8_t *bytes, size_t byte_length) {
+    g_error.clear();
+    if (!ctx || !bytes || !byte_length) {
+        g_error = "Invalid upload payload";
+        return nullptr;
+    }
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    void *p = nullptr;
+    if (check_hip(hipMalloc(&p, byte_length), "hipMalloc upload")) return nullptr;
+    if (check_hip(hipMemcpy(p, bytes, byte_length, hipMemcpyHostToDevice), "hipMemcpy upload")) {
+        (void)hipFree(p);
+        return nullptr;
+    }
+    return p;
+}
+
+int mslim_attn_buf_free(void *ctx, void *buffer) {
+    g_error.clear();
+    if (!ctx || !buffer) return fail("invalid buffer handle");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    if (int rc = check_hip(hipStreamSynchronize(c.stream), "hipStreamSynchronize before free")) return rc;
+    return check_hip(hipFree(buffer), "hipFree buffer");
+}
+
+int mslim_attn_buf_read(void *ctx, const void *buffer, size_t offset, uint8_t *out, size_t size) {
+    g_error.clear();
+    if (!ctx || !buffer || !out || !size) return fail("invalid buffer readback");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    if (int rc = check_hip(hipMemcpyAsync(out, static_cast<const char *>(buffer) + offset, size,
+                                          hipMemcpyDeviceToHost, c.stream),
+                           "hipMemcpy readback"))
+        return rc;
+    return check_hip(hipStreamSynchronize(c.stream), "hipStreamSynchronize readback");
+}
+
+int mslim_attn_buf_write(void *ctx, void *buffer, size_t offset, const uint8_t *in, size_t size) {
+    g_error.clear();
+    if (!ctx || !buffer || !in || !size) return fail("invalid buffer write");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    if (int rc = check_hip(hipMemcpyAsync(static_cast<char *>(buffer) + offset, in, size,
+                                          hipMemcpyHostToDevice, c.stream),
+                           "hipMemcpy write"))
+        return rc;
+    return check_hip(hipStreamSynchronize(c.stream), "hipStreamSynchronize write");
+}
+
+int mslim_attn_decode_dense(void *ctx, const void *q, const void *k, const void *v, void *out,
+                            int batch, const int32_t *seq_lens, int64_t seq_stride_tokens,
+                            int q_heads, int kv_heads, int head_dim, float scale,
+                            int split_tokens) {
+    g_error.clear();
+    if (!ctx) return fail("null context");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    mslim::DecodeLaunch l{};
+    l.q = static_cast<const uint16_t *>(q);
+    l.k = static_cast<const uint16_t *>(k);
+    l.v = static_cast<const uint16_t *>(v);
+    l.out = static_cast<uint16_t *>(out);
+    l.batch = batch; l.q_heads = q_heads; l.kv_heads = kv_heads; l.head_dim = head_dim;
+    l.scale = scale;
+    l.paged = false;
+    l.seq_stride_tokens = seq_stride_tokens;
+    if (seq_lens && batch >= 1 && batch <= MSLIM_ATTN_MAX_BATCH) {
+        for (int i = 0; i < batch; ++i)
+            if (seq_lens[i] > seq_stride_tokens && batch > 1)
+                return fail("dense decode: seq_lens exceed seq_stride_tokens");
+    }
+    if (batch > 1 && seq_stride_tokens < 1) return fail("dense decode: seq_stride_tokens must be >= 1");
+    return decode_common(c, l, seq_lens, split_tokens);
+}
+
+int mslim_attn_decode_paged(void *ctx, const void *q, const void *k_pool, const void *v_pool,
+                            void *out, int batch, const int32_t *seq_lens,
+                            const int32_t *page_table, int pages_per_seq, int page_tokens,
+                            int q_heads, int kv_heads, int head_dim, float scale,
+                            int split_tokens) {
+    g_error.clear();
+    if (!ctx) return fail("null context");
+    if (!page_table) return fail("paged decode needs a device page table");
+    if (!is_pow2(page_tokens) || page_tokens < 16 || page_tokens > 4096)
+        return fail("page_tokens must be a power of two in 16..4096");
+    if (seq_lens && batch >= 1 && batch <= MSLIM_ATTN_MAX_BATCH) {
+        for (int i = 0; i < batch; ++i)
+            if ((int64_t)pages_per_seq * page_tokens < seq_lens[i])
+                return fail("paged decode: page table row shorter than the sequence");
+    }
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    mslim::DecodeLaunch l{};
+    l.q = static_cast<const uint16_t *>(q);
+    l.k = static_cast<const uint16_t *>(k_pool);
+    l.v = static_cast<const uint16_t *>(v_pool);
+    l.out = static_cast<uint16_t *>(out);
+    l.batch = batch; l.q_heads = q_heads; l.kv_heads = kv_heads; l.head_dim = head_dim;
+    l.scale = scale;
+    l.paged = true;
+    l.page_table = page_table;
+    l.pages_per_seq = pages_per_seq;
+    l.page_tokens = page_tokens;
+    return decode_common(c, l, seq_lens, split_tokens);
+}
+
+int mslim_attn_prefill_causal(void *ctx, const void *q, const void *k, const void *v, void *out,
+                              int queries, int prior, int q_heads, int kv_heads, int head_dim,
+                              float scale) {
+    g_error.clear();
+    if (!ctx) return fail("null context");
+    if (!valid_geometry(q_heads, kv_heads, head_dim)) return fail("prefill geometry invalid");
+    if (queries < 1 || prior < 0 || (int64_t)queries + prior > INT32_MAX - 64)
+        return fail("prefill needs queries >= 1, prior >= 0 and a 32-bit history");
+    if (!q || !k || !v || !out) return fail("prefill needs non-null q, k, v, out");
+    if (out == q || out == k || out == v) return fail("prefill output must not alias read-only Q/K/V");
+    if (!(scale > 0.0f) || !std::isfinite(scale)) return fail("prefill scale must be finite and > 0");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    mslim::PrefillLaunch l{};
+    l.q = static_cast<const uint16_t *>(q);
+    l.k = static_cast<const uint16_t *>(k);
+    l.v = static_cast<const uint16_t *>(v);
+    l.out = static_cast<uint16_t *>(out);
+    l.queries = queries; l.prior = prior; l.q_heads = q_heads; l.kv_heads = kv_heads;
+    l.head_dim = head_dim; l.scale = scale;
+    if (int rc = check_hip(mslim::launch_prefill(l, c.stream), "prefill attention launch")) return rc;
+    return 0;
+}
+
+int mslim_attn_rmsnorm(void *ctx, const void *input, const void *weight, void *output, int tokens,
+                       int hidden, float epsilon) {
+    g_error.clear();
+    if (!ctx || !input || !weight || !output || tokens < 1 || hidden < 1 || !std::isfinite(epsilon) ||
+        epsilon < 0.0f)
+        return fail("invalid RMSNorm arguments");
+    if (output == input || output == weight) return fail("RMSNorm output must not alias its inputs");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    return check_hip(mslim::launch_rmsnorm(static_cast<const uint16_t *>(input),
+                                           static_cast<const uint16_t *>(weight),
+                                           static_cast<uint16_t *>(output), tokens, hidden, epsilon,
+                                           c.stream),
+                     "RMSNorm launch");
+}
+
+int mslim_attn_rope(void *ctx, const void *input, void *output, int tokens, int heads, int head_dim,
+                    int start_position, float theta, int llama3_scaling, float factor,
+                    float low_freq_factor, float high_freq_factor, float original_max_position) {
+    g_error.clear();
+    if (!ctx || !input || !output || tokens < 1 || heads < 1 || head_dim < 2 || head_dim % 2 ||
+        start_position < 0 || !(theta > 0.0f) || !std::isfinite(theta))
+        return fail("invalid RoPE arguments");
+    if (output == input) return fail("RoPE output must not alias its input");
+    if (llama3_scaling && (!(factor > 0.0f) || !(high_freq_factor > low_freq_factor) ||
+                           !(low_freq_factor > 0.0f) || !(original_max_position > 0.0f)))
+        return fail("invalid llama3 RoPE scaling parameters");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    return check_hip(mslim::launch_rope(static_cast<const uint16_t *>(input),
+                                        static_cast<uint16_t *>(output), tokens, heads, head_dim,
+                                        start_position, theta, llama3_scaling, factor,
+                                        low_freq_factor, high_freq_factor, original_max_position,
+                                        c.stream),
+                     "RoPE launch");
+}
+
+int mslim_attn_swiglu(void *ctx, const void *gate, const void *up, void *output, size_t n) {
+    g_error.clear();
+    if (!ctx || !gate || !up || !output || !n) return fail("invalid SwiGLU arguments");
+    if (output == gate || output == up) return fail("SwiGLU output must not alias its inputs");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    return check_hip(mslim::launch_swiglu(static_cast<const uint16_t *>(gate),
+                                          static_cast<const uint16_t *>(up),
+                                          static_cast<uint16_t *>(output), n, c.stream),
+                     "SwiGLU launch");
+}
+
+int mslim_attn_pages_write(void *ctx, void *k_pool, void *v_pool, const int32_t *page_table,
+                           int page_tokens, int kv_heads, int head_dim, int64_t first_token,
+                           int64_t tokens, const void *k_rows, const void *v_rows) {
+    g_error.clear();
+    if (!ctx || !k_pool || !v_pool || !page_table || !k_rows || !v_rows || tokens < 1 ||
+        first_token < 0 || kv_heads < 1 || head_dim < 8 || head_dim % 8 || !is_pow2(page_tokens) ||
+        page_tokens < 16)
+        return fail("invalid page write arguments");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    return check_hip(mslim::launch_pages_write(
+                         static_cast<uint16_t *>(k_pool), static_cast<uint16_t *>(v_pool), page_table,
+                         page_tokens, kv_heads, head_dim, first_token, tokens,
+                         static_cast<const uint16_t *>(k_rows), static_cast<const uint16_t *>(v_rows),
+                         c.stream),
+                     "page write launch");
+}
+
+int mslim_attn_pages_gather(void *ctx, const void *pool, const int32_t *page_table, int page_tokens,
+                            int kv_heads, int head_dim, int64_t first_token, int64_t tokens,
+                            void *rows_out) {
+    g_error.clear();
+    if (!ctx || !pool || !page_table || !rows_out || tokens < 1 || first_token < 0 || kv_heads < 1 ||
+        head_dim < 8 || head_dim % 8 || !is_pow2(page_tokens) || page_tokens < 16)
+        return fail("invalid page gather arguments");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    return check_hip(mslim::launch_pages_gather(static_cast<const uint16_t *>(pool), page_table,
+                                                page_tokens, kv_heads, head_dim, first_token, tokens,
+                                                static_cast<uint16_t *>(rows_out), c.stream),
+                     "page gather launch");
+}
+
+int mslim_attn_logical_kv_sha256(void *ctx, int layers, int64_t tokens, int kv_heads, int head_dim,
+                                 const void *const *keys, const void *const *values,
+                                 const int32_t *const *page_tables, int page_tokens,
+                                 char *hex_out) {
+    g_error.clear();
+    if (!ctx || layers < 1 || tokens < 0 || kv_heads < 1 || head_dim < 8 || head_dim % 8 || !keys ||
+        !values || !hex_out)
+        return fail("invalid logical K/V digest arguments");
+    if (page_tables && (!is_pow2(page_tokens) || page_tokens < 16))
+        return fail("paged digest needs page_tokens a power of two >= 16");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    mslim::Sha256 sha;
+    static const char tag[] = "mslim-dense-kv-state-v1";
+    sha.update(tag, sizeof tag - 1);
+    uint8_t le[8];
+    for (int i = 0; i < 8; ++i) le[i] = (uint8_t)((uint64_t)tokens >> (8 * i));
+    sha.update(le, 8);
+    const int64_t chunk_tokens = std::max<int64_t>(1, std::min<int64_t>(tokens, (int64_t)1 << 16));
+    const size_t chunk_bytes = (size_t)chunk_tokens * head_dim * 2;
+    if (tokens > 0) {
+        if (int rc = grow_device(c, &c.staging, &c.staging_bytes, chunk_bytes, "hipMalloc digest staging"))
+            return rc;
+        if (int rc = grow_host(&c.host_staging, &c.host_staging_bytes, chunk_bytes,
+                               "hipHostMalloc digest staging"))
+            return rc;
+    }
+    for (int layer = 0; layer < layers && tokens > 0; ++layer) {
+        const void *parts[2] = {keys[layer], values[layer]};
+        const int32_t *table = page_tables ? page_tables[layer] : nullptr;
+        if (!parts[0] || !parts[1] || (page_tables && !table))
+            return fail("logical K/V digest: null layer buffer");
+        for (int p = 0; p < 2; ++p)
+            for (int h = 0; h < kv_heads; ++h)
+                for (int64_t t0 = 0; t0 < tokens; t0 += chunk_tokens) {
+                    const int64_t n = std::min(chunk_tokens, tokens - t0);
+                    if (int rc = check_hip(mslim::launch_canonical_rows(
+                                               static_cast<const uint16_t *>(parts[p]), table, page_tokens,
+                                               kv_heads, head_dim, h, t0, n,
+                                               static_cast<uint16_t *>(c.staging), c.stream),
+                                           "digest serialisation launch"))
+                        return rc;
+                    const size_t bytes = (size_t)n * head_dim * 2;
+                    if (int rc = check_hip(hipMemcpyAsync(c.host_staging, c.staging, bytes,
+                                                          hipMemcpyDeviceToHost, c.stream),
+                                           "digest readback"))
+                        return rc;
+                    if (int rc = check_hip(hipStreamSynchronize(c.stream), "digest readback sync"))
+                        return rc;
+                    sha.update(c.host_staging, bytes);
+                }
+    }
+    uint8_t digest[32];
+    sha.finish(digest);
+    static const char hexd[] = "0123456789abcdef";
+    for (int i = 0; i < 32; ++i) {
+        hex_out[2 * i] = hexd[digest[i] >> 4];
+        hex_out[2 * i + 1] = hexd[digest[i] & 15];
+    }
+    hex_out[64] = '\0';
+    return 0;
+}
+
+}  // extern "C"

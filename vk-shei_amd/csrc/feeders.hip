@@ -1,0 +1,135 @@
+// RMSNorm, RoPE and SwiGLU feeding the attention path.
+//
+// These keep the reference's BF16 stage roundings and reduction order exactly
+// (gpu_llm.cl:72-146, :225-237, :378-456), so for identical inputs they are
+// bit-identical to the C restatement used as the checker.  Two choices make
+// that possible and are the only departures from the OpenCL text:
+//   * 1/sqrt is the correctly rounded square root followed by a correctly
+//     rounded division (OpenCL's rsqrt has no fixed rounding);
+//   * exp, log, sin and cos are evaluated in double precision and rounded
+//     once to float.
+// No multiply-add is contracted: every stage rounds as written.
+#include "common.hpp"
+#include "kernels.hpp"
+
+#pragma clang fp contract(off)
+
+namespace mslim {
+
+namespace {
+
+// llm_rmsnorm / llm_prefill_norm (gpu_llm.cl:72-98, :378-408): one workgroup
+// of 128 lanes per token, strided FMA sum of squares, 64..1 tree.
+__global__ __launch_bounds__(128) void rmsnorm_kernel(const uint16_t *in, const uint16_t *w,
+                                                      uint16_t *out, int hidden, float eps) {
+    __shared__ float partials[128];
+    const int tid = threadIdx.x;
+    const uint16_t *row = in + (int64_t)blockIdx.x * hidden;
+    uint16_t *dst = out + (int64_t)blockIdx.x * hidden;
+    float s = 0.0f;
+    for (int i = tid; i < hidden; i += 128) {
+        const float v = read_bf16(row[i]);
+        s = __fmaf_rn(v, v, s);
+    }
+    partials[tid] = s;
+    __syncthreads();
+    for (int stride = 64; stride > 0; stride >>= 1) {
+        if (tid < stride) partials[tid] = __fadd_rn(partials[tid], partials[tid + stride]);
+        __syncthreads();
+    }
+    const float mean = __fdiv_rn(partials[0], (float)hidden);
+    const float factor = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, eps)));
+    for (int i = tid; i < hidden; i += 128) {
+        const uint16_t normalized = write_bf16(__fmul_rn(read_bf16(row[i]), factor));
+        dst[i] = write_bf16(__fmul_rn(read_bf16(normalized), read_bf16(w[i])));
+    }
+}
+
+// Inverse frequency of rotary dimension pair `fd` (kernels.rs:51-66,
+// gpu_llm.cl:123-138), f32 arithmetic with once-rounded log and exp.
+__device__ float rope_inverse_frequency(int fd, int head_dim, float theta, int llama3, float factor,
+                                        float low, float high, float original_max) {
+    const float log_theta = (float)log((double)theta);
+    const float exponent = __fdiv_rn(__fmul_rn(-(float)fd, log_theta), (float)head_dim);
+    float inv = (float)exp((double)exponent);
+    if (llama3) {
+        const float wavelength = __fdiv_rn(6.28318530717958647692f, inv);
+        const float low_wavelength = __fdiv_rn(original_max, low);
+        const float high_wavelength = __fdiv_rn(original_max, high);
+        if (wavelength > low_wavelength) {
+            inv = __fdiv_rn(inv, factor);
+        } else if (wavelength >= high_wavelength) {
+            const float smooth = __fdiv_rn(__fsub_rn(__fdiv_rn(original_max, wavelength), low),
+                                           __fsub_rn(high, low));
+            inv = __fadd_rn(__fmul_rn(__fsub_rn(1.0f, smooth), __fdiv_rn(inv, factor)),
+                            __fmul_rn(smooth, inv));
+        }
+    }
+    return inv;
+}
+
+// llm_rope / llm_prefill_rope (gpu_llm.cl:102-146, :412-456): one lane per
+// element, rotate-half partner, c and s rounded to BF16.
+__global__ __launch_bounds__(256) void rope_kernel(const uint16_t *in, uint16_t *out, int64_t total,
+                                                   int heads, int head_dim, int start, float theta,
+                                                   int llama3, float factor, float low, float high,
+                                                   float original_max) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= total) return;
+    const int64_t elements = (int64_t)heads * head_dim;
+    const int64_t token = i / elements;
+    const int in_token = (int)(i % elements);
+    const int head = in_token / head_dim;
+    const int d = in_token % head_dim;
+    const int half = head_dim / 2;
+    const int64_t src = token * elements + (int64_t)head * head_dim + (d < half ? d + half : d - half);
+    const float partner = read_bf16(in[src]);
+    const float rotated = d < half ? -partner : partner;
+    const int fd = (d % half) * 2;
+    const float inv = rope_inverse_frequency(fd, head_dim, theta, llama3, factor, low, high, original_max);
+    const float phase = __fmul_rn((float)(start + token), inv);
+    const float cs = round_bf16((float)cos((double)phase));
+    const float sn = round_bf16((float)sin((double)phase));
+    const float left = round_bf16(__fmul_rn(read_bf16(in[i]), cs));
+    const float right = round_bf16(__fmul_rn(rotated, sn));
+    out[i] = write_bf16(__fadd_rn(left, right));
+}
+
+// llm_swiglu (gpu_llm.cl:225-237): BF16(BF16(g / (1 + e^-g)) * u).
+__global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t *gate, const uint16_t *up,
+                                                     uint16_t *out, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float g = read_bf16(gate[i]);
+    const float e = (float)exp(-(double)g);
+    const float activated = __fdiv_rn(g, __fadd_rn(1.0f, e));
+    out[i] = write_bf16(__fmul_rn(round_bf16(activated), read_bf16(up[i])));
+}
+
+}  // namespace
+
+hipError_t launch_rmsnorm(const uint16_t *in, const uint16_t *w, uint16_t *out, int tokens,
+                          int hidden, float eps, hipStream_t stream) {
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)tokens), dim3(128), 0, stream, in, w, out, hidden,
+                       eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope(const uint16_t *in, uint16_t *out, int tokens, int heads, int head_dim,
+                       int start, float theta, int llama3, float factor, float low, float high,
+                       float original_max, hipStream_t stream) {
+    const int64_t total = (int64_t)tokens * heads * head_dim;
+    const unsigned blocks = (unsigned)((total + 255) / 256);
+    hipLaunchKernelGGL(rope_kernel, dim3(blocks), dim3(256), 0, stream, in, out, total, heads, head_dim,
+                       start, theta, llama3, factor, low, high, original_max);
+    return hipGetLastError();
+}
+
+hipError_t launch_swiglu(const uint16_t *gate, const uint16_t *up, uint16_t *out, size_t n,
+                         hipStream_t stream) {
+    const unsigned blocks = (unsigned)((n + 255) / 256);
+    hipLaunchKernelGGL(swiglu_kernel, dim3(blocks), dim3(256), 0, stream, gate, up, out, (int64_t)n);
+    return hipGetLastError();
+}
+
+}  // namespace mslim

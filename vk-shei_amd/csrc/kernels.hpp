@@ -1,0 +1,74 @@
+// Host-side launch interface of the gfx950 kernels (one translation unit per
+// kernel family).  Every launcher validates nothing: the C ABI layer checks
+// shapes, pointers and limits before calling it.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mslim {
+
+constexpr int kMaxBatch = 64;
+
+struct DecodeLaunch {
+    const uint16_t *q;
+    const uint16_t *k;  // dense cache base or K page pool
+    const uint16_t *v;  // dense cache base or V page pool
+    uint16_t *out;
+    float *partial_ml;   // [splits_total][kv_heads][G][2]
+    float *partial_acc;  // [splits_total][kv_heads][G][D]
+    const int32_t *page_table;  // paged only: [batch][pages_per_seq]
+    int64_t seq_stride_tokens;  // dense only
+    int pages_per_seq;
+    int page_tokens;            // paged only, multiple of 16
+    int batch, q_heads, kv_heads, head_dim;
+    float scale;
+    int split_tokens;           // multiple of 64
+    int seq_len[kMaxBatch];
+    int split_begin[kMaxBatch + 1];
+    bool paged;
+};
+
+// Number of split partitions of a sequence of `tokens` tokens.
+inline int decode_splits(int tokens, int split_tokens) {
+    return (tokens + split_tokens - 1) / split_tokens;
+}
+// Library choice of split_tokens for a batch: about 2048 wavefronts in total,
+// at least 64 and at most 4096 tokens per split.
+int decode_auto_split_tokens(const int32_t *seq_lens, int batch, int kv_heads);
+// True when the MFMA fast path covers this geometry.
+bool decode_fast_path(int head_dim, int group);
+hipError_t launch_decode(const DecodeLaunch &a, hipStream_t stream);
+
+struct PrefillLaunch {
+    const uint16_t *q, *k, *v;
+    uint16_t *out;
+    int queries, prior, q_heads, kv_heads, head_dim;
+    float scale;
+};
+bool prefill_fast_path(int head_dim, int group);
+hipError_t launch_prefill(const PrefillLaunch &a, hipStream_t stream);
+
+hipError_t launch_rmsnorm(const uint16_t *in, const uint16_t *w, uint16_t *out, int tokens,
+                          int hidden, float eps, hipStream_t stream);
+hipError_t launch_rope(const uint16_t *in, uint16_t *out, int tokens, int heads, int head_dim,
+                       int start, float theta, int llama3, float factor, float low, float high,
+                       float original_max, hipStream_t stream);
+hipError_t launch_swiglu(const uint16_t *gate, const uint16_t *up, uint16_t *out, size_t n,
+                         hipStream_t stream);
+
+hipError_t launch_pages_write(uint16_t *k_pool, uint16_t *v_pool, const int32_t *page_table,
+                              int page_tokens, int kv_heads, int head_dim, int64_t first_token,
+                              int64_t tokens, const uint16_t *k_rows, const uint16_t *v_rows,
+                              hipStream_t stream);
+hipError_t launch_pages_gather(const uint16_t *pool, const int32_t *page_table, int page_tokens,
+                               int kv_heads, int head_dim, int64_t first_token, int64_t tokens,
+                               uint16_t *rows_out, hipStream_t stream);
+// Canonical head-major serialisation of one layer tensor: tokens
+// [first, first+count) of kv head `head` into out[count][head_dim]
+// (dense token-major source when page_table is null).
+hipError_t launch_canonical_rows(const uint16_t *src, const int32_t *page_table, int page_tokens,
+                                 int kv_heads, int head_dim, int head, int64_t first,
+                                 int64_t count, uint16_t *out, hipStream_t stream);
+
+}  // namespace mslim

@@ -1,0 +1,244 @@
+"""Python binding of libmslim_attn, the gfx950 attention hot path of M-SLIM.
+
+The library is a C ABI (``include/mslim_attn.h``); this module binds it with
+ctypes the way ``native_hip.rs`` binds the reference bridge with libloading:
+fixed in-tree path, every symbol resolved up front, a context handle, and
+failures turned into exceptions carrying ``"{stage} failed: code={code}:
+{details}"`` (native_hip.rs:38-49).
+
+PyTorch is used only as plumbing: tensors provide device memory and the current
+HIP stream.  There is no CPU or torch fallback: if the library is missing or
+the device is not gfx950 the calls raise.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+import os
+from typing import Optional, Sequence
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libmslim_attn.so")
+
+MAX_BATCH = 64
+
+EXPORTS = (
+    "mslim_attn_last_error",
+    "mslim_attn_ctx_new",
+    "mslim_attn_ctx_destroy",
+    "mslim_attn_ctx_set_stream",
+    "mslim_attn_synchronize",
+    "mslim_attn_buf_alloc",
+    "mslim_attn_buf_upload",
+    "mslim_attn_buf_free",
+    "mslim_attn_buf_read",
+    "mslim_attn_buf_write",
+    "mslim_attn_decode_dense",
+    "mslim_attn_decode_paged",
+    "mslim_attn_prefill_causal",
+    "mslim_attn_rmsnorm",
+    "mslim_attn_rope",
+    "mslim_attn_swiglu",
+    "mslim_attn_pages_write",
+    "mslim_attn_pages_gather",
+    "mslim_attn_logical_kv_sha256",
+)
+
+
+class MslimAttnError(RuntimeError):
+    def __init__(self, stage: str, code: int, details: str):
+        super().__init__(f"{stage} failed: code={code}: {details}")
+        self.stage = stage
+        self.code = code
+        self.details = details
+
+
+class LibraryMissing(MslimAttnError):
+    pass
+
+
+_lib: Optional[C.CDLL] = None
+
+
+def library() -> C.CDLL:
+    """Load the in-tree libmslim_attn.so and declare every exported symbol."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise LibraryMissing("load libmslim_attn", -1,
+                             f"{LIB_PATH} is not built (run __graft_entry__.build())")
+    lib = C.CDLL(LIB_PATH)
+    P, I, SZ, F, I64 = C.c_void_p, C.c_int, C.c_size_t, C.c_float, C.c_int64
+    PI32 = C.POINTER(C.c_int32)
+    sigs = {
+        "mslim_attn_last_error": (C.c_char_p, []),
+        "mslim_attn_ctx_new": (P, []),
+        "mslim_attn_ctx_destroy": (None, [P]),
+        "mslim_attn_ctx_set_stream": (I, [P, P]),
+        "mslim_attn_synchronize": (I, [P]),
+        "mslim_attn_buf_alloc": (P, [P, SZ]),
+        "mslim_attn_buf_upload": (P, [P, P, SZ]),
+        "mslim_attn_buf_free": (I, [P, P]),
+        "mslim_attn_buf_read": (I, [P, P, SZ, P, SZ]),
+        "mslim_attn_buf_write": (I, [P, P, SZ, P, SZ]),
+        "mslim_attn_decode_dense": (I, [P, P, P, P, P, I, PI32, I64, I, I, I, F, I]),
+        "mslim_attn_decode_paged": (I, [P, P, P, P, P, I, PI32, P, I, I, I, I, I, F, I]),
+        "mslim_attn_prefill_causal": (I, [P, P, P, P, P, I, I, I, I, I, F]),
+        "mslim_attn_rmsnorm": (I, [P, P, P, P, I, I, F]),
+        "mslim_attn_rope": (I, [P, P, P, I, I, I, I, F, I, F, F, F, F]),
+        "mslim_attn_swiglu": (I, [P, P, P, P, SZ]),
+        "mslim_attn_pages_write": (I, [P, P, P, P, I, I, I, I64, I64, P, P]),
+        "mslim_attn_pages_gather": (I, [P, P, P, I, I, I, I64, I64, P]),
+        "mslim_attn_logical_kv_sha256": (I, [P, I, I64, I, I, P, P, P, I, C.c_char_p]),
+    }
+    for name in EXPORTS:
+        res, args = sigs[name]
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def last_error() -> str:
+    msg = library().mslim_attn_last_error()
+    return msg.decode("utf-8", "replace") if msg else "native error unavailable"
+
+
+def _ptr(t) -> int:
+    """Device pointer of a torch tensor (or an int that already is one)."""
+    if isinstance(t, int):
+        return t
+    if t is None:
+        return 0
+    if not t.is_contiguous():
+        raise ValueError("mslim_attn needs contiguous tensors")
+    return t.data_ptr()
+
+
+def _lens(seq_lens: Sequence[int]):
+    arr = (C.c_int32 * len(seq_lens))(*[int(x) for x in seq_lens])
+    return arr
+
+
+def default_scale(head_dim: int) -> float:
+    """f32 1/sqrt(D) as the reference computes it (native_cpu_adapter.rs:235-237)."""
+    import numpy as np
+    return float(np.float32(1.0) / np.sqrt(np.float32(head_dim)))
+
+
+class Context:
+    """A gfx950 context: owns the split-KV workspace and a HIP stream."""
+
+    def __init__(self, stream: Optional[int] = None):
+        lib = library()
+        handle = lib.mslim_attn_ctx_new()
+        if not handle:
+            raise MslimAttnError("mslim_attn_ctx_new", 0, last_error())
+        self._h = handle
+        self._lib = lib
+        if stream is not None:
+            self.set_stream(stream)
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self._lib.mslim_attn_ctx_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, stage: str, rc: int) -> None:
+        if rc != 0:
+            raise MslimAttnError(stage, rc, last_error())
+
+    @property
+    def handle(self) -> int:
+        return self._h
+
+    def set_stream(self, stream: Optional[int]) -> None:
+        """Run on HIP stream `stream` (0 or None is the null stream)."""
+        self._check("set_stream", self._lib.mslim_attn_ctx_set_stream(self._h, stream or None))
+
+    def use_torch_stream(self) -> None:
+        import torch
+        self.set_stream(torch.cuda.current_stream().cuda_stream)
+
+    def synchronize(self) -> None:
+        self._check("synchronize", self._lib.mslim_attn_synchronize(self._h))
+
+    # ---- attention -----------------------------------------------------
+    def decode_dense(self, q, k, v, out, seq_lens: Sequence[int], q_heads: int, kv_heads: int,
+                     head_dim: int, seq_stride_tokens: int = 0, scale: Optional[float] = None,
+                     split_tokens: int = 0) -> None:
+        scale = default_scale(head_dim) if scale is None else scale
+        self._check("decode_dense", self._lib.mslim_attn_decode_dense(
+            self._h, _ptr(q), _ptr(k), _ptr(v), _ptr(out), len(seq_lens), _lens(seq_lens),
+            seq_stride_tokens, q_heads, kv_heads, head_dim, scale, split_tokens))
+
+    def decode_paged(self, q, k_pool, v_pool, out, seq_lens: Sequence[int], page_table,
+                     pages_per_seq: int, page_tokens: int, q_heads: int, kv_heads: int,
+                     head_dim: int, scale: Optional[float] = None, split_tokens: int = 0) -> None:
+        scale = default_scale(head_dim) if scale is None else scale
+        self._check("decode_paged", self._lib.mslim_attn_decode_paged(
+            self._h, _ptr(q), _ptr(k_pool), _ptr(v_pool), _ptr(out), len(seq_lens),
+            _lens(seq_lens), _ptr(page_table), pages_per_seq, page_tokens, q_heads, kv_heads,
+            head_dim, scale, split_tokens))
+
+    def prefill_causal(self, q, k, v, out, queries: int, prior: int, q_heads: int,
+                       kv_heads: int, head_dim: int, scale: Optional[float] = None) -> None:
+        scale = default_scale(head_dim) if scale is None else scale
+        self._check("prefill_causal", self._lib.mslim_attn_prefill_causal(
+            self._h, _ptr(q), _ptr(k), _ptr(v), _ptr(out), queries, prior, q_heads, kv_heads,
+            head_dim, scale))
+
+    # ---- feeders --------------------------------------------------------
+    def rmsnorm(self, x, weight, out, tokens: int, hidden: int, eps: float) -> None:
+        self._check("rmsnorm", self._lib.mslim_attn_rmsnorm(
+            self._h, _ptr(x), _ptr(weight), _ptr(out), tokens, hidden, eps))
+
+    def rope(self, x, out, tokens: int, heads: int, head_dim: int, start_position: int,
+             theta: float, llama3_scaling: bool = False, factor: float = 1.0,
+             low_freq_factor: float = 1.0, high_freq_factor: float = 2.0,
+             original_max_position: float = 1.0) -> None:
+        self._check("rope", self._lib.mslim_attn_rope(
+            self._h, _ptr(x), _ptr(out), tokens, heads, head_dim, start_position, theta,
+            int(bool(llama3_scaling)), factor, low_freq_factor, high_freq_factor,
+            original_max_position))
+
+    def swiglu(self, gate, up, out, n: int) -> None:
+        self._check("swiglu", self._lib.mslim_attn_swiglu(self._h, _ptr(gate), _ptr(up),
+                                                          _ptr(out), n))
+
+    # ---- ColdStore-exact page pool --------------------------------------
+    def pages_write(self, k_pool, v_pool, page_table_row, page_tokens: int, kv_heads: int,
+                    head_dim: int, first_token: int, tokens: int, k_rows, v_rows) -> None:
+        self._check("pages_write", self._lib.mslim_attn_pages_write(
+            self._h, _ptr(k_pool), _ptr(v_pool), _ptr(page_table_row), page_tokens, kv_heads,
+            head_dim, first_token, tokens, _ptr(k_rows), _ptr(v_rows)))
+
+    def pages_gather(self, pool, page_table_row, page_tokens: int, kv_heads: int, head_dim: int,
+                     first_token: int, tokens: int, rows_out) -> None:
+        self._check("pages_gather", self._lib.mslim_attn_pages_gather(
+            self._h, _ptr(pool), _ptr(page_table_row), page_tokens, kv_heads, head_dim,
+            first_token, tokens, _ptr(rows_out)))
+
+    def logical_kv_sha256(self, keys: Sequence, values: Sequence, tokens: int, kv_heads: int,
+                          head_dim: int, page_tables: Optional[Sequence] = None,
+                          page_tokens: int = 0) -> str:
+        n = len(keys)
+        kp = (C.c_void_p * n)(*[_ptr(k) for k in keys])
+        vp = (C.c_void_p * n)(*[_ptr(v) for v in values])
+        tp = (C.c_void_p * n)(*[_ptr(t) for t in page_tables]) if page_tables else None
+        out = C.create_string_buffer(65)
+        self._check("logical_kv_sha256", self._lib.mslim_attn_logical_kv_sha256(
+            self._h, n, tokens, kv_heads, head_dim, kp, vp, tp, page_tokens, out))
+        return out.value.decode()
+
+
+def split_count(tokens: int, split_tokens: int) -> int:
+    return math.ceil(tokens / split_tokens)
