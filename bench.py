@@ -1,0 +1,356 @@
+#!/usr/bin/env python3
+"""Benchmark of the M-SLIM attention hot path on one MI355X.
+
+Workload (the largest single-GPU configuration and
+the one the targets are quoted on):
+  * decode: batch 4 x 32,768-token context, 64 query / 8 KV heads, head_dim
+    128, BF16 K/V in the ColdStore-exact page pool (16-token pages): cold
+    pages in a seeded random permutation plus a contiguous 4,096-token hot
+    recent window per sequence;
+  * causal prefill of 8,192 tokens at the same head shape.
+One step = one paged decode pass + one causal prefill pass.  Inputs are
+resident in HBM before timing starts.
+
+`value` is the decode's achieved HBM bandwidth (algorithmic K+V+Q+O bytes /
+average decode launch time measured with HIP events on the launch stream);
+the prefill's TFLOP/s is reported beside it under "prefill".  The CPU
+baseline is the C oracle's restatement of the reference CPU attention
+(native_cpu_adapter.rs:253-307), parallel over query heads like the
+reference's rayon loop (:273-276), timed on a bounded sample of the same
+workload on this host.
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--cpu-seconds 10]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "vk-shei_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "decode-attn HBM GB/s (% of peak) + causal prefill TFLOP/s, bf16 GQA d=128"
+PEAK_HBM_GBPS = 8000.0      # MI355X HBM3E, published
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense BF16 MFMA, published
+
+B, T, QH, KVH, D = 4, 32768, 64, 8, 128
+PAGE_TOKENS, HOT_WINDOW = 16, 4096
+S_PREFILL = 8192
+
+
+def decode_bytes() -> int:
+    # K + V read once, Q read, O written (BF16).
+    return B * T * KVH * D * 2 * 2 + B * QH * D * 2 * 2
+
+
+def prefill_flops() -> int:
+    # causal incl. diagonal, QK^T + PV at 2 FLOP/MAC: 2*D*QH*S*(S+1)
+    return 2 * D * QH * S_PREFILL * (S_PREFILL + 1)
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def build_page_pool(ctx, torch, k_dense, v_dense, seed: int):
+    """Scatter the dense caches into a page pool: per sequence the cold pages
+    are a seeded random permutation of pool slots, the hot window is one
+    contiguous run of slots."""
+    import numpy as np
+
+    pages_per_seq = T // PAGE_TOKENS
+    hot_pages = HOT_WINDOW // PAGE_TOKENS
+    cold_pages = pages_per_seq - hot_pages
+    total = B * pages_per_seq
+    rng = np.random.default_rng(seed)
+    cold_slots = rng.permutation(B * cold_pages).astype(np.int32)
+    table = np.zeros((B, pages_per_seq), np.int32)
+    for b in range(B):
+        table[b, :cold_pages] = cold_slots[b * cold_pages:(b + 1) * cold_pages]
+        table[b, cold_pages:] = B * cold_pages + b * hot_pages + np.arange(hot_pages, dtype=np.int32)
+    table_t = torch.from_numpy(table).cuda()
+    k_pool = torch.empty((total, KVH, PAGE_TOKENS, D), dtype=torch.int16, device="cuda")
+    v_pool = torch.empty_like(k_pool)
+    for b in range(B):
+        ctx.pages_write(k_pool, v_pool, table_t[b], PAGE_TOKENS, KVH, D, 0, T, k_dense[b], v_dense[b])
+    return k_pool, v_pool, table_t, pages_per_seq
+
+
+def cpu_threads() -> int:
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+def cpu_decode_baseline(k_host, v_host, q_host, seconds: float):
+    """Oracle dense_attention_bf16 over whole cfg4 sequences, one task per
+    query head (rayon's par_chunks_mut over heads), until `seconds` pass."""
+    import numpy as np
+    from concurrent.futures import ThreadPoolExecutor
+
+    import oracle
+
+    threads = cpu_threads()
+    group = QH // KVH
+    per_head_k = [np.ascontiguousarray(k_host[:, :, h, :]) for h in range(KVH)]
+    per_head_v = [np.ascontiguousarray(v_host[:, :, h, :]) for h in range(KVH)]
+    q_f32 = oracle.read_bf16(q_host)
+
+    def head(args):
+        b, qh = args
+        kv = qh // group
+        return oracle.dense_attention_bf16(q_f32[b, qh], per_head_k[kv][b], per_head_v[kv][b], 1, 1, D)
+
+    seqs = 0
+    start = time.perf_counter()
+    with ThreadPoolExecutor(threads) as pool:
+        while True:
+            b = seqs % B
+            list(pool.map(head, [(b, h) for h in range(QH)]))
+            seqs += 1
+            if time.perf_counter() - start >= seconds:
+                break
+    elapsed = time.perf_counter() - start
+    per_seq_bytes = decode_bytes() // B
+    return {
+        "value": round(seqs * per_seq_bytes / elapsed / 1e9, 4),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"{seqs} cfg4 decode sequences (32,768 tokens, 64/8 heads, d=128) through the "
+                   f"oracle's dense_attention_bf16 (native_cpu_adapter.rs:253-307), one task per "
+                   f"query head, {elapsed:.1f} s"),
+    }
+
+
+def cpu_prefill_baseline(q_host, k_host, v_host, seconds: float):
+    """Per-row causal loop (the CPU decoder's prompt path) on sampled rows of
+    the 8,192-token prefill; FLOP counted exactly for the rows done."""
+    import numpy as np
+    from concurrent.futures import ThreadPoolExecutor
+
+    import oracle
+
+    threads = cpu_threads()
+    group = QH // KVH
+    per_head_k = [np.ascontiguousarray(k_host[:, h, :]) for h in range(KVH)]
+    per_head_v = [np.ascontiguousarray(v_host[:, h, :]) for h in range(KVH)]
+    q_f32 = oracle.read_bf16(q_host)
+    rows = [int(r) for r in np.random.default_rng(7).permutation(S_PREFILL)]
+
+    def head(args):
+        r, qh = args
+        kv = qh // group
+        return oracle.dense_attention_bf16(q_f32[r, qh], per_head_k[kv][:r + 1], per_head_v[kv][:r + 1],
+                                           1, 1, D)
+
+    done, flops = 0, 0
+    start = time.perf_counter()
+    with ThreadPoolExecutor(threads) as pool:
+        while done < len(rows):
+            r = rows[done]
+            list(pool.map(head, [(r, h) for h in range(QH)]))
+            flops += 4 * QH * D * (r + 1)
+            done += 1
+            if time.perf_counter() - start >= seconds:
+                break
+    elapsed = time.perf_counter() - start
+    return {
+        "value": round(flops / elapsed / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"{done} random rows of the 8,192-token causal prefill (64/8 heads, d=128), each "
+                   f"row a dense_attention_bf16 over its causal prefix, {elapsed:.1f} s; rate "
+                   f"extrapolates to the full prefill by exact FLOP count"),
+    }
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="CPU baseline budget per leg (0 skips the CPU baseline)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
+              f"(no multi-GPU path is built; see DESIGN.md for how decode and prefill would shard)",
+              file=sys.stderr)
+        return 2
+    if args.steps < 1 or args.warmup < 0:
+        print("--steps must be >= 1 and --warmup >= 0", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    import mslim_attn
+
+    torch.cuda.set_device(0)
+    ctx = mslim_attn.Context()
+    ctx.use_torch_stream()
+
+    log("bench: generating cfg4 inputs on device")
+    gen = torch.Generator(device="cuda").manual_seed(0x4D534C49)
+
+    def randn(shape):
+        return torch.randn(shape, generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+
+    k_dense = randn((B, T, KVH, D))
+    v_dense = randn((B, T, KVH, D))
+    q_dec = randn((B, QH, D))
+    k_pool, v_pool, table, pages_per_seq = build_page_pool(ctx, torch, k_dense, v_dense, seed=20261201)
+    out_dec = torch.empty_like(q_dec)
+    out_dense = torch.empty_like(q_dec)
+    q_pre = randn((S_PREFILL, QH, D))
+    k_pre = randn((S_PREFILL, KVH, D))
+    v_pre = randn((S_PREFILL, KVH, D))
+    out_pre = torch.empty_like(q_pre)
+    lens = [T] * B
+
+    def decode():
+        ctx.decode_paged(q_dec, k_pool, v_pool, out_dec, lens, table, pages_per_seq, PAGE_TOKENS,
+                         QH, KVH, D)
+
+    def prefill():
+        ctx.prefill_causal(q_pre, k_pre, v_pre, out_pre, S_PREFILL, 0, QH, KVH, D)
+
+    # The paged ColdStore-exact decode must equal the dense decode bit for bit.
+    decode()
+    ctx.decode_dense(q_dec, k_dense, v_dense, out_dense, lens, QH, KVH, D, seq_stride_tokens=T)
+    torch.cuda.synchronize()
+    paged_equals_dense = bool(torch.equal(out_dec, out_dense))
+
+    log(f"bench: warmup {args.warmup} steps")
+    for _ in range(args.warmup):
+        decode()
+        prefill()
+    torch.cuda.synchronize()
+
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
+           torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start_all = torch.cuda.Event(enable_timing=True)
+    end_all = torch.cuda.Event(enable_timing=True)
+    start_all.record()
+    for i in range(args.steps):
+        ev[i][0].record()
+        decode()
+        ev[i][1].record()
+        prefill()
+        ev[i][2].record()
+    end_all.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    step_ms = start_all.elapsed_time(end_all) / args.steps
+    dec_ms = [a.elapsed_time(b) for a, b, _ in ev]
+    pre_ms = [b.elapsed_time(c) for _, b, c in ev]
+    dec_avg = sum(dec_ms) / len(dec_ms)
+    pre_avg = sum(pre_ms) / len(pre_ms)
+    log(f"bench: {args.steps} steps, {step_ms:.3f} ms/step (wall {wall * 1e3 / args.steps:.3f}), "
+        f"decode {dec_avg * 1e3:.1f} us, prefill {pre_avg * 1e3:.1f} us")
+
+    # dense decode on the same data, for reference
+    for _ in range(3):
+        ctx.decode_dense(q_dec, k_dense, v_dense, out_dense, lens, QH, KVH, D, seq_stride_tokens=T)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        ctx.decode_dense(q_dec, k_dense, v_dense, out_dense, lens, QH, KVH, D, seq_stride_tokens=T)
+    e1.record()
+    torch.cuda.synchronize()
+    dense_ms = e0.elapsed_time(e1) / args.steps
+
+    dec_gbps = decode_bytes() / (dec_avg * 1e-3) / 1e9
+    pre_tflops = prefill_flops() / (pre_avg * 1e-3) / 1e12
+    dense_gbps = decode_bytes() / (dense_ms * 1e-3) / 1e9
+
+    traffic = None
+    traffic_file = os.path.join(ROOT, "profiles", "decode_paged_cfg4_traffic.json")
+    if os.path.exists(traffic_file):
+        with open(traffic_file) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    cpu = None
+    if args.cpu_seconds > 0:
+        log("bench: CPU baseline (oracle on host cores)")
+        k_h = k_dense.cpu().numpy().view(np.uint16)
+        v_h = v_dense.cpu().numpy().view(np.uint16)
+        q_h = q_dec.cpu().numpy().view(np.uint16)
+        cpu = cpu_decode_baseline(k_h, v_h, q_h, args.cpu_seconds)
+        cpu["prefill"] = cpu_prefill_baseline(q_pre.cpu().numpy().view(np.uint16),
+                                              k_pre.cpu().numpy().view(np.uint16),
+                                              v_pre.cpu().numpy().view(np.uint16), args.cpu_seconds)
+        cpu["host_cpu"] = cpu_model()
+        cpu["host_nproc"] = os.cpu_count()
+
+    result = {
+        "metric": METRIC,
+        "value": round(dec_gbps, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: torch.randn N(0,1) with a fixed seed on device, rounded to bf16 (RNE)",
+        "config": {
+            "workload": "BASELINE cfg4: paged ColdStore-exact decode B=4 x T=32768 (4096-token hot "
+                        "window + cold 16-token pages) and causal prefill S=8192, 64/8 heads, d=128",
+            "batch": B, "context_tokens": T, "q_heads": QH, "kv_heads": KVH, "head_dim": D,
+            "page_tokens": PAGE_TOKENS, "hot_window_tokens": HOT_WINDOW,
+            "prefill_tokens": S_PREFILL,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(dec_gbps, 2),
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": round(dec_gbps / PEAK_HBM_GBPS, 4),
+            "traffic": traffic,
+            "kernel": "decode paged (split + merge launches), algorithmic bytes "
+                      f"{decode_bytes()} per launch",
+        },
+        "prefill": {
+            "value": round(pre_tflops, 2),
+            "unit": "TFLOP/s",
+            "ms": round(pre_avg, 4),
+            "roofline": {
+                "bound": "mfma",
+                "achieved": round(pre_tflops, 2),
+                "peak": PEAK_BF16_TFLOPS,
+                "unit": "TFLOP/s",
+                "frac": round(pre_tflops / PEAK_BF16_TFLOPS, 4),
+                "traffic": None,
+                "kernel": f"prefill_mfma_kernel<128,4>, algorithmic FLOP {prefill_flops()} per launch",
+            },
+        },
+        "decode_ms": round(dec_avg, 5),
+        "decode_dense_gbps": round(dense_gbps, 2),
+        "paged_equals_dense": paged_equals_dense,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+    ctx.close()
+    return 0 if paged_equals_dense else 1
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -37,7 +37,7 @@ struct Context {
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
     std::mutex mutex;
-    void *workspace = nullptr;
+    void *workspace = nullptr;      // decode split partials
     size_t workspace_bytes = 0;
     void *staging = nullptr;       // device, digest serialisation
     size_t staging_bytes = 0;

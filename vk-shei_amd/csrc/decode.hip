@@ -6,18 +6,22 @@
 // (tiled_attention.cl:9-155).
 //
 // Decode reads every K and V byte once, so it is an HBM stream.  One
-// wavefront owns one (sequence, kv head, split) partition of `split_tokens`
-// logical tokens and serves all G query heads of the GQA group from the same
-// K/V bytes:
+// workgroup of four wavefronts owns one (sequence, kv head, split)
+// partition of `split_tokens` logical tokens and serves all G query heads of
+// the GQA group from the same K/V bytes:
+//   * the four wavefronts take interleaved 32-token tiles, so together they
+//     stream one contiguous region;
+//   * each wavefront keeps a ring of DEPTH tiles of K and V in registers, so
+//     DEPTH-1 tiles stay in flight while one is computed;
 //   * Q.K^T for the group runs on v_mfma_f32_16x16x32_bf16 with the 16 tokens
-//     of a block as M and the (zero padded) G heads as N.  Each lane loads
-//     64 contiguous bytes of one K row as its A operand, so a 16-token block
-//     is four 128-bit loads per lane and no K byte passes through LDS.
+//     of a block as M and the (zero padded) G heads as N.  Each lane loads 64
+//     contiguous bytes of one K row as its A operand, so no K byte passes
+//     through LDS;
 //   * the online softmax max / sum run on 64-lane butterflies;
 //   * P.V accumulates in fp32 on the VALU from 128-bit V loads (16 lanes per
 //     256-byte row for D = 128), with P broadcast through a 2 KB LDS tile;
-//   * the next 32-token tile's K and V are in flight while the current one is
-//     computed.
+//   * the four wavefronts merge in LDS; the partitions of one (sequence, kv
+//     head) are merged in fixed partition order by a second, small launch.
 // Partitions are fixed by logical token index, and the paged and dense
 // variants differ only in how a 16-token block's base address is formed, so
 // both produce bit-identical outputs (the reference's dense == ColdStore
@@ -30,6 +34,9 @@
 namespace mslim {
 
 namespace {
+
+constexpr int kWaves = 4;
+constexpr int kTile = 32;
 
 struct DeviceArgs {
     const uint16_t *q, *k, *v;
@@ -46,8 +53,7 @@ struct DeviceArgs {
     int split_begin[kMaxBatch + 1];
 };
 
-// Base of the 16-token block starting at logical token t0 (a multiple of 16)
-// and the element stride between its rows.
+// Base of the 16-token block starting at logical token t0 (a multiple of 16).
 template <int D, bool PAGED>
 __device__ __forceinline__ const uint16_t *block_base(const DeviceArgs &a, const uint16_t *cache,
                                                       int b, int kvh, int t0) {
@@ -61,31 +67,61 @@ __device__ __forceinline__ const uint16_t *block_base(const DeviceArgs &a, const
     }
 }
 
+// Element stride between consecutive token rows inside a 16-token block.
 template <int D, bool PAGED>
-__device__ __forceinline__ int64_t row_stride(const DeviceArgs &a) {
+__device__ __forceinline__ int row_stride(const DeviceArgs &a) {
     if constexpr (PAGED) return D;
-    else return (int64_t)a.kv_heads * D;
+    else return a.kv_heads * D;
 }
 
-// Sequence owning global split index sg (uniform scalar search).
 __device__ __forceinline__ int sequence_of(const DeviceArgs &a, int sg) {
     int b = 0;
     while (b + 1 < a.batch && a.split_begin[b + 1] <= sg) ++b;
     return b;
 }
 
-template <int D, int G, bool PAGED>
-__global__ __launch_bounds__(64) void decode_split_kernel(DeviceArgs a) {
-    constexpr int KS = D / 32;        // MFMA k-steps per 16-token block
+// Ordering point for LDS traffic inside one wavefront: a wavefront's LDS
+// operations execute in order, so only the compiler must not move them.
+__device__ __forceinline__ void wave_lds_fence() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int D>
+struct TileRegs {
+    static constexpr int KS = D / 32;
+    static constexpr int NV = D / 16;  // 128-bit V loads per 32-token tile
+    bf16x8_t k[2][KS];
+    uint4 v[NV];
+};
+
+// Byte pick for v_perm_b32: low half = bf16 `e` of `lo_src`, high half =
+// bf16 `e` of `hi_src` (e = 0 or 1 inside the dword).
+__device__ __forceinline__ uint32_t pair_bf16(uint32_t hi_src, uint32_t lo_src, int e) {
+    // v_perm_b32 numbering: bytes 0-3 come from the second operand, 4-7 from
+    // the first.
+    const uint32_t sel = e ? 0x07060302u : 0x05040100u;
+    return __builtin_amdgcn_perm(hi_src, lo_src, sel);
+}
+
+template <int D, int G, bool PAGED, int DEPTH>
+__global__ __launch_bounds__(64 * kWaves, 2) void decode_kernel(DeviceArgs a) {
+    constexpr int KS = D / 32;        // Q.K MFMA k-steps per 16-token block
     constexpr int LPR = D / 8;        // lanes per V row (8 BF16 per lane)
     constexpr int RPI = 64 / LPR;     // V rows per load instruction
-    constexpr int NV = 32 / RPI;      // V loads per 32-token tile
-    constexpr int GP = G < 4 ? 4 : G; // LDS row of P, float4 aligned
+    constexpr int NV = kTile / RPI;   // V loads per tile = consecutive rows per lane
+    constexpr int NS = D / 16;        // P.V MFMA output slices of 16 dims
+    constexpr int VT = kTile + 8;     // transposed V row (one dim), in elements
+    static_assert(G <= 16, "one MFMA N tile covers the GQA group");
 
-    __shared__ float p_lds[2][32][GP];
-    __shared__ float alpha_lds[2][GP];
+    __shared__ __align__(16) uint16_t vt_lds[kWaves][D * VT];
+    __shared__ float comb_ml[kWaves][G][2];
+    __shared__ float comb_acc[kWaves][G][D];
 
-    const int lane = threadIdx.x;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int row16 = lane & 15;
     const int grp = lane >> 4;
     const int kvh = blockIdx.x % a.kv_heads;
@@ -96,73 +132,83 @@ __global__ __launch_bounds__(64) void decode_split_kernel(DeviceArgs a) {
     const int seq_len = a.seq_len[b];
     const int begin = split * a.split_tokens;
     const int end = min(seq_len, begin + a.split_tokens);
+    const int ntiles = (end - begin + kTile - 1) / kTile;
     const int qh0 = kvh * G;
     const float c = a.scale_log2e;
-    const int64_t rs = row_stride<D, PAGED>(a);
+    const int rs = row_stride<D, PAGED>(a);
+    uint16_t *vt = vt_lds[wave];
 
-    // Q as the B operand: lane holds head row16, dims j*32 + grp*8 .. +8.
+    // Q as the B operand of S^T = K.Q^T: lane holds head row16, dims
+    // j*32 + grp*8 .. +8 (heads >= G are zero).
     bf16x8_t qf[KS];
 #pragma unroll
     for (int j = 0; j < KS; ++j) {
-        if (row16 < G) {
+        if (row16 < G)
             qf[j] = *reinterpret_cast<const bf16x8_t *>(
                 a.q + ((int64_t)b * a.q_heads + qh0 + row16) * D + j * 32 + grp * 8);
-        } else {
+        else
             qf[j] = bf16x8_t{};
-        }
     }
 
-    // Tile registers: K in MFMA A layout, V in VALU layout.
-    bf16x8_t kr[2][KS];
-    uint4 vr[NV];
-
-    auto load_tile = [&](int t0, bf16x8_t (&kd)[2][KS], uint4 (&vd)[NV]) {
-        const bool tail = t0 + 32 > end;
-        const int last = end - 1;
+    // Loads of a tile never branch: rows past the last valid token are
+    // clamped to it (their scores are masked to -inf), so every call issues
+    // the same loads and the wait counts stay exact.
+    //   K: MFMA A layout, lane = (token row16 of a 16-token block, dims grp*8
+    //      + 32j), 64 contiguous bytes of one row per lane.
+    //   V: lane (vh = lane / LPR, vc = lane % LPR) loads dims vc*8..+8 of the
+    //      NV consecutive rows vh*NV .. vh*NV+NV-1; each load instruction
+    //      covers RPI whole rows.
+    const int last = end - 1;
+    const int vh = lane / LPR;
+    const int vc = lane % LPR;
+    auto load_tile = [&](TileRegs<D> &r, int tile) {
+        const int t0 = begin + tile * kTile;
 #pragma unroll
         for (int blk = 0; blk < 2; ++blk) {
-            int bt = t0 + blk * 16;
-            int row = row16;
-            if (tail) {
-                const int bt_c = min(bt, last & ~15);
-                row = min(bt + row16, last) - bt_c;
-                bt = bt_c;
-            }
+            const int bt = min(t0 + blk * 16, last & ~15);
+            const int row = min(t0 + blk * 16 + row16, last) - bt;
             const uint16_t *p = block_base<D, PAGED>(a, a.k, b, kvh, bt) + row * rs + grp * 8;
 #pragma unroll
-            for (int j = 0; j < KS; ++j) kd[blk][j] = *reinterpret_cast<const bf16x8_t *>(p + j * 32);
+            for (int j = 0; j < KS; ++j) r.k[blk][j] = *reinterpret_cast<const bf16x8_t *>(p + j * 32);
         }
+        const uint16_t *vb0 = block_base<D, PAGED>(a, a.v, b, kvh, min(t0, last & ~15));
+        const uint16_t *vb1 = block_base<D, PAGED>(a, a.v, b, kvh, min(t0 + 16, last & ~15));
+        const int blk = (vh * NV) >> 4;  // rows of one lane never straddle a block
+        const int bt = min(t0 + blk * 16, last & ~15);
+        const uint16_t *vb = blk ? vb1 : vb0;
 #pragma unroll
-        for (int r = 0; r < NV; ++r) {
-            const int trow = r * RPI + lane / LPR;  // 0..31 within the tile
-            int bt = t0 + (trow & 16);
-            int row = trow & 15;
-            if (tail) {
-                const int bt_c = min(bt, last & ~15);
-                row = min(bt + row, last) - bt_c;
-                bt = bt_c;
-            }
-            const uint16_t *p = block_base<D, PAGED>(a, a.v, b, kvh, bt) + row * rs + (lane % LPR) * 8;
-            vd[r] = *reinterpret_cast<const uint4 *>(p);
+        for (int i = 0; i < NV; ++i) {
+            const int row = min(t0 + vh * NV + i, last) - bt;
+            r.v[i] = *reinterpret_cast<const uint4 *>(vb + row * rs + vc * 8);
         }
     };
 
     float m_run = -INFINITY;
     float l_run = 0.0f;
-    float acc[G][8];
+    floatx4_t o[NS];  // O[head 4*grp+i][dim 16*slice + row16]
 #pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[g][e] = 0.0f;
+    for (int sl = 0; sl < NS; ++sl) o[sl] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    const int ntiles = (end - begin + 31) >> 5;
-    load_tile(begin, kr, vr);
-    for (int it = 0; it < ntiles; ++it) {
-        const int t0 = begin + it * 32;
-        const int buf = it & 1;
-        bf16x8_t kn[2][KS];
-        uint4 vn[NV];
-        if (it + 1 < ntiles) load_tile(t0 + 32, kn, vn);
+    auto compute_tile = [&](const TileRegs<D> &r, int tile) {
+        const int t0 = begin + tile * kTile;
+        // Stage V transposed: vt[dim][token].  A lane owns NV consecutive
+        // tokens of 8 dims, i.e. NV*2 contiguous bytes of 8 rows of vt.
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            uint32_t w[NV / 2];
+#pragma unroll
+            for (int k = 0; k < NV / 2; ++k) {
+                const uint32_t lo = (&r.v[2 * k].x)[e >> 1];
+                const uint32_t hi = (&r.v[2 * k + 1].x)[e >> 1];
+                w[k] = pair_bf16(hi, lo, e & 1);
+            }
+            uint16_t *dst = vt + (vc * 8 + e) * VT + vh * NV;
+            if constexpr (NV == 8) {
+                *reinterpret_cast<uint4 *>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+            } else if constexpr (NV == 4) {
+                *reinterpret_cast<uint2 *>(dst) = make_uint2(w[0], w[1]);
+            }
+        }
 
         // S^T block = K (16 tokens x D) . Q^T (D x 16 heads).
         floatx4_t s[2];
@@ -171,10 +217,10 @@ __global__ __launch_bounds__(64) void decode_split_kernel(DeviceArgs a) {
             s[blk] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int j = 0; j < KS; ++j)
-                s[blk] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kr[blk][j], qf[j], s[blk], 0, 0, 0);
+                s[blk] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(r.k[blk][j], qf[j], s[blk], 0, 0, 0);
         }
         // Lane holds head row16, tokens t0 + blk*16 + grp*4 + i.
-        if (t0 + 32 > end) {
+        if (t0 + kTile > end) {
 #pragma unroll
             for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
@@ -188,6 +234,10 @@ __global__ __launch_bounds__(64) void decode_split_kernel(DeviceArgs a) {
         const float m_new = fmaxf(m_run, mx);
         const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * c);
         const float mc = m_new * c;
+        // P as the A operand of O = P.V: row = head row16, k-slot j of lane
+        // group grp = token (j < 4 ? 4*grp + j : 16 + 4*grp + j - 4), which is
+        // exactly where the S^T accumulator left it.
+        bf16x8_t pa;
         float psum = 0.0f;
 #pragma unroll
         for (int blk = 0; blk < 2; ++blk)
@@ -195,124 +245,142 @@ __global__ __launch_bounds__(64) void decode_split_kernel(DeviceArgs a) {
             for (int i = 0; i < 4; ++i) {
                 const float p = __builtin_amdgcn_exp2f(fmaf(s[blk][i], c, -mc));
                 psum += p;
-                if (row16 < G) p_lds[buf][blk * 16 + grp * 4 + i][row16] = p;
+                pa[blk * 4 + i] = (__bf16)p;
             }
         l_run = l_run * alpha + psum;
         m_run = m_new;
-        if (grp == 0 && row16 < G) alpha_lds[buf][row16] = alpha;
-        __syncthreads();
-
-        float al[GP];
+        // Rows of the O accumulator are heads 4*grp + i: fetch their alphas.
 #pragma unroll
-        for (int g4 = 0; g4 < GP; g4 += 4) {
-            const float4 t = *reinterpret_cast<const float4 *>(&alpha_lds[buf][g4]);
-            al[g4] = t.x; al[g4 + 1] = t.y; al[g4 + 2] = t.z; al[g4 + 3] = t.w;
+        for (int i = 0; i < 4; ++i) {
+            const float ai = __shfl(alpha, 4 * grp + i, 64);
+#pragma unroll
+            for (int sl = 0; sl < NS; ++sl) o[sl][i] *= ai;
         }
+        wave_lds_fence();
+        // V as the B operand: col = dim 16*slice + row16, k-slots of lane
+        // group grp = the same tokens as P's.
 #pragma unroll
-        for (int g = 0; g < G; ++g)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[g][e] *= al[g];
-
-#pragma unroll
-        for (int r = 0; r < NV; ++r) {
-            const int trow = r * RPI + lane / LPR;
-            float p[GP];
-#pragma unroll
-            for (int g4 = 0; g4 < GP; g4 += 4) {
-                const float4 t = *reinterpret_cast<const float4 *>(&p_lds[buf][trow][g4]);
-                p[g4] = t.x; p[g4 + 1] = t.y; p[g4 + 2] = t.z; p[g4 + 3] = t.w;
-            }
-            const uint4 w = vr[r];
-            const float v[8] = {bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y),
-                                bf16_lo(w.z), bf16_hi(w.z), bf16_lo(w.w), bf16_hi(w.w)};
-#pragma unroll
-            for (int g = 0; g < G; ++g)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(p[g], v[e], acc[g][e]);
+        for (int sl = 0; sl < NS; ++sl) {
+            const uint16_t *src = vt + (sl * 16 + row16) * VT + 4 * grp;
+            const uint2 lo = *reinterpret_cast<const uint2 *>(src);
+            const uint2 hi = *reinterpret_cast<const uint2 *>(src + 16);
+            const bf16x8_t vb = __builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+            o[sl] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vb, o[sl], 0, 0, 0);
         }
+        wave_lds_fence();
+    };
 
+    // Ring of DEPTH tile buffers over this wavefront's tiles wave, wave+4,
+    // ...; the loop is unrolled by DEPTH so every buffer index is a
+    // compile-time constant, and DEPTH-1 tiles are in flight during compute.
+    const int my_tiles = ntiles > wave ? (ntiles - wave + kWaves - 1) / kWaves : 0;
+    auto tile_of = [&](int i) { return wave + kWaves * min(i, my_tiles - 1); };
+    TileRegs<D> ring[DEPTH];
+    if (my_tiles > 0) {
 #pragma unroll
-        for (int blk = 0; blk < 2; ++blk)
+        for (int d = 0; d < DEPTH - 1; ++d) load_tile(ring[d], tile_of(d));
+    }
+    for (int base = 0; base < my_tiles; base += DEPTH) {
 #pragma unroll
-            for (int j = 0; j < KS; ++j) kr[blk][j] = kn[blk][j];
-#pragma unroll
-        for (int r = 0; r < NV; ++r) vr[r] = vn[r];
+        for (int s = 0; s < DEPTH; ++s) {
+            const int i = base + s;
+            if (i >= my_tiles) break;
+            load_tile(ring[(s + DEPTH - 1) % DEPTH], tile_of(i + DEPTH - 1));
+            __builtin_amdgcn_sched_barrier(0);
+            compute_tile(ring[s], tile_of(i));
+        }
     }
 
-    // Combine the four lane groups: l over groups of the same head, acc over
-    // lanes holding the same 8 dims of different token rows.
+    // Per wavefront: l over the four lane groups of each head; O rows are
+    // heads 4*grp + i, dims 16*slice + row16.
     l_run = wave_xor_sum(l_run, 16);
     l_run = wave_xor_sum(l_run, 32);
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+    for (int i = 0; i < 4; ++i) {
+        const int h = 4 * grp + i;
+        if (h < G) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-#pragma unroll
-            for (int mask = LPR; mask < 64; mask <<= 1) acc[g][e] = wave_xor_sum(acc[g][e], mask);
+            for (int sl = 0; sl < NS; ++sl) comb_acc[wave][h][sl * 16 + row16] = o[sl][i];
         }
+    }
+    if (lane < G) {
+        comb_ml[wave][lane][0] = m_run;  // -inf for a wavefront without tiles
+        comb_ml[wave][lane][1] = l_run;
+    }
+    __syncthreads();
 
-    const int chunk = lane % LPR;
-    const int slot = lane / LPR;
-    if (nsplit == 1) {
+    // Combine the four wavefronts in fixed order: thread -> (head, 4 dims).
+    constexpr int ITEMS = G * D / 4;
+    const bool final_write = nsplit == 1;
+    const int64_t part = ((int64_t)sg * a.kv_heads + kvh) * G;
+    for (int it = tid; it < ITEMS; it += 64 * kWaves) {
+        const int g = it / (D / 4);
+        const int d = (it % (D / 4)) * 4;
+        float m = -INFINITY;
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const float l = __shfl(l_run, g, 64);
-            if (slot == g % RPI) {
-                uint4 o;
-                o.x = pack_bf16x2(acc[g][0] / l, acc[g][1] / l);
-                o.y = pack_bf16x2(acc[g][2] / l, acc[g][3] / l);
-                o.z = pack_bf16x2(acc[g][4] / l, acc[g][5] / l);
-                o.w = pack_bf16x2(acc[g][6] / l, acc[g][7] / l);
-                *reinterpret_cast<uint4 *>(a.out + ((int64_t)b * a.q_heads + qh0 + g) * D + chunk * 8) = o;
-            }
-        }
-    } else {
-        const int64_t base = ((int64_t)sg * a.kv_heads + kvh) * G;
+        for (int w = 0; w < kWaves; ++w) m = fmaxf(m, comb_ml[w][g][0]);
+        float l = 0.0f;
+        float4 ov = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            if (slot == g % RPI) {
-                float *dst = a.partial_acc + (base + g) * D + chunk * 8;
-                *reinterpret_cast<float4 *>(dst) = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
-                *reinterpret_cast<float4 *>(dst + 4) = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
-            }
+        for (int w = 0; w < kWaves; ++w) {
+            const float wt = __builtin_amdgcn_exp2f((comb_ml[w][g][0] - m) * c);
+            l = fmaf(comb_ml[w][g][1], wt, l);
+            const float4 x = *reinterpret_cast<const float4 *>(&comb_acc[w][g][d]);
+            ov.x = fmaf(x.x, wt, ov.x); ov.y = fmaf(x.y, wt, ov.y);
+            ov.z = fmaf(x.z, wt, ov.z); ov.w = fmaf(x.w, wt, ov.w);
         }
-        if (lane < G) {
-            *reinterpret_cast<float2 *>(a.partial_ml + (base + lane) * 2) = make_float2(m_run, l_run);
+        if (final_write) {
+            uint2 packed;
+            packed.x = pack_bf16x2(ov.x / l, ov.y / l);
+            packed.y = pack_bf16x2(ov.z / l, ov.w / l);
+            *reinterpret_cast<uint2 *>(a.out + ((int64_t)b * a.q_heads + qh0 + g) * D + d) = packed;
+        } else {
+            *reinterpret_cast<float4 *>(a.partial_acc + (part + g) * D + d) = ov;
+            if (d == 0) *reinterpret_cast<float2 *>(a.partial_ml + (part + g) * 2) = make_float2(m, l);
         }
     }
 }
 
-// Fixed-order log-sum-exp merge of split partials (the deterministic
-// counterpart of mslim_attention_merge, tiled_attention.cl:131-155).
-template <int D>
-__global__ __launch_bounds__(64) void decode_merge_kernel(DeviceArgs a) {
-    const int b = blockIdx.x / a.q_heads;
-    const int qh = blockIdx.x % a.q_heads;
+// Fixed-order log-sum-exp merge of the split partials of one (sequence, kv
+// head): thread -> (head, 4 dims), one online pass over the partitions.  Runs
+// as its own launch after the split kernel, so no device-scope fence is
+// needed between them (the deterministic counterpart of
+// mslim_attention_merge, tiled_attention.cl:131-155).
+template <int D, int G>
+__global__ __launch_bounds__(256) void decode_merge_kernel(DeviceArgs a) {
+    const int kvh = blockIdx.x % a.kv_heads;
+    const int b = blockIdx.x / a.kv_heads;
     const int nsplit = a.split_begin[b + 1] - a.split_begin[b];
     if (nsplit <= 1) return;
-    const int group = a.q_heads / a.kv_heads;
-    const int kvh = qh / group, g = qh % group;
-    const float c = a.scale_log2e;
     const int s0 = a.split_begin[b];
-    auto idx = [&](int s) { return ((int64_t)(s0 + s) * a.kv_heads + kvh) * group + g; };
-    float m = -INFINITY;
-    for (int s = 0; s < nsplit; ++s) m = fmaxf(m, a.partial_ml[idx(s) * 2]);
-    float l = 0.0f;
-    for (int s = 0; s < nsplit; ++s) {
-        const float w = __builtin_amdgcn_exp2f((a.partial_ml[idx(s) * 2] - m) * c);
-        l = fmaf(a.partial_ml[idx(s) * 2 + 1], w, l);
-    }
-    for (int d = threadIdx.x; d < D; d += 64) {
-        float o = 0.0f;
+    const float c = a.scale_log2e;
+    const int qh0 = kvh * G;
+    for (int it = threadIdx.x; it < G * D / 4; it += 256) {
+        const int g = it / (D / 4);
+        const int d = (it % (D / 4)) * 4;
+        float m = -INFINITY, l = 0.0f;
+        float4 ov = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll 8
         for (int s = 0; s < nsplit; ++s) {
-            const float w = __builtin_amdgcn_exp2f((a.partial_ml[idx(s) * 2] - m) * c);
-            o = fmaf(a.partial_acc[idx(s) * D + d], w, o);
+            const int64_t idx = ((int64_t)(s0 + s) * a.kv_heads + kvh) * G + g;
+            const float2 ml = *reinterpret_cast<const float2 *>(a.partial_ml + idx * 2);
+            const float4 x = *reinterpret_cast<const float4 *>(a.partial_acc + idx * D + d);
+            const float m_new = fmaxf(m, ml.x);
+            const float wo = __builtin_amdgcn_exp2f((m - m_new) * c);
+            const float wn = __builtin_amdgcn_exp2f((ml.x - m_new) * c);
+            l = fmaf(l, wo, ml.y * wn);
+            ov.x = fmaf(ov.x, wo, x.x * wn); ov.y = fmaf(ov.y, wo, x.y * wn);
+            ov.z = fmaf(ov.z, wo, x.z * wn); ov.w = fmaf(ov.w, wo, x.w * wn);
+            m = m_new;
         }
-        a.out[((int64_t)b * a.q_heads + qh) * D + d] = write_bf16(o / l);
+        uint2 packed;
+        packed.x = pack_bf16x2(ov.x / l, ov.y / l);
+        packed.y = pack_bf16x2(ov.z / l, ov.w / l);
+        *reinterpret_cast<uint2 *>(a.out + ((int64_t)b * a.q_heads + qh0 + g) * D + d) = packed;
     }
 }
 
-// Any-geometry fallback (head_dim not a multiple of 32, or groups above 8):
+// Any-geometry fallback (head_dim not 64/128, or groups outside 1/2/4/8):
 // one wavefront per (sequence, query head), 64-token tiles, one token per
 // lane for Q.K, dims across lanes for P.V.  Same addressing rule as the fast
 // kernel, so dense and paged stay bit-identical here too.
@@ -376,18 +444,23 @@ __global__ __launch_bounds__(64) void decode_generic_kernel(DeviceArgs a, int D)
     }
 }
 
+#ifndef MSLIM_DECODE_DEPTH
+#define MSLIM_DECODE_DEPTH 2
+#endif
+
 template <int D, int G>
 hipError_t launch_fast(const DeviceArgs &a, bool paged, int total_splits, bool merge,
                        hipStream_t stream) {
     const dim3 grid((unsigned)(total_splits * a.kv_heads));
-    if (paged) {
-        hipLaunchKernelGGL((decode_split_kernel<D, G, true>), grid, dim3(64), 0, stream, a);
-    } else {
-        hipLaunchKernelGGL((decode_split_kernel<D, G, false>), grid, dim3(64), 0, stream, a);
-    }
+    if (paged)
+        hipLaunchKernelGGL((decode_kernel<D, G, true, MSLIM_DECODE_DEPTH>), grid, dim3(64 * kWaves), 0,
+                           stream, a);
+    else
+        hipLaunchKernelGGL((decode_kernel<D, G, false, MSLIM_DECODE_DEPTH>), grid, dim3(64 * kWaves), 0,
+                           stream, a);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess || !merge) return err;
-    hipLaunchKernelGGL((decode_merge_kernel<D>), dim3((unsigned)(a.batch * a.q_heads)), dim3(64), 0,
+    hipLaunchKernelGGL((decode_merge_kernel<D, G>), dim3((unsigned)(a.batch * a.kv_heads)), dim3(256), 0,
                        stream, a);
     return hipGetLastError();
 }
@@ -395,16 +468,20 @@ hipError_t launch_fast(const DeviceArgs &a, bool paged, int total_splits, bool m
 }  // namespace
 
 int decode_auto_split_tokens(const int32_t *seq_lens, int batch, int kv_heads) {
+    // About one workgroup per CU (256 on MI355X): long partitions keep each
+    // workgroup's load pipeline full and measured fastest at the BASELINE
+    // shapes (4096 tokens per partition for 4 x 32k x 8 kv heads).  Multiple
+    // of 256, between 256 and 16384 tokens.
     int64_t total = 0;
     for (int i = 0; i < batch; ++i) total += seq_lens[i];
-    int64_t per = (total * kv_heads + 2047) / 2048;
-    per = (per + 63) / 64 * 64;
-    return (int)std::min<int64_t>(4096, std::max<int64_t>(64, per));
+    int64_t per = (total * kv_heads + 255) / 256;
+    per = (per + 255) / 256 * 256;
+    return (int)std::min<int64_t>(16384, std::max<int64_t>(256, per));
 }
 
 bool decode_fast_path(int head_dim, int group) {
     return (head_dim == 64 || head_dim == 128) &&
-           (group == 1 || group == 2 || group == 4 || group == 8);
+           (group == 1 || group == 2 || group == 4 || group == 8 || group == 16);
 }
 
 hipError_t launch_decode(const DecodeLaunch &l, hipStream_t stream) {
@@ -426,9 +503,9 @@ hipError_t launch_decode(const DecodeLaunch &l, hipStream_t stream) {
     for (int i = 0; i < l.batch; ++i) {
         a.seq_len[i] = l.seq_len[i];
         a.split_begin[i] = total;
-        const int s = decode_splits(l.seq_len[i], l.split_tokens);
-        merge |= s > 1;
-        total += s;
+        const int n = decode_splits(l.seq_len[i], l.split_tokens);
+        merge |= n > 1;
+        total += n;
     }
     a.split_begin[l.batch] = total;
     const int group = l.q_heads / l.kv_heads;
@@ -442,10 +519,12 @@ hipError_t launch_decode(const DecodeLaunch &l, hipStream_t stream) {
     }
 #define MSLIM_DECODE_CASE(DD, GG) \
     if (l.head_dim == DD && group == GG) return launch_fast<DD, GG>(a, l.paged, total, merge, stream);
+    MSLIM_DECODE_CASE(128, 16)
     MSLIM_DECODE_CASE(128, 8)
     MSLIM_DECODE_CASE(128, 4)
     MSLIM_DECODE_CASE(128, 2)
     MSLIM_DECODE_CASE(128, 1)
+    MSLIM_DECODE_CASE(64, 16)
     MSLIM_DECODE_CASE(64, 8)
     MSLIM_DECODE_CASE(64, 4)
     MSLIM_DECODE_CASE(64, 2)
