@@ -339,7 +339,7 @@ def main() -> int:
                 "unit": "TFLOP/s",
                 "frac": round(pre_tflops / PEAK_BF16_TFLOPS, 4),
                 "traffic": None,
-                "kernel": f"prefill_mfma_kernel<128,4>, algorithmic FLOP {prefill_flops()} per launch",
+                "kernel": f"prefill_mfma_kernel<128,8,8,2>, algorithmic FLOP {prefill_flops()} per launch",
             },
         },
         "decode_ms": round(dec_avg, 5),
