@@ -19,7 +19,16 @@ baseline is the C oracle's restatement of the reference CPU attention
 reference's rayon loop (:273-276), timed on a bounded sample of the same
 workload on this host.
 
+Before each timed loop a short device sleep is queued behind the final
+synchronize so that the first timed launch does not wait on host launch
+latency; every timed call is then back-to-back device work.
+
+`--kernel decode|prefill|copy` runs only that workload (warmup + steps, no
+CPU baseline) for counter collection: `copy` is a plain 1 GiB device copy
+whose FETCH_SIZE / WRITE_SIZE readings calibrate the byte counters.
+
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--cpu-seconds 10]
+                       [--kernel all|decode|prefill|copy]
 """
 import argparse
 import json
@@ -177,6 +186,55 @@ def cpu_model() -> str:
     return "unknown"
 
 
+QUEUE_FILL_CYCLES = 2_000_000  # device sleep ahead of a timed loop (about 1 ms)
+COPY_BYTES = 1 << 30             # calibration copy: 1 GiB read + 1 GiB written
+
+
+def measured_traffic(name: str):
+    """HBM bytes per launch from the committed counter summary
+    profiles/<name>_traffic.json (FETCH_SIZE + WRITE_SIZE, calibrated), or
+    None when it has not been measured."""
+    path = os.path.join(ROOT, "profiles", f"{name}_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("hbm_bytes_per_launch")
+
+
+def timed_calls(torch, fn, steps: int) -> float:
+    """Average device time in ms of `steps` back-to-back calls of fn."""
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(QUEUE_FILL_CYCLES)
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def one_workload(torch, ctx, fn, args) -> int:
+    for _ in range(args.warmup):
+        fn()
+    ms = timed_calls(torch, fn, args.steps)
+    print(json.dumps({"kernel": args.kernel, "steps": args.steps, "ms_per_call": round(ms, 5)}), flush=True)
+    ctx.close()
+    return 0
+
+
+def copy_only(torch, args) -> int:
+    src = torch.ones(COPY_BYTES // 2, dtype=torch.int16, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(args.warmup):
+        dst.copy_(src)
+    ms = timed_calls(torch, lambda: dst.copy_(src), args.steps)
+    print(json.dumps({"kernel": "copy", "bytes_read": COPY_BYTES, "bytes_written": COPY_BYTES,
+                      "steps": args.steps, "ms_per_call": round(ms, 5),
+                      "gbps": round(2 * COPY_BYTES / (ms * 1e-3) / 1e9, 1)}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -184,6 +242,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="CPU baseline budget per leg (0 skips the CPU baseline)")
+    ap.add_argument("--kernel", choices=("all", "decode", "prefill", "copy"), default="all",
+                    help="run one workload only, for counter collection")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
@@ -200,6 +260,8 @@ def main() -> int:
     import mslim_attn
 
     torch.cuda.set_device(0)
+    if args.kernel == "copy":
+        return copy_only(torch, args)
     ctx = mslim_attn.Context()
     ctx.use_torch_stream()
 
@@ -228,6 +290,9 @@ def main() -> int:
     def prefill():
         ctx.prefill_causal(q_pre, k_pre, v_pre, out_pre, S_PREFILL, 0, QH, KVH, D)
 
+    if args.kernel != "all":
+        return one_workload(torch, ctx, decode if args.kernel == "decode" else prefill, args)
+
     # The paged ColdStore-exact decode must equal the dense decode bit for bit.
     decode()
     ctx.decode_dense(q_dec, k_dense, v_dense, out_dense, lens, QH, KVH, D, seq_stride_tokens=T)
@@ -244,6 +309,7 @@ def main() -> int:
            torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    torch.cuda._sleep(QUEUE_FILL_CYCLES)
     start_all = torch.cuda.Event(enable_timing=True)
     end_all = torch.cuda.Event(enable_timing=True)
     start_all.record()
@@ -267,7 +333,9 @@ def main() -> int:
     # dense decode on the same data, for reference
     for _ in range(3):
         ctx.decode_dense(q_dec, k_dense, v_dense, out_dense, lens, QH, KVH, D, seq_stride_tokens=T)
+    torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(QUEUE_FILL_CYCLES)
     e0.record()
     for _ in range(args.steps):
         ctx.decode_dense(q_dec, k_dense, v_dense, out_dense, lens, QH, KVH, D, seq_stride_tokens=T)
@@ -279,11 +347,8 @@ def main() -> int:
     pre_tflops = prefill_flops() / (pre_avg * 1e-3) / 1e12
     dense_gbps = decode_bytes() / (dense_ms * 1e-3) / 1e9
 
-    traffic = None
-    traffic_file = os.path.join(ROOT, "profiles", "decode_paged_cfg4_traffic.json")
-    if os.path.exists(traffic_file):
-        with open(traffic_file) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+    traffic = measured_traffic("decode_paged_cfg4")
+    pre_traffic = measured_traffic("prefill_causal_s8192")
 
     cpu = None
     if args.cpu_seconds > 0:
@@ -338,7 +403,7 @@ def main() -> int:
                 "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s",
                 "frac": round(pre_tflops / PEAK_BF16_TFLOPS, 4),
-                "traffic": None,
+                "traffic": pre_traffic,
                 "kernel": f"prefill_mfma_kernel<128,8,8,2>, algorithmic FLOP {prefill_flops()} per launch",
             },
         },
