@@ -131,6 +131,52 @@ int mslim_attn_prefill_causal(void *ctx, const void *q, const void *k, const voi
                               void *out, int queries, int prior, int q_heads,
                               int kv_heads, int head_dim, float scale);
 
+/* ---- Portable backend (exact K/V frames) ------------------------------------ */
+
+/* K/V frame formats: the dtype codes of gpu_backend.rs:258-262. */
+#define MSLIM_ATTN_FORMAT_BF16 1
+#define MSLIM_ATTN_FORMAT_F16 2
+#define MSLIM_ATTN_FORMAT_F32 3
+/* Return code for a non-finite query or output (PortableError::NonFinite,
+ * portable.rs:43, raised at gpu_backend.rs:154-156 and :363-365). */
+#define MSLIM_ATTN_ERR_NONFINITE (-2)
+
+/* Per-call report of mslim_attn_backend_decode; mirrors GpuTimings
+ * (gpu_backend.rs:34-44).  The reference's three kernel times become one:
+ * QK, softmax and P.V run fused. */
+typedef struct {
+    double dispatch_ms;       /* whole call: uploads, kernels, readback */
+    double kernel_ms;         /* attention kernels (HIP events) */
+    uint64_t input_kv_bytes;  /* K + V payload bytes uploaded */
+    uint64_t scratch_bytes;   /* split partials in device memory */
+    uint64_t output_bytes;
+} mslim_attn_timings;
+
+/* Single-token decode over exact K/V frames on device buffers: the work of
+ * GpuBackend::decode (gpu_backend.rs:149-377; kernels mslim_qk / mslim_softmax
+ * / mslim_pv, gpu_attention.cl:35-82).
+ *   query: f32 [q_heads][head_dim].
+ *   keys / values: raw little-endian [tokens][kv_heads][head_dim] in
+ *   key_format / value_format (MSLIM_ATTN_FORMAT_*), the frames concatenated
+ *   in append order as gpu_backend.rs:186-198 concatenates them.
+ *   out: f32 [q_heads][head_dim]; scale 1/sqrt(head_dim) (gpu_attention.cl:48).
+ *   tokens == 0 writes zeros (gpu_backend.rs:157-159).  head_dim <= 1024.
+ * Stream-ordered: non-finite inputs propagate into the output unchecked. */
+int mslim_attn_frames_decode(void *ctx, const float *query, const void *keys, int key_format,
+                             const void *values, int value_format, float *out, int64_t tokens,
+                             int q_heads, int kv_heads, int head_dim);
+
+/* The blocking host-memory form, one call per AttentionBackend::decode
+ * (portable.rs:561-565, gpu_backend.rs:370-377): uploads the host query and
+ * frames into context-owned device buffers (reused across calls, unlike the
+ * reference's per-call allocation), runs mslim_attn_frames_decode, reads the
+ * output back and returns MSLIM_ATTN_ERR_NONFINITE for a non-finite query
+ * ("GPU Q") or output ("GPU output").  `timings` may be NULL. */
+int mslim_attn_backend_decode(void *ctx, const float *query, const void *keys, int key_format,
+                              const void *values, int value_format, int64_t tokens, int q_heads,
+                              int kv_heads, int head_dim, float *out,
+                              mslim_attn_timings *timings);
+
 /* ---- Feeder kernels ------------------------------------------------------- */
 
 /* RMSNorm over `tokens` rows of `hidden` BF16 values: 128-lane strided FMA

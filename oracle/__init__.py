@@ -44,6 +44,7 @@ def _load() -> C.CDLL:
         "orc_f32_to_bf16_array": (None, [P, P, SZ]),
         "orc_dense_attention_bf16": (I, [I, I, I, P, P, P, I, P]),
         "orc_cpu_reference_decode": (I, [I, I, I, P, P, P, I, I, P]),
+        "orc_cpu_reference_decode_formats": (I, [I, I, I, P, P, I, P, I, I, P]),
         "orc_prefill_causal_cpu": (I, [I, I, I, P, P, P, I, I, P]),
         "orc_gpu_reference_attention": (I, [I, I, I, P, P, P, I, I, P]),
         "orc_rms_norm_cpu": (None, [P, P, I, F, P]),
@@ -132,6 +133,19 @@ def cpu_reference_decode(q: np.ndarray, k: np.ndarray, v: np.ndarray, dtype: int
     tokens = k.size // (kvh * d)
     out = np.empty(qh * d, np.float32)
     rc = lib().orc_cpu_reference_decode(qh, kvh, d, _p(q), _p(k), _p(v), dtype, tokens, _p(out))
+    return rc, out
+
+
+def cpu_reference_decode_formats(q: np.ndarray, k: np.ndarray, key_dtype: int, v: np.ndarray,
+                                 value_dtype: int, qh: int, kvh: int, d: int):
+    """portable.rs:575-646 with separate K and V formats; returns (rc, out)."""
+    q = np.ascontiguousarray(q, np.float32).reshape(-1)
+    k = np.ascontiguousarray(k)
+    v = np.ascontiguousarray(v)
+    tokens = k.size // (kvh * d)
+    out = np.empty(qh * d, np.float32)
+    rc = lib().orc_cpu_reference_decode_formats(qh, kvh, d, _p(q), _p(k), key_dtype, _p(v),
+                                                value_dtype, tokens, _p(out))
     return rc, out
 
 

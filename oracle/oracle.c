@@ -142,8 +142,17 @@ int orc_cpu_reference_decode(int query_heads, int kv_heads, int head_dim,
                              const float *query, const void *keys,
                              const void *values, int dtype, int tokens,
                              float *out) {
+    return orc_cpu_reference_decode_formats(query_heads, kv_heads, head_dim, query, keys, dtype,
+                                            values, dtype, tokens, out);
+}
+
+int orc_cpu_reference_decode_formats(int query_heads, int kv_heads, int head_dim,
+                                     const float *query, const void *keys, int key_dtype,
+                                     const void *values, int value_dtype, int tokens,
+                                     float *out) {
     if (query_heads <= 0 || kv_heads <= 0 || head_dim <= 0 || query_heads % kv_heads ||
-        dtype < 1 || dtype > 3 || tokens < 0) return 1;
+        key_dtype < 1 || key_dtype > 3 || value_dtype < 1 || value_dtype > 3 || tokens < 0)
+        return 1;
     const size_t qn = (size_t)query_heads * head_dim;
     for (size_t i = 0; i < qn; ++i) if (!isfinite(query[i])) return 2;
     if (tokens == 0) { for (size_t i = 0; i < qn; ++i) out[i] = 0.0f; return 0; }
@@ -160,7 +169,7 @@ int orc_cpu_reference_decode(int query_heads, int kv_heads, int head_dim,
             const size_t off = ((size_t)t * kv_heads + kh) * head_dim;
             double dot = 0.0;
             for (int d = 0; d < head_dim; ++d) {
-                const float kv = element(keys, off + d, dtype);
+                const float kv = element(keys, off + d, key_dtype);
                 if (!isfinite(kv)) { free(weighted); return 2; }
                 dot += (double)q[d] * (double)kv;
             }
@@ -171,7 +180,7 @@ int orc_cpu_reference_decode(int query_heads, int kv_heads, int head_dim,
             const double current = exp(score - next_max);
             denominator = denominator * prior + current;
             for (int d = 0; d < head_dim; ++d) {
-                const float item = element(values, off + d, dtype);
+                const float item = element(values, off + d, value_dtype);
                 if (!isfinite(item)) { free(weighted); return 2; }
                 weighted[d] = weighted[d] * prior + current * (double)item;
             }

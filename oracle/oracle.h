@@ -63,6 +63,13 @@ int orc_cpu_reference_decode(int query_heads, int kv_heads, int head_dim,
                              const float *query, const void *keys,
                              const void *values, int dtype, int tokens,
                              float *out);
+/* The same with separate K and V formats: the reference decodes every frame
+ * element through its own tensor's dtype (portable.rs:120-145), and the GPU
+ * backend takes one key and one value format (gpu_backend.rs:187-199). */
+int orc_cpu_reference_decode_formats(int query_heads, int kv_heads, int head_dim,
+                                     const float *query, const void *keys, int key_dtype,
+                                     const void *values, int value_dtype, int tokens,
+                                     float *out);
 
 /* Causal prefill on the CPU path: the reference CPU decoder processes a prompt
  * token by token (native_cpu_adapter.rs:486-534), so query row i attends to

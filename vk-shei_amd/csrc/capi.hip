@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -43,12 +44,18 @@ struct Context {
     size_t staging_bytes = 0;
     void *host_staging = nullptr;  // pinned host, digest readback
     size_t host_staging_bytes = 0;
+    void *backend = nullptr;       // device, backend_decode query/frames/output
+    size_t backend_bytes = 0;
+    hipEvent_t ev_start = nullptr, ev_end = nullptr;
 
     ~Context() {
         if (stream) (void)hipStreamSynchronize(stream);
         if (workspace) (void)hipFree(workspace);
         if (staging) (void)hipFree(staging);
         if (host_staging) (void)hipHostFree(host_staging);
+        if (backend) (void)hipFree(backend);
+        if (ev_start) (void)hipEventDestroy(ev_start);
+        if (ev_end) (void)hipEventDestroy(ev_end);
         if (own_stream) (void)hipStreamDestroy(own_stream);
     }
 };
@@ -124,6 +131,44 @@ int decode_common(Context &c, mslim::DecodeLaunch &l, const int32_t *seq_lens, i
     return check_hip(mslim::launch_decode(l, c.stream), "decode attention launch");
 }
 
+
+// Checks shared by both portable-backend entry points (portable.rs:420-441
+// geometry rules; the kernel holds the query in LDS, so head_dim <= 1024).
+int frames_validate(int key_format, int value_format, int64_t tokens, int q_heads, int kv_heads,
+                    int head_dim) {
+    auto fmt_ok = [](int f) { return f >= MSLIM_ATTN_FORMAT_BF16 && f <= MSLIM_ATTN_FORMAT_F32; };
+    if (!fmt_ok(key_format) || !fmt_ok(value_format))
+        return fail("K/V format must be 1 (BF16), 2 (F16) or 3 (F32)");
+    if (q_heads <= 0 || kv_heads <= 0 || head_dim <= 0 || q_heads % kv_heads)
+        return fail("invalid geometry: heads and dimension must be positive, q_heads divisible by kv_heads");
+    if (head_dim > mslim::kFramesMaxDim) return fail("invalid geometry: head_dim above 1024");
+    if (tokens < 0 || tokens > ((int64_t)1 << 40) / ((int64_t)kv_heads * head_dim))
+        return fail("invalid geometry: token count out of range");
+    return 0;
+}
+
+size_t format_bytes(int format) { return format == MSLIM_ATTN_FORMAT_F32 ? 4 : 2; }
+
+// Enqueue split + merge on the context stream; returns the scratch bytes used.
+int frames_enqueue(Context &c, mslim::FramesLaunch &l, uint64_t *scratch) {
+    *scratch = 0;
+    l.scale = (float)(1.0 / std::sqrt((double)l.head_dim));
+    l.split_tokens = l.tokens > 0 ? mslim::frames_split_tokens(l.tokens, l.q_heads) : 256;
+    const int64_t splits = (l.tokens + l.split_tokens - 1) / l.split_tokens;
+    if (splits > 1) {
+        const size_t ml = (size_t)l.q_heads * splits * 2 * sizeof(float);
+        const size_t acc = (size_t)l.q_heads * splits * l.head_dim * sizeof(float);
+        if (int rc = grow_device(c, &c.workspace, &c.workspace_bytes, ml + acc,
+                                 "hipMalloc frames split workspace"))
+            return rc;
+        l.partial_ml = static_cast<float *>(c.workspace);
+        l.partial_acc = reinterpret_cast<float *>(static_cast<char *>(c.workspace) + ml);
+        *scratch = ml + acc;
+    }
+    return check_hip(mslim::launch_frames_decode(l, c.stream), "frames decode launch");
+}
+
+size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 }  // namespace
 
 extern "C" {
@@ -325,6 +370,92 @@ int mslim_attn_prefill_causal(void *ctx, const void *q, const void *k, const voi
     l.queries = queries; l.prior = prior; l.q_heads = q_heads; l.kv_heads = kv_heads;
     l.head_dim = head_dim; l.scale = scale;
     if (int rc = check_hip(mslim::launch_prefill(l, c.stream), "prefill attention launch")) return rc;
+    return 0;
+}
+
+int mslim_attn_frames_decode(void *ctx, const float *query, const void *keys, int key_format,
+                             const void *values, int value_format, float *out, int64_t tokens,
+                             int q_heads, int kv_heads, int head_dim) {
+    g_error.clear();
+    if (!ctx) return fail("null context");
+    if (int rc = frames_validate(key_format, value_format, tokens, q_heads, kv_heads, head_dim)) return rc;
+    if (!query || !out || (tokens > 0 && (!keys || !values)))
+        return fail("frames decode needs non-null query, out and (for tokens > 0) keys, values");
+    if ((const void *)out == (const void *)query || (const void *)out == keys ||
+        (const void *)out == values)
+        return fail("frames decode output must not alias read-only query/keys/values");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    mslim::FramesLaunch l{};
+    l.q = query; l.k = keys; l.v = values; l.out = out;
+    l.key_format = key_format; l.value_format = value_format;
+    l.tokens = tokens; l.q_heads = q_heads; l.kv_heads = kv_heads; l.head_dim = head_dim;
+    uint64_t scratch = 0;
+    return frames_enqueue(c, l, &scratch);
+}
+
+int mslim_attn_backend_decode(void *ctx, const float *query, const void *keys, int key_format,
+                              const void *values, int value_format, int64_t tokens, int q_heads,
+                              int kv_heads, int head_dim, float *out,
+                              mslim_attn_timings *timings) {
+    g_error.clear();
+    const auto start = std::chrono::steady_clock::now();
+    if (!ctx) return fail("null context");
+    if (int rc = frames_validate(key_format, value_format, tokens, q_heads, kv_heads, head_dim)) return rc;
+    if (!query || !out || (tokens > 0 && (!keys || !values)))
+        return fail("backend decode needs host query, out and (for tokens > 0) keys, values");
+    const size_t qn = (size_t)q_heads * head_dim;
+    // gpu_backend.rs:154-159: the query is checked before the empty-cache case.
+    for (size_t i = 0; i < qn; ++i)
+        if (!std::isfinite(query[i])) return fail("non-finite computation: GPU Q", MSLIM_ATTN_ERR_NONFINITE);
+    if (tokens == 0) {
+        std::fill(out, out + qn, 0.0f);
+        return 0;
+    }
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    const size_t row = (size_t)kv_heads * head_dim;
+    const size_t kb = (size_t)tokens * row * format_bytes(key_format);
+    const size_t vb = (size_t)tokens * row * format_bytes(value_format);
+    const size_t q_off = 0, k_off = align256(qn * 4), v_off = k_off + align256(kb);
+    const size_t o_off = v_off + align256(vb), total = o_off + align256(qn * 4);
+    if (int rc = grow_device(c, &c.backend, &c.backend_bytes, total, "hipMalloc backend buffers")) return rc;
+    if (!c.ev_start) {
+        if (int rc = check_hip(hipEventCreate(&c.ev_start), "hipEventCreate")) return rc;
+        if (int rc = check_hip(hipEventCreate(&c.ev_end), "hipEventCreate")) return rc;
+    }
+    char *base = static_cast<char *>(c.backend);
+    if (int rc = check_hip(hipMemcpyAsync(base + q_off, query, qn * 4, hipMemcpyHostToDevice, c.stream), "write Q"))
+        return rc;
+    if (int rc = check_hip(hipMemcpyAsync(base + k_off, keys, kb, hipMemcpyHostToDevice, c.stream), "write K"))
+        return rc;
+    if (int rc = check_hip(hipMemcpyAsync(base + v_off, values, vb, hipMemcpyHostToDevice, c.stream), "write V"))
+        return rc;
+    mslim::FramesLaunch l{};
+    l.q = reinterpret_cast<const float *>(base + q_off);
+    l.k = base + k_off; l.v = base + v_off;
+    l.out = reinterpret_cast<float *>(base + o_off);
+    l.key_format = key_format; l.value_format = value_format;
+    l.tokens = tokens; l.q_heads = q_heads; l.kv_heads = kv_heads; l.head_dim = head_dim;
+    uint64_t scratch = 0;
+    if (int rc = check_hip(hipEventRecord(c.ev_start, c.stream), "hipEventRecord")) return rc;
+    if (int rc = frames_enqueue(c, l, &scratch)) return rc;
+    if (int rc = check_hip(hipEventRecord(c.ev_end, c.stream), "hipEventRecord")) return rc;
+    if (int rc = check_hip(hipMemcpyAsync(out, l.out, qn * 4, hipMemcpyDeviceToHost, c.stream), "GPU output readback"))
+        return rc;
+    if (int rc = check_hip(hipStreamSynchronize(c.stream), "finish GPU")) return rc;
+    float kernel_ms = 0.0f;
+    if (int rc = check_hip(hipEventElapsedTime(&kernel_ms, c.ev_start, c.ev_end), "hipEventElapsedTime")) return rc;
+    if (timings) {
+        timings->dispatch_ms =
+            std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - start).count();
+        timings->kernel_ms = kernel_ms;
+        timings->input_kv_bytes = kb + vb;
+        timings->scratch_bytes = scratch;
+        timings->output_bytes = qn * 4;
+    }
+    for (size_t i = 0; i < qn; ++i)
+        if (!std::isfinite(out[i])) return fail("non-finite computation: GPU output", MSLIM_ATTN_ERR_NONFINITE);
     return 0;
 }
 

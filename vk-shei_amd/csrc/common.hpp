@@ -29,6 +29,12 @@ __device__ __forceinline__ uint16_t write_bf16(float value) {
 
 __device__ __forceinline__ float round_bf16(float value) { return read_bf16(write_bf16(value)); }
 
+// IEEE binary16 -> f32, exact for every encoding (subnormals, inf, NaN
+// payloads) through the hardware conversion.
+__device__ __forceinline__ float half_to_float(uint16_t bits) {
+    return (float)__builtin_bit_cast(_Float16, bits);
+}
+
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     return (uint32_t)write_bf16(lo) | ((uint32_t)write_bf16(hi) << 16);
 }

@@ -49,6 +49,24 @@ struct PrefillLaunch {
 bool prefill_fast_path(int head_dim, int group);
 hipError_t launch_prefill(const PrefillLaunch &a, hipStream_t stream);
 
+// Portable-backend decode: f32 query, raw K/V frames, f32 output.
+constexpr int kFormatBf16 = 1, kFormatF16 = 2, kFormatF32 = 3;  // gpu_backend.rs:258-262
+constexpr int kFramesMaxDim = 1024;
+struct FramesLaunch {
+    const float *q;
+    const void *k, *v;
+    int key_format, value_format;
+    float *out;
+    float *partial_ml, *partial_acc;  // [q_heads][splits][2], [q_heads][splits][D]
+    int64_t tokens;                   // >= 1
+    int q_heads, kv_heads, head_dim;
+    int split_tokens;                 // multiple of 256
+    float scale;
+};
+// Tokens per split for a launch of `tokens` tokens and q_heads heads.
+int frames_split_tokens(int64_t tokens, int q_heads);
+hipError_t launch_frames_decode(const FramesLaunch &l, hipStream_t stream);
+
 hipError_t launch_rmsnorm(const uint16_t *in, const uint16_t *w, uint16_t *out, int tokens,
                           int hidden, float eps, hipStream_t stream);
 hipError_t launch_rope(const uint16_t *in, uint16_t *out, int tokens, int heads, int head_dim,

@@ -21,6 +21,18 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmslim_attn.so")
 
 MAX_BATCH = 64
+FORMAT_BF16, FORMAT_F16, FORMAT_F32 = 1, 2, 3  # gpu_backend.rs:258-262
+ERR_NONFINITE = -2
+
+
+class Timings(C.Structure):
+    """mslim_attn_timings (GpuTimings, gpu_backend.rs:34-44)."""
+    _fields_ = [("dispatch_ms", C.c_double), ("kernel_ms", C.c_double),
+                ("input_kv_bytes", C.c_uint64), ("scratch_bytes", C.c_uint64),
+                ("output_bytes", C.c_uint64)]
+
+    def as_dict(self) -> dict:
+        return {name: getattr(self, name) for name, _ in self._fields_}
 
 EXPORTS = (
     "mslim_attn_last_error",
@@ -36,6 +48,8 @@ EXPORTS = (
     "mslim_attn_decode_dense",
     "mslim_attn_decode_paged",
     "mslim_attn_prefill_causal",
+    "mslim_attn_frames_decode",
+    "mslim_attn_backend_decode",
     "mslim_attn_rmsnorm",
     "mslim_attn_rope",
     "mslim_attn_swiglu",
@@ -85,6 +99,8 @@ def library() -> C.CDLL:
         "mslim_attn_decode_dense": (I, [P, P, P, P, P, I, PI32, I64, I, I, I, F, I]),
         "mslim_attn_decode_paged": (I, [P, P, P, P, P, I, PI32, P, I, I, I, I, I, F, I]),
         "mslim_attn_prefill_causal": (I, [P, P, P, P, P, I, I, I, I, I, F]),
+        "mslim_attn_frames_decode": (I, [P, P, P, I, P, I, P, I64, I, I, I]),
+        "mslim_attn_backend_decode": (I, [P, P, P, I, P, I, I64, I, I, I, P, C.POINTER(Timings)]),
         "mslim_attn_rmsnorm": (I, [P, P, P, P, I, I, F]),
         "mslim_attn_rope": (I, [P, P, P, I, I, I, I, F, I, F, F, F, F]),
         "mslim_attn_swiglu": (I, [P, P, P, P, SZ]),
@@ -195,6 +211,31 @@ class Context:
         self._check("prefill_causal", self._lib.mslim_attn_prefill_causal(
             self._h, _ptr(q), _ptr(k), _ptr(v), _ptr(out), queries, prior, q_heads, kv_heads,
             head_dim, scale))
+
+    # ---- portable backend (exact K/V frames) -----------------------------
+    def frames_decode(self, query, keys, key_format: int, values, value_format: int, out,
+                      tokens: int, q_heads: int, kv_heads: int, head_dim: int) -> None:
+        """Device buffers: f32 query/out, raw K/V frames [tokens][kv_heads][D]."""
+        self._check("frames_decode", self._lib.mslim_attn_frames_decode(
+            self._h, _ptr(query), _ptr(keys), key_format, _ptr(values), value_format, _ptr(out),
+            tokens, q_heads, kv_heads, head_dim))
+
+    def backend_decode(self, query, keys: bytes, key_format: int, values: bytes,
+                       value_format: int, tokens: int, q_heads: int, kv_heads: int,
+                       head_dim: int):
+        """Blocking host-memory decode; returns (f32 numpy output, Timings)."""
+        import numpy as np
+        q = np.ascontiguousarray(query, np.float32)
+        out = np.empty(q_heads * head_dim, np.float32)
+        kb = np.frombuffer(bytes(keys), np.uint8) if keys is not None else None
+        vb = np.frombuffer(bytes(values), np.uint8) if values is not None else None
+        t = Timings()
+        rc = self._lib.mslim_attn_backend_decode(
+            self._h, q.ctypes.data, kb.ctypes.data if kb is not None and kb.size else None,
+            key_format, vb.ctypes.data if vb is not None and vb.size else None, value_format,
+            tokens, q_heads, kv_heads, head_dim, out.ctypes.data, C.byref(t))
+        self._check("backend_decode", rc)
+        return out, t
 
     # ---- feeders --------------------------------------------------------
     def rmsnorm(self, x, weight, out, tokens: int, hidden: int, eps: float) -> None:
