@@ -62,6 +62,22 @@ void *mslim_attn_ctx_new(void);
 /* Replaces tv_hip_destroy (hipblaslt_bridge.cpp:170-172, native_hip.rs:103). */
 void mslim_attn_ctx_destroy(void *ctx);
 
+/* Device report, the GpuDeviceInfo of gpu_backend.rs:21-32 (OpenCL
+ * clGetDeviceInfo fields) from hipGetDeviceProperties.  max_allocation_bytes
+ * is the memory free at the time of the call (HIP has no per-allocation
+ * limit below it). */
+typedef struct {
+    char name[256];
+    char arch[64];   /* gcnArchName, "gfx950:..." */
+    char vendor[64];
+    int driver_version;
+    uint32_t compute_units;
+    uint64_t global_memory_bytes;
+    uint64_t max_allocation_bytes;
+    uint32_t lds_bytes_per_workgroup;
+} mslim_attn_device_info;
+int mslim_attn_get_device_info(void *ctx, mslim_attn_device_info *out);
+
 /* Route this context's work onto an existing HIP stream; NULL names the HIP
  * null (legacy default) stream.  Until this is called the context uses a
  * stream of its own.  No reference counterpart: the OpenCL engine owns its

@@ -212,6 +212,29 @@ void *mslim_attn_ctx_new(void) {
 
 void mslim_attn_ctx_destroy(void *ctx) { delete ctx_of(ctx); }
 
+int mslim_attn_get_device_info(void *ctx, mslim_attn_device_info *out) {
+    g_error.clear();
+    if (!ctx || !out) return fail("device info needs a context and an output struct");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    hipDeviceProp_t prop{};
+    if (int rc = check_hip(hipGetDeviceProperties(&prop, c.device), "hipGetDeviceProperties")) return rc;
+    int driver = 0;
+    if (int rc = check_hip(hipDriverGetVersion(&driver), "hipDriverGetVersion")) return rc;
+    size_t free_bytes = 0, total_bytes = 0;
+    if (int rc = check_hip(hipMemGetInfo(&free_bytes, &total_bytes), "hipMemGetInfo")) return rc;
+    std::memset(out, 0, sizeof *out);
+    std::snprintf(out->name, sizeof out->name, "%s", prop.name);
+    std::snprintf(out->arch, sizeof out->arch, "%s", prop.gcnArchName);
+    std::snprintf(out->vendor, sizeof out->vendor, "%s", "Advanced Micro Devices, Inc.");
+    out->driver_version = driver;
+    out->compute_units = (uint32_t)prop.multiProcessorCount;
+    out->global_memory_bytes = (uint64_t)prop.totalGlobalMem;
+    out->max_allocation_bytes = (uint64_t)free_bytes;
+    out->lds_bytes_per_workgroup = (uint32_t)prop.sharedMemPerBlock;
+    return 0;
+}
+
 int mslim_attn_ctx_set_stream(void *ctx, void *hip_stream) {
     g_error.clear();
     if (!ctx) return fail("null context");

@@ -29,7 +29,6 @@ template <int FMT>
 struct Fmt;
 template <>
 struct Fmt<kFormatBf16> {
-    static constexpr int kBytes = 2;
     __device__ static float at(const void *p, int64_t i) {
         return read_bf16(static_cast<const uint16_t *>(p)[i]);
     }
@@ -44,7 +43,6 @@ struct Fmt<kFormatBf16> {
 };
 template <>
 struct Fmt<kFormatF16> {
-    static constexpr int kBytes = 2;
     __device__ static float at(const void *p, int64_t i) {
         return half_to_float(static_cast<const uint16_t *>(p)[i]);
     }
@@ -59,7 +57,6 @@ struct Fmt<kFormatF16> {
 };
 template <>
 struct Fmt<kFormatF32> {
-    static constexpr int kBytes = 4;
     __device__ static float at(const void *p, int64_t i) { return static_cast<const float *>(p)[i]; }
 };
 

@@ -55,7 +55,7 @@ struct Swz {
 
 // s_waitcnt immediate that waits until at most n vector-memory operations
 // are outstanding and leaves the LDS/scalar and export counters alone.
-constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+[[maybe_unused]] constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
 
 // WAVES wavefronts per workgroup cover HW heads x (WAVES/HW) row blocks of
 // 32 rows; STAGES K/V tiles live in LDS (STAGES-1 in flight).

@@ -25,6 +25,14 @@ FORMAT_BF16, FORMAT_F16, FORMAT_F32 = 1, 2, 3  # gpu_backend.rs:258-262
 ERR_NONFINITE = -2
 
 
+class DeviceInfo(C.Structure):
+    """mslim_attn_device_info (GpuDeviceInfo, gpu_backend.rs:21-32)."""
+    _fields_ = [("name", C.c_char * 256), ("arch", C.c_char * 64), ("vendor", C.c_char * 64),
+                ("driver_version", C.c_int), ("compute_units", C.c_uint32),
+                ("global_memory_bytes", C.c_uint64), ("max_allocation_bytes", C.c_uint64),
+                ("lds_bytes_per_workgroup", C.c_uint32)]
+
+
 class Timings(C.Structure):
     """mslim_attn_timings (GpuTimings, gpu_backend.rs:34-44)."""
     _fields_ = [("dispatch_ms", C.c_double), ("kernel_ms", C.c_double),
@@ -38,6 +46,7 @@ EXPORTS = (
     "mslim_attn_last_error",
     "mslim_attn_ctx_new",
     "mslim_attn_ctx_destroy",
+    "mslim_attn_get_device_info",
     "mslim_attn_ctx_set_stream",
     "mslim_attn_synchronize",
     "mslim_attn_buf_alloc",
@@ -89,6 +98,7 @@ def library() -> C.CDLL:
         "mslim_attn_last_error": (C.c_char_p, []),
         "mslim_attn_ctx_new": (P, []),
         "mslim_attn_ctx_destroy": (None, [P]),
+        "mslim_attn_get_device_info": (I, [P, C.POINTER(DeviceInfo)]),
         "mslim_attn_ctx_set_stream": (I, [P, P]),
         "mslim_attn_synchronize": (I, [P]),
         "mslim_attn_buf_alloc": (P, [P, SZ]),
@@ -183,6 +193,12 @@ class Context:
     def use_torch_stream(self) -> None:
         import torch
         self.set_stream(torch.cuda.current_stream().cuda_stream)
+
+    def device_info(self) -> dict:
+        info = DeviceInfo()
+        self._check("device_info", self._lib.mslim_attn_get_device_info(self._h, C.byref(info)))
+        return {name: (getattr(info, name).decode() if isinstance(getattr(info, name), bytes)
+                       else getattr(info, name)) for name, _ in DeviceInfo._fields_}
 
     def synchronize(self) -> None:
         self._check("synchronize", self._lib.mslim_attn_synchronize(self._h))
