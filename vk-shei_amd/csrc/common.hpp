@@ -49,6 +49,30 @@ __device__ __forceinline__ void dma16(const void *global, void *lds_base) {
     __builtin_amdgcn_global_load_lds(global, lds_base, 16, 0, 0);
 }
 
+// LDS offset (wave-uniform, in an SGPR) of a __shared__ address.
+__device__ __forceinline__ uint32_t lds_offset(const void *lds) {
+    return __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)lds);
+}
+
+// The same copy as dma16, issued through inline assembly so that the
+// compiler does not order later LDS reads behind it (it cannot tell which
+// LDS stage an in-flight copy targets and would wait for all of them).  The
+// caller waits for it explicitly: s_waitcnt vmcnt, then a barrier, before any
+// wavefront reads the destination.
+// M0 is reserved by the compiler, so the asm saves and restores it.
+__device__ __forceinline__ void dma16_async(const void *global, uint32_t lds_base) {
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "global_load_lds_dwordx4 %1, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(global), "s"(lds_base)
+        : "memory");
+}
+
 // ds_read_b64_tr_b16: within each 16-lane quarter wave, lane i receives
 // element i%4 of the 8 bytes read by lanes i/4, 4+i/4, 8+i/4, 12+i/4.
 __device__ __forceinline__ short4_t lds_read_tr16(const uint16_t *lds) {
@@ -67,6 +91,20 @@ __device__ __forceinline__ float add_bf16_pair(bf16x2_t pair, float acc) {
     ones[1] = (__bf16)1.0f;
     return __builtin_amdgcn_fdot2_f32_bf16(pair, ones, acc, false);
 }
+
+// Maximum of a lane's value and its partner's in the other 32-lane half
+// (v_permlane32_swap: lanes 0-31 receive the upper half's values in the first
+// result, lanes 32-63 the lower half's in the second).
+__device__ __forceinline__ float half_pair_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __builtin_fmaxf(x, __builtin_fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1])));
+}
+
+// Keeps a value's computation at this point of the program: an empty asm
+// that reads and writes it cannot be moved, so the value must be ready here
+// (used to hold VALU work between the MFMAs it is meant to overlap).
+__device__ __forceinline__ void pin_value(uint32_t &x) { asm volatile("" : "+v"(x)); }
+__device__ __forceinline__ void pin_value(float &x) { asm volatile("" : "+v"(x)); }
 
 // Butterfly reductions across the 64-lane wavefront.
 __device__ __forceinline__ float wave_xor_max(float v, int mask) {
