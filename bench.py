@@ -8,8 +8,11 @@ the one the targets are quoted on):
     pages in a seeded random permutation plus a contiguous 4,096-token hot
     recent window per sequence;
   * causal prefill of 8,192 tokens at the same head shape.
-One step = one paged decode pass + one causal prefill pass.  Inputs are
-resident in HBM before timing starts.
+One step = one paged decode pass + one causal prefill pass.  The timed
+region runs the K decode passes back to back and then the K prefill passes,
+with events on the launch stream around each phase.  Inputs are resident in
+HBM before timing starts.  A decode launched directly after a prefill is
+timed separately and reported as `decode_after_prefill_ms`.
 
 `value` is the decode's achieved HBM bandwidth (algorithmic K+V+Q+O bytes /
 average decode launch time measured with HIP events on the launch stream);
@@ -305,30 +308,41 @@ def main() -> int:
         prefill()
     torch.cuda.synchronize()
 
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
-           torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    # Timed region: K steps = K decode launches back to back, then K prefill
+    # launches back to back, with events on the launch stream around each
+    # phase, so each kernel's average is its steady-state launch duration.
+    mk = lambda: torch.cuda.Event(enable_timing=True)
+    start_all, mid, end_all = mk(), mk(), mk()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     torch.cuda._sleep(QUEUE_FILL_CYCLES)
-    start_all = torch.cuda.Event(enable_timing=True)
-    end_all = torch.cuda.Event(enable_timing=True)
     start_all.record()
-    for i in range(args.steps):
-        ev[i][0].record()
+    for _ in range(args.steps):
         decode()
-        ev[i][1].record()
+    mid.record()
+    for _ in range(args.steps):
         prefill()
-        ev[i][2].record()
     end_all.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     step_ms = start_all.elapsed_time(end_all) / args.steps
-    dec_ms = [a.elapsed_time(b) for a, b, _ in ev]
-    pre_ms = [b.elapsed_time(c) for _, b, c in ev]
-    dec_avg = sum(dec_ms) / len(dec_ms)
-    pre_avg = sum(pre_ms) / len(pre_ms)
+    dec_avg = start_all.elapsed_time(mid) / args.steps
+    pre_avg = mid.elapsed_time(end_all) / args.steps
     log(f"bench: {args.steps} steps, {step_ms:.3f} ms/step (wall {wall * 1e3 / args.steps:.3f}), "
         f"decode {dec_avg * 1e3:.1f} us, prefill {pre_avg * 1e3:.1f} us")
+
+    # Informational: decode launched directly after a prefill (the prefill's
+    # output is still being written back and the clock is recovering).
+    pairs = [(mk(), mk()) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    torch.cuda._sleep(QUEUE_FILL_CYCLES)
+    for a, b in pairs:
+        prefill()
+        a.record()
+        decode()
+        b.record()
+    torch.cuda.synchronize()
+    dec_after_prefill = sum(a.elapsed_time(b) for a, b in pairs) / args.steps
 
     # dense decode on the same data, for reference
     for _ in range(3):
@@ -390,8 +404,8 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(dec_gbps / PEAK_HBM_GBPS, 4),
             "traffic": traffic,
-            "kernel": "decode paged (split + merge launches), algorithmic bytes "
-                      f"{decode_bytes()} per launch",
+            "kernel": "decode_kernel<128,8,paged,2,fused> (one launch; the last workgroup of each "
+                      f"(sequence, kv head) merges the splits), algorithmic bytes {decode_bytes()} per launch",
         },
         "prefill": {
             "value": round(pre_tflops, 2),
@@ -404,10 +418,11 @@ def main() -> int:
                 "unit": "TFLOP/s",
                 "frac": round(pre_tflops / PEAK_BF16_TFLOPS, 4),
                 "traffic": pre_traffic,
-                "kernel": f"prefill_mfma_kernel<128,8,8,2>, algorithmic FLOP {prefill_flops()} per launch",
+                "kernel": f"prefill_mfma_kernel<128,8>, algorithmic FLOP {prefill_flops()} per launch",
             },
         },
         "decode_ms": round(dec_avg, 5),
+        "decode_after_prefill_ms": round(dec_after_prefill, 5),
         "decode_dense_gbps": round(dense_gbps, 2),
         "paged_equals_dense": paged_equals_dense,
         "cpu_baseline": cpu,

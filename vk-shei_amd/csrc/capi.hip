@@ -40,6 +40,8 @@ struct Context {
     std::mutex mutex;
     void *workspace = nullptr;      // decode split partials
     size_t workspace_bytes = 0;
+    int *counters = nullptr;        // decode split counters, zero between launches
+    size_t counter_bytes = 0;
     void *staging = nullptr;       // device, digest serialisation
     size_t staging_bytes = 0;
     void *host_staging = nullptr;  // pinned host, digest readback
@@ -51,6 +53,7 @@ struct Context {
     ~Context() {
         if (stream) (void)hipStreamSynchronize(stream);
         if (workspace) (void)hipFree(workspace);
+        if (counters) (void)hipFree(counters);
         if (staging) (void)hipFree(staging);
         if (host_staging) (void)hipHostFree(host_staging);
         if (backend) (void)hipFree(backend);
@@ -128,6 +131,18 @@ int decode_common(Context &c, mslim::DecodeLaunch &l, const int32_t *seq_lens, i
         return rc;
     l.partial_ml = static_cast<float *>(c.workspace);
     l.partial_acc = reinterpret_cast<float *>(static_cast<char *>(c.workspace) + ml_bytes);
+    // One split counter per (sequence, kv head); the kernel leaves them at
+    // zero, so they are cleared only when the buffer is (re)allocated.
+    const size_t ctr_bytes = (size_t)MSLIM_ATTN_MAX_BATCH * l.kv_heads * sizeof(int);
+    if (c.counter_bytes < ctr_bytes) {
+        void *mem = c.counters;
+        if (int rc = grow_device(c, &mem, &c.counter_bytes, ctr_bytes, "hipMalloc decode split counters"))
+            return rc;
+        c.counters = static_cast<int *>(mem);
+        if (int rc = check_hip(hipMemsetAsync(c.counters, 0, ctr_bytes, c.stream), "hipMemset split counters"))
+            return rc;
+    }
+    l.counters = c.counters;
     return check_hip(mslim::launch_decode(l, c.stream), "decode attention launch");
 }
 

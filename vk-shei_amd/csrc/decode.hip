@@ -43,6 +43,7 @@ struct DeviceArgs {
     uint16_t *out;
     float *partial_ml;
     float *partial_acc;
+    int *counters;  // [batch][kv_heads] splits finished, zero between launches
     const int32_t *page_table;
     int64_t seq_stride_tokens;
     int pages_per_seq, page_shift;
@@ -105,7 +106,19 @@ __device__ __forceinline__ uint32_t pair_bf16(uint32_t hi_src, uint32_t lo_src, 
     return __builtin_amdgcn_perm(hi_src, lo_src, sel);
 }
 
-template <int D, int G, bool PAGED, int DEPTH>
+// Relaxed agent-scope atomics: coherent across the XCDs' L2 caches.
+__device__ __forceinline__ void store_coherent(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(const float *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int D, int G>
+__device__ __forceinline__ void merge_splits(const DeviceArgs &a, int b, int kvh, int tid, int nthreads,
+                                             bool coherent);
+
+template <int D, int G, bool PAGED, int DEPTH, bool FUSED>
 __global__ __launch_bounds__(64 * kWaves, 2) void decode_kernel(DeviceArgs a) {
     constexpr int KS = D / 32;        // Q.K MFMA k-steps per 16-token block
     constexpr int LPR = D / 8;        // lanes per V row (8 BF16 per lane)
@@ -334,28 +347,58 @@ __global__ __launch_bounds__(64 * kWaves, 2) void decode_kernel(DeviceArgs a) {
             packed.x = pack_bf16x2(ov.x / l, ov.y / l);
             packed.y = pack_bf16x2(ov.z / l, ov.w / l);
             *reinterpret_cast<uint2 *>(a.out + ((int64_t)b * a.q_heads + qh0 + g) * D + d) = packed;
+        } else if constexpr (FUSED) {
+            // Agent-scope atomic stores are written through to the
+            // device-coherent level, so no cache writeback is needed before
+            // the counter below publishes them.
+            float *pa = a.partial_acc + (part + g) * D + d;
+            store_coherent(pa + 0, ov.x);
+            store_coherent(pa + 1, ov.y);
+            store_coherent(pa + 2, ov.z);
+            store_coherent(pa + 3, ov.w);
+            if (d == 0) {
+                store_coherent(a.partial_ml + (part + g) * 2, m);
+                store_coherent(a.partial_ml + (part + g) * 2 + 1, l);
+            }
         } else {
             *reinterpret_cast<float4 *>(a.partial_acc + (part + g) * D + d) = ov;
             if (d == 0) *reinterpret_cast<float2 *>(a.partial_ml + (part + g) * 2) = make_float2(m, l);
         }
     }
+    if constexpr (FUSED) {
+        if (final_write) return;
+        // Every store of this workgroup has completed before thread 0 counts
+        // the split; the workgroup that finishes a (sequence, kv head) last
+        // merges its partitions in fixed order, as decode_merge_kernel does.
+        __builtin_amdgcn_s_waitcnt(0);
+        __shared__ int last;
+        __syncthreads();
+        if (tid == 0) {
+            int *ctr = a.counters + (int64_t)b * a.kv_heads + kvh;
+            const int done = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last = done == nsplit - 1;
+            if (last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (!last) return;
+        merge_splits<D, G>(a, b, kvh, tid, 64 * kWaves, true);
+    }
 }
 
 // Fixed-order log-sum-exp merge of the split partials of one (sequence, kv
-// head): thread -> (head, 4 dims), one online pass over the partitions.  Runs
-// as its own launch after the split kernel, so no device-scope fence is
-// needed between them (the deterministic counterpart of
-// mslim_attention_merge, tiled_attention.cl:131-155).
+// head): thread -> (head, 4 dims), one online pass over the partitions (the
+// deterministic counterpart of mslim_attention_merge,
+// tiled_attention.cl:131-155).  Run either by the last split workgroup of
+// the decode kernel (partials read with coherent loads) or as a launch of its
+// own after it.
 template <int D, int G>
-__global__ __launch_bounds__(256) void decode_merge_kernel(DeviceArgs a) {
-    const int kvh = blockIdx.x % a.kv_heads;
-    const int b = blockIdx.x / a.kv_heads;
+__device__ __forceinline__ void merge_splits(const DeviceArgs &a, int b, int kvh, int tid, int nthreads,
+                                             bool coherent) {
     const int nsplit = a.split_begin[b + 1] - a.split_begin[b];
-    if (nsplit <= 1) return;
     const int s0 = a.split_begin[b];
     const float c = a.scale_log2e;
     const int qh0 = kvh * G;
-    for (int it = threadIdx.x; it < G * D / 4; it += 256) {
+    for (int it = tid; it < G * D / 4; it += nthreads) {
         const int g = it / (D / 4);
         const int d = (it % (D / 4)) * 4;
         float m = -INFINITY, l = 0.0f;
@@ -363,8 +406,17 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DeviceArgs a) {
 #pragma unroll 8
         for (int s = 0; s < nsplit; ++s) {
             const int64_t idx = ((int64_t)(s0 + s) * a.kv_heads + kvh) * G + g;
-            const float2 ml = *reinterpret_cast<const float2 *>(a.partial_ml + idx * 2);
-            const float4 x = *reinterpret_cast<const float4 *>(a.partial_acc + idx * D + d);
+            float2 ml;
+            float4 x;
+            if (coherent) {
+                ml = make_float2(load_coherent(a.partial_ml + idx * 2), load_coherent(a.partial_ml + idx * 2 + 1));
+                const float *pa = a.partial_acc + idx * D + d;
+                x = make_float4(load_coherent(pa), load_coherent(pa + 1), load_coherent(pa + 2),
+                                load_coherent(pa + 3));
+            } else {
+                ml = *reinterpret_cast<const float2 *>(a.partial_ml + idx * 2);
+                x = *reinterpret_cast<const float4 *>(a.partial_acc + idx * D + d);
+            }
             const float m_new = fmaxf(m, ml.x);
             const float wo = __builtin_amdgcn_exp2f((m - m_new) * c);
             const float wn = __builtin_amdgcn_exp2f((ml.x - m_new) * c);
@@ -378,6 +430,14 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DeviceArgs a) {
         packed.y = pack_bf16x2(ov.z / l, ov.w / l);
         *reinterpret_cast<uint2 *>(a.out + ((int64_t)b * a.q_heads + qh0 + g) * D + d) = packed;
     }
+}
+
+template <int D, int G>
+__global__ __launch_bounds__(256) void decode_merge_kernel(DeviceArgs a) {
+    const int kvh = blockIdx.x % a.kv_heads;
+    const int b = blockIdx.x / a.kv_heads;
+    if (a.split_begin[b + 1] - a.split_begin[b] <= 1) return;
+    merge_splits<D, G>(a, b, kvh, threadIdx.x, 256, false);
 }
 
 // Any-geometry fallback (head_dim not 64/128, or groups outside 1/2/4/8):
@@ -447,19 +507,23 @@ __global__ __launch_bounds__(64) void decode_generic_kernel(DeviceArgs a, int D)
 #ifndef MSLIM_DECODE_DEPTH
 #define MSLIM_DECODE_DEPTH 2
 #endif
+#ifndef MSLIM_DECODE_FUSED
+#define MSLIM_DECODE_FUSED 1
+#endif
 
 template <int D, int G>
 hipError_t launch_fast(const DeviceArgs &a, bool paged, int total_splits, bool merge,
                        hipStream_t stream) {
     const dim3 grid((unsigned)(total_splits * a.kv_heads));
+    constexpr bool F = MSLIM_DECODE_FUSED != 0;
     if (paged)
-        hipLaunchKernelGGL((decode_kernel<D, G, true, MSLIM_DECODE_DEPTH>), grid, dim3(64 * kWaves), 0,
+        hipLaunchKernelGGL((decode_kernel<D, G, true, MSLIM_DECODE_DEPTH, F>), grid, dim3(64 * kWaves), 0,
                            stream, a);
     else
-        hipLaunchKernelGGL((decode_kernel<D, G, false, MSLIM_DECODE_DEPTH>), grid, dim3(64 * kWaves), 0,
+        hipLaunchKernelGGL((decode_kernel<D, G, false, MSLIM_DECODE_DEPTH, F>), grid, dim3(64 * kWaves), 0,
                            stream, a);
     hipError_t err = hipGetLastError();
-    if (err != hipSuccess || !merge) return err;
+    if (err != hipSuccess || !merge || F) return err;
     hipLaunchKernelGGL((decode_merge_kernel<D, G>), dim3((unsigned)(a.batch * a.kv_heads)), dim3(256), 0,
                        stream, a);
     return hipGetLastError();
@@ -488,6 +552,7 @@ hipError_t launch_decode(const DecodeLaunch &l, hipStream_t stream) {
     DeviceArgs a{};
     a.q = l.q; a.k = l.k; a.v = l.v; a.out = l.out;
     a.partial_ml = l.partial_ml; a.partial_acc = l.partial_acc;
+    a.counters = l.counters;
     a.page_table = l.page_table;
     a.seq_stride_tokens = l.seq_stride_tokens;
     a.pages_per_seq = l.pages_per_seq;

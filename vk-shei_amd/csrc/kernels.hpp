@@ -17,6 +17,7 @@ struct DecodeLaunch {
     uint16_t *out;
     float *partial_ml;   // [splits_total][kv_heads][G][2]
     float *partial_acc;  // [splits_total][kv_heads][G][D]
+    int *counters;       // [batch][kv_heads], all zero between launches
     const int32_t *page_table;  // paged only: [batch][pages_per_seq]
     int64_t seq_stride_tokens;  // dense only
     int pages_per_seq;
