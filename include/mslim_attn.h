@@ -250,6 +250,63 @@ int mslim_attn_logical_kv_sha256(void *ctx, int layers, int64_t tokens, int kv_h
                                  const int32_t *const *page_tables, int page_tokens,
                                  char *hex_out);
 
+/* ---- ColdStore record frames ----------------------------------------------- */
+
+/* One ColdStore record to be made from a pool page: its header fields
+ * (cold_store.rs:291-309) and the pool page holding its K and V payloads in
+ * rows 0..tokens-1 of every head. */
+typedef struct {
+    uint64_t page_id;
+    uint64_t token_start;
+    uint32_t layer;
+    uint32_t tokens;    /* 1..page_tokens */
+    int32_t pool_page;  /* 0..pool_pages-1 */
+    uint32_t reserved;  /* ignored */
+} mslim_attn_page_record;
+
+#define MSLIM_ATTN_RECORD_HEADER_BYTES 104 /* cold_store.rs:23 */
+#define MSLIM_ATTN_RECORD_FOOTER_BYTES 56  /* cold_store.rs:24 */
+
+/* Bytes of one frame slot for pools of `page_tokens`-token pages:
+ * 104 + 16 * page_tokens + 56. */
+int64_t mslim_attn_record_frame_bytes(int page_tokens);
+
+/* Compute, on the device, everything of a ColdStore record except its
+ * payloads, for `count` records whose K/V payloads sit in pool pages.  The
+ * device counterpart of ColdStore::prepare_page (cold_store.rs:269-349) with
+ * token_hashes (:725-742), checksum / checksum_many (:909-922) and the
+ * SHA-256 record digest (:924-930); byte-identical to them.
+ *   k_pool, v_pool: page pools [pool_pages][kv_heads][page_tokens][head_dim]
+ *     BF16 (head_dim * 2 bytes per row).
+ *   records: device array [count].
+ *   frames: device output [count][mslim_attn_record_frame_bytes(page_tokens)];
+ *     slot i holds header (104 B) | K token hashes (8 * tokens_i B) | V token
+ *     hashes (8 * tokens_i B) | zeros | footer (56 B, the slot's last bytes).
+ * Record i's file bytes are slot[0 .. 104 + 16 * tokens_i) | K payload |
+ * V payload | slot footer, the payloads being the head-major
+ * [kv_heads][tokens_i][head_dim] rows of pool page pool_page.  A record
+ * whose tokens or pool_page is out of range gets an all-zero slot (no
+ * header magic).  `tile` must divide head_dim (cold_store.rs:690-692).
+ * Stream-ordered. */
+int mslim_attn_record_frames(void *ctx, const void *k_pool, const void *v_pool, int64_t pool_pages,
+                             int page_tokens, int kv_heads, int head_dim, uint32_t tile,
+                             const mslim_attn_page_record *records, int count, void *frames);
+
+/* Move the payloads of `count` records between their pool pages and
+ * contiguous staging, so a batch of records crosses PCIe as one copy each
+ * way.  Staging slot i (kv_heads * page_tokens * head_dim * 2 bytes in
+ * k_stage and in v_stage) holds record i's payload compacted to
+ * [kv_heads][tokens_i][head_dim]: exactly the bytes ColdStore stores
+ * (cold_store.rs:480-483).  direction 0: pool -> staging (sealing pages into
+ * the ColdStore, the device side of GpuRegionStore::append_batch,
+ * gpu_region_store.rs:452-472); direction 1: staging -> pool (restoring
+ * verified pages, replacing the per-chunk read_values + H2D staging of
+ * gpu_resources.rs:1017-1048).  Records out of range are skipped.
+ * Stream-ordered. */
+int mslim_attn_record_payloads(void *ctx, void *k_pool, void *v_pool, int64_t pool_pages, int page_tokens,
+                               int kv_heads, int head_dim, const mslim_attn_page_record *records,
+                               int count, void *k_stage, void *v_stage, int direction);
+
 #ifdef __cplusplus
 }
 #endif

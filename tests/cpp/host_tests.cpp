@@ -15,6 +15,7 @@
 #include <vector>
 
 #include "../../oracle/oracle.h"
+#include "harness.hpp"
 #include "../../vk-shei_amd/host/attention_kernel.hpp"
 #include "../../vk-shei_amd/host/portable.hpp"
 #include "../../vk-shei_amd/host/tiled_attention.hpp"
@@ -24,39 +25,8 @@ using namespace mslim::portable;
 
 namespace {
 
-struct Case {
-    const char *name;
-    std::function<void()> fn;
-};
-std::vector<Case> &registry() {
-    static std::vector<Case> r;
-    return r;
-}
-struct Register {
-    Register(const char *n, std::function<void()> f) { registry().push_back({n, std::move(f)}); }
-};
-#define TEST(name)                                   \
-    static void name();                              \
-    static Register reg_##name(#name, name);         \
-    static void name()
-
-struct Failure : std::runtime_error {
-    using std::runtime_error::runtime_error;
-};
-#define CHECK(cond)                                                                                   \
-    do {                                                                                              \
-        if (!(cond)) throw Failure(std::string(__FILE__ ":") + std::to_string(__LINE__) + ": " #cond); \
-    } while (0)
-
-template <class E = std::exception, class F>
-std::string expect_throw(F f) {
-    try {
-        f();
-    } catch (const E &e) {
-        return e.what();
-    }
-    throw Failure("expected an exception");
-}
+using harness::expect_throw;
+using harness::Failure;
 
 template <class F>
 PortableError::Kind expect_portable(F f) {
@@ -472,29 +442,4 @@ TEST(gpu_tiled_attention_multi_query_prefill) {
 
 }  // namespace
 
-int main(int argc, char **argv) {
-    if (argc == 2 && std::strcmp(argv[1], "--list") == 0) {
-        for (const auto &c : registry()) std::printf("%s\n", c.name);
-        return 0;
-    }
-    int failed = 0, ran = 0;
-    for (const auto &c : registry()) {
-        bool wanted = argc == 1;
-        for (int i = 1; i < argc; ++i) wanted = wanted || std::strcmp(argv[i], c.name) == 0;
-        if (!wanted) continue;
-        ++ran;
-        try {
-            c.fn();
-            std::printf("PASS %s\n", c.name);
-        } catch (const std::exception &e) {
-            ++failed;
-            std::printf("FAIL %s: %s\n", c.name, e.what());
-        }
-        std::fflush(stdout);
-    }
-    if (ran == 0) {
-        std::printf("no such case\n");
-        return 2;
-    }
-    return failed ? 1 : 0;
-}
+int main(int argc, char **argv) { return harness::run_cases(argc, argv); }

@@ -1,0 +1,727 @@
+// Tests of the C++ ColdStore and exact region store
+// (vk-shei_amd/host/cold_store.*, region_store.*), restating the reference's
+// own tests (cold_store.rs:963-1284, gpu_region_store.rs:963-1085) and
+// checking every record byte against the CPU oracle's restatement of
+// ColdStore::prepare_page.  Cases named gpu_* use the device page pool.
+#include <fcntl.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <random>
+#include <string>
+#include <vector>
+
+#include "../../oracle/oracle.h"
+#include "../../vk-shei_amd/host/cold_store.hpp"
+#include "../../vk-shei_amd/host/native.hpp"
+#include "../../vk-shei_amd/host/region_store.hpp"
+#include "harness.hpp"
+
+using namespace mslim;
+using cold::ColdStore;
+using cold::ColdStoreError;
+using cold::PageGeometry;
+using Kind = cold::ColdStoreError::Kind;
+using harness::Failure;
+
+namespace {
+
+// A fresh path under TMPDIR, removed with its directory at scope exit.
+struct TempPath {
+    std::string dir, path;
+    explicit TempPath(const char *name) {
+        const char *tmp = std::getenv("TMPDIR");
+        std::string pattern = std::string(tmp && *tmp ? tmp : "/tmp") + "/mslim-cold-test-XXXXXX";
+        std::vector<char> buf(pattern.begin(), pattern.end());
+        buf.push_back('\0');
+        if (!mkdtemp(buf.data())) throw Failure("mkdtemp");
+        dir = buf.data();
+        path = dir + "/" + name;
+    }
+    ~TempPath() {
+        ::unlink(path.c_str());
+        ::unlink((dir + "/pages-exact.kv").c_str());
+        ::rmdir(dir.c_str());
+    }
+};
+
+uint64_t file_size(const std::string &path) {
+    struct stat st;
+    if (stat(path.c_str(), &st) != 0) throw Failure("stat " + path);
+    return (uint64_t)st.st_size;
+}
+
+std::vector<uint8_t> read_file(const std::string &path) {
+    std::vector<uint8_t> out(file_size(path));
+    FILE *f = std::fopen(path.c_str(), "rb");
+    if (!f) throw Failure("open " + path);
+    const size_t n = std::fread(out.data(), 1, out.size(), f);
+    std::fclose(f);
+    if (n != out.size()) throw Failure("short read " + path);
+    return out;
+}
+
+void append_bytes(const std::string &path, const uint8_t *p, size_t n) {
+    FILE *f = std::fopen(path.c_str(), "ab");
+    if (!f) throw Failure("open " + path);
+    std::fwrite(p, 1, n, f);
+    std::fclose(f);
+}
+
+void write_at(const std::string &path, uint64_t offset, const uint8_t *p, size_t n) {
+    const int fd = ::open(path.c_str(), O_WRONLY);
+    if (fd < 0 || pwrite(fd, p, n, (off_t)offset) != (ssize_t)n) throw Failure("pwrite " + path);
+    fdatasync(fd);
+    ::close(fd);
+}
+
+template <class F>
+Kind expect_kind(F f) {
+    try {
+        f();
+    } catch (const ColdStoreError &e) {
+        return e.kind();
+    }
+    throw Failure("expected a ColdStoreError");
+}
+
+std::vector<uint8_t> filled(size_t n, uint8_t v) { return std::vector<uint8_t>(n, v); }
+
+// cold_store.rs:976-985
+PageGeometry geometry(uint64_t page) {
+    PageGeometry g;
+    g.layer = 3;
+    g.token_start = page * 4;
+    g.tokens = 4;
+    g.heads = 2;
+    g.head_dim = 4;
+    g.tile = 4;
+    return g;
+}
+
+std::vector<uint8_t> oracle_record(uint64_t page_id, const PageGeometry &g, const std::vector<uint8_t> &k,
+                                   const std::vector<uint8_t> &v) {
+    const size_t n = orc_coldstore_record(page_id, g.layer, g.token_start, g.tokens, g.heads, g.head_dim, g.tile,
+                                          k.data(), k.size(), v.data(), v.size(), nullptr, 0);
+    std::vector<uint8_t> out(n);
+    orc_coldstore_record(page_id, g.layer, g.token_start, g.tokens, g.heads, g.head_dim, g.tile, k.data(), k.size(),
+                         v.data(), v.size(), out.data(), out.size());
+    return out;
+}
+
+}  // namespace
+
+// ---- ColdStore: the reference's tests ------------------------------------------
+
+TEST(cold_read_only_reopen_rejects_append_and_preserves_bytes) {
+    TempPath t("readonly");
+    {
+        ColdStore store = ColdStore::create(t.path, 0);
+        store.append_page(geometry(0), filled(64, 7), filled(64, 11), false);
+    }
+    ColdStore frozen = ColdStore::open_read_only(t.path, 0);
+    CHECK(frozen.is_read_only());
+    frozen.audit_mapped();
+    CHECK(frozen.read_key(0) == filled(64, 7));
+    const auto k = filled(64, 1), v = filled(64, 2);
+    cold::PreparedPage prepared = ColdStore::prepare_page(1, geometry(1), k.data(), k.size(), v.data(), v.size());
+    CHECK(expect_kind([&] { frozen.append_prepared(prepared, false); }) == Kind::InvalidData);
+}
+
+TEST(cold_mapped_audit_verifies_committed_payload_without_resident_cache) {
+    TempPath t("mapped");
+    ColdStore store = ColdStore::create(t.path, 0);
+    store.append_page(geometry(0), filled(64, 7), filled(64, 11), false);
+    store.audit_mapped();
+    const auto s = store.stats();
+    CHECK(s.reads == 0);
+    CHECK(s.hot_bytes == 0);
+    CHECK(s.cryptographic_digests_verified == 1);
+}
+
+TEST(cold_append_reopen_selective_read_and_audit) {
+    TempPath t("roundtrip");
+    {
+        ColdStore store = ColdStore::create(t.path, 2);
+        for (uint64_t page = 0; page < 4; ++page) {
+            const auto meta = store.append_page(geometry(page), filled(32, (uint8_t)page),
+                                                filled(32, (uint8_t)(100 + page)), false);
+            CHECK(meta.page_id == page);
+        }
+    }
+    ColdStore reopened = ColdStore::open(t.path, 2);
+    CHECK(reopened.metadata().size() == 4);
+    CHECK(reopened.read_page(2)->key == filled(32, 2));
+    CHECK(reopened.read_page(2)->value == filled(32, 102));
+    reopened.audit();
+    CHECK(reopened.stats().reads == 1);
+    CHECK(reopened.stats().cache_hits == 1);
+}
+
+TEST(cold_selected_value_tokens_keep_head_major_layout_and_detect_corruption) {
+    TempPath t("selected-tokens");
+    ColdStore store = ColdStore::create(t.path, 0);
+    std::vector<uint8_t> key, value;
+    for (uint8_t head = 0; head < 2; ++head)
+        for (uint8_t token = 0; token < 4; ++token)
+            for (int i = 0; i < 4; ++i) {
+                key.push_back((uint8_t)(100 + head * 10 + token));
+                value.push_back((uint8_t)(head * 10 + token));
+            }
+    const auto meta = store.append_page(geometry(0), key, value, true);
+    auto cat = [](std::initializer_list<std::vector<uint8_t>> parts) {
+        std::vector<uint8_t> out;
+        for (const auto &p : parts) out.insert(out.end(), p.begin(), p.end());
+        return out;
+    };
+    CHECK(store.read_value_tokens(0, {1, 3}) == cat({filled(4, 1), filled(4, 3), filled(4, 11), filled(4, 13)}));
+    auto s = store.stats();
+    CHECK(s.partial_value_reads == 1);
+    CHECK(s.partial_value_payload_bytes == 16);
+    CHECK(s.partial_value_bytes_avoided == 16);
+    CHECK(s.bytes_read == 48);
+    CHECK(store.read_key_tokens(0, {0, 2}) == cat({filled(4, 100), filled(4, 102), filled(4, 110), filled(4, 112)}));
+    s = store.stats();
+    CHECK(s.partial_key_reads == 1);
+    CHECK(s.partial_key_payload_bytes == 16);
+    CHECK(s.partial_key_bytes_avoided == 16);
+
+    const uint8_t bad = 99;
+    write_at(t.path, meta.payload_offset + 2 * 4, &bad, 1);
+    CHECK(expect_kind([&] { store.read_key_tokens(0, {2}); }) == Kind::InvalidData);
+    write_at(t.path, meta.payload_offset + meta.key_len + 3 * 4, &bad, 1);
+    CHECK(expect_kind([&] { store.read_value_tokens(0, {3}); }) == Kind::InvalidData);
+}
+
+TEST(cold_lru_is_strictly_bounded) {
+    TempPath t("lru");
+    ColdStore store = ColdStore::create(t.path, 2);
+    for (uint64_t page = 0; page < 3; ++page)
+        store.append_page(geometry(page), filled(32, (uint8_t)page), filled(32, (uint8_t)page), false);
+    store.read_page(0);
+    store.read_page(1);
+    store.read_page(0);
+    store.read_page(2);
+    CHECK(store.hot_contains(0));
+    CHECK(!store.hot_contains(1));
+    CHECK(store.hot_contains(2));
+    CHECK(store.stats().hot_pages == 2);
+    CHECK(store.stats().evictions == 1);
+}
+
+TEST(cold_torn_final_append_is_not_catalogued) {
+    TempPath t("torn");
+    {
+        ColdStore store = ColdStore::create(t.path, 0);
+        store.append_page(geometry(0), filled(32, 1), filled(32, 2), true);
+    }
+    append_bytes(t.path, reinterpret_cast<const uint8_t *>("TSKVPG04"), 8);
+    {
+        ColdStore reopened = ColdStore::open(t.path, 0);
+        CHECK(reopened.metadata().size() == 1);
+        CHECK(reopened.stats().committed_bytes == 104 + 4 * 8 * 2 + 64 + 56);  // cold_store.rs:1141-1144
+        reopened.append_page(geometry(1), filled(32, 3), filled(32, 4), true);
+    }
+    ColdStore again = ColdStore::open(t.path, 0);
+    CHECK(again.metadata().size() == 2);
+}
+
+TEST(cold_failed_partial_append_followed_by_append_still_reopens) {
+    TempPath t("partial-then-append");
+    uint64_t committed = 0;
+    {
+        ColdStore store = ColdStore::create(t.path, 0);
+        store.append_page(geometry(0), filled(32, 1), filled(32, 2), true);
+        store.fail_next_append_after(104 + 40);
+        CHECK(expect_kind([&] { store.append_page(geometry(1), filled(32, 3), filled(32, 4), true); }) == Kind::Other);
+        CHECK(store.metadata().size() == 1);
+        committed = store.stats().committed_bytes;
+        CHECK(file_size(t.path) == committed);
+        const auto meta = store.append_page(geometry(1), filled(32, 5), filled(32, 6), true);
+        CHECK(meta.page_id == 1);
+        CHECK(meta.record_offset == committed);
+    }
+    ColdStore reopened = ColdStore::open(t.path, 0);
+    CHECK(reopened.metadata().size() == 2);
+    CHECK(reopened.read_page(1)->key == filled(32, 5));
+    reopened.audit();
+}
+
+TEST(cold_external_torn_tail_before_append_is_discarded) {
+    TempPath t("external-torn-then-append");
+    {
+        ColdStore store = ColdStore::create(t.path, 0);
+        store.append_page(geometry(0), filled(32, 1), filled(32, 2), true);
+        const auto k = filled(32, 3), v = filled(32, 4);
+        const auto torn = ColdStore::prepare_page(1, geometry(1), k.data(), k.size(), v.data(), v.size());
+        append_bytes(t.path, torn.record.data(), 104 + 40);
+        store.append_page(geometry(1), filled(32, 5), filled(32, 6), true);
+    }
+    ColdStore reopened = ColdStore::open(t.path, 0);
+    CHECK(reopened.metadata().size() == 2);
+    CHECK(reopened.read_page(1)->value == filled(32, 6));
+}
+
+TEST(cold_read_only_open_ignores_torn_tail_without_truncating) {
+    TempPath t("readonly-torn");
+    {
+        ColdStore store = ColdStore::create(t.path, 0);
+        store.append_page(geometry(0), filled(32, 7), filled(32, 9), true);
+    }
+    const auto k = filled(32, 3), v = filled(32, 4);
+    const auto torn = ColdStore::prepare_page(1, geometry(1), k.data(), k.size(), v.data(), v.size());
+    append_bytes(t.path, torn.record.data(), 104 + 40);
+    const uint64_t before = file_size(t.path);
+    {
+        ColdStore frozen = ColdStore::open_read_only(t.path, 0);
+        CHECK(frozen.metadata().size() == 1);
+        CHECK(frozen.read_key(0) == filled(32, 7));
+        frozen.audit_mapped();
+    }
+    CHECK(file_size(t.path) == before);
+}
+
+TEST(cold_committed_corruption_is_rejected) {
+    TempPath t("corrupt");
+    uint64_t payload_offset = 0;
+    {
+        ColdStore store = ColdStore::create(t.path, 0);
+        payload_offset = store.append_page(geometry(0), filled(32, 7), filled(32, 9), true).payload_offset;
+    }
+    const uint8_t b = 8;
+    write_at(t.path, payload_offset + 4, &b, 1);
+    CHECK(expect_kind([&] { ColdStore::open(t.path, 0); }) == Kind::InvalidData);
+}
+
+TEST(cold_cryptographic_digest_corruption_is_rejected_even_when_fast_checksums_match) {
+    TempPath t("digest-corrupt");
+    uint64_t last = 0;
+    {
+        ColdStore store = ColdStore::create(t.path, 0);
+        const auto meta = store.append_page(geometry(0), filled(32, 11), filled(32, 13), true);
+        last = meta.record_offset + meta.record_len - 1;
+    }
+    const std::vector<uint8_t> bytes = read_file(t.path);
+    const uint8_t flipped = bytes[last] ^ 0xff;
+    write_at(t.path, last, &flipped, 1);
+    CHECK(expect_kind([&] { ColdStore::open(t.path, 0); }) == Kind::InvalidData);
+}
+
+// ---- ColdStore: further cases -------------------------------------------------
+
+TEST(cold_second_writer_would_block_and_paths_report_kinds) {
+    TempPath t("lock");
+    ColdStore store = ColdStore::create(t.path, 0);
+    CHECK(expect_kind([&] { ColdStore::open(t.path, 0); }) == Kind::WouldBlock);
+    CHECK(expect_kind([&] { ColdStore::create(t.path, 0); }) == Kind::AlreadyExists);
+    CHECK(expect_kind([&] { ColdStore::open(t.path + ".absent", 0); }) == Kind::NotFound);
+    CHECK(expect_kind([&] { store.read_page(0); }) == Kind::NotFound);
+    ColdStore reader = ColdStore::open_read_only(t.path, 0);  // readers take no lock
+    CHECK(reader.metadata().empty());
+}
+
+TEST(cold_geometry_and_coordinate_rejections) {
+    TempPath t("reject");
+    ColdStore store = ColdStore::create(t.path, 0);
+    PageGeometry g = geometry(0);
+    g.tile = 3;  // head_dim 4 is not a multiple of 3
+    CHECK(expect_kind([&] { store.append_page(g, filled(32, 1), filled(32, 1), false); }) == Kind::InvalidData);
+    CHECK(expect_kind([&] { store.append_page(geometry(0), filled(31, 1), filled(32, 1), false); }) ==
+          Kind::InvalidData);
+    CHECK(expect_kind([&] { store.append_page(geometry(0), {}, filled(32, 1), false); }) == Kind::InvalidData);
+    store.append_page(geometry(0), filled(32, 1), filled(32, 2), false);
+    CHECK(expect_kind([&] { store.read_value_tokens(0, {}); }) == Kind::InvalidData);
+    CHECK(expect_kind([&] { store.read_value_tokens(0, {4}); }) == Kind::InvalidData);
+    CHECK(expect_kind([&] { store.read_value_tokens(0, {2, 1}); }) == Kind::InvalidData);
+    CHECK(expect_kind([&] { store.read_value_tokens(0, {1, 1}); }) == Kind::InvalidData);
+    CHECK(store.read_value_tokens(0, {0, 1, 2, 3}) == filled(32, 2));  // full range: whole-value read
+    CHECK(store.stats().partial_value_reads == 0);
+}
+
+TEST(cold_records_equal_oracle_prepare_page) {
+    std::mt19937_64 rng(2026);
+    TempPath t("oracle");
+    std::vector<uint8_t> expected_file;
+    const uint32_t shapes[][3] = {{4, 2, 4}, {16, 8, 128}, {1, 8, 128}, {64, 8, 128}, {5, 3, 80}, {7, 1, 2}};
+    uint64_t page_id = 0;
+    {
+        ColdStore store = ColdStore::create(t.path, 0);
+        for (const auto &s : shapes) {
+            PageGeometry g;
+            g.layer = (uint32_t)(rng() % 80);
+            g.token_start = rng() % (1ull << 34);
+            g.tokens = s[0];
+            g.heads = s[1];
+            g.head_dim = s[2];
+            g.tile = s[2] % 16 == 0 ? 16 : 1;
+            std::vector<uint8_t> k(g.tokens * g.heads * g.head_dim * 2), v(k.size());
+            for (auto &b : k) b = (uint8_t)rng();
+            for (auto &b : v) b = (uint8_t)rng();
+            const auto prepared = ColdStore::prepare_page(page_id, g, k.data(), k.size(), v.data(), v.size());
+            const auto want = oracle_record(page_id, g, k, v);
+            CHECK(prepared.record == want);
+            const auto meta = store.append_prepared(prepared, false);
+            CHECK(meta.record_len == want.size());
+            expected_file.insert(expected_file.end(), want.begin(), want.end());
+            ++page_id;
+        }
+    }
+    CHECK(read_file(t.path) == expected_file);
+    ColdStore reopened = ColdStore::open(t.path, 0);
+    CHECK(reopened.metadata().size() == page_id);
+    reopened.audit();
+    reopened.audit_mapped();
+}
+
+TEST(cold_append_framed_writes_the_same_file) {
+    TempPath a("page"), b("framed");
+    ColdStore sa = ColdStore::create(a.path, 0), sb = ColdStore::create(b.path, 0);
+    std::mt19937_64 rng(9);
+    for (uint64_t page = 0; page < 3; ++page) {
+        PageGeometry g;
+        g.layer = 1;
+        g.token_start = page * 16;
+        g.tokens = page == 2 ? 5 : 16;
+        g.heads = 8;
+        g.head_dim = 128;
+        g.tile = 16;
+        std::vector<uint8_t> k(g.tokens * 8 * 256), v(k.size());
+        for (auto &x : k) x = (uint8_t)rng();
+        for (auto &x : v) x = (uint8_t)rng();
+        const auto prepared = ColdStore::prepare_page(page, g, k.data(), k.size(), v.data(), v.size());
+        sa.append_prepared(prepared, false);
+        // The frame slot layout of mslim_attn_record_frames (16-token slots).
+        const size_t prefix = 104 + 16 * g.tokens, slot = 104 + 16 * 16 + 56;
+        std::vector<uint8_t> frame(slot, 0);
+        std::memcpy(frame.data(), prepared.record.data(), prefix);
+        std::memcpy(frame.data() + slot - 56, prepared.record.data() + prepared.record.size() - 56, 56);
+        sb.append_framed(frame.data(), slot, k.data(), v.data(), k.size(), false);
+    }
+    CHECK(read_file(a.path) == read_file(b.path));
+    // A frame whose footer length disagrees with the payloads is rejected.
+    std::vector<uint8_t> k(16 * 8 * 256, 1), v(k.size(), 2);
+    PageGeometry g;
+    g.layer = 1; g.token_start = 48; g.tokens = 16; g.heads = 8; g.head_dim = 128; g.tile = 16;
+    auto p = ColdStore::prepare_page(3, g, k.data(), k.size(), v.data(), v.size());
+    std::vector<uint8_t> frame(104 + 256 + 56, 0);
+    std::memcpy(frame.data(), p.record.data(), 104 + 256);
+    std::memcpy(frame.data() + frame.size() - 56, p.record.data() + p.record.size() - 56, 56);
+    CHECK(expect_kind([&] { sb.append_framed(frame.data(), frame.size(), k.data(), v.data(), k.size() - 16, false); }) ==
+          Kind::InvalidData);
+}
+
+// ---- Region store: the reference's exact-mode tests -----------------------------
+
+namespace {
+
+portable::AttentionGeometry geom() { return portable::AttentionGeometry::create(4, 2, 4); }
+
+std::vector<uint8_t> bits(const std::vector<float> &xs) {
+    std::vector<uint8_t> out;
+    for (float x : xs) {
+        const uint16_t b = orc_write_bf16(x);
+        out.push_back((uint8_t)b);
+        out.push_back((uint8_t)(b >> 8));
+    }
+    return out;
+}
+
+std::vector<uint8_t> repeat(const std::vector<uint8_t> &x, int n) {
+    std::vector<uint8_t> out;
+    for (int i = 0; i < n; ++i) out.insert(out.end(), x.begin(), x.end());
+    return out;
+}
+
+}  // namespace
+
+TEST(region_canonical_cpu_index_and_cold_store_reused_exactly) {
+    region::RegionStore store(geom(), 1, region::RegionConfig{});
+    const auto k = bits({0, 1, 2, 3, 4, 5, 6, 7});
+    const auto v = bits({1, 0, -2, 3, 4, -5, 6, 7});
+    for (size_t t = 0; t < 5; ++t) store.append(0, t, k.data(), v.data(), k.size());
+    CHECK(store.layer_tokens(0) == 5);
+    CHECK(store.axis_token_len() == 5);
+    CHECK(store.storage_metrics().committed_bytes > 0);
+    const auto selection = store.select_dense_exact(0);
+    CHECK((selection.positions == std::vector<size_t>{0, 1, 2, 3, 4}));
+    CHECK(selection.omitted == 0);
+    for (double b : selection.bounds) CHECK(b == 0.0);
+    CHECK(store.read_values(0, selection.positions) == repeat(v, 5));
+    CHECK(store.stats.exact_v_tokens_read_from_cold == 5);
+}
+
+TEST(region_batched_pages_preserve_every_bf16_value_and_reduce_page_reads) {
+    const size_t count = 37;
+    std::vector<float> key_items(count * 8), value_items(count * 8);
+    for (size_t i = 0; i < count * 8; ++i) {
+        key_items[i] = (float)((double)(i % 59) - 29.0) * 0.03125f;
+        value_items[i] = (float)((double)(i % 61) - 30.0) * 0.0625f;
+    }
+    const auto keys = bits(key_items), values = bits(value_items);
+    region::RegionStore grouped(geom(), 1, region::RegionConfig{});
+    grouped.append_batch(0, 0, keys, values, 8);
+    CHECK(grouped.layer_tokens(0) == count);
+    CHECK(grouped.axis_token_len() == count);
+    CHECK(grouped.storage_metrics().pages == 5);
+    CHECK(grouped.stats.physical_cold_store_pages == 5);
+    std::vector<size_t> original(count);
+    for (size_t i = 0; i < count; ++i) original[i] = i;
+    CHECK(grouped.read_values(0, original) == values);
+    CHECK(grouped.storage_metrics().reads == 5);
+    const std::vector<size_t> sparse{0, 2, 4, 7, 8, 11, 23, 24, 36};
+    std::vector<uint8_t> want;
+    for (size_t i : sparse) want.insert(want.end(), values.begin() + i * 16, values.begin() + (i + 1) * 16);
+    CHECK(grouped.read_values(0, sparse) == want);
+    region::RegionStore token_pages(geom(), 1, region::RegionConfig{});
+    for (size_t t = 0; t < count; ++t) token_pages.append(0, t, keys.data() + t * 16, values.data() + t * 16, 16);
+    CHECK(token_pages.storage_metrics().pages == count);
+    CHECK(token_pages.read_values(0, original) == values);
+    CHECK(token_pages.storage_metrics().reads == count);
+    CHECK(grouped.storage_metrics().reads == 10);
+    CHECK(grouped.storage_metrics().committed_bytes < token_pages.storage_metrics().committed_bytes);
+}
+
+TEST(region_configured_cold_directory_reopens_exact_prefix) {
+    TempPath dir("unused");
+    region::RegionConfig config;
+    config.cold_directory = dir.dir;
+    const size_t count = 9;
+    std::vector<float> kf(count * 8), vf(count * 8);
+    for (size_t i = 0; i < count * 8; ++i) {
+        kf[i] = (float)i * 0.03125f;
+        vf[i] = 1.0f - (float)i * 0.015625f;
+    }
+    const auto keys = bits(kf), values = bits(vf);
+    std::string digest;
+    {
+        region::RegionStore first(geom(), 1, config);
+        first.append_batch(0, 0, keys, values, 4);
+        digest = first.logical_kv_sha256();
+    }
+    region::RegionStore reopened(geom(), 1, config);
+    CHECK(reopened.layer_tokens(0) == count);
+    CHECK(reopened.axis_token_len() == count);
+    std::vector<size_t> all(count);
+    for (size_t i = 0; i < count; ++i) all[i] = i;
+    CHECK(reopened.read_values(0, all) == values);
+    CHECK(reopened.read_keys(0, all) == keys);
+    CHECK(reopened.logical_kv_sha256() == digest);
+}
+
+TEST(region_canonical_exact_storage_rejects_nan) {
+    region::RegionStore store(geom(), 1, region::RegionConfig{});
+    const float nan = std::nanf("");
+    const auto key = bits({nan, nan, nan, nan, nan, nan, nan, nan});
+    const auto value = bits({1, 1, 1, 1, 1, 1, 1, 1});
+    CHECK(!harness::expect_throw<Error>([&] { store.append(0, 0, key.data(), value.data(), key.size()); }).empty());
+    CHECK(store.layer_tokens(0) == 0);
+    // V is checked on every layer, K only on layer zero (gpu_region_store.rs:420-450).
+    region::RegionStore two(geom(), 2, region::RegionConfig{});
+    const auto ok = bits({1, 2, 3, 4, 5, 6, 7, 8});
+    two.append(1, 0, key.data(), ok.data(), key.size());
+    CHECK(two.layer_tokens(1) == 1);
+    const std::string msg = harness::expect_throw<Error>([&] { two.append(1, 1, ok.data(), key.data(), ok.size()); });
+    CHECK(msg == "GPU ColdStore V nonfinite");
+    CHECK(two.layer_tokens(1) == 1);
+}
+
+TEST(region_config_and_append_rejections) {
+    region::RegionConfig c;
+    c.epsilon = 0.2;
+    CHECK(harness::expect_throw<Error>([&] { c.validate(); }) == "LOD epsilon must be finite within 0..=0.1");
+    c.epsilon = 0.0;
+    c.stage_tokens = 0;
+    CHECK(harness::expect_throw<Error>([&] { c.validate(); }) == "LOD stage_tokens must be in 1..=1024");
+    c.stage_tokens = 64;
+    c.cold_directory = std::string("/nonexistent-mslim-dir");
+    CHECK(harness::expect_throw<Error>([&] { c.validate(); }).find("LOD cold directory does not exist") == 0);
+    region::RegionStore store(geom(), 1, region::RegionConfig{});
+    const auto kv = bits({1, 2, 3, 4, 5, 6, 7, 8});
+    CHECK(harness::expect_throw<Error>([&] { store.append_batch(0, 0, kv, kv, 0); }) ==
+          "GPU ColdStore page size must be 1..512 tokens");
+    CHECK(harness::expect_throw<Error>([&] { store.append_batch(0, 1, kv, kv, 1); }) ==
+          "GPU LOD append needs sequential tokens");
+    CHECK(harness::expect_throw<Error>([&] { store.append_batch(2, 0, kv, kv, 1); }) ==
+          "GPU LOD batch layer out of range");
+    CHECK(harness::expect_throw<Error>([&] { store.select_dense_exact(0); }) == "no BF16 K/V tokens for exact LOD");
+}
+
+TEST(region_logical_sha_equals_oracle) {
+    const auto g = portable::AttentionGeometry::create(8, 2, 16);
+    region::RegionStore store(g, 2, region::RegionConfig{});
+    std::mt19937_64 rng(77);
+    const size_t tokens = 21, token_bytes = 2 * 16 * 2;
+    std::vector<std::vector<uint8_t>> keys(2), values(2);
+    for (int layer = 0; layer < 2; ++layer) {
+        std::vector<float> kf(tokens * 32), vf(tokens * 32);
+        std::normal_distribution<float> n(0.0f, 1.0f);
+        for (auto &x : kf) x = n(rng);
+        for (auto &x : vf) x = n(rng);
+        keys[layer] = bits(kf);
+        values[layer] = bits(vf);
+        store.append_batch(layer, 0, keys[layer], values[layer], layer ? 16 : 5);
+    }
+    const uint8_t *kp[2] = {keys[0].data(), keys[1].data()};
+    const uint8_t *vp[2] = {values[0].data(), values[1].data()};
+    uint8_t digest[32];
+    orc_logical_kv_sha256(2, tokens, 2, 32, kp, vp, digest);
+    static const char d[] = "0123456789abcdef";
+    std::string want;
+    for (uint8_t b : digest) {
+        want.push_back(d[b >> 4]);
+        want.push_back(d[b & 15]);
+    }
+    CHECK(store.logical_kv_sha256() == want);
+    (void)token_bytes;
+}
+
+// ---- device page pool ----------------------------------------------------------------
+
+namespace {
+
+struct DeviceVec {
+    std::shared_ptr<NativeContext> ctx;
+    void *ptr = nullptr;
+    size_t bytes = 0;
+    DeviceVec(std::shared_ptr<NativeContext> c, const std::vector<uint8_t> &host) : ctx(std::move(c)), bytes(host.size()) {
+        ptr = mslim_attn_buf_upload(ctx->handle(), host.data(), host.size());
+        if (!ptr) throw Failure(mslim_attn_last_error());
+    }
+    ~DeviceVec() { mslim_attn_buf_free(ctx->handle(), ptr); }
+    std::vector<uint8_t> read() const {
+        std::vector<uint8_t> out(bytes);
+        ctx->check("read", mslim_attn_buf_read(ctx->handle(), ptr, 0, out.data(), bytes));
+        return out;
+    }
+};
+
+// Finite random BF16 bytes.
+std::vector<uint8_t> finite_bf16(std::mt19937_64 &rng, size_t elements) {
+    std::vector<uint8_t> out(elements * 2);
+    std::normal_distribution<float> n(0.0f, 2.0f);
+    for (size_t i = 0; i < elements; ++i) {
+        const uint16_t b = orc_write_bf16(n(rng));
+        out[2 * i] = (uint8_t)b;
+        out[2 * i + 1] = (uint8_t)(b >> 8);
+    }
+    return out;
+}
+
+}  // namespace
+
+TEST(gpu_region_device_seal_writes_the_host_append_file_and_restores) {
+    auto ctx = NativeContext::create();
+    const size_t kvh = 8, d = 128, P = 16, pool_pages = 40, tokens = 16 * 9 + 7;  // last page partial
+    const auto g = portable::AttentionGeometry::create(64, kvh, d);
+    const size_t page_bytes = kvh * P * d * 2, token_bytes = kvh * d * 2;
+    std::mt19937_64 rng(31);
+    // Token-major rows, and the same rows placed into a pool through a
+    // permuted page table (head-major pages).
+    const auto k_rows = finite_bf16(rng, tokens * kvh * d), v_rows = finite_bf16(rng, tokens * kvh * d);
+    std::vector<int32_t> blocks{17, 3, 29, 0, 38, 12, 5, 21, 33, 8};
+    std::vector<uint8_t> k_pool(pool_pages * page_bytes, 0xEE), v_pool(pool_pages * page_bytes, 0xEE);
+    for (size_t t = 0; t < tokens; ++t)
+        for (size_t h = 0; h < kvh; ++h) {
+            const size_t dst = (size_t)blocks[t / P] * page_bytes + (h * P + t % P) * d * 2;
+            std::memcpy(k_pool.data() + dst, k_rows.data() + t * token_bytes + h * d * 2, d * 2);
+            std::memcpy(v_pool.data() + dst, v_rows.data() + t * token_bytes + h * d * 2, d * 2);
+        }
+    DeviceVec dk(ctx, k_pool), dv(ctx, v_pool);
+    region::DevicePagePool pool;
+    pool.k_pool = dk.ptr;
+    pool.v_pool = dv.ptr;
+    pool.pool_pages = (int64_t)pool_pages;
+    pool.page_tokens = (int)P;
+
+    TempPath da("unused-a"), db("unused-b");
+    region::RegionConfig ca, cb;
+    ca.cold_directory = da.dir;
+    cb.cold_directory = db.dir;
+    std::string digest;
+    {
+        region::RegionStore host(g, 2, ca), dev(g, 2, cb);
+        host.append_batch(0, 0, k_rows, v_rows, P);
+        host.append_batch(1, 0, v_rows, k_rows, P);
+        dev.seal_device_pages(*ctx, 0, 0, pool, blocks, tokens);
+        region::DevicePagePool swapped = pool;
+        std::swap(swapped.k_pool, swapped.v_pool);
+        dev.seal_device_pages(*ctx, 1, 0, swapped, blocks, tokens);
+        CHECK(dev.stats.device_sealed_pages == 20);
+        CHECK(dev.logical_kv_sha256() == host.logical_kv_sha256());
+        digest = host.logical_kv_sha256();
+    }
+    // The device-framed store is byte-identical to the host-framed one.
+    CHECK(read_file(da.dir + "/pages-exact.kv") == read_file(db.dir + "/pages-exact.kv"));
+
+    // Restore layer 0 into a fresh pool through another page table; the
+    // gathered rows equal the originals.
+    region::RegionStore reopened(g, 2, cb);
+    CHECK(reopened.logical_kv_sha256() == digest);
+    std::vector<uint8_t> zeros(pool_pages * page_bytes, 0);
+    DeviceVec rk(ctx, zeros), rv(ctx, zeros);
+    region::DevicePagePool fresh = pool;
+    fresh.k_pool = rk.ptr;
+    fresh.v_pool = rv.ptr;
+    std::vector<int32_t> blocks2{4, 9, 14, 19, 24, 29, 34, 39, 1, 6};
+    reopened.restore_to_device(*ctx, 0, fresh, blocks2);
+    CHECK(reopened.stats.device_restored_pages == 10);
+    const auto kk = rk.read(), vv = rv.read();
+    for (size_t t = 0; t < tokens; ++t)
+        for (size_t h = 0; h < kvh; ++h) {
+            const size_t src = (size_t)blocks2[t / P] * page_bytes + (h * P + t % P) * d * 2;
+            CHECK(std::memcmp(kk.data() + src, k_rows.data() + t * token_bytes + h * d * 2, d * 2) == 0);
+            CHECK(std::memcmp(vv.data() + src, v_rows.data() + t * token_bytes + h * d * 2, d * 2) == 0);
+        }
+}
+
+TEST(gpu_region_device_restore_detects_corruption_and_seal_rejects_nonfinite) {
+    auto ctx = NativeContext::create();
+    const size_t kvh = 8, d = 128, P = 16, pool_pages = 4, tokens = 48;
+    const auto g = portable::AttentionGeometry::create(8, kvh, d);
+    const size_t page_bytes = kvh * P * d * 2;
+    std::mt19937_64 rng(5);
+    auto k_pool = finite_bf16(rng, pool_pages * kvh * P * d), v_pool = finite_bf16(rng, pool_pages * kvh * P * d);
+    DeviceVec dk(ctx, k_pool), dv(ctx, v_pool);
+    region::DevicePagePool pool;
+    pool.k_pool = dk.ptr;
+    pool.v_pool = dv.ptr;
+    pool.pool_pages = (int64_t)pool_pages;
+    pool.page_tokens = (int)P;
+    TempPath dir("unused");
+    region::RegionConfig c;
+    c.cold_directory = dir.dir;
+    const std::vector<int32_t> blocks{2, 0, 3};
+    {
+        region::RegionStore store(g, 1, c);
+        store.seal_device_pages(*ctx, 0, 0, pool, blocks, tokens);
+        // Flip one V byte of the second record in the file.
+        const auto &meta = store.cold_store().metadata().at(1);
+        const std::string path = dir.dir + "/pages-exact.kv";
+        std::vector<uint8_t> bytes = read_file(path);
+        const uint64_t off = meta.payload_offset + meta.key_len + 777;
+        const uint8_t flipped = bytes[off] ^ 0x10;
+        write_at(path, off, &flipped, 1);
+        const std::vector<int32_t> other{1, 2, 0};
+        CHECK(expect_kind([&] { store.restore_to_device(*ctx, 0, pool, other); }) == Kind::InvalidData);
+    }
+    // A NaN in V of a fresh pool page: the seal is rejected before any commit.
+    std::vector<uint8_t> v_bad = v_pool;
+    v_bad[1 * page_bytes + 300 * 2 + 1] = 0x7f;
+    v_bad[1 * page_bytes + 300 * 2] = 0xc0;
+    DeviceVec dvb(ctx, v_bad);
+    region::DevicePagePool bad = pool;
+    bad.v_pool = dvb.ptr;
+    TempPath dir2("unused");
+    region::RegionConfig c2;
+    c2.cold_directory = dir2.dir;
+    region::RegionStore store2(g, 1, c2);
+    CHECK(harness::expect_throw<Error>([&] { store2.seal_device_pages(*ctx, 0, 0, bad, {0, 1, 2}, tokens); }) ==
+          "GPU ColdStore V nonfinite");
+    CHECK(store2.layer_tokens(0) == 0);
+    CHECK(store2.storage_metrics().pages == 0);
+}
+
+int main(int argc, char **argv) { return harness::run_cases(argc, argv); }

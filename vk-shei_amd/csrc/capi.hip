@@ -642,4 +642,66 @@ int mslim_attn_logical_kv_sha256(void *ctx, int layers, int64_t tokens, int kv_h
     return 0;
 }
 
+
+int64_t mslim_attn_record_frame_bytes(int page_tokens) {
+    return page_tokens >= 1 ? mslim::record_frame_bytes(page_tokens) : -1;
+}
+
+int mslim_attn_record_frames(void *ctx, const void *k_pool, const void *v_pool, int64_t pool_pages,
+                             int page_tokens, int kv_heads, int head_dim, uint32_t tile,
+                             const mslim_attn_page_record *records, int count, void *frames) {
+    g_error.clear();
+    if (!ctx || !k_pool || !v_pool || !records || !frames || count < 0 || pool_pages < 1)
+        return fail("invalid record frame arguments");
+    if (!is_pow2(page_tokens) || page_tokens > 512 || kv_heads < 1 || head_dim < 8 || head_dim % 8)
+        return fail("record frames need page_tokens a power of two <= 512, kv_heads >= 1 and "
+                    "head_dim a multiple of 8");
+    if (tile == 0 || (uint32_t)head_dim % tile) return fail("head_dim is not a multiple of tile");
+    if ((uintptr_t)k_pool % 16 || (uintptr_t)v_pool % 16 || (uintptr_t)frames % 8)
+        return fail("record frames need 16-byte aligned pools and an 8-byte aligned frame buffer");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    mslim::FramesCodecLaunch l;
+    l.k_pool = k_pool;
+    l.v_pool = v_pool;
+    l.pool_pages = pool_pages;
+    l.page_tokens = page_tokens;
+    l.kv_heads = kv_heads;
+    l.head_dim = head_dim;
+    l.tile = tile;
+    l.records = reinterpret_cast<const mslim::RecordDesc *>(records);
+    l.count = count;
+    l.frames = frames;
+    l.frame_bytes = mslim::record_frame_bytes(page_tokens);
+    return check_hip(mslim::launch_record_frames(l, c.stream), "record frame launch");
+}
+
+int mslim_attn_record_payloads(void *ctx, void *k_pool, void *v_pool, int64_t pool_pages, int page_tokens,
+                               int kv_heads, int head_dim, const mslim_attn_page_record *records, int count,
+                               void *k_stage, void *v_stage, int direction) {
+    g_error.clear();
+    if (!ctx || !k_pool || !v_pool || !records || !k_stage || !v_stage || count < 0 || pool_pages < 1 ||
+        (direction != 0 && direction != 1))
+        return fail("invalid record payload arguments");
+    if (!is_pow2(page_tokens) || page_tokens > 512 || kv_heads < 1 || head_dim < 8 || head_dim % 8)
+        return fail("record payloads need page_tokens a power of two <= 512, kv_heads >= 1 and "
+                    "head_dim a multiple of 8");
+    if ((uintptr_t)k_pool % 16 || (uintptr_t)v_pool % 16 || (uintptr_t)k_stage % 16 || (uintptr_t)v_stage % 16)
+        return fail("record payloads need 16-byte aligned pools and staging");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    mslim::PayloadMoveLaunch l;
+    l.k_pool = k_pool;
+    l.v_pool = v_pool;
+    l.pool_pages = pool_pages;
+    l.page_tokens = page_tokens;
+    l.kv_heads = kv_heads;
+    l.head_dim = head_dim;
+    l.records = reinterpret_cast<const mslim::RecordDesc *>(records);
+    l.count = count;
+    l.k_stage = k_stage;
+    l.v_stage = v_stage;
+    return check_hip(mslim::launch_record_payloads(l, direction == 0, c.stream), "record payload launch");
+}
+
 }  // extern "C"

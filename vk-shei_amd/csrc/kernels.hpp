@@ -76,6 +76,42 @@ hipError_t launch_rope(const uint16_t *in, uint16_t *out, int tokens, int heads,
 hipError_t launch_swiglu(const uint16_t *gate, const uint16_t *up, uint16_t *out, size_t n,
                          hipStream_t stream);
 
+// ColdStore record frames of pool pages (record header, token-hash tables
+// and footer; the payloads stay in the pool).
+constexpr int kRecordHeaderBytes = 104;  // cold_store.rs:23
+constexpr int kRecordFooterBytes = 56;   // cold_store.rs:24
+constexpr uint32_t kRecordVersion = 3;   // cold_store.rs:22
+struct RecordDesc {                      // layout of mslim_attn_page_record
+    uint64_t page_id;
+    uint64_t token_start;
+    uint32_t layer;
+    uint32_t tokens;
+    int32_t pool_page;
+    uint32_t reserved;
+};
+static_assert(sizeof(RecordDesc) == 32, "RecordDesc must match mslim_attn_page_record");
+struct FramesCodecLaunch {
+    const void *k_pool, *v_pool;
+    int64_t pool_pages;
+    int page_tokens, kv_heads, head_dim;
+    uint32_t tile;
+    const RecordDesc *records;
+    int count;
+    void *frames;
+    int64_t frame_bytes;
+};
+int64_t record_frame_bytes(int page_tokens);
+hipError_t launch_record_frames(const FramesCodecLaunch &a, hipStream_t stream);
+struct PayloadMoveLaunch {
+    void *k_pool, *v_pool;
+    int64_t pool_pages;
+    int page_tokens, kv_heads, head_dim;
+    const RecordDesc *records;
+    int count;
+    void *k_stage, *v_stage;  // [count][kv_heads * page_tokens * head_dim] BF16 slots
+};
+hipError_t launch_record_payloads(const PayloadMoveLaunch &a, bool to_staging, hipStream_t stream);
+
 hipError_t launch_pages_write(uint16_t *k_pool, uint16_t *v_pool, const int32_t *page_table,
                               int page_tokens, int kv_heads, int head_dim, int64_t first_token,
                               int64_t tokens, const uint16_t *k_rows, const uint16_t *v_rows,

@@ -65,7 +65,19 @@ EXPORTS = (
     "mslim_attn_pages_write",
     "mslim_attn_pages_gather",
     "mslim_attn_logical_kv_sha256",
+    "mslim_attn_record_frame_bytes",
+    "mslim_attn_record_frames",
+    "mslim_attn_record_payloads",
 )
+
+RECORD_HEADER_BYTES = 104  # cold_store.rs:23
+RECORD_FOOTER_BYTES = 56   # cold_store.rs:24
+
+
+class PageRecord(C.Structure):
+    """mslim_attn_page_record: header fields of one record and its pool page."""
+    _fields_ = [("page_id", C.c_uint64), ("token_start", C.c_uint64), ("layer", C.c_uint32),
+                ("tokens", C.c_uint32), ("pool_page", C.c_int32), ("reserved", C.c_uint32)]
 
 
 class MslimAttnError(RuntimeError):
@@ -117,6 +129,9 @@ def library() -> C.CDLL:
         "mslim_attn_pages_write": (I, [P, P, P, P, I, I, I, I64, I64, P, P]),
         "mslim_attn_pages_gather": (I, [P, P, P, I, I, I, I64, I64, P]),
         "mslim_attn_logical_kv_sha256": (I, [P, I, I64, I, I, P, P, P, I, C.c_char_p]),
+        "mslim_attn_record_frame_bytes": (I64, [I]),
+        "mslim_attn_record_frames": (I, [P, P, P, I64, I, I, I, C.c_uint32, P, I, P]),
+        "mslim_attn_record_payloads": (I, [P, P, P, I64, I, I, I, P, I, P, P, I]),
     }
     for name in EXPORTS:
         res, args = sigs[name]
@@ -295,6 +310,26 @@ class Context:
         self._check("logical_kv_sha256", self._lib.mslim_attn_logical_kv_sha256(
             self._h, n, tokens, kv_heads, head_dim, kp, vp, tp, page_tokens, out))
         return out.value.decode()
+
+    # ---- ColdStore record frames ------------------------------------------
+    @staticmethod
+    def record_frame_bytes(page_tokens: int) -> int:
+        return int(library().mslim_attn_record_frame_bytes(page_tokens))
+
+    def record_frames(self, k_pool, v_pool, pool_pages: int, page_tokens: int, kv_heads: int,
+                      head_dim: int, tile: int, records, count: int, frames) -> None:
+        """`records`: device array of PageRecord; `frames`: device output of
+        count * record_frame_bytes(page_tokens) bytes."""
+        self._check("record_frames", self._lib.mslim_attn_record_frames(
+            self._h, _ptr(k_pool), _ptr(v_pool), pool_pages, page_tokens, kv_heads, head_dim,
+            tile, _ptr(records), count, _ptr(frames)))
+
+    def record_payloads(self, k_pool, v_pool, pool_pages: int, page_tokens: int, kv_heads: int,
+                        head_dim: int, records, count: int, k_stage, v_stage, to_staging: bool) -> None:
+        """Pool pages <-> compacted staging slots of kv_heads*page_tokens*head_dim BF16."""
+        self._check("record_payloads", self._lib.mslim_attn_record_payloads(
+            self._h, _ptr(k_pool), _ptr(v_pool), pool_pages, page_tokens, kv_heads, head_dim,
+            _ptr(records), count, _ptr(k_stage), _ptr(v_stage), 0 if to_staging else 1))
 
 
 def split_count(tokens: int, split_tokens: int) -> int:
