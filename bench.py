@@ -22,6 +22,11 @@ baseline is the C oracle's restatement of the reference CPU attention
 reference's rayon loop (:273-276), timed on a bounded sample of the same
 workload on this host.
 
+The ColdStore seal of every pool page (device record frames: per-token FNV
+tables, checksums, SHA-256; cold_store.rs:269-349) is timed on the same pool
+and reported under "coldstore_seal", with the oracle's restatement of the
+reference codec timed on the host cores beside it.
+
 Before each timed loop a short device sleep is queued behind the final
 synchronize so that the first timed launch does not wait on host launch
 latency; every timed call is then back-to-back device work.
@@ -176,6 +181,42 @@ def cpu_prefill_baseline(q_host, k_host, v_host, seconds: float):
         "sample": (f"{done} random rows of the 8,192-token causal prefill (64/8 heads, d=128), each "
                    f"row a dense_attention_bf16 over its causal prefix, {elapsed:.1f} s; rate "
                    f"extrapolates to the full prefill by exact FLOP count"),
+    }
+
+
+def cpu_seal_baseline(k_pages, v_pages, seconds: float):
+    """The reference's record codec (ColdStore::prepare_page: token hashes,
+    FNV checksums, SHA-256; cold_store.rs:269-349) as restated by the C
+    oracle, one page per task over the host cores, on pages of the bench
+    pool until `seconds` pass."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    import oracle
+
+    threads = cpu_threads()
+    total = k_pages.shape[0]
+
+    def page(i):
+        return oracle.coldstore_record(i, 0, i * PAGE_TOKENS, PAGE_TOKENS, KVH, D, 16,
+                                       k_pages[i].tobytes(), v_pages[i].tobytes())
+
+    done = 0
+    start = time.perf_counter()
+    with ThreadPoolExecutor(threads) as pool:
+        while True:
+            list(pool.map(page, [(done + j) % total for j in range(threads * 4)]))
+            done += threads * 4
+            if time.perf_counter() - start >= seconds:
+                break
+    elapsed = time.perf_counter() - start
+    payload = done * 2 * KVH * PAGE_TOKENS * D * 2
+    return {
+        "value": round(payload / elapsed / 1e9, 4),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"{done} pool pages (16 tokens, 8 heads, d=128, K+V 64 KiB) through the oracle's "
+                   f"restatement of ColdStore::prepare_page, one page per task, {elapsed:.1f} s"),
     }
 
 
@@ -357,6 +398,22 @@ def main() -> int:
     torch.cuda.synchronize()
     dense_ms = e0.elapsed_time(e1) / args.steps
 
+    # ColdStore seal of every pool page (record frames on the device).
+    total_pages = k_pool.shape[0]
+    recs = (mslim_attn.PageRecord * total_pages)()
+    for i in range(total_pages):
+        recs[i] = mslim_attn.PageRecord(i, i * PAGE_TOKENS, 0, PAGE_TOKENS, i, 0)
+    recs_dev = torch.frombuffer(bytearray(bytes(recs)), dtype=torch.uint8).cuda()
+    slot = mslim_attn.Context.record_frame_bytes(PAGE_TOKENS)
+    frames = torch.empty(total_pages * slot, dtype=torch.uint8, device="cuda")
+
+    def seal():
+        ctx.record_frames(k_pool, v_pool, total_pages, PAGE_TOKENS, KVH, D, 16, recs_dev, total_pages, frames)
+
+    seal()
+    seal_ms = timed_calls(torch, seal, max(3, args.steps // 4))
+    seal_payload = total_pages * 2 * KVH * PAGE_TOKENS * D * 2
+
     dec_gbps = decode_bytes() / (dec_avg * 1e-3) / 1e9
     pre_tflops = prefill_flops() / (pre_avg * 1e-3) / 1e12
     dense_gbps = decode_bytes() / (dense_ms * 1e-3) / 1e9
@@ -374,6 +431,8 @@ def main() -> int:
         cpu["prefill"] = cpu_prefill_baseline(q_pre.cpu().numpy().view(np.uint16),
                                               k_pre.cpu().numpy().view(np.uint16),
                                               v_pre.cpu().numpy().view(np.uint16), args.cpu_seconds)
+        cpu["coldstore_seal"] = cpu_seal_baseline(k_pool.cpu().numpy().view(np.uint16),
+                                                  v_pool.cpu().numpy().view(np.uint16), args.cpu_seconds)
         cpu["host_cpu"] = cpu_model()
         cpu["host_nproc"] = os.cpu_count()
 
@@ -420,6 +479,15 @@ def main() -> int:
                 "traffic": pre_traffic,
                 "kernel": f"prefill_mfma_kernel<128,8>, algorithmic FLOP {prefill_flops()} per launch",
             },
+        },
+        "coldstore_seal": {
+            "value": round(seal_payload / (seal_ms * 1e-3) / 1e9, 2),
+            "unit": "GB/s",
+            "ms": round(seal_ms, 4),
+            "records": total_pages,
+            "kernel": "token_hashes_kernel + frame_kernel: ColdStore record frames (header, per-token "
+                      "FNV tables, record FNV, SHA-256) of every cfg4 pool page; value = K+V payload "
+                      "bytes sealed per second",
         },
         "decode_ms": round(dec_avg, 5),
         "decode_after_prefill_ms": round(dec_after_prefill, 5),

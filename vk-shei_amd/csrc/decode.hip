@@ -35,7 +35,10 @@ namespace mslim {
 
 namespace {
 
-constexpr int kWaves = 4;
+#ifndef MSLIM_DECODE_WAVES
+#define MSLIM_DECODE_WAVES 4
+#endif
+constexpr int kWaves = MSLIM_DECODE_WAVES;
 constexpr int kTile = 32;
 
 struct DeviceArgs {
