@@ -16,6 +16,7 @@
 
 #include "../../oracle/oracle.h"
 #include "../../vk-shei_amd/host/cold_store.hpp"
+#include "../../vk-shei_amd/host/json.hpp"
 #include "../../vk-shei_amd/host/native.hpp"
 #include "../../vk-shei_amd/host/region_store.hpp"
 #include "harness.hpp"
@@ -411,6 +412,54 @@ TEST(cold_append_framed_writes_the_same_file) {
     std::memcpy(frame.data() + frame.size() - 56, p.record.data() + p.record.size() - 56, 56);
     CHECK(expect_kind([&] { sb.append_framed(frame.data(), frame.size(), k.data(), v.data(), k.size() - 16, false); }) ==
           Kind::InvalidData);
+}
+
+namespace {
+
+std::vector<uint8_t> from_hex(const std::string &h) {
+    std::vector<uint8_t> out(h.size() / 2);
+    for (size_t i = 0; i < out.size(); ++i) out[i] = (uint8_t)std::stoul(h.substr(2 * i, 2), nullptr, 16);
+    return out;
+}
+
+// tests/golden/fixtures.json, located from this binary (tests/cpp/_build/).
+std::string fixtures_text() {
+    char exe[4096];
+    const ssize_t n = readlink("/proc/self/exe", exe, sizeof exe - 1);
+    if (n <= 0) throw Failure("readlink /proc/self/exe");
+    exe[n] = '\0';
+    std::string dir(exe);
+    dir = dir.substr(0, dir.rfind('/'));
+    const std::string path = dir + "/../../golden/fixtures.json";
+    FILE *f = std::fopen(path.c_str(), "rb");
+    if (!f) throw Failure("open " + path);
+    std::string text;
+    char buf[4096];
+    size_t got;
+    while ((got = std::fread(buf, 1, sizeof buf, f)) > 0) text.append(buf, got);
+    std::fclose(f);
+    return text;
+}
+
+}  // namespace
+
+TEST(cold_golden_fixture_records) {
+    const json::Value root = json::parse(fixtures_text());
+    const json::Value *recs = root.find("coldstore_records");
+    CHECK(recs && recs->items.size() == 4);
+    for (const json::Value &r : recs->items) {
+        PageGeometry g;
+        g.layer = (uint32_t)r.find("layer")->as_usize("layer");
+        g.token_start = r.find("token_start")->as_usize("token_start");
+        g.tokens = (uint32_t)r.find("tokens")->as_usize("tokens");
+        g.heads = (uint32_t)r.find("heads")->as_usize("heads");
+        g.head_dim = (uint32_t)r.find("head_dim")->as_usize("head_dim");
+        g.tile = (uint32_t)r.find("tile")->as_usize("tile");
+        const auto k = from_hex(r.find("key")->text), v = from_hex(r.find("value")->text);
+        const auto p = ColdStore::prepare_page(r.find("page_id")->as_usize("page_id"), g, k.data(), k.size(),
+                                               v.data(), v.size());
+        CHECK(p.record == from_hex(r.find("record")->text));
+    }
 }
 
 // ---- Region store: the reference's exact-mode tests -----------------------------
