@@ -53,10 +53,15 @@ struct Swz {
     static constexpr int RPC = 1024 / (2 * D);       // rows per 1 KB DMA chunk
     static constexpr int CHUNKS = kBN * D * 2 / 1024; // DMA chunks per tile
     // K: slot ^ (row % NSLOT) keeps 16 consecutive rows' reads of one slot on
-    // distinct banks.  V: slot ^ 2*(row % (NSLOT/2)) keeps the four rows and
-    // two slots of a transpose read on distinct banks.
+    // distinct banks.  V: a transpose read serves 32 lanes per cycle from
+    // four consecutive rows and four consecutive slots (8 bytes each half);
+    // the XOR must spread those 16 (row, slot) pairs over all 16 slot
+    // positions of a 256-byte row (D = 128: slot ^ 4*(row % 4)), or over the
+    // two row parities x 8 slots of a 128-byte row (D = 64: slot ^ 2*row).
     __device__ static int k(int row, int slot) { return slot ^ (row & (NSLOT - 1)); }
-    __device__ static int v(int row, int slot) { return slot ^ ((2 * row) & (NSLOT - 1)); }
+    __device__ static int v(int row, int slot) {
+        return NSLOT == 16 ? slot ^ (4 * (row & 3)) : slot ^ ((2 * row) & (NSLOT - 1));
+    }
 };
 
 // s_waitcnt immediate that waits until at most n vector-memory operations
