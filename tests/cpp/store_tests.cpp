@@ -7,6 +7,7 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -771,6 +772,121 @@ TEST(gpu_region_device_restore_detects_corruption_and_seal_rejects_nonfinite) {
           "GPU ColdStore V nonfinite");
     CHECK(store2.layer_tokens(0) == 0);
     CHECK(store2.storage_metrics().pages == 0);
+}
+
+// Four-route parity of the attention path, after the reference's adapter
+// parity harness (src/bin/mslim-adapter-parity.rs:64-163, metrics of
+// conformance.rs:75-155) restated for one decode step instead of model
+// logits: CPU over hot K/V, CPU over K/V read back from the ColdStore, HIP
+// dense, HIP over pages restored from the ColdStore into the device pool.
+// Same-backend routes must agree bit for bit, CPU vs HIP within 2e-2, and the
+// logical K/V digest is the same on every route.
+namespace {
+
+struct Diff {
+    double max_abs = 0, mean_abs = 0, p95_abs = 0;
+};
+
+Diff compare(const std::vector<float> &ref, const std::vector<float> &got) {
+    std::vector<double> d(ref.size());
+    Diff r;
+    for (size_t i = 0; i < ref.size(); ++i) {
+        d[i] = std::fabs((double)ref[i] - (double)got[i]);
+        r.max_abs = std::max(r.max_abs, d[i]);
+        r.mean_abs += d[i];
+    }
+    r.mean_abs /= (double)d.size();
+    std::sort(d.begin(), d.end());
+    r.p95_abs = d[((d.size() - 1) * 95) / 100];
+    return r;
+}
+
+std::vector<float> bf16_bytes_to_f32(const std::vector<uint8_t> &b) {
+    std::vector<float> out(b.size() / 2);
+    for (size_t i = 0; i < out.size(); ++i) out[i] = orc_read_bf16((uint16_t)(b[2 * i] | (b[2 * i + 1] << 8)));
+    return out;
+}
+
+}  // namespace
+
+TEST(gpu_four_route_attention_parity) {
+    auto ctx = NativeContext::create();
+    const int qh = 64, kvh = 8, d = 128, tokens = 16 * 40 + 9, P = 16;
+    const auto g = portable::AttentionGeometry::create(qh, kvh, d);
+    std::mt19937_64 rng(2718);
+    const auto k_rows = finite_bf16(rng, (size_t)tokens * kvh * d), v_rows = finite_bf16(rng, (size_t)tokens * kvh * d);
+    const auto q_bits = finite_bf16(rng, (size_t)qh * d);
+    std::vector<float> q(qh * d);
+    for (int i = 0; i < qh * d; ++i) q[i] = orc_read_bf16((uint16_t)(q_bits[2 * i] | (q_bits[2 * i + 1] << 8)));
+    auto as_u16 = [](const std::vector<uint8_t> &b) {
+        std::vector<uint16_t> out(b.size() / 2);
+        std::memcpy(out.data(), b.data(), b.size());
+        return out;
+    };
+
+    // Route 1: CPU over hot (token-major) K/V.
+    std::vector<float> cpu_hot(qh * d);
+    CHECK(orc_dense_attention_bf16(qh, kvh, d, q.data(), as_u16(k_rows).data(), as_u16(v_rows).data(), tokens,
+                                   cpu_hot.data()) == 0);
+
+    // Route 2: CPU over K/V read back from the ColdStore (verified reads).
+    TempPath dir("unused");
+    region::RegionConfig config;
+    config.cold_directory = dir.dir;
+    region::RegionStore store(g, 1, config);
+    store.append_batch(0, 0, k_rows, v_rows, P);
+    std::vector<size_t> all(tokens);
+    for (int i = 0; i < tokens; ++i) all[i] = (size_t)i;
+    const auto k_cold = store.read_keys(0, all), v_cold = store.read_values(0, all);
+    CHECK(k_cold == k_rows && v_cold == v_rows);
+    std::vector<float> cpu_cold(qh * d);
+    CHECK(orc_dense_attention_bf16(qh, kvh, d, q.data(), as_u16(k_cold).data(), as_u16(v_cold).data(), tokens,
+                                   cpu_cold.data()) == 0);
+    CHECK(std::memcmp(cpu_hot.data(), cpu_cold.data(), cpu_hot.size() * 4) == 0);
+
+    // Route 3: HIP dense decode.
+    const float scale = 1.0f / std::sqrt((float)d);
+    const int32_t lens[1] = {tokens};
+    DeviceVec dq(ctx, q_bits), dk(ctx, k_rows), dv(ctx, v_rows);
+    DeviceVec dout(ctx, std::vector<uint8_t>((size_t)qh * d * 2, 0));
+    ctx->check("decode_dense", mslim_attn_decode_dense(ctx->handle(), dq.ptr, dk.ptr, dv.ptr, dout.ptr, 1, lens,
+                                                       tokens, qh, kvh, d, scale, 0));
+    const auto hip_dense_bits = dout.read();
+
+    // Route 4: HIP paged decode over pages restored (and verified on the
+    // device) from the ColdStore into a permuted pool.
+    const int pages = (tokens + P - 1) / P, pool_pages = pages + 5;
+    std::vector<int32_t> blocks(pages);
+    for (int i = 0; i < pages; ++i) blocks[i] = (int32_t)((i * 7 + 3) % pool_pages);
+    const size_t page_bytes = (size_t)kvh * P * d * 2;
+    DeviceVec kp(ctx, std::vector<uint8_t>(pool_pages * page_bytes, 0)), vp(ctx, std::vector<uint8_t>(pool_pages * page_bytes, 0));
+    region::DevicePagePool pool{kp.ptr, vp.ptr, pool_pages, P};
+    store.restore_to_device(*ctx, 0, pool, blocks);
+    std::vector<uint8_t> table_bytes(pages * 4);
+    std::memcpy(table_bytes.data(), blocks.data(), table_bytes.size());
+    DeviceVec dtable(ctx, table_bytes);
+    DeviceVec dout2(ctx, std::vector<uint8_t>((size_t)qh * d * 2, 0));
+    ctx->check("decode_paged", mslim_attn_decode_paged(ctx->handle(), dq.ptr, kp.ptr, vp.ptr, dout2.ptr, 1, lens,
+                                                       static_cast<const int32_t *>(dtable.ptr), pages, P, qh, kvh,
+                                                       d, scale, 0));
+    const auto hip_cold_bits = dout2.read();
+    CHECK(hip_dense_bits == hip_cold_bits);
+
+    // Cross-backend metrics (conformance.rs:75-155) within the tolerance.
+    const Diff diff = compare(cpu_hot, bf16_bytes_to_f32(hip_dense_bits));
+    std::printf("four-route: max_abs %.3g mean_abs %.3g p95_abs %.3g\n", diff.max_abs, diff.mean_abs, diff.p95_abs);
+    CHECK(diff.max_abs <= 2e-2);
+
+    // Logical K/V digest: dense device buffers, device pool and ColdStore agree.
+    char hex_dense[65], hex_pool[65];
+    const void *keys[1] = {dk.ptr}, *values[1] = {dv.ptr};
+    ctx->check("sha dense", mslim_attn_logical_kv_sha256(ctx->handle(), 1, tokens, kvh, d, keys, values, nullptr, 0,
+                                                         hex_dense));
+    const void *pk[1] = {kp.ptr}, *pv[1] = {vp.ptr};
+    const int32_t *tables[1] = {static_cast<const int32_t *>(dtable.ptr)};
+    ctx->check("sha pool", mslim_attn_logical_kv_sha256(ctx->handle(), 1, tokens, kvh, d, pk, pv, tables, P, hex_pool));
+    const std::string cold_hex = store.logical_kv_sha256();
+    CHECK(cold_hex == hex_dense && cold_hex == hex_pool);
 }
 
 int main(int argc, char **argv) { return harness::run_cases(argc, argv); }
