@@ -16,13 +16,13 @@
 //     FNV-1a-64 of that token's bytes over all heads (cold_store.rs:725-742).
 //     These lanes are independent, so this launch streams the payloads at
 //     close to HBM rate;
-//   * frame_kernel: one lane per record computes the payload and hash-table
-//     checksums (FNV-1a-64, cold_store.rs:909-922), assembles the header,
-//     then runs the record checksum and SHA-256 (FIPS 180-4) over
-//     header | hashes | K | V and writes the footer.  FNV-1a and SHA-256 are
-//     sequential chains over the record's bytes, so this launch is bounded by
-//     one lane's chain length, not by bandwidth; it is meant for sealing or
-//     verifying many records at once.
+//   * frame_kernel: one lane of each of two wavefronts per record computes
+//     the payload and hash-table checksums (FNV-1a-64, cold_store.rs:909-922),
+//     assembles the header, then runs the record checksum and SHA-256
+//     (FIPS 180-4) over header | hashes | K | V and writes the footer.  FNV-1a
+//     and SHA-256 are sequential chains over the record's bytes, so this
+//     launch is bounded by the longest chain (SHA-256 of one record), not by
+//     bandwidth; it is meant for sealing or verifying many records at once.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -293,26 +293,34 @@ __device__ __forceinline__ uint32_t hi32(uint64_t x) { return (uint32_t)(x >> 32
 
 constexpr int kFramePrefetch = 8;
 
-__global__ __launch_bounds__(kFrameThreads) void frame_kernel(FramesCodecLaunch a) {
+// Two wavefronts per 64 records, each running one chain per lane: in the
+// first pass wavefront 0 checksums the K payloads and wavefront 1 the V
+// payloads; in the second, over header | tables | K | V, wavefront 0 runs
+// SHA-256 and wavefront 1 the record FNV.  A lane's chains are sequential,
+// so splitting them over the two wavefronts (on different SIMDs) shortens
+// the critical path; they meet through LDS at two barriers.
+__global__ __launch_bounds__(2 * kFrameThreads) void frame_kernel(FramesCodecLaunch a) {
     __shared__ uint32_t rings[kRingWords * kFrameThreads];
-    const int lane = threadIdx.x;
+    __shared__ uint64_t payload_sums[2][kFrameThreads];
+    __shared__ uint64_t record_sums[kFrameThreads];
+    const int lane = threadIdx.x & (kFrameThreads - 1);
+    const int role = threadIdx.x / kFrameThreads;  // wavefront 0 or 1
     const int rec = blockIdx.x * kFrameThreads + lane;
-    if (rec >= a.count) return;
-    const RecordDesc r = a.records[rec];
+    const bool live = rec < a.count;
+    RecordDesc r = {};
+    if (live) r = a.records[rec];
+    const bool valid = live && record_valid(r, a.page_tokens, a.pool_pages);
     uint32_t *frame_words = reinterpret_cast<uint32_t *>(static_cast<unsigned char *>(a.frames) +
-                                                         (int64_t)rec * a.frame_bytes);
+                                                         (int64_t)(live ? rec : 0) * a.frame_bytes);
     const int frame_words_n = (int)(a.frame_bytes / 4);
-    if (!record_valid(r, a.page_tokens, a.pool_pages)) {
-        for (int i = 0; i < frame_words_n; ++i) frame_words[i] = 0u;
-        return;
-    }
-    const int tokens = (int)r.tokens;
+    const int tokens = valid ? (int)r.tokens : 0;
     const int row_bytes = a.head_dim * 2;
     const int64_t page_bytes = (int64_t)a.kv_heads * a.page_tokens * row_bytes;
     const int64_t payload_len = (int64_t)a.kv_heads * tokens * row_bytes;
     const int64_t payload_chunks = payload_len / 16;
-    const unsigned char *kpage = static_cast<const unsigned char *>(a.k_pool) + (int64_t)r.pool_page * page_bytes;
-    const unsigned char *vpage = static_cast<const unsigned char *>(a.v_pool) + (int64_t)r.pool_page * page_bytes;
+    const int64_t pool_page = valid ? r.pool_page : 0;
+    const unsigned char *kpage = static_cast<const unsigned char *>(a.k_pool) + pool_page * page_bytes;
+    const unsigned char *vpage = static_cast<const unsigned char *>(a.v_pool) + pool_page * page_bytes;
 
     // Head-major payload of `tokens` rows per head inside a pool page.
     auto payload_walk = [&](const unsigned char *page) __attribute__((always_inline)) {
@@ -326,24 +334,29 @@ __global__ __launch_bounds__(kFrameThreads) void frame_kernel(FramesCodecLaunch 
         w.rows_per_head = tokens;
         return w;
     };
+    auto no_group = []() __attribute__((always_inline)) {};
 
-    // Payload checksums: two independent chains over K and V.
-    uint64_t key_sum = kFnvOffset, value_sum = kFnvOffset;
-    stream_chunks2<kFramePrefetch>(payload_walk(kpage), payload_walk(vpage), payload_chunks,
-                                   [&](const u32x4_t &kc, const u32x4_t &vc) __attribute__((always_inline)) {
-                                       key_sum = fnv_chunk(key_sum, kc);
-                                       value_sum = fnv_chunk(value_sum, vc);
-                                   });
+    // Pass 1: payload checksums, K on wavefront 0 and V on wavefront 1.
+    {
+        uint64_t sum = kFnvOffset;
+        if (valid)
+            stream_chunks<kFramePrefetch>(payload_walk(role == 0 ? kpage : vpage), payload_chunks,
+                                          [&](const u32x4_t &c) __attribute__((always_inline)) {
+                                              sum = fnv_chunk(sum, c);
+                                          },
+                                          no_group);
+        payload_sums[role][lane] = sum;
+    }
+    __syncthreads();
+    const uint64_t key_sum = payload_sums[0][lane], value_sum = payload_sums[1][lane];
+
     // Hash-table checksums over the little-endian u64 tables (written by
-    // token_hashes_kernel into this frame).
+    // token_hashes_kernel into this frame) and the header
+    // (cold_store.rs:291-309), on both wavefronts.
     const uint32_t *tables = frame_words + kHeaderWords;
     uint64_t key_hashes_sum = kFnvOffset, value_hashes_sum = kFnvOffset;
     for (int i = 0; i < 2 * tokens; ++i) key_hashes_sum = fnv_word(key_hashes_sum, tables[i]);
     for (int i = 2 * tokens; i < 4 * tokens; ++i) value_hashes_sum = fnv_word(value_hashes_sum, tables[i]);
-
-    // Header (cold_store.rs:291-309), little-endian fields.  It is written
-    // into the frame first and then streamed back from there with the
-    // tables, so the prefix is one contiguous run of words.
     uint32_t hdr[kHeaderWords];
     hdr[0] = 0x564b5354u;  // "TSKV"
     hdr[1] = 0x34304750u;  // "PG04"
@@ -371,42 +384,61 @@ __global__ __launch_bounds__(kFrameThreads) void frame_kernel(FramesCodecLaunch 
     hdr[23] = hi32(key_hashes_sum);
     hdr[24] = lo32(value_hashes_sum);
     hdr[25] = hi32(value_hashes_sum);
-#pragma unroll
-    for (int i = 0; i < kHeaderWords; ++i) frame_words[i] = hdr[i];
 
-    // Record checksum and SHA-256 over header | tables | K | V.
-    ShaStream sha;
-    sha.init(rings + lane);
-    uint64_t record_sum = kFnvOffset;
-    const int prefix_words = kHeaderWords + 4 * tokens;
-    for (int i = 0; i < prefix_words; ++i) {
-        const uint32_t w = frame_words[i];
-        record_sum = fnv_word(record_sum, w);
-        sha.push_be(__builtin_bswap32(w));
-        if (sha.wpos - sha.rpos >= 16) sha.drain();
-    }
-    auto push_chunk = [&](const u32x4_t &c) __attribute__((always_inline)) {
-        record_sum = fnv_chunk(record_sum, c);
-        sha.push_be(__builtin_bswap32(c[0]));
-        sha.push_be(__builtin_bswap32(c[1]));
-        sha.push_be(__builtin_bswap32(c[2]));
-        sha.push_be(__builtin_bswap32(c[3]));
-    };
-    auto drain = [&]() __attribute__((always_inline)) { sha.drain(); };
-    stream_chunks<kFramePrefetch>(payload_walk(kpage), payload_chunks, push_chunk, drain);
-    stream_chunks<kFramePrefetch>(payload_walk(vpage), payload_chunks, push_chunk, drain);
-
-    // FIPS 180-4 padding: 0x80, zeros to 56 mod 64, 64-bit big-endian length.
+    // Pass 2 over header | tables | K | V: SHA-256 on wavefront 0, the record
+    // FNV on wavefront 1.
     const uint64_t record_len =
         (uint64_t)kRecordHeaderBytes + 16ull * tokens + 2ull * (uint64_t)payload_len + kRecordFooterBytes;
-    const uint64_t message_bits = (record_len - kRecordFooterBytes) * 8;
-    sha.push_be(0x80000000u);
-    while (((sha.wpos - sha.rpos) & 15) != 14) sha.push_be(0u);
-    sha.push_be(hi32(message_bits));
-    sha.push_be(lo32(message_bits));
-    sha.drain();
-
-    for (int i = prefix_words; i < frame_words_n - kFooterWords; ++i) frame_words[i] = 0u;
+    ShaStream sha;
+    sha.init(rings + lane);
+    if (role == 0) {
+        if (valid) {
+#pragma unroll
+            for (int i = 0; i < kHeaderWords; ++i) sha.push_be(__builtin_bswap32(hdr[i]));
+            sha.drain();
+            for (int i = 0; i < 4 * tokens; ++i) {
+                sha.push_be(__builtin_bswap32(tables[i]));
+                if (sha.wpos - sha.rpos >= 16) sha.drain();
+            }
+            auto push_chunk = [&](const u32x4_t &c) __attribute__((always_inline)) {
+                sha.push_be(__builtin_bswap32(c[0]));
+                sha.push_be(__builtin_bswap32(c[1]));
+                sha.push_be(__builtin_bswap32(c[2]));
+                sha.push_be(__builtin_bswap32(c[3]));
+            };
+            auto drain = [&]() __attribute__((always_inline)) { sha.drain(); };
+            stream_chunks<kFramePrefetch>(payload_walk(kpage), payload_chunks, push_chunk, drain);
+            stream_chunks<kFramePrefetch>(payload_walk(vpage), payload_chunks, push_chunk, drain);
+            // FIPS 180-4 padding: 0x80, zeros to 56 mod 64, 64-bit big-endian length.
+            const uint64_t message_bits = (record_len - kRecordFooterBytes) * 8;
+            sha.push_be(0x80000000u);
+            while (((sha.wpos - sha.rpos) & 15) != 14) sha.push_be(0u);
+            sha.push_be(hi32(message_bits));
+            sha.push_be(lo32(message_bits));
+            sha.drain();
+        }
+    } else {
+        uint64_t record_sum = kFnvOffset;
+        if (valid) {
+#pragma unroll
+            for (int i = 0; i < kHeaderWords; ++i) record_sum = fnv_word(record_sum, hdr[i]);
+            for (int i = 0; i < 4 * tokens; ++i) record_sum = fnv_word(record_sum, tables[i]);
+            auto fnv_of = [&](const u32x4_t &c) __attribute__((always_inline)) { record_sum = fnv_chunk(record_sum, c); };
+            stream_chunks<kFramePrefetch>(payload_walk(kpage), payload_chunks, fnv_of, no_group);
+            stream_chunks<kFramePrefetch>(payload_walk(vpage), payload_chunks, fnv_of, no_group);
+        }
+        record_sums[lane] = record_sum;
+    }
+    __syncthreads();
+    if (role != 0 || !live) return;
+    if (!valid) {
+        for (int i = 0; i < frame_words_n; ++i) frame_words[i] = 0u;
+        return;
+    }
+    const uint64_t record_sum = record_sums[lane];
+#pragma unroll
+    for (int i = 0; i < kHeaderWords; ++i) frame_words[i] = hdr[i];
+    for (int i = kHeaderWords + 4 * tokens; i < frame_words_n - kFooterWords; ++i) frame_words[i] = 0u;
     uint32_t *footer = frame_words + frame_words_n - kFooterWords;
     footer[0] = 0x564b5354u;  // "TSKV"
     footer[1] = 0x54494d43u;  // "CMIT"
@@ -464,7 +496,7 @@ hipError_t launch_record_frames(const FramesCodecLaunch &a, hipStream_t stream) 
     hipLaunchKernelGGL(token_hashes_kernel, dim3((unsigned)((lanes + 255) / 256)), dim3(256), 0, stream, a);
     if (hipError_t e = hipGetLastError()) return e;
     hipLaunchKernelGGL(frame_kernel, dim3((unsigned)((a.count + kFrameThreads - 1) / kFrameThreads)),
-                       dim3(kFrameThreads), 0, stream, a);
+                       dim3(2 * kFrameThreads), 0, stream, a);
     return hipGetLastError();
 }
 
