@@ -489,6 +489,8 @@ def main() -> int:
                       "FNV tables, record FNV, SHA-256) of every cfg4 pool page; value = K+V payload "
                       "bytes sealed per second",
         },
+        "decode_tokens_per_s": round(B / (dec_avg * 1e-3), 1),
+        "prefill_tokens_per_s": round(S_PREFILL / (pre_avg * 1e-3), 1),
         "decode_ms": round(dec_avg, 5),
         "decode_after_prefill_ms": round(dec_after_prefill, 5),
         "decode_dense_gbps": round(dense_gbps, 2),
