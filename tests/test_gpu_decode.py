@@ -54,24 +54,34 @@ def test_decode_cfg1_parity_repeatability_and_inputs_untouched(ctx):
     assert np.array_equal(from_torch(k), kb) and np.array_equal(from_torch(v), vb)
 
 
+# The reference's tiled-attention geometries (tiled_attention.rs:412-419:
+# (64, 4/4), (128, 8/2), (128, 4/1), (80, 4/2), (256, 4/1)) and the shapes of
+# the BASELINE configs.
 GEOMS = [(32, 8, 128), (64, 8, 128), (8, 8, 128), (16, 8, 128), (8, 2, 64), (32, 4, 64),
-         (4, 2, 80), (4, 1, 256), (12, 4, 128)]
-HISTORIES = [1, 2, 15, 31, 33, 63, 65, 129, 375, 2049]
+         (4, 2, 80), (4, 1, 256), (12, 4, 128), (4, 4, 64), (8, 2, 128), (4, 1, 128)]
+# tiled_attention.rs:430 histories and the fused-vs-three-kernel lengths of
+# gpu_llm/mod.rs:4311-4415.
+HISTORIES = [1, 2, 15, 31, 32, 33, 63, 65, 127, 129, 375, 512, 1024, 2048, 2049, 4097]
+# tiled_attention.rs:374-378: an online (flash) kernel against the reference
+# GPU three-kernel arithmetic on these synthetic vectors.
+ONLINE_TOL = 0.0078125
 
 
 @pytest.mark.parametrize("qh,kvh,d", GEOMS)
 def test_decode_histories_and_geometries(ctx, qh, kvh, d):
-    # tiled_attention.rs:408-434 histories and head dims; the reference's
-    # deterministic synthetic inputs (tiled_attention.rs:305-312).
+    # The reference's deterministic synthetic inputs (tiled_attention.rs:305-312).
     for t in HISTORIES:
         qb = tiled_input(qh * d, 3).reshape(1, qh, d)
         kb = tiled_input(t * kvh * d, 7).reshape(t, kvh, d)
         vb = tiled_input(t * kvh * d, 11).reshape(t, kvh, d)
         ref = _oracle_decode(qb, kb, vb, qh, kvh, d)
+        gpu_ref = oracle.gpu_reference_attention(qb, kb, vb, qh, kvh, d, 1, t - 1)
         for split in (0, 64):
             got = _decode(ctx, qb, kb, vb, [t], qh, kvh, d, split=split)
             err = max_abs_bf16(got, ref)
             assert err <= TOL, (qh, kvh, d, t, split, err)
+            err_gpu = max_abs_bf16(got, oracle.read_bf16(gpu_ref))
+            assert err_gpu <= ONLINE_TOL, (qh, kvh, d, t, split, err_gpu)
 
 
 def test_decode_ragged_batch_dense(ctx):
