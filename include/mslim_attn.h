@@ -307,6 +307,27 @@ int mslim_attn_record_payloads(void *ctx, void *k_pool, void *v_pool, int64_t po
                                int kv_heads, int head_dim, const mslim_attn_page_record *records,
                                int count, void *k_stage, void *v_stage, int direction);
 
+/* ---- Projection GEMM -------------------------------------------------------- */
+
+/* Replaces tv_hip_matrix_multiply (hipblaslt_bridge.cpp:203-233, bound at
+ * native_hip.rs:19-20): output[tokens][rows] = BF16(input[tokens][inner] .
+ * weight[rows][inner]^T), fp32 accumulation rounded once, through hipBLASLt.
+ * weight is a device buffer (mslim_attn_buf_upload); input and output are
+ * HOST buffers of BF16 bits and the call blocks, as in the reference.
+ * Limits as the reference: 0 < tokens <= 512, 0 < inner <= 32768,
+ * 0 < rows <= 500000.  Codes: -1 arguments, 100+hipError_t, 200+hipBLASLt
+ * status, 400/401 staging allocation, 402 H2D, 403 no algorithm, 404
+ * matmul, 405 D2H (hipblaslt_bridge.cpp:217-231). */
+int mslim_attn_matrix_multiply(void *ctx, const void *weight, const uint8_t *input, uint8_t *output,
+                               int inner, int rows, int tokens);
+
+/* The same product on device buffers (input [tokens][inner], output
+ * [tokens][rows]), stream-ordered: the form the device-resident layer
+ * (norm -> QKV -> RoPE -> attention -> O -> SwiGLU -> down) chains without
+ * host round trips.  output must not alias input or weight. */
+int mslim_attn_gemm_bf16(void *ctx, const void *weight, const void *input, void *output, int inner,
+                         int rows, int tokens);
+
 #ifdef __cplusplus
 }
 #endif

@@ -53,6 +53,7 @@ def _load() -> C.CDLL:
         "orc_rope_gpu": (None, [P, P, I, I, I, I, F, I, F, F, F, F]),
         "orc_rope_cpu": (None, [P, I, I, I, F]),
         "orc_swiglu": (None, [P, P, SZ, P]),
+        "orc_matmul_bf16": (None, [P, P, I, I, I, P]),
         "orc_softmax": (None, [P, I]),
         "orc_fnv1a64": (U64, [P, SZ, U64]),
         "orc_sha256": (None, [P, SZ, P]),
@@ -226,6 +227,15 @@ def swiglu(gate_bits, up_bits) -> np.ndarray:
     u = np.ascontiguousarray(up_bits, np.uint16)
     out = np.empty(g.size, np.uint16)
     lib().orc_swiglu(_p(g), _p(u), g.size, _p(out))
+    return out
+
+
+def matmul_bf16(w_bits, in_bits, inner: int, rows: int, tokens: int) -> np.ndarray:
+    """hipblaslt_bridge.cpp:203-233 product: BF16 bits out [tokens][rows]."""
+    w = np.ascontiguousarray(w_bits, np.uint16)
+    x = np.ascontiguousarray(in_bits, np.uint16)
+    out = np.empty(tokens * rows, np.uint16)
+    lib().orc_matmul_bf16(_p(w), _p(x), inner, rows, tokens, _p(out))
     return out
 
 

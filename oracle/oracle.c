@@ -361,6 +361,21 @@ void orc_swiglu(const uint16_t *gate, const uint16_t *up, size_t n, uint16_t *ou
     }
 }
 
+/* hipblaslt_bridge.cpp:203-233 tv_hip_matrix_multiply: out[t][r] =
+ * BF16(sum_i in[t][i] * w[r][i]), products and sum in fp32 (ascending i),
+ * one rounding at the end.  pin: identity weight reproduces the input bit for
+ * bit, linearity in the weight, f64 brute force on small shapes. */
+void orc_matmul_bf16(const uint16_t *w, const uint16_t *in, int inner, int rows, int tokens, uint16_t *out) {
+    for (int t = 0; t < tokens; ++t)
+        for (int r = 0; r < rows; ++r) {
+            float acc = 0.0f;
+            const uint16_t *wr = w + (size_t)r * inner;
+            const uint16_t *xt = in + (size_t)t * inner;
+            for (int i = 0; i < inner; ++i) acc = fmaf(orc_read_bf16(wr[i]), orc_read_bf16(xt[i]), acc);
+            out[(size_t)t * rows + r] = orc_write_bf16(acc);
+        }
+}
+
 /* ---- Integrity primitives ----------------------------------------------- */
 uint64_t orc_fnv1a64(const uint8_t *bytes, size_t n, uint64_t state) {
     for (size_t i = 0; i < n; ++i) {

@@ -119,6 +119,10 @@ void orc_swiglu(const uint16_t *gate, const uint16_t *up, size_t n, uint16_t *ou
 /* native_cpu_adapter.rs:223-233 `softmax` (f32). pin: sums to 1 (:1003-1008) */
 void orc_softmax(float *values, int n);
 
+/* hipblaslt_bridge.cpp:203-233: out[t][r] = BF16(sum_i in[t][i] * w[r][i]),
+ * fp32 accumulation (fma, ascending i), one rounding. */
+void orc_matmul_bf16(const uint16_t *w, const uint16_t *in, int inner, int rows, int tokens, uint16_t *out);
+
 /* ---- Integrity primitives ----------------------------------------------- */
 /* cold_store.rs:909-922 FNV-1a-64 over concatenated parts.
  * pin: published vectors ("" -> cbf29ce484222325, "a" -> af63dc4c8601ec8c). */

@@ -1,0 +1,87 @@
+"""GPU parity of the projection GEMM (mslim_attn_matrix_multiply, the
+tv_hip_matrix_multiply replacement, and its device form) against the oracle's
+restatement of the reference product (hipblaslt_bridge.cpp:203-233).  Both
+accumulate in fp32, in different orders, so both are held to the same bound
+against the exact (f64) product: one BF16 ulp of the exact value (the final
+rounding) plus 1e-5 * sum_i |w_i x_i| (fp32 accumulation).  Near-cancelling
+outputs are thereby judged in absolute terms, as their terms demand."""
+import numpy as np
+import pytest
+import torch
+
+import mslim_attn
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def bf16(rng, n, scale=1.0):
+    return oracle.write_bf16(rng.standard_normal(n, dtype=np.float32) * np.float32(scale))
+
+
+def within_bound(got_bits, w_bits, x_bits, inner, rows, tokens):
+    w = oracle.read_bf16(w_bits).astype(np.float64).reshape(rows, inner)
+    x = oracle.read_bf16(x_bits[: tokens * inner]).astype(np.float64).reshape(tokens, inner)
+    exact = (x @ w.T).reshape(-1)
+    scale = (np.abs(x) @ np.abs(w).T).reshape(-1)
+    got = oracle.read_bf16(got_bits[: tokens * rows]).astype(np.float64)
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(exact), 1e-30))) - 7)
+    return bool(np.all(np.abs(got - exact) <= ulp + 1e-5 * scale))
+
+
+def upload(ctx, bits):
+    return ctx.buf_upload(np.ascontiguousarray(bits, np.uint16).tobytes())
+
+
+@pytest.mark.parametrize("inner,rows,tokens", [
+    (4096, 6144, 1),    # fused QKV of the cfg5 shape, decode
+    (4096, 4096, 8),    # O projection, B = 8
+    (14336, 4096, 8),   # down projection
+    (4096, 28672, 2),   # gate + up
+    (128, 96, 3),
+    (4096, 6144, 512),  # prefill chunk, first rows checked
+])
+def test_matrix_multiply_matches_oracle(ctx, inner, rows, tokens):
+    rng = np.random.default_rng(inner + rows + tokens)
+    w = bf16(rng, rows * inner, 0.02)
+    x = bf16(rng, tokens * inner)
+    wd = upload(ctx, w)
+    try:
+        got = ctx.matrix_multiply(wd, x, inner, rows, tokens)
+        check = min(tokens, 4)
+        assert within_bound(got, w, x, inner, rows, check)
+        # the oracle's restatement meets the same bound
+        want = oracle.matmul_bf16(w, x[: check * inner], inner, rows, check)
+        assert within_bound(want, w, x, inner, rows, check)
+        # the device form gives the same bits
+        xin = torch.from_numpy(x.view(np.int16).copy()).cuda()
+        out = torch.empty(tokens * rows, dtype=torch.int16, device="cuda")
+        ctx.gemm_bf16(wd, xin, out, inner, rows, tokens)
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy().view(np.uint16), got)
+    finally:
+        ctx.buf_free(wd)
+
+
+def test_identity_weight_is_exact(ctx):
+    n = 256
+    rng = np.random.default_rng(3)
+    x = bf16(rng, 5 * n)
+    eye = oracle.write_bf16(np.eye(n, dtype=np.float32).reshape(-1))
+    wd = upload(ctx, eye)
+    try:
+        assert np.array_equal(ctx.matrix_multiply(wd, x, n, n, 5), x)
+    finally:
+        ctx.buf_free(wd)
+
+
+def test_matrix_multiply_rejects_bad_arguments(ctx):
+    wd = upload(ctx, np.zeros(64, np.uint16))
+    try:
+        x = np.zeros(8 * 513, np.uint16)
+        with pytest.raises(mslim_attn.MslimAttnError, match="code=-1"):
+            ctx.matrix_multiply(wd, x, 8, 8, 513)
+        with pytest.raises(mslim_attn.MslimAttnError, match="code=-1"):
+            ctx.matrix_multiply(wd, x, 0, 8, 1)
+    finally:
+        ctx.buf_free(wd)

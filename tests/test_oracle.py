@@ -395,3 +395,24 @@ def test_reference_tiled_input_generator():
     # tiled_attention.rs:305-312 first values for salt 3: i=0 -> (39 % 257 - 128)/128
     vals = oracle.read_bf16(tiled_input(3, 3))
     assert vals.tolist() == [(39 - 128) / 128, (76 - 128) / 128, (113 - 128) / 128]
+
+
+def test_matmul_bf16_pins():
+    """orc_matmul_bf16 (hipblaslt_bridge.cpp:203-233 product): identity weight
+    reproduces the input bit for bit, exact scaling of the weight by 2
+    doubles the output exactly, and f64 brute force agrees to one BF16 ulp."""
+    rng = np.random.default_rng(5)
+    inner = rows = 32
+    x = oracle.write_bf16(rng.standard_normal(3 * inner, dtype=np.float32))
+    eye = oracle.write_bf16(np.eye(rows, inner, dtype=np.float32).reshape(-1))
+    assert np.array_equal(oracle.matmul_bf16(eye, x, inner, rows, 3), x)
+    inner, rows, tokens = 96, 40, 4
+    w = oracle.write_bf16(rng.standard_normal(rows * inner, dtype=np.float32) * np.float32(0.05))
+    x = oracle.write_bf16(rng.standard_normal(tokens * inner, dtype=np.float32))
+    out = oracle.read_bf16(oracle.matmul_bf16(w, x, inner, rows, tokens))
+    w2 = oracle.write_bf16(oracle.read_bf16(w) * np.float32(2))
+    assert np.array_equal(oracle.read_bf16(oracle.matmul_bf16(w2, x, inner, rows, tokens)), out * 2)
+    ref = (oracle.read_bf16(x).astype(np.float64).reshape(tokens, inner)
+           @ oracle.read_bf16(w).astype(np.float64).reshape(rows, inner).T).reshape(-1)
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(ref), 1e-30))) - 7)
+    assert np.all(np.abs(out - ref) <= ulp)

@@ -49,9 +49,15 @@ struct Context {
     void *backend = nullptr;       // device, backend_decode query/frames/output
     size_t backend_bytes = 0;
     hipEvent_t ev_start = nullptr, ev_end = nullptr;
+    mslim::GemmState *gemm = nullptr;  // hipBLASLt handle and plans, created on first use
+    void *gemm_in = nullptr, *gemm_out = nullptr;  // device staging of matrix_multiply
+    size_t gemm_in_bytes = 0, gemm_out_bytes = 0;
 
     ~Context() {
         if (stream) (void)hipStreamSynchronize(stream);
+        mslim::gemm_state_destroy(gemm);
+        if (gemm_in) (void)hipFree(gemm_in);
+        if (gemm_out) (void)hipFree(gemm_out);
         if (workspace) (void)hipFree(workspace);
         if (counters) (void)hipFree(counters);
         if (staging) (void)hipFree(staging);
@@ -702,6 +708,48 @@ int mslim_attn_record_payloads(void *ctx, void *k_pool, void *v_pool, int64_t po
     l.k_stage = k_stage;
     l.v_stage = v_stage;
     return check_hip(mslim::launch_record_payloads(l, direction == 0, c.stream), "record payload launch");
+}
+
+// tv_hip_matrix_multiply's argument limits (hipblaslt_bridge.cpp:207-210).
+static bool gemm_args_ok(const void *ctx, const void *w, const void *in, const void *out, int inner, int rows,
+                         int tokens) {
+    return ctx && w && in && out && inner > 0 && rows > 0 && tokens > 0 && tokens <= 512 && inner <= 32768 &&
+           rows <= 500000;
+}
+
+int mslim_attn_matrix_multiply(void *ctx, const void *weight, const uint8_t *input, uint8_t *output, int inner,
+                               int rows, int tokens) {
+    g_error.clear();
+    if (!gemm_args_ok(ctx, weight, input, output, inner, rows, tokens))
+        return fail("invalid BF16 matrix dimensions/arguments");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    const size_t insize = (size_t)inner * tokens * 2, outsize = (size_t)rows * tokens * 2;
+    if (grow_device(c, &c.gemm_in, &c.gemm_in_bytes, insize, "hipMalloc BF16 input")) return 400;
+    if (grow_device(c, &c.gemm_out, &c.gemm_out_bytes, outsize, "hipMalloc BF16 output")) return 401;
+    if (check_hip(hipMemcpyAsync(c.gemm_in, input, insize, hipMemcpyHostToDevice, c.stream), "BF16 matrix input H2D"))
+        return 402;
+    std::string err;
+    if (int code = mslim::gemm_bf16(c.gemm, weight, c.gemm_in, c.gemm_out, inner, rows, tokens, c.stream, err))
+        return fail(err, code);
+    if (check_hip(hipMemcpyAsync(output, c.gemm_out, outsize, hipMemcpyDeviceToHost, c.stream),
+                  "BF16 matrix output D2H"))
+        return 405;
+    return check_hip(hipStreamSynchronize(c.stream), "BF16 matrix output D2H") ? 405 : 0;
+}
+
+int mslim_attn_gemm_bf16(void *ctx, const void *weight, const void *input, void *output, int inner, int rows,
+                         int tokens) {
+    g_error.clear();
+    if (!gemm_args_ok(ctx, weight, input, output, inner, rows, tokens))
+        return fail("invalid BF16 matrix dimensions/arguments");
+    if (output == input || output == weight) return fail("GEMM output must not alias its inputs");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    std::string err;
+    if (int code = mslim::gemm_bf16(c.gemm, weight, input, output, inner, rows, tokens, c.stream, err))
+        return fail(err, code);
+    return 0;
 }
 
 }  // extern "C"

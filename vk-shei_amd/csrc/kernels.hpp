@@ -6,6 +6,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <string>
+
 namespace mslim {
 
 constexpr int kMaxBatch = 64;
@@ -111,6 +113,15 @@ struct PayloadMoveLaunch {
     void *k_stage, *v_stage;  // [count][kv_heads * page_tokens * head_dim] BF16 slots
 };
 hipError_t launch_record_payloads(const PayloadMoveLaunch &a, bool to_staging, hipStream_t stream);
+
+// BF16 projection GEMM through hipBLASLt (csrc/gemm.hip).
+struct GemmState;
+void gemm_state_destroy(GemmState *state);
+// out[tokens][rows] = BF16(in[tokens][inner] . weight[rows][inner]^T) on
+// device buffers, stream-ordered.  Returns 0, 100+hipError_t, 200+hipBLASLt
+// status, 403 (no plan) or 404 (matmul failed) with `err` set.
+int gemm_bf16(GemmState *&state, const void *weight, const void *input, void *output, int inner, int rows,
+              int tokens, hipStream_t stream, std::string &err);
 
 hipError_t launch_pages_write(uint16_t *k_pool, uint16_t *v_pool, const int32_t *page_table,
                               int page_tokens, int kv_heads, int head_dim, int64_t first_token,

@@ -68,6 +68,8 @@ EXPORTS = (
     "mslim_attn_record_frame_bytes",
     "mslim_attn_record_frames",
     "mslim_attn_record_payloads",
+    "mslim_attn_matrix_multiply",
+    "mslim_attn_gemm_bf16",
 )
 
 RECORD_HEADER_BYTES = 104  # cold_store.rs:23
@@ -132,6 +134,8 @@ def library() -> C.CDLL:
         "mslim_attn_record_frame_bytes": (I64, [I]),
         "mslim_attn_record_frames": (I, [P, P, P, I64, I, I, I, C.c_uint32, P, I, P]),
         "mslim_attn_record_payloads": (I, [P, P, P, I64, I, I, I, P, I, P, P, I]),
+        "mslim_attn_matrix_multiply": (I, [P, P, P, P, I, I, I]),
+        "mslim_attn_gemm_bf16": (I, [P, P, P, P, I, I, I]),
     }
     for name in EXPORTS:
         res, args = sigs[name]
@@ -219,6 +223,33 @@ class Context:
         self._check("synchronize", self._lib.mslim_attn_synchronize(self._h))
 
     # ---- attention -----------------------------------------------------
+    # ---- Device buffers (tv_hip_load_weight / free_weight / read_weight) ----
+    def buf_upload(self, data: bytes) -> int:
+        """Allocate a device buffer holding `data`; returns its device pointer."""
+        buf = C.create_string_buffer(bytes(data), len(data))
+        ptr = self._lib.mslim_attn_buf_upload(self._h, C.addressof(buf), len(data))
+        if not ptr:
+            raise MslimAttnError("buf_upload", -1, last_error())
+        return int(ptr)
+
+    def buf_alloc(self, nbytes: int) -> int:
+        ptr = self._lib.mslim_attn_buf_alloc(self._h, nbytes)
+        if not ptr:
+            raise MslimAttnError("buf_alloc", -1, last_error())
+        return int(ptr)
+
+    def buf_free(self, ptr: int) -> None:
+        self._check("buf_free", self._lib.mslim_attn_buf_free(self._h, ptr))
+
+    def buf_read(self, ptr: int, offset: int, nbytes: int) -> bytes:
+        out = C.create_string_buffer(nbytes)
+        self._check("buf_read", self._lib.mslim_attn_buf_read(self._h, ptr, offset, C.addressof(out), nbytes))
+        return out.raw
+
+    def buf_write(self, ptr: int, offset: int, data: bytes) -> None:
+        buf = C.create_string_buffer(bytes(data), len(data))
+        self._check("buf_write", self._lib.mslim_attn_buf_write(self._h, ptr, offset, C.addressof(buf), len(data)))
+
     def decode_dense(self, q, k, v, out, seq_lens: Sequence[int], q_heads: int, kv_heads: int,
                      head_dim: int, seq_stride_tokens: int = 0, scale: Optional[float] = None,
                      split_tokens: int = 0) -> None:
@@ -324,12 +355,31 @@ class Context:
             self._h, _ptr(k_pool), _ptr(v_pool), pool_pages, page_tokens, kv_heads, head_dim,
             tile, _ptr(records), count, _ptr(frames)))
 
+    # ---- Projection GEMM --------------------------------------------------
+    def matrix_multiply(self, weight, input_bits, inner: int, rows: int, tokens: int):
+        """tv_hip_matrix_multiply: host BF16 bits in [tokens][inner], host out
+        [tokens][rows]; weight is a device buffer [rows][inner]."""
+        import numpy as np
+        x = np.ascontiguousarray(input_bits, np.uint16)
+        out = np.empty(tokens * rows, np.uint16)
+        self._check("matrix_multiply", self._lib.mslim_attn_matrix_multiply(
+            self._h, _ptr(weight), x.ctypes.data, out.ctypes.data, inner, rows, tokens))
+        return out
+
+    def gemm_bf16(self, weight, input_dev, output_dev, inner: int, rows: int, tokens: int) -> None:
+        self._check("gemm_bf16", self._lib.mslim_attn_gemm_bf16(
+            self._h, _ptr(weight), _ptr(input_dev), _ptr(output_dev), inner, rows, tokens))
+
     def record_payloads(self, k_pool, v_pool, pool_pages: int, page_tokens: int, kv_heads: int,
                         head_dim: int, records, count: int, k_stage, v_stage, to_staging: bool) -> None:
         """Pool pages <-> compacted staging slots of kv_heads*page_tokens*head_dim BF16."""
         self._check("record_payloads", self._lib.mslim_attn_record_payloads(
             self._h, _ptr(k_pool), _ptr(v_pool), pool_pages, page_tokens, kv_heads, head_dim,
             _ptr(records), count, _ptr(k_stage), _ptr(v_stage), 0 if to_staging else 1))
+
+
+def _host_ptr(a) -> int:
+    return a.ctypes.data
 
 
 def split_count(tokens: int, split_tokens: int) -> int:
