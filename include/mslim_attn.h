@@ -212,9 +212,34 @@ int mslim_attn_rope(void *ctx, const void *input, void *output, int tokens, int 
                     float factor, float low_freq_factor, float high_freq_factor,
                     float original_max_position);
 
+/* The same RoPE with row t at position positions[t] (device int32 [tokens],
+ * each >= 0): one decode row per sequence of a batch, each sequence at its own
+ * position.  The reference rotates one sequence per call (llm_rope's `pos`,
+ * gpu_llm.cl:102-146; gpu_resources.rs:509-537). */
+int mslim_attn_rope_rows(void *ctx, const void *input, void *output, int tokens, int heads,
+                         int head_dim, const int32_t *positions, float theta, int llama3_scaling,
+                         float factor, float low_freq_factor, float high_freq_factor,
+                         float original_max_position);
+
 /* out = BF16(BF16(silu(gate)) * up) over n elements.  Replaces
  * GpuEngine::swiglu (gpu_resources.rs:561-581, llm_swiglu gpu_llm.cl:225-237). */
 int mslim_attn_swiglu(void *ctx, const void *gate, const void *up, void *output, size_t n);
+
+/* output = BF16(a + b) over n elements (llm_add, gpu_llm.cl:214-222): the
+ * residual adds of a decoder layer. */
+int mslim_attn_add(void *ctx, const void *a, const void *b, void *output, size_t n);
+
+/* Rows `ids[t]` (device int32 [tokens]) of a [vocab][hidden] BF16 table into
+ * output [tokens][hidden] (llm_embed, gpu_llm.cl:24-33).  An id outside
+ * [0, vocab) gives a zero row and, when `bad` (device int) is not NULL, sets
+ * *bad = 1.  hidden must be a multiple of 8. */
+int mslim_attn_embed(void *ctx, const void *table, int vocab, int hidden, const int32_t *ids,
+                     int tokens, void *output, int *bad);
+
+/* Greedy token of each of `rows` rows of BF16 logits [rows][vocab] into device
+ * int32 out[rows], the first index winning ties (llm_argmax,
+ * gpu_llm.cl:239-270). */
+int mslim_attn_argmax(void *ctx, const void *logits, int rows, int vocab, int32_t *out);
 
 /* ---- ColdStore-exact page pool --------------------------------------------- */
 
@@ -226,6 +251,17 @@ int mslim_attn_swiglu(void *ctx, const void *gate, const void *up, void *output,
 int mslim_attn_pages_write(void *ctx, void *k_pool, void *v_pool, const int32_t *page_table,
                            int page_tokens, int kv_heads, int head_dim, int64_t first_token,
                            int64_t tokens, const void *k_rows, const void *v_rows);
+
+/* Decode-step append of one token to each of `batch` sequences: K/V row b
+ * ([batch][kv_heads][head_dim]) goes to logical position positions[b] (device
+ * int32) through page-table row b of the device table [batch][pages_per_seq].
+ * A position outside [0, pages_per_seq * page_tokens) writes nothing.  The
+ * batched form of the per-token KV append of run_layer (gpu_llm/mod.rs:
+ * 2103-2136) into the page layout of gpu_region_store.rs:391-520. */
+int mslim_attn_pages_append(void *ctx, void *k_pool, void *v_pool, const int32_t *page_table,
+                            int pages_per_seq, int page_tokens, int kv_heads, int head_dim,
+                            int batch, const int32_t *positions, const void *k_rows,
+                            const void *v_rows);
 
 /* Gather `tokens` logical positions [first_token, first_token+tokens) of one
  * sequence from a page pool into token-major rows [tokens][kv_heads][head_dim].

@@ -1,0 +1,83 @@
+/* Decoder runner over libmslim_attn (exported by libmslim_host).
+ *
+ * The per-layer order of the reference GPU runtime -- run_layer
+ * (src/gpu_llm/mod.rs:2056-2350) for decode and run_batch_layer
+ * (src/gpu_llm/prefill.rs:897-1061) for prompt chunks -- chained on device
+ * buffers through the attention library:
+ *   embed -> per layer [RMSNorm -> Q,K,V projections -> RoPE(Q,K) -> K/V into
+ *   the ColdStore-exact page pool (16-token pages) -> attention -> O
+ *   projection -> residual add -> RMSNorm -> gate, up -> SwiGLU -> down ->
+ *   residual add] -> RMSNorm -> LM head -> greedy token (first index on ties).
+ * The reference drives one session per GpuLlm; a runner here holds
+ * `max_batch` sequence slots whose decode steps run as one batch.
+ * Every entry point returns 0 on success and -1 with mslim_model_last_error()
+ * set on failure; calls on one runner are serialised by the caller. */
+#ifndef MSLIM_MODEL_H
+#define MSLIM_MODEL_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Weight tensors per layer, in the order of the `weights` array below. */
+#define MSLIM_MODEL_LAYER_TENSORS 9
+
+/* ModelSpec fields a layer uses (src/model_config.rs:22-42) and the RoPE
+ * arguments of RopeKernelConfig (src/gpu_llm/kernels.rs:15-23). */
+typedef struct {
+    int layers, hidden, q_heads, kv_heads, head_dim, intermediate, vocab;
+    float rms_eps, rope_theta;
+    int llama3_scaling;
+    float rope_factor, rope_low_freq_factor, rope_high_freq_factor, rope_original_max_position;
+} mslim_model_spec;
+
+const char *mslim_model_last_error(void);
+
+/* A runner on an attention-library context (mslim_attn_ctx_new), which must
+ * outlive it.  `weights` holds 3 + 9 * layers device BF16 pointers:
+ *   [0] embedding [vocab][hidden], [1] final norm [hidden],
+ *   [2] LM head [vocab][hidden] (the embedding when tied), then per layer
+ *   input norm [hidden], q [q_heads*head_dim][hidden], k and v
+ *   [kv_heads*head_dim][hidden], o [hidden][q_heads*head_dim], post norm
+ *   [hidden], gate and up [intermediate][hidden], down [hidden][intermediate].
+ * max_batch <= 64 slots, chunk_tokens <= 512 prompt tokens per causal chunk,
+ * max_context tokens per slot.  The runner allocates its K/V page pools and
+ * activations on the context's device.  Replaces GpuLlm::load_dense_native_hip
+ * (src/gpu_llm/mod.rs:308) for weights already on the device. */
+void *mslim_model_new(void *attn_ctx, const mslim_model_spec *spec, const void *const *weights,
+                      int max_batch, int chunk_tokens, int max_context);
+void mslim_model_destroy(void *model);
+
+/* Prompt of slot `seq` from position 0; *next_token = greedy token after the
+ * prompt, not appended (GpuLlm::prefill_only, src/gpu_llm/mod.rs:2499-2570). */
+int mslim_model_prefill(void *model, int seq, const int32_t *prompt, int tokens,
+                        int32_t *next_token);
+
+/* One token for each of slots 0..batch-1 at that slot's position
+ * (GpuLlm::forward_token, src/gpu_llm/mod.rs:2457-2484, for a batch). */
+int mslim_model_forward_batch(void *model, const int32_t *tokens, int batch,
+                              int32_t *next_tokens);
+
+/* Slot 0: prefill, then greedy tokens until max_new or an EOS id; out holds
+ * max_new ids (GpuLlm::generate, src/gpu_llm/mod.rs:2571-2700). */
+int mslim_model_generate(void *model, const int32_t *prompt, int tokens, int max_new,
+                         const int32_t *eos_ids, int eos_count, int32_t *out, int *generated);
+
+/* Tokens held by slot `seq`, or -1 (GpuLlm::position, mod.rs:1314). */
+int64_t mslim_model_position(void *model, int seq);
+/* Empty slot `seq` (GpuLlm::reset_session, mod.rs:1530). */
+int mslim_model_reset(void *model, int seq);
+/* BF16 bits of the last logits: 1 row after prefill, one per slot after a
+ * batch step (GpuStep::logits, mod.rs:116-118). */
+int mslim_model_logits(void *model, uint16_t *out, size_t capacity, int *rows);
+/* GpuLlm::logical_kv_sha256 (mod.rs:1981-2028) of slot `seq`, hex with NUL. */
+int mslim_model_logical_kv_sha256(void *model, int seq, char *hex_out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MSLIM_MODEL_H */

@@ -54,6 +54,8 @@ def _load() -> C.CDLL:
         "orc_rope_cpu": (None, [P, I, I, I, F]),
         "orc_swiglu": (None, [P, P, SZ, P]),
         "orc_matmul_bf16": (None, [P, P, I, I, I, P]),
+        "orc_add_bf16": (None, [P, P, SZ, P]),
+        "orc_argmax_bf16": (None, [P, I, I, P]),
         "orc_softmax": (None, [P, I]),
         "orc_fnv1a64": (U64, [P, SZ, U64]),
         "orc_sha256": (None, [P, SZ, P]),
@@ -228,6 +230,29 @@ def swiglu(gate_bits, up_bits) -> np.ndarray:
     out = np.empty(g.size, np.uint16)
     lib().orc_swiglu(_p(g), _p(u), g.size, _p(out))
     return out
+
+
+def add_bf16(a_bits, b_bits) -> np.ndarray:
+    """gpu_llm.cl:214-222 llm_add: BF16(a + b)."""
+    a = np.ascontiguousarray(a_bits, np.uint16).reshape(-1)
+    b = np.ascontiguousarray(b_bits, np.uint16).reshape(-1)
+    out = np.empty(a.size, np.uint16)
+    lib().orc_add_bf16(_p(a), _p(b), a.size, _p(out))
+    return out
+
+
+def argmax_bf16(logits_bits, rows: int, vocab: int) -> np.ndarray:
+    """gpu_llm.cl:239-270 llm_argmax per row: int32 [rows]."""
+    x = np.ascontiguousarray(logits_bits, np.uint16).reshape(-1)
+    out = np.empty(rows, np.int32)
+    lib().orc_argmax_bf16(_p(x), rows, vocab, _p(out))
+    return out
+
+
+def embed_rows(table_bits, ids, hidden: int) -> np.ndarray:
+    """gpu_llm.cl:24-33 llm_embed, one row per id: [len(ids)][hidden] bits."""
+    table = np.ascontiguousarray(table_bits, np.uint16).reshape(-1, hidden)
+    return table[np.asarray(ids, np.int64)].copy()
 
 
 def matmul_bf16(w_bits, in_bits, inner: int, rows: int, tokens: int) -> np.ndarray:

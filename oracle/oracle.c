@@ -361,6 +361,29 @@ void orc_swiglu(const uint16_t *gate, const uint16_t *up, size_t n, uint16_t *ou
     }
 }
 
+/* gpu_llm.cl:214-222 llm_add: one f32 add, one BF16 rounding. */
+void orc_add_bf16(const uint16_t *a, const uint16_t *b, size_t n, uint16_t *out) {
+    for (size_t i = 0; i < n; ++i) out[i] = orc_write_bf16(orc_read_bf16(a[i]) + orc_read_bf16(b[i]));
+}
+
+/* gpu_llm.cl:239-270 llm_argmax with one lane: the scan's update rule alone
+ * fixes the result, whatever the lane count of the reduction. */
+void orc_argmax_bf16(const uint16_t *logits, int rows, int vocab, int32_t *out) {
+    for (int r = 0; r < rows; ++r) {
+        const uint16_t *l = logits + (size_t)r * vocab;
+        float best = -INFINITY;
+        int32_t index = 0;
+        for (int i = 0; i < vocab; ++i) {
+            const float x = orc_read_bf16(l[i]);
+            if (x > best || (x == best && i < index)) {
+                best = x;
+                index = i;
+            }
+        }
+        out[r] = index;
+    }
+}
+
 /* hipblaslt_bridge.cpp:203-233 tv_hip_matrix_multiply: out[t][r] =
  * BF16(sum_i in[t][i] * w[r][i]), products and sum in fp32 (ascending i),
  * one rounding at the end.  pin: identity weight reproduces the input bit for

@@ -119,6 +119,16 @@ void orc_swiglu(const uint16_t *gate, const uint16_t *up, size_t n, uint16_t *ou
 /* native_cpu_adapter.rs:223-233 `softmax` (f32). pin: sums to 1 (:1003-1008) */
 void orc_softmax(float *values, int n);
 
+/* gpu_llm.cl:214-222 `llm_add`: out = BF16(a + b).
+ * pin: sums of small integers are exact; a + (-a) = +0; ties to even at the
+ * BF16 boundary (1 + 2^-8 -> 1, 1 + 3*2^-8 -> 1 + 2^-6). */
+void orc_add_bf16(const uint16_t *a, const uint16_t *b, size_t n, uint16_t *out);
+/* gpu_llm.cl:239-270 `llm_argmax` over each of `rows` rows: start from
+ * (-inf, 0), take a value that is greater or equal with a lower index.
+ * pin: numpy.argmax on rows of distinct finite values; first index on ties;
+ * NaN never chosen; a row of -inf (or NaN) gives 0. */
+void orc_argmax_bf16(const uint16_t *logits, int rows, int vocab, int32_t *out);
+
 /* hipblaslt_bridge.cpp:203-233: out[t][r] = BF16(sum_i in[t][i] * w[r][i]),
  * fp32 accumulation (fma, ascending i), one rounding. */
 void orc_matmul_bf16(const uint16_t *w, const uint16_t *in, int inner, int rows, int tokens, uint16_t *out);

@@ -47,3 +47,22 @@ def max_abs_bf16(a_bits: np.ndarray, b) -> float:
     a = oracle.read_bf16(a_bits).astype(np.float64).reshape(-1)
     b = np.asarray(b, np.float64).reshape(-1)
     return float(np.max(np.abs(a - b))) if a.size else 0.0
+
+
+# Model-level logit tolerance of the decoder runner against the CPU decoder
+# oracle.  Every non-attention stage is bit-exact; the attention kernels
+# (online softmax, BF16 P on the MFMA path) are within 2e-2 of the reference
+# arithmetic, which after two layers spreads to about 1.2e-2 relative L2 and
+# 0.06 absolute on logits of magnitude 4-8 (one BF16 ulp there is 0.031).
+# The bounds sit about 2x above that and at least 4x below the deviation of
+# the planted wiring mistakes in tests/test_oracle.py (RoPE position off by
+# one on decode steps: rel2 >= 0.11; reversed GQA head map: rel2 >= 1).
+MODEL_LOGIT_MAX_ABS = 0.125
+MODEL_LOGIT_REL2 = 2.5e-2
+
+
+def logit_error(got_bits, want_bits) -> tuple:
+    """(max abs, relative L2) of BF16 logits against the oracle's."""
+    got = oracle.read_bf16(np.asarray(got_bits, np.uint16)).astype(np.float64).reshape(-1)
+    want = oracle.read_bf16(np.asarray(want_bits, np.uint16)).astype(np.float64).reshape(-1)
+    return float(np.max(np.abs(got - want))), float(np.linalg.norm(got - want) / np.linalg.norm(want))

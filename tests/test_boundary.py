@@ -65,3 +65,17 @@ def test_split_auto_policy_is_layout_independent():
     assert split_count(1024, 64) == 16
     assert split_count(1, 64) == 1
     assert split_count(65, 64) == 2
+
+
+def test_host_library_exports_the_model_runner():
+    # include/mslim_model.h is the runner's boundary, exported by libmslim_host
+    from mslim_attn import model
+
+    text = re.sub(r"/\*.*?\*/", "", open(os.path.join(ROOT, "include", "mslim_model.h")).read(), flags=re.S)
+    declared = sorted(set(re.findall(r"\b(mslim_model_[a-z0-9_]+)\s*\(", text)))
+    assert declared == sorted(model.MODEL_EXPORTS)
+    if not os.path.exists(model.HOST_LIB_PATH):
+        pytest.fail("libmslim_host.so is not built: run __graft_entry__.build()")
+    model.host_library()
+    lib = ctypes.CDLL(model.HOST_LIB_PATH)
+    assert [n for n in declared if not hasattr(lib, n)] == []

@@ -1,0 +1,280 @@
+"""GPU parity of the decoder glue kernels (bit-exact against the oracle's
+restatements of llm_add, llm_embed, llm_argmax, llm_rope and the page
+layout) and of the C++ decoder runner (libmslim_host) against the CPU
+decoder forward composed from the pinned stage functions (oracle/decoder.py).
+
+Every runner stage except attention and the hipBLASLt projections is
+bit-exact against the oracle; one-token prompts (attention output = V
+exactly) isolate the projections' rounding-order flips.  Longer histories
+carry the attention kernels' difference from the reference arithmetic, bounded at model level by MODEL_LOGIT_MAX_ABS and
+MODEL_LOGIT_REL2 (tests/_data.py, which states how they were set and which
+planted mistakes they reject).  Greedy tokens must agree wherever the
+oracle's top-1/top-2 margin exceeds 2 * MODEL_LOGIT_MAX_ABS.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle.decoder import DecoderOracle, Spec, random_weights
+from _data import MODEL_LOGIT_MAX_ABS, MODEL_LOGIT_REL2, from_torch, logit_error, normal_bf16, to_torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev_i32(values):
+    return torch.tensor(np.asarray(values, np.int32), dtype=torch.int32, device="cuda")
+
+
+# ---- glue kernels ------------------------------------------------------------
+
+@pytest.mark.parametrize("n", [1, 255, 256, 257, 100003])
+def test_add_bit_exact(ctx, n):
+    rng = np.random.default_rng(n)
+    a, b = normal_bf16(rng, (n,), 3.0), normal_bf16(rng, (n,))
+    if n >= 4:
+        a[:4] = oracle.write_bf16(np.float32([np.inf, -np.inf, np.nan, 65504.0]))
+    out = torch.empty(n, dtype=torch.int16, device="cuda")
+    ctx.add(to_torch(a), to_torch(b), out, n)
+    torch.cuda.synchronize()
+    got, want = from_torch(out), oracle.add_bf16(a, b)
+    nan = np.isnan(oracle.read_bf16(want))
+    assert np.array_equal(np.isnan(oracle.read_bf16(got)), nan)
+    assert np.array_equal(got[~nan], want[~nan])
+
+
+def test_add_in_place(ctx):
+    rng = np.random.default_rng(2)
+    a, b = normal_bf16(rng, (4096,)), normal_bf16(rng, (4096,))
+    ta = to_torch(a)
+    ctx.add(ta, to_torch(b), ta, 4096)
+    torch.cuda.synchronize()
+    assert np.array_equal(from_torch(ta), oracle.add_bf16(a, b))
+
+
+def test_embed_rows_and_bad_ids(ctx):
+    rng = np.random.default_rng(4)
+    vocab, hidden = 1000, 264
+    table = normal_bf16(rng, (vocab, hidden))
+    ids = np.array([0, 999, 5, 5, 321], np.int32)
+    out = torch.empty((ids.size, hidden), dtype=torch.int16, device="cuda")
+    bad = _dev_i32([0])
+    ctx.embed(to_torch(table), vocab, hidden, _dev_i32(ids), ids.size, out, bad)
+    torch.cuda.synchronize()
+    assert np.array_equal(from_torch(out), oracle.embed_rows(table, ids, hidden))
+    assert bad.item() == 0
+    ids2 = np.array([7, -1, 1000, 3], np.int32)
+    out2 = torch.empty((4, hidden), dtype=torch.int16, device="cuda")
+    ctx.embed(to_torch(table), vocab, hidden, _dev_i32(ids2), 4, out2, bad)
+    torch.cuda.synchronize()
+    got = from_torch(out2)
+    assert bad.item() == 1
+    assert np.array_equal(got[0], table[7]) and np.array_equal(got[3], table[3])
+    assert not got[1].any() and not got[2].any()
+
+
+@pytest.mark.parametrize("rows,vocab", [(1, 128256), (5, 1000), (3, 1), (2, 257)])
+def test_argmax_bit_exact(ctx, rows, vocab):
+    rng = np.random.default_rng(vocab + rows)
+    x = normal_bf16(rng, (rows, vocab), 4.0)
+    out = _dev_i32(np.zeros(rows))
+    ctx.argmax(to_torch(x), rows, vocab, out)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), oracle.argmax_bf16(x, rows, vocab))
+
+
+def test_argmax_ties_nan_and_infinities(ctx):
+    f = np.float32
+    vocab = 600
+    rows = []
+    base = np.full(vocab, -1.0, f)
+    r = base.copy(); r[[10, 300, 599]] = 7.0; rows.append(r)          # ties: first index
+    r = base.copy(); r[0] = np.nan; r[450] = 2.0; rows.append(r)        # NaN never wins
+    rows.append(np.full(vocab, -np.inf, f))                            # nothing above -inf -> 0
+    rows.append(np.full(vocab, np.nan, f))
+    r = base.copy(); r[[511, 256]] = np.inf; rows.append(r)            # +inf tie across lanes
+    r = np.full(vocab, -np.inf, f); r[[3, 400]] = np.nan; r[599] = -1e30; rows.append(r)
+    x = oracle.write_bf16(np.stack(rows).reshape(-1)).reshape(len(rows), vocab)
+    out = _dev_i32(np.zeros(len(rows)))
+    ctx.argmax(to_torch(x), len(rows), vocab, out)
+    torch.cuda.synchronize()
+    want = oracle.argmax_bf16(x, len(rows), vocab)
+    assert list(want) == [10, 450, 0, 0, 256, 599]
+    assert np.array_equal(out.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("llama3", [False, True])
+def test_rope_rows_bit_exact(ctx, llama3):
+    rng = np.random.default_rng(8)
+    heads, d = 8, 128
+    positions = np.array([0, 1, 4095, 17, 32760, 9], np.int32)
+    n = positions.size
+    xb = normal_bf16(rng, (n, heads, d))
+    params = (8.0, 1.0, 4.0, 8192.0) if llama3 else (1.0, 1.0, 2.0, 1.0)
+    out = torch.empty((n, heads, d), dtype=torch.int16, device="cuda")
+    ctx.rope_rows(to_torch(xb), out, n, heads, d, _dev_i32(positions), 500000.0, llama3, *params)
+    torch.cuda.synchronize()
+    got = from_torch(out).reshape(n, -1)
+    for t, pos in enumerate(positions):
+        want = oracle.rope_gpu(xb[t], 1, heads, d, int(pos), 500000.0, int(llama3), *params)
+        assert np.array_equal(got[t], want), (t, pos)
+
+
+def test_pages_append_matches_pages_write(ctx):
+    rng = np.random.default_rng(9)
+    kvh, d, pt, pps, batch = 4, 128, 16, 6, 5
+    pool_pages = batch * pps
+    table = rng.permutation(pool_pages).astype(np.int32).reshape(batch, pps)
+    positions = np.array([0, 15, 16, 95, 40], np.int32)
+    k_rows, v_rows = normal_bf16(rng, (batch, kvh, d)), normal_bf16(rng, (batch, kvh, d))
+    shape = (pool_pages, kvh, pt, d)
+    k_a = torch.zeros(shape, dtype=torch.int16, device="cuda")
+    v_a = torch.zeros(shape, dtype=torch.int16, device="cuda")
+    k_b, v_b = k_a.clone(), v_a.clone()
+    t_dev = _dev_i32(table)
+    ctx.pages_append(k_a, v_a, t_dev, pps, pt, kvh, d, batch, _dev_i32(positions), to_torch(k_rows),
+                     to_torch(v_rows))
+    for b in range(batch):
+        ctx.pages_write(k_b, v_b, t_dev[b], pt, kvh, d, int(positions[b]), 1, to_torch(k_rows[b]),
+                        to_torch(v_rows[b]))
+    torch.cuda.synchronize()
+    assert torch.equal(k_a, k_b) and torch.equal(v_a, v_b)
+    # a position outside the slot's pages writes nothing
+    k_c, v_c = k_a.clone(), v_a.clone()
+    ctx.pages_append(k_c, v_c, t_dev, pps, pt, kvh, d, 2, _dev_i32([pps * pt, -1]), to_torch(k_rows[:2]),
+                     to_torch(v_rows[:2]))
+    torch.cuda.synchronize()
+    assert torch.equal(k_c, k_a) and torch.equal(v_c, v_a)
+
+
+# ---- decoder runner ------------------------------------------------------------
+
+SPEC = Spec(layers=2, hidden=256, q_heads=8, kv_heads=2, head_dim=64, intermediate=512, vocab=1000)
+
+
+@pytest.fixture(scope="module")
+def tiny_model(ctx):
+    from mslim_attn.model import Model, ModelSpec
+
+    w = random_weights(SPEC, np.random.default_rng(20261201))
+    dev = {k: to_torch(v) for k, v in w.items()}
+    spec = ModelSpec(SPEC.layers, SPEC.hidden, SPEC.q_heads, SPEC.kv_heads, SPEC.head_dim,
+                     SPEC.intermediate, SPEC.vocab, SPEC.rms_eps, SPEC.rope_theta)
+    model = Model(ctx, spec, dev, max_batch=3, chunk_tokens=16, max_context=80)
+    yield w, model
+    model.close()
+
+
+def _check_logits(got_bits, want_bits, label):
+    m, r = logit_error(got_bits, want_bits)
+    assert m <= MODEL_LOGIT_MAX_ABS and r <= MODEL_LOGIT_REL2, f"{label}: max abs {m:.4f}, rel L2 {r:.2e}"
+
+
+def _margin(bits):
+    v = np.sort(oracle.read_bf16(bits).astype(np.float64))
+    return v[-1] - v[-2]
+
+
+def _check_token(got, want_bits, label):
+    want = int(oracle.argmax_bf16(want_bits, 1, SPEC.vocab)[0])
+    if _margin(want_bits) > 2 * MODEL_LOGIT_MAX_ABS:
+        assert got == want, f"{label}: token {got} != oracle {want}"
+
+
+def test_runner_one_token_prompts(tiny_model):
+    # A one-token history attends only to itself (attention output = V), so
+    # the only difference left is hipBLASLt's accumulation order, which now and
+    # then moves a projection output across a BF16 rounding boundary (the GEMM
+    # test bounds it against the f64 product).  Most prompts come out bit for
+    # bit (165 of 200 measured); the rest stay within half the model bounds.
+    w, model = tiny_model
+    ref = DecoderOracle(SPEC, w)
+    exact = 0
+    tokens = range(0, SPEC.vocab, 25)
+    for token in tokens:
+        got = model.prefill_only(0, [token])
+        want_logits, want = ref.prefill(0, [token])
+        got_logits = model.logits()[0]
+        exact += bool(np.array_equal(got_logits, want_logits))
+        m, r = logit_error(got_logits, want_logits)
+        assert m <= MODEL_LOGIT_MAX_ABS / 2 and r <= MODEL_LOGIT_REL2 / 2, (token, m, r)
+        _check_token(got, want_logits, f"one-token prompt {token}")
+    assert exact >= len(tokens) // 2, f"only {exact} of {len(tokens)} one-token prompts bit-exact"
+
+
+def test_runner_prefill_and_batched_decode_match_oracle(tiny_model):
+    w, model = tiny_model
+    ref = DecoderOracle(SPEC, w)
+    rng = np.random.default_rng(31)
+    # slot 0 spans three causal chunks (16 + 16 + 5), exercising the page gather
+    prompts = [list(rng.integers(0, SPEC.vocab, n)) for n in (37, 16, 1)]
+    tokens = []
+    for seq, prompt in enumerate(prompts):
+        tok = model.prefill_only(seq, prompt)
+        want_logits, _ = ref.prefill(seq, prompt)
+        _check_logits(model.logits()[0], want_logits, f"prefill slot {seq}")
+        _check_token(tok, want_logits, f"prefill slot {seq}")
+        assert model.position(seq) == len(prompt)
+        tokens.append(tok)
+    for step in range(6):
+        nxt = model.forward_batch(tokens)
+        got_logits = model.logits()
+        for seq in range(3):
+            want_logits, _ = ref.step(seq, tokens[seq])  # teacher-forced with the GPU token
+            _check_logits(got_logits[seq], want_logits, f"step {step} slot {seq}")
+            _check_token(nxt[seq], want_logits, f"step {step} slot {seq}")
+            assert model.position(seq) == len(prompts[seq]) + step + 1
+        tokens = nxt
+
+
+def test_runner_is_deterministic_and_digest_tracks_pages(tiny_model):
+    w, model = tiny_model
+    prompt = [5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18, 19, 20, 21, 22]
+    t1 = model.prefill_only(0, prompt)
+    l1 = model.logits().copy()
+    d1 = model.logical_kv_sha256(0)
+    n1 = model.forward_batch([t1])
+    l2a = model.logits().copy()
+    model.reset(0)
+    assert model.position(0) == 0
+    t2 = model.prefill_only(0, prompt)
+    assert t2 == t1 and np.array_equal(model.logits(), l1)
+    assert model.logical_kv_sha256(0) == d1
+    assert model.forward_batch([t2]) == n1 and np.array_equal(model.logits(), l2a)
+    assert model.logical_kv_sha256(0) != d1  # one more token in the digest
+    # the digest covers exactly the slot's tokens: a different slot differs
+    model.prefill_only(1, prompt[:5])
+    assert model.logical_kv_sha256(1) != model.logical_kv_sha256(0)
+
+
+def test_runner_generate_is_prefill_plus_steps(tiny_model):
+    w, model = tiny_model
+    prompt = [42, 7, 99, 3]
+    got = model.generate(prompt, 5)
+    assert len(got) == 5
+    first = model.prefill_only(0, prompt)
+    steps = [first]
+    for _ in range(4):
+        steps.append(model.forward_batch([steps[-1]])[0])
+    assert got == steps
+    # an EOS id stops before it is emitted
+    eos = got[2]
+    assert model.generate(prompt, 5, eos_ids=[eos]) == got[:got.index(eos)]
+
+
+def test_runner_rejects_bad_requests(tiny_model):
+    from mslim_attn import MslimAttnError
+
+    w, model = tiny_model
+    with pytest.raises(MslimAttnError, match="vocabulary"):
+        model.prefill_only(0, [SPEC.vocab])
+    with pytest.raises(MslimAttnError, match="empty"):
+        model.prefill_only(0, [])
+    with pytest.raises(MslimAttnError, match="capacity"):
+        model.prefill_only(0, list(range(80)))
+    with pytest.raises(MslimAttnError, match="slot"):
+        model.prefill_only(3, [1])
+    with pytest.raises(MslimAttnError, match="batch"):
+        model.forward_batch([1, 2, 3, 4])
+    with pytest.raises(MslimAttnError, match="capacity"):
+        model.generate([1] * 78, 5)

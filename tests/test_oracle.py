@@ -416,3 +416,117 @@ def test_matmul_bf16_pins():
            @ oracle.read_bf16(w).astype(np.float64).reshape(rows, inner).T).reshape(-1)
     ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(ref), 1e-30))) - 7)
     assert np.all(np.abs(out - ref) <= ulp)
+
+
+def test_add_bf16_pins():
+    # sums of small integers are exact; a + (-a) = +0; ties to even at the BF16 boundary
+    ints = np.arange(-64, 64, dtype=np.float32)
+    a, b = oracle.write_bf16(ints), oracle.write_bf16(ints[::-1] * np.float32(2))
+    assert np.array_equal(oracle.read_bf16(oracle.add_bf16(a, b)), ints + ints[::-1] * 2)
+    neg = oracle.write_bf16(-ints)
+    assert np.all(oracle.add_bf16(a, neg) == 0)  # +0 bits, not -0
+    one = oracle.write_bf16(np.float32([1.0, 1.0]))
+    small = oracle.write_bf16(np.float32([2.0 ** -8, 3 * 2.0 ** -8]))
+    got = oracle.read_bf16(oracle.add_bf16(one, small))
+    assert got[0] == 1.0 and got[1] == np.float32(1.0 + 2.0 ** -6)
+
+
+def test_argmax_bf16_pins():
+    rng = np.random.default_rng(3)
+    # distinct finite values: numpy.argmax is the answer
+    rows = np.stack([rng.permutation(np.arange(-300, 300, dtype=np.float32)) for _ in range(4)])
+    bits = oracle.write_bf16(rows.reshape(-1))
+    assert np.array_equal(oracle.argmax_bf16(bits, 4, 600), np.argmax(rows, axis=1))
+    # ties keep the first index; NaN never wins; all -inf or NaN gives 0
+    f = np.float32
+    cases = [([1, 5, 5, 2], 1), ([np.nan, 0, 3, 3], 2), ([-np.inf] * 4, 0),
+             ([np.nan] * 4, 0), ([-np.inf, np.nan, -1e30, -np.inf], 2), ([np.inf, np.inf, 1, 2], 0)]
+    for values, want in cases:
+        assert oracle.argmax_bf16(oracle.write_bf16(np.array(values, f)), 1, 4)[0] == want, values
+
+
+def _tiny_decoder(seed, **kw):
+    from oracle.decoder import DecoderOracle, Spec, random_weights
+    spec = Spec(**{**dict(layers=2, hidden=64, q_heads=4, kv_heads=2, head_dim=16,
+                         intermediate=96, vocab=80), **kw})
+    w = random_weights(spec, np.random.default_rng(seed))
+    return spec, w, DecoderOracle
+
+
+def test_decoder_oracle_zero_projections_is_embedding_head():
+    # every projection zero: each residual add leaves x = embedding, logits =
+    # lm_head . rmsnorm(embedding row)
+    spec, w, Decoder = _tiny_decoder(5)
+    for key in list(w):
+        if key.startswith("layers.") and not key.endswith("norm"):
+            w[key] = np.zeros_like(w[key])
+    dec = Decoder(spec, w)
+    prompt = [3, 17, 42]
+    logits, token = dec.prefill(0, prompt)
+    emb = w["embed"][prompt[-1]]
+    want = oracle.matmul_bf16(w["lm_head"], oracle.rmsnorm_gpu(emb, w["final_norm"], 1, spec.hidden, 1e-5),
+                              spec.hidden, spec.vocab, 1)
+    assert np.array_equal(logits, want)
+    assert token == int(oracle.argmax_bf16(want, 1, spec.vocab)[0])
+
+
+def test_decoder_oracle_single_token_attends_to_itself():
+    # a one-token prompt: attention output = V of the mapped kv head, so with
+    # Wo = I (hidden = q_heads*head_dim) and an all-zero MLP the first layer
+    # output is embedding + BF16(V row of head h // group)
+    spec, w, Decoder = _tiny_decoder(6, layers=1)
+    qd = spec.q_heads * spec.head_dim
+    w["layers.0.o"] = oracle.write_bf16(np.eye(spec.hidden, qd, dtype=np.float32))
+    for name in ("gate", "up", "down"):
+        w[f"layers.0.{name}"] = np.zeros_like(w[f"layers.0.{name}"])
+    dec = Decoder(spec, w)
+    dec.reset(0)
+    x = dec.hidden_rows(0, [9])[0]
+    emb = w["embed"][9]
+    h = oracle.rmsnorm_gpu(emb, w["layers.0.input_norm"], 1, spec.hidden, 1e-5)
+    v = oracle.matmul_bf16(w["layers.0.v"], h, spec.hidden, spec.kv_heads * spec.head_dim, 1)
+    group = spec.q_heads // spec.kv_heads
+    attn = np.concatenate([v[(hq // group) * spec.head_dim:(hq // group + 1) * spec.head_dim]
+                           for hq in range(spec.q_heads)])
+    assert np.array_equal(x, oracle.add_bf16(emb, attn))
+    assert np.array_equal(dec.sessions[0].values[0][0], v)
+
+
+def test_decoder_oracle_prefill_equals_token_steps():
+    # causal and row-independent: a prompt in one chunk and the same prompt
+    # token by token give bit-identical K/V caches and final logits (every
+    # stage works per row, and row i of the attention sees keys 0..i only)
+    spec, w, Decoder = _tiny_decoder(7)
+    prompt = [1, 2, 3, 4, 5, 6, 7]
+    a = Decoder(spec, w)
+    la, ta = a.prefill(0, prompt)
+    b = Decoder(spec, w)
+    b.reset(0)
+    for t in prompt:
+        lb, tb = b.step(0, t)
+    for l in range(spec.layers):
+        assert np.array_equal(a.sessions[0].keys[l], b.sessions[0].keys[l])
+        assert np.array_equal(a.sessions[0].values[l], b.sessions[0].values[l])
+    assert np.array_equal(la, lb) and ta == tb
+
+
+def test_model_logit_tolerance_separates_planted_mistakes():
+    # the runner's model-level tolerance must reject plausible wiring errors:
+    # each planted mistake moves the logits at least 4x beyond both bounds
+    from _data import MODEL_LOGIT_MAX_ABS, MODEL_LOGIT_REL2, logit_error
+    from oracle.decoder import DecoderOracle, Spec, random_weights
+    spec = Spec(layers=2, hidden=256, q_heads=8, kv_heads=2, head_dim=64, intermediate=512, vocab=1000)
+    w = random_weights(spec, np.random.default_rng(20261201))
+    prompt = list(np.random.default_rng(31).integers(0, spec.vocab, 37))
+    for mistake in ("rope", "gqa"):
+        good, bad = DecoderOracle(spec, w), DecoderOracle(spec, w)
+        bad.kv_head_reversed = mistake == "gqa"  # q head h attends kv head reversed(h // group)
+        lg, token = good.prefill(0, prompt)
+        lb, _ = bad.prefill(0, prompt)
+        bad.rope_shift = 1 if mistake == "rope" else 0  # decode steps rotate one position late
+        for _ in range(3):
+            lg, nxt = good.step(0, token)
+            lb, _ = bad.step(0, token)
+            m, r = logit_error(lb, lg)
+            assert m > 4 * MODEL_LOGIT_MAX_ABS and r > 4 * MODEL_LOGIT_REL2, (mistake, m, r)
+            token = nxt

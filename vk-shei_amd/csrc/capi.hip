@@ -534,9 +534,29 @@ int mslim_attn_rope(void *ctx, const void *input, void *output, int tokens, int 
     Lock lock(c);
     return check_hip(mslim::launch_rope(static_cast<const uint16_t *>(input),
                                         static_cast<uint16_t *>(output), tokens, heads, head_dim,
-                                        start_position, theta, llama3_scaling, factor,
+                                        start_position, nullptr, theta, llama3_scaling, factor,
                                         low_freq_factor, high_freq_factor, original_max_position,
                                         c.stream),
+                     "RoPE launch");
+}
+
+int mslim_attn_rope_rows(void *ctx, const void *input, void *output, int tokens, int heads, int head_dim,
+                         const int32_t *positions, float theta, int llama3_scaling, float factor,
+                         float low_freq_factor, float high_freq_factor, float original_max_position) {
+    g_error.clear();
+    if (!ctx || !input || !output || !positions || tokens < 1 || heads < 1 || head_dim < 2 ||
+        head_dim % 2 || !(theta > 0.0f) || !std::isfinite(theta))
+        return fail("invalid RoPE arguments");
+    if (output == input) return fail("RoPE output must not alias its input");
+    if (llama3_scaling && (!(factor > 0.0f) || !(high_freq_factor > low_freq_factor) ||
+                           !(low_freq_factor > 0.0f) || !(original_max_position > 0.0f)))
+        return fail("invalid llama3 RoPE scaling parameters");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    return check_hip(mslim::launch_rope(static_cast<const uint16_t *>(input),
+                                        static_cast<uint16_t *>(output), tokens, heads, head_dim, 0,
+                                        positions, theta, llama3_scaling, factor, low_freq_factor,
+                                        high_freq_factor, original_max_position, c.stream),
                      "RoPE launch");
 }
 
@@ -550,6 +570,37 @@ int mslim_attn_swiglu(void *ctx, const void *gate, const void *up, void *output,
                                           static_cast<const uint16_t *>(up),
                                           static_cast<uint16_t *>(output), n, c.stream),
                      "SwiGLU launch");
+}
+
+int mslim_attn_add(void *ctx, const void *a, const void *b, void *output, size_t n) {
+    g_error.clear();
+    if (!ctx || !a || !b || !output || !n) return fail("invalid residual add arguments");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    return check_hip(mslim::launch_add(static_cast<const uint16_t *>(a), static_cast<const uint16_t *>(b),
+                                       static_cast<uint16_t *>(output), n, c.stream),
+                     "residual add launch");
+}
+
+int mslim_attn_embed(void *ctx, const void *table, int vocab, int hidden, const int32_t *ids, int tokens,
+                     void *output, int *bad) {
+    g_error.clear();
+    if (!ctx || !table || !ids || !output || vocab < 1 || hidden < 8 || hidden % 8 || tokens < 1)
+        return fail("invalid embedding arguments (hidden must be a positive multiple of 8)");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    return check_hip(mslim::launch_embed(static_cast<const uint16_t *>(table), ids, tokens, hidden, vocab,
+                                         static_cast<uint16_t *>(output), bad, c.stream),
+                     "embedding launch");
+}
+
+int mslim_attn_argmax(void *ctx, const void *logits, int rows, int vocab, int32_t *out) {
+    g_error.clear();
+    if (!ctx || !logits || !out || rows < 1 || vocab < 1) return fail("invalid argmax arguments");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    return check_hip(mslim::launch_argmax(static_cast<const uint16_t *>(logits), rows, vocab, out, c.stream),
+                     "argmax launch");
 }
 
 int mslim_attn_pages_write(void *ctx, void *k_pool, void *v_pool, const int32_t *page_table,
@@ -568,6 +619,24 @@ int mslim_attn_pages_write(void *ctx, void *k_pool, void *v_pool, const int32_t 
                          static_cast<const uint16_t *>(k_rows), static_cast<const uint16_t *>(v_rows),
                          c.stream),
                      "page write launch");
+}
+
+int mslim_attn_pages_append(void *ctx, void *k_pool, void *v_pool, const int32_t *page_table,
+                            int pages_per_seq, int page_tokens, int kv_heads, int head_dim, int batch,
+                            const int32_t *positions, const void *k_rows, const void *v_rows) {
+    g_error.clear();
+    if (!ctx || !k_pool || !v_pool || !page_table || !positions || !k_rows || !v_rows || batch < 1 ||
+        pages_per_seq < 1 || kv_heads < 1 || head_dim < 8 || head_dim % 8 || !is_pow2(page_tokens) ||
+        page_tokens < 16)
+        return fail("invalid page append arguments");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    return check_hip(mslim::launch_pages_append(
+                         static_cast<uint16_t *>(k_pool), static_cast<uint16_t *>(v_pool), page_table,
+                         pages_per_seq, page_tokens, kv_heads, head_dim, batch, positions,
+                         static_cast<const uint16_t *>(k_rows), static_cast<const uint16_t *>(v_rows),
+                         c.stream),
+                     "page append launch");
 }
 
 int mslim_attn_pages_gather(void *ctx, const void *pool, const int32_t *page_table, int page_tokens,

@@ -69,9 +69,12 @@ __device__ float rope_inverse_frequency(int fd, int head_dim, float theta, int l
 }
 
 // llm_rope / llm_prefill_rope (gpu_llm.cl:102-146, :412-456): one lane per
-// element, rotate-half partner, c and s rounded to BF16.
+// element, rotate-half partner, c and s rounded to BF16.  Row t sits at
+// position start + t, or at positions[t] when a position array is given (one
+// decode row per sequence of a batch).
 __global__ __launch_bounds__(256) void rope_kernel(const uint16_t *in, uint16_t *out, int64_t total,
-                                                   int heads, int head_dim, int start, float theta,
+                                                   int heads, int head_dim, int start,
+                                                   const int32_t *positions, float theta,
                                                    int llama3, float factor, float low, float high,
                                                    float original_max) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -87,7 +90,8 @@ __global__ __launch_bounds__(256) void rope_kernel(const uint16_t *in, uint16_t 
     const float rotated = d < half ? -partner : partner;
     const int fd = (d % half) * 2;
     const float inv = rope_inverse_frequency(fd, head_dim, theta, llama3, factor, low, high, original_max);
-    const float phase = __fmul_rn((float)(start + token), inv);
+    const int64_t position = positions ? (int64_t)positions[token] : start + token;
+    const float phase = __fmul_rn((float)position, inv);
     const float cs = round_bf16((float)cos((double)phase));
     const float sn = round_bf16((float)sin((double)phase));
     const float left = round_bf16(__fmul_rn(read_bf16(in[i]), cs));
@@ -106,6 +110,65 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t *gate, const
     out[i] = write_bf16(__fmul_rn(round_bf16(activated), read_bf16(up[i])));
 }
 
+// Residual add with one BF16 rounding (llm_add, gpu_llm.cl:214-222).
+__global__ __launch_bounds__(256) void add_kernel(const uint16_t *a, const uint16_t *b, uint16_t *out,
+                                                  int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = write_bf16(__fadd_rn(read_bf16(a[i]), read_bf16(b[i])));
+}
+
+// Embedding rows of `tokens` ids (llm_embed, gpu_llm.cl:24-33), 16 bytes per
+// lane.  Ids out of range write zeros and set *bad when bad is given.
+__global__ __launch_bounds__(256) void embed_kernel(const uint16_t *table, const int32_t *ids, int tokens,
+                                                    int hidden, int vocab, uint16_t *out, int *bad) {
+    const int chunks = hidden / 8;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)tokens * chunks) return;
+    const int t = (int)(i / chunks), c = (int)(i % chunks);
+    const int id = ids[t];
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (id >= 0 && id < vocab) v = *reinterpret_cast<const uint4 *>(table + (int64_t)id * hidden + c * 8);
+    else if (c == 0 && bad) *bad = 1;
+    *reinterpret_cast<uint4 *>(out + (int64_t)t * hidden + c * 8) = v;
+}
+
+// Greedy token of each row of BF16 logits (llm_argmax, gpu_llm.cl:239-270),
+// one workgroup of 256 per row.  Every lane starts from (-inf, index 0) and
+// takes a value that is greater, or equal with a lower index: NaN never wins,
+// the first index wins ties, and a row with nothing above -inf gives 0.  The
+// result is the same for any lane count.
+__global__ __launch_bounds__(256) void argmax_kernel(const uint16_t *logits, int rows, int vocab, int32_t *out) {
+    __shared__ float values[256];
+    __shared__ int indices[256];
+    const int row = blockIdx.x;
+    const int tid = threadIdx.x;
+    const uint16_t *l = logits + (int64_t)row * vocab;
+    float best = -INFINITY;
+    int index = 0;
+    for (int i = tid; i < vocab; i += 256) {
+        const float x = read_bf16(l[i]);
+        if (x > best || (x == best && i < index)) {
+            best = x;
+            index = i;
+        }
+    }
+    values[tid] = best;
+    indices[tid] = index;
+    __syncthreads();
+    for (int stride = 128; stride > 0; stride >>= 1) {
+        if (tid < stride) {
+            const float ov = values[tid + stride];
+            const int oi = indices[tid + stride];
+            if (ov > values[tid] || (ov == values[tid] && oi < indices[tid])) {
+                values[tid] = ov;
+                indices[tid] = oi;
+            }
+        }
+        __syncthreads();
+    }
+    if (tid == 0) out[row] = indices[0];
+}
+
 }  // namespace
 
 hipError_t launch_rmsnorm(const uint16_t *in, const uint16_t *w, uint16_t *out, int tokens,
@@ -116,12 +179,12 @@ hipError_t launch_rmsnorm(const uint16_t *in, const uint16_t *w, uint16_t *out, 
 }
 
 hipError_t launch_rope(const uint16_t *in, uint16_t *out, int tokens, int heads, int head_dim,
-                       int start, float theta, int llama3, float factor, float low, float high,
-                       float original_max, hipStream_t stream) {
+                       int start, const int32_t *positions, float theta, int llama3, float factor,
+                       float low, float high, float original_max, hipStream_t stream) {
     const int64_t total = (int64_t)tokens * heads * head_dim;
     const unsigned blocks = (unsigned)((total + 255) / 256);
     hipLaunchKernelGGL(rope_kernel, dim3(blocks), dim3(256), 0, stream, in, out, total, heads, head_dim,
-                       start, theta, llama3, factor, low, high, original_max);
+                       start, positions, theta, llama3, factor, low, high, original_max);
     return hipGetLastError();
 }
 
@@ -129,6 +192,24 @@ hipError_t launch_swiglu(const uint16_t *gate, const uint16_t *up, uint16_t *out
                          hipStream_t stream) {
     const unsigned blocks = (unsigned)((n + 255) / 256);
     hipLaunchKernelGGL(swiglu_kernel, dim3(blocks), dim3(256), 0, stream, gate, up, out, (int64_t)n);
+    return hipGetLastError();
+}
+
+hipError_t launch_add(const uint16_t *a, const uint16_t *b, uint16_t *out, size_t n, hipStream_t stream) {
+    hipLaunchKernelGGL(add_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, a, b, out, (int64_t)n);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed(const uint16_t *table, const int32_t *ids, int tokens, int hidden, int vocab,
+                        uint16_t *out, int *bad, hipStream_t stream) {
+    const int64_t work = (int64_t)tokens * (hidden / 8);
+    hipLaunchKernelGGL(embed_kernel, dim3((unsigned)((work + 255) / 256)), dim3(256), 0, stream, table, ids, tokens,
+                       hidden, vocab, out, bad);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax(const uint16_t *logits, int rows, int vocab, int32_t *out, hipStream_t stream) {
+    hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)rows), dim3(256), 0, stream, logits, rows, vocab, out);
     return hipGetLastError();
 }
 

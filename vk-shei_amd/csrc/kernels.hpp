@@ -72,11 +72,16 @@ hipError_t launch_frames_decode(const FramesLaunch &l, hipStream_t stream);
 
 hipError_t launch_rmsnorm(const uint16_t *in, const uint16_t *w, uint16_t *out, int tokens,
                           int hidden, float eps, hipStream_t stream);
+// Row t at position start + t, or positions[t] (device int32) when not null.
 hipError_t launch_rope(const uint16_t *in, uint16_t *out, int tokens, int heads, int head_dim,
-                       int start, float theta, int llama3, float factor, float low, float high,
-                       float original_max, hipStream_t stream);
+                       int start, const int32_t *positions, float theta, int llama3, float factor,
+                       float low, float high, float original_max, hipStream_t stream);
 hipError_t launch_swiglu(const uint16_t *gate, const uint16_t *up, uint16_t *out, size_t n,
                          hipStream_t stream);
+hipError_t launch_add(const uint16_t *a, const uint16_t *b, uint16_t *out, size_t n, hipStream_t stream);
+hipError_t launch_embed(const uint16_t *table, const int32_t *ids, int tokens, int hidden, int vocab,
+                        uint16_t *out, int *bad, hipStream_t stream);
+hipError_t launch_argmax(const uint16_t *logits, int rows, int vocab, int32_t *out, hipStream_t stream);
 
 // ColdStore record frames of pool pages (record header, token-hash tables
 // and footer; the payloads stay in the pool).
@@ -127,6 +132,13 @@ hipError_t launch_pages_write(uint16_t *k_pool, uint16_t *v_pool, const int32_t 
                               int page_tokens, int kv_heads, int head_dim, int64_t first_token,
                               int64_t tokens, const uint16_t *k_rows, const uint16_t *v_rows,
                               hipStream_t stream);
+// One token per sequence of a batch: row b goes to position positions[b]
+// (device int32) through page-table row b; positions outside
+// [0, pages_per_seq * page_tokens) are skipped.
+hipError_t launch_pages_append(uint16_t *k_pool, uint16_t *v_pool, const int32_t *page_table,
+                               int pages_per_seq, int page_tokens, int kv_heads, int head_dim,
+                               int batch, const int32_t *positions, const uint16_t *k_rows,
+                               const uint16_t *v_rows, hipStream_t stream);
 hipError_t launch_pages_gather(const uint16_t *pool, const int32_t *page_table, int page_tokens,
                                int kv_heads, int head_dim, int64_t first_token, int64_t tokens,
                                uint16_t *rows_out, hipStream_t stream);

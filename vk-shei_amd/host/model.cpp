@@ -1,0 +1,449 @@
+// Decoder runner over the C ABI: see model.hpp for the layer order.
+#include "model.hpp"
+
+#include <climits>
+#include <cmath>
+#include <cstring>
+
+#include "../../include/mslim_model.h"
+
+namespace mslim {
+namespace model {
+
+void ModelSpec::validate() const {
+    ensure(layers > 0 && hidden > 0 && intermediate > 0 && vocab > 0, "model dimensions must be positive");
+    ensure(q_heads > 0 && kv_heads > 0 && q_heads % kv_heads == 0, "query heads must be a multiple of kv heads");
+    ensure(head_dim >= 8 && head_dim <= 256 && head_dim % 8 == 0, "head_dim must be a multiple of 8 up to 256");
+    ensure(hidden % 8 == 0, "hidden size must be a multiple of 8");
+    ensure(hidden <= 32768 && intermediate <= 32768 && (int64_t)q_heads * head_dim <= 32768,
+           "projection inner dimension above 32768");
+    ensure(rms_eps > 0.0f && std::isfinite(rms_eps), "rms_norm_eps must be positive");
+    ensure(rope_theta > 0.0f && std::isfinite(rope_theta), "rope_theta must be positive");
+    if (llama3)
+        ensure(rope_factor > 0.0f && rope_low > 0.0f && rope_high > rope_low && rope_original_max > 0.0f,
+               "invalid llama3 RoPE scaling");
+}
+
+DecoderRunner::DecoderRunner(std::shared_ptr<NativeContext> ctx, ModelSpec spec, ModelWeights weights,
+                             int max_batch, int chunk_tokens, int max_context)
+    : ctx_(std::move(ctx)), spec_(spec), w_(std::move(weights)), max_batch_(max_batch),
+      chunk_tokens_(chunk_tokens), max_context_(max_context) {
+    ensure(ctx_ != nullptr, "no device context");
+    spec_.validate();
+    ensure((int)w_.layers.size() == spec_.layers, "layer weight count does not match the model");
+    ensure(w_.embed && w_.final_norm && w_.lm_head, "embedding, final norm and LM head weights are required");
+    for (const auto &l : w_.layers)
+        ensure(l.input_norm && l.q && l.k && l.v && l.o && l.post_norm && l.gate && l.up && l.down,
+               "every layer needs all nine weight tensors");
+    ensure(max_batch_ >= 1 && max_batch_ <= MSLIM_ATTN_MAX_BATCH, "max_batch must be 1..=64");
+    ensure(chunk_tokens_ >= 1 && chunk_tokens_ <= 512, "prefill chunk must be 1..=512 tokens");
+    ensure(max_context_ >= 1 && max_context_ <= (1 << 24), "max_context must be 1..=16777216 tokens");
+    pages_per_seq_ = (max_context_ + kPageTokens - 1) / kPageTokens;
+    rows_cap_ = std::max(max_batch_, chunk_tokens_);
+    scale_ = (float)(1.0 / std::sqrt((double)spec_.head_dim));
+    positions_.assign(max_batch_, 0);
+
+    const size_t kvd = (size_t)spec_.kv_heads * spec_.head_dim, qd = (size_t)spec_.q_heads * spec_.head_dim;
+    const size_t pool_pages = (size_t)max_batch_ * pages_per_seq_;
+    try {
+        for (int l = 0; l < spec_.layers; ++l) {
+            k_pools_.push_back(alloc(pool_pages * kPageTokens * kvd * 2));
+            v_pools_.push_back(alloc(pool_pages * kPageTokens * kvd * 2));
+        }
+        // Slot s, logical page p -> physical page p * max_batch + s: the
+        // slots interleave in the pool, so every read goes through the table.
+        std::vector<int32_t> table(pool_pages);
+        for (int s = 0; s < max_batch_; ++s)
+            for (int p = 0; p < pages_per_seq_; ++p)
+                table[(size_t)s * pages_per_seq_ + p] = (int32_t)((size_t)p * max_batch_ + s);
+        table_ = static_cast<int32_t *>(alloc(table.size() * 4));
+        ctx_->check("upload page table", mslim_attn_buf_write(ctx_->handle(), table_, 0,
+                                                              reinterpret_cast<const uint8_t *>(table.data()),
+                                                              table.size() * 4));
+        const size_t r = rows_cap_;
+        ids_ = static_cast<int32_t *>(alloc(r * 4));
+        pos_ = static_cast<int32_t *>(alloc(r * 4));
+        next_ = static_cast<int32_t *>(alloc(r * 4));
+        x_ = static_cast<uint16_t *>(alloc(r * spec_.hidden * 2));
+        norm_ = static_cast<uint16_t *>(alloc(r * spec_.hidden * 2));
+        q_ = static_cast<uint16_t *>(alloc(r * qd * 2));
+        qr_ = static_cast<uint16_t *>(alloc(r * qd * 2));
+        attn_ = static_cast<uint16_t *>(alloc(r * qd * 2));
+        k_ = static_cast<uint16_t *>(alloc(r * kvd * 2));
+        kr_ = static_cast<uint16_t *>(alloc(r * kvd * 2));
+        v_ = static_cast<uint16_t *>(alloc(r * kvd * 2));
+        proj_ = static_cast<uint16_t *>(alloc(r * spec_.hidden * 2));
+        gate_ = static_cast<uint16_t *>(alloc(r * spec_.intermediate * 2));
+        up_ = static_cast<uint16_t *>(alloc(r * spec_.intermediate * 2));
+        act_ = static_cast<uint16_t *>(alloc(r * spec_.intermediate * 2));
+        kd_ = static_cast<uint16_t *>(alloc((size_t)max_context_ * kvd * 2));
+        vd_ = static_cast<uint16_t *>(alloc((size_t)max_context_ * kvd * 2));
+        logits_ = static_cast<uint16_t *>(alloc((size_t)max_batch_ * spec_.vocab * 2));
+    } catch (...) {
+        for (void *p : owned_) mslim_attn_buf_free(ctx_->handle(), p);
+        throw;
+    }
+}
+
+DecoderRunner::~DecoderRunner() {
+    for (void *p : owned_) mslim_attn_buf_free(ctx_->handle(), p);
+}
+
+void *DecoderRunner::alloc(size_t bytes) {
+    void *p = mslim_attn_buf_alloc(ctx_->handle(), bytes ? bytes : 1);
+    if (!p) throw NativeError("allocate runner buffer", 0, mslim_attn_last_error());
+    owned_.push_back(p);
+    return p;
+}
+
+void DecoderRunner::gemm(const void *w, const void *in, void *out, int inner, int rows, int tokens) {
+    ctx_->check("projection", mslim_attn_gemm_bf16(ctx_->handle(), w, in, out, inner, rows, tokens));
+}
+
+// Final norm, LM head and greedy token of `rows` hidden rows.
+void DecoderRunner::head(const uint16_t *rows_in, int rows) {
+    void *h = ctx_->handle();
+    ctx_->check("final norm", mslim_attn_rmsnorm(h, rows_in, w_.final_norm, norm_, rows, spec_.hidden,
+                                                 spec_.rms_eps));
+    gemm(w_.lm_head, norm_, logits_, spec_.hidden, spec_.vocab, rows);
+    ctx_->check("argmax", mslim_attn_argmax(h, logits_, rows, spec_.vocab, next_));
+    logits_rows_ = rows;
+}
+
+// One causal chunk of slot `seq`: tokens ids[0..n) at positions prior..prior+n
+// (run_batch_layer, prefill.rs:897-1061, for every layer).
+void DecoderRunner::chunk(int seq, const int32_t *ids, int n, int64_t prior) {
+    void *h = ctx_->handle();
+    const ModelSpec &s = spec_;
+    const int qd = s.q_heads * s.head_dim, kvd = s.kv_heads * s.head_dim;
+    ctx_->check("upload token ids", mslim_attn_buf_write(h, ids_, 0, reinterpret_cast<const uint8_t *>(ids),
+                                                         (size_t)n * 4));
+    ctx_->check("embed", mslim_attn_embed(h, w_.embed, s.vocab, s.hidden, ids_, n, x_, nullptr));
+    for (int l = 0; l < s.layers; ++l) {
+        const LayerWeights &w = w_.layers[l];
+        ctx_->check("input norm", mslim_attn_rmsnorm(h, x_, w.input_norm, norm_, n, s.hidden, s.rms_eps));
+        gemm(w.q, norm_, q_, s.hidden, qd, n);
+        gemm(w.k, norm_, k_, s.hidden, kvd, n);
+        gemm(w.v, norm_, v_, s.hidden, kvd, n);
+        ctx_->check("query RoPE", mslim_attn_rope(h, q_, qr_, n, s.q_heads, s.head_dim, (int)prior, s.rope_theta,
+                                                  s.llama3, s.rope_factor, s.rope_low, s.rope_high,
+                                                  s.rope_original_max));
+        ctx_->check("key RoPE", mslim_attn_rope(h, k_, kr_, n, s.kv_heads, s.head_dim, (int)prior, s.rope_theta,
+                                                s.llama3, s.rope_factor, s.rope_low, s.rope_high,
+                                                s.rope_original_max));
+        ctx_->check("page write", mslim_attn_pages_write(h, k_pools_[l], v_pools_[l], table_row(seq), kPageTokens,
+                                                         s.kv_heads, s.head_dim, prior, n, kr_, v_));
+        const void *keys = kr_, *values = v_;
+        if (prior > 0) {
+            // Earlier chunks live only in the pages: gather the slot's whole
+            // history token-major for the causal kernel.
+            ctx_->check("gather keys", mslim_attn_pages_gather(h, k_pools_[l], table_row(seq), kPageTokens,
+                                                               s.kv_heads, s.head_dim, 0, prior + n, kd_));
+            ctx_->check("gather values", mslim_attn_pages_gather(h, v_pools_[l], table_row(seq), kPageTokens,
+                                                                 s.kv_heads, s.head_dim, 0, prior + n, vd_));
+            keys = kd_;
+            values = vd_;
+        }
+        ctx_->check("causal attention", mslim_attn_prefill_causal(h, qr_, keys, values, attn_, n, (int)prior,
+                                                                  s.q_heads, s.kv_heads, s.head_dim, scale_));
+        gemm(w.o, attn_, proj_, qd, s.hidden, n);
+        ctx_->check("attention residual", mslim_attn_add(h, x_, proj_, x_, (size_t)n * s.hidden));
+        ctx_->check("post norm", mslim_attn_rmsnorm(h, x_, w.post_norm, norm_, n, s.hidden, s.rms_eps));
+        gemm(w.gate, norm_, gate_, s.hidden, s.intermediate, n);
+        gemm(w.up, norm_, up_, s.hidden, s.intermediate, n);
+        ctx_->check("swiglu", mslim_attn_swiglu(h, gate_, up_, act_, (size_t)n * s.intermediate));
+        gemm(w.down, act_, proj_, s.intermediate, s.hidden, n);
+        ctx_->check("mlp residual", mslim_attn_add(h, x_, proj_, x_, (size_t)n * s.hidden));
+    }
+}
+
+Step DecoderRunner::prefill_only(int seq, const std::vector<int32_t> &prompt) {
+    ensure(seq >= 0 && seq < max_batch_, "sequence slot out of range");
+    ensure(!prompt.empty(), "GPU prompt IDs empty");
+    ensure(prompt.size() < (size_t)max_context_, "GPU context capacity not large enough for prompt");
+    for (int32_t id : prompt) ensure(id >= 0 && id < spec_.vocab, "token id outside the vocabulary");
+    std::lock_guard<std::mutex> lock(ctx_->mutex());
+    positions_[seq] = 0;
+    const int n_total = (int)prompt.size();
+    for (int start = 0; start < n_total; start += chunk_tokens_) {
+        const int n = std::min(chunk_tokens_, n_total - start);
+        chunk(seq, prompt.data() + start, n, start);
+        if (start + n == n_total) head(x_ + (size_t)(n - 1) * spec_.hidden, 1);
+    }
+    positions_[seq] = n_total;
+    int32_t next = 0;
+    ctx_->check("read greedy token", mslim_attn_buf_read(ctx_->handle(), next_, 0,
+                                                         reinterpret_cast<uint8_t *>(&next), 4));
+    return Step{next, n_total};
+}
+
+std::vector<Step> DecoderRunner::forward_batch(const std::vector<int32_t> &tokens) {
+    const int b = (int)tokens.size();
+    ensure(b >= 1 && b <= max_batch_, "decode batch must be 1..=max_batch slots");
+    for (int32_t id : tokens) ensure(id >= 0 && id < spec_.vocab, "token id outside the vocabulary");
+    std::vector<int32_t> pos(b), lens(b);
+    for (int i = 0; i < b; ++i) {
+        ensure(positions_[i] < max_context_, "GPU KV capacity exceeded: configure larger --max-context-tokens");
+        pos[i] = (int32_t)positions_[i];
+        lens[i] = pos[i] + 1;
+    }
+    std::lock_guard<std::mutex> lock(ctx_->mutex());
+    void *h = ctx_->handle();
+    const ModelSpec &s = spec_;
+    const int qd = s.q_heads * s.head_dim, kvd = s.kv_heads * s.head_dim;
+    ctx_->check("upload token ids", mslim_attn_buf_write(h, ids_, 0, reinterpret_cast<const uint8_t *>(tokens.data()),
+                                                         (size_t)b * 4));
+    ctx_->check("upload positions", mslim_attn_buf_write(h, pos_, 0, reinterpret_cast<const uint8_t *>(pos.data()),
+                                                         (size_t)b * 4));
+    ctx_->check("embed", mslim_attn_embed(h, w_.embed, s.vocab, s.hidden, ids_, b, x_, nullptr));
+    for (int l = 0; l < s.layers; ++l) {
+        const LayerWeights &w = w_.layers[l];
+        ctx_->check("input norm", mslim_attn_rmsnorm(h, x_, w.input_norm, norm_, b, s.hidden, s.rms_eps));
+        gemm(w.q, norm_, q_, s.hidden, qd, b);
+        gemm(w.k, norm_, k_, s.hidden, kvd, b);
+        gemm(w.v, norm_, v_, s.hidden, kvd, b);
+        ctx_->check("query RoPE", mslim_attn_rope_rows(h, q_, qr_, b, s.q_heads, s.head_dim, pos_, s.rope_theta,
+                                                       s.llama3, s.rope_factor, s.rope_low, s.rope_high,
+                                                       s.rope_original_max));
+        ctx_->check("key RoPE", mslim_attn_rope_rows(h, k_, kr_, b, s.kv_heads, s.head_dim, pos_, s.rope_theta,
+                                                     s.llama3, s.rope_factor, s.rope_low, s.rope_high,
+                                                     s.rope_original_max));
+        ctx_->check("page append", mslim_attn_pages_append(h, k_pools_[l], v_pools_[l], table_, pages_per_seq_,
+                                                           kPageTokens, s.kv_heads, s.head_dim, b, pos_, kr_, v_));
+        ctx_->check("paged attention",
+                    mslim_attn_decode_paged(h, qr_, k_pools_[l], v_pools_[l], attn_, b, lens.data(), table_,
+                                            pages_per_seq_, kPageTokens, s.q_heads, s.kv_heads, s.head_dim,
+                                            scale_, 0));
+        gemm(w.o, attn_, proj_, qd, s.hidden, b);
+        ctx_->check("attention residual", mslim_attn_add(h, x_, proj_, x_, (size_t)b * s.hidden));
+        ctx_->check("post norm", mslim_attn_rmsnorm(h, x_, w.post_norm, norm_, b, s.hidden, s.rms_eps));
+        gemm(w.gate, norm_, gate_, s.hidden, s.intermediate, b);
+        gemm(w.up, norm_, up_, s.hidden, s.intermediate, b);
+        ctx_->check("swiglu", mslim_attn_swiglu(h, gate_, up_, act_, (size_t)b * s.intermediate));
+        gemm(w.down, act_, proj_, s.intermediate, s.hidden, b);
+        ctx_->check("mlp residual", mslim_attn_add(h, x_, proj_, x_, (size_t)b * s.hidden));
+    }
+    head(x_, b);
+    std::vector<int32_t> next(b);
+    ctx_->check("read greedy tokens", mslim_attn_buf_read(h, next_, 0, reinterpret_cast<uint8_t *>(next.data()),
+                                                          (size_t)b * 4));
+    std::vector<Step> steps(b);
+    for (int i = 0; i < b; ++i) {
+        positions_[i] += 1;
+        steps[i] = Step{next[i], positions_[i]};
+    }
+    return steps;
+}
+
+std::vector<int32_t> DecoderRunner::generate(int seq, const std::vector<int32_t> &prompt, int max_new,
+                                             const std::vector<int32_t> &eos_ids) {
+    ensure(max_new > 0, "max_new_tokens must be positive");
+    ensure(prompt.size() + (size_t)max_new <= (size_t)max_context_,
+           "GPU context capacity not large enough for prompt + generation");
+    ensure(seq == 0, "generate drives slot 0; use forward_batch for several slots");
+    Step current = prefill_only(seq, prompt);
+    std::vector<int32_t> generated;
+    for (int step = 0; step < max_new; ++step) {
+        const int32_t token = current.argmax_token;
+        bool eos = false;
+        for (int32_t e : eos_ids) eos = eos || e == token;
+        if (eos) break;
+        generated.push_back(token);
+        if (step + 1 < max_new) current = forward_batch({token})[0];
+    }
+    return generated;
+}
+
+void DecoderRunner::reset(int seq) {
+    ensure(seq >= 0 && seq < max_batch_, "sequence slot out of range");
+    positions_[seq] = 0;
+}
+
+std::vector<uint16_t> DecoderRunner::last_logits() const {
+    std::vector<uint16_t> out((size_t)logits_rows_ * spec_.vocab);
+    if (!out.empty())
+        ctx_->check("read logits", mslim_attn_buf_read(ctx_->handle(), logits_, 0,
+                                                       reinterpret_cast<uint8_t *>(out.data()), out.size() * 2));
+    return out;
+}
+
+std::string DecoderRunner::logical_kv_sha256(int seq) const {
+    ensure(seq >= 0 && seq < max_batch_, "sequence slot out of range");
+    std::vector<const int32_t *> tables(spec_.layers, table_row(seq));
+    std::vector<const void *> keys(k_pools_.begin(), k_pools_.end()), values(v_pools_.begin(), v_pools_.end());
+    char hex[65] = {0};
+    ctx_->check("logical K/V digest",
+                mslim_attn_logical_kv_sha256(ctx_->handle(), spec_.layers, positions_[seq], spec_.kv_heads,
+                                             spec_.head_dim, keys.data(), values.data(), tables.data(),
+                                             kPageTokens, hex));
+    return std::string(hex);
+}
+
+}  // namespace model
+}  // namespace mslim
+
+// ---- C API ------------------------------------------------------------------
+
+namespace {
+
+thread_local std::string g_model_error;
+
+int model_fail(const std::exception &e) {
+    g_model_error = e.what();
+    return -1;
+}
+
+struct ModelHandle {
+    std::unique_ptr<mslim::model::DecoderRunner> runner;
+};
+
+mslim::model::DecoderRunner &runner_of(void *m) {
+    mslim::ensure(m != nullptr, "null model handle");
+    return *static_cast<ModelHandle *>(m)->runner;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *mslim_model_last_error(void) { return g_model_error.c_str(); }
+
+void *mslim_model_new(void *attn_ctx, const mslim_model_spec *spec, const void *const *weights, int max_batch,
+                      int chunk_tokens, int max_context) {
+    g_model_error.clear();
+    try {
+        mslim::ensure(attn_ctx && spec && weights, "null model arguments");
+        mslim::model::ModelSpec s;
+        s.layers = spec->layers;
+        s.hidden = spec->hidden;
+        s.q_heads = spec->q_heads;
+        s.kv_heads = spec->kv_heads;
+        s.head_dim = spec->head_dim;
+        s.intermediate = spec->intermediate;
+        s.vocab = spec->vocab;
+        s.rms_eps = spec->rms_eps;
+        s.rope_theta = spec->rope_theta;
+        s.llama3 = spec->llama3_scaling;
+        s.rope_factor = spec->rope_factor;
+        s.rope_low = spec->rope_low_freq_factor;
+        s.rope_high = spec->rope_high_freq_factor;
+        s.rope_original_max = spec->rope_original_max_position;
+        mslim::ensure(s.layers > 0 && s.layers <= 4096, "layer count must be 1..=4096");
+        mslim::model::ModelWeights w;
+        w.embed = weights[0];
+        w.final_norm = weights[1];
+        w.lm_head = weights[2];
+        for (int l = 0; l < s.layers; ++l) {
+            const void *const *p = weights + 3 + (size_t)l * MSLIM_MODEL_LAYER_TENSORS;
+            mslim::model::LayerWeights lw;
+            lw.input_norm = p[0];
+            lw.q = p[1];
+            lw.k = p[2];
+            lw.v = p[3];
+            lw.o = p[4];
+            lw.post_norm = p[5];
+            lw.gate = p[6];
+            lw.up = p[7];
+            lw.down = p[8];
+            w.layers.push_back(lw);
+        }
+        auto handle = std::make_unique<ModelHandle>();
+        handle->runner = std::make_unique<mslim::model::DecoderRunner>(
+            mslim::NativeContext::borrow(attn_ctx), s, std::move(w), max_batch, chunk_tokens, max_context);
+        return handle.release();
+    } catch (const std::exception &e) {
+        model_fail(e);
+        return nullptr;
+    }
+}
+
+void mslim_model_destroy(void *model) { delete static_cast<ModelHandle *>(model); }
+
+int mslim_model_prefill(void *model, int seq, const int32_t *prompt, int tokens, int32_t *next_token) {
+    g_model_error.clear();
+    try {
+        mslim::ensure(next_token && tokens >= 0 && (prompt || !tokens), "invalid prefill arguments");
+        const std::vector<int32_t> ids = tokens ? std::vector<int32_t>(prompt, prompt + tokens) : std::vector<int32_t>();
+        *next_token = runner_of(model).prefill_only(seq, ids).argmax_token;
+        return 0;
+    } catch (const std::exception &e) {
+        return model_fail(e);
+    }
+}
+
+int mslim_model_forward_batch(void *model, const int32_t *tokens, int batch, int32_t *next_tokens) {
+    g_model_error.clear();
+    try {
+        mslim::ensure(tokens && batch > 0 && next_tokens, "invalid forward arguments");
+        const auto steps = runner_of(model).forward_batch(std::vector<int32_t>(tokens, tokens + batch));
+        for (int i = 0; i < batch; ++i) next_tokens[i] = steps[i].argmax_token;
+        return 0;
+    } catch (const std::exception &e) {
+        return model_fail(e);
+    }
+}
+
+int mslim_model_generate(void *model, const int32_t *prompt, int tokens, int max_new, const int32_t *eos_ids,
+                         int eos_count, int32_t *out, int *generated) {
+    g_model_error.clear();
+    try {
+        mslim::ensure(prompt && tokens > 0 && out && generated && eos_count >= 0 && (eos_ids || !eos_count),
+                      "invalid generate arguments");
+        const auto got = runner_of(model).generate(0, std::vector<int32_t>(prompt, prompt + tokens), max_new,
+                                                   std::vector<int32_t>(eos_ids, eos_ids + eos_count));
+        std::memcpy(out, got.data(), got.size() * 4);
+        *generated = (int)got.size();
+        return 0;
+    } catch (const std::exception &e) {
+        return model_fail(e);
+    }
+}
+
+int64_t mslim_model_position(void *model, int seq) {
+    g_model_error.clear();
+    try {
+        return runner_of(model).position(seq);
+    } catch (const std::exception &e) {
+        model_fail(e);
+        return -1;
+    }
+}
+
+int mslim_model_reset(void *model, int seq) {
+    g_model_error.clear();
+    try {
+        runner_of(model).reset(seq);
+        return 0;
+    } catch (const std::exception &e) {
+        return model_fail(e);
+    }
+}
+
+int mslim_model_logits(void *model, uint16_t *out, size_t capacity, int *rows) {
+    g_model_error.clear();
+    try {
+        mslim::ensure(out && rows, "invalid logits arguments");
+        auto &r = runner_of(model);
+        const auto l = r.last_logits();
+        mslim::ensure(l.size() <= capacity, "logits buffer too small");
+        std::memcpy(out, l.data(), l.size() * 2);
+        *rows = (int)(l.size() / r.spec().vocab);
+        return 0;
+    } catch (const std::exception &e) {
+        return model_fail(e);
+    }
+}
+
+int mslim_model_logical_kv_sha256(void *model, int seq, char *hex_out) {
+    g_model_error.clear();
+    try {
+        mslim::ensure(hex_out != nullptr, "null digest buffer");
+        const std::string hex = runner_of(model).logical_kv_sha256(seq);
+        std::memcpy(hex_out, hex.c_str(), hex.size() + 1);
+        return 0;
+    } catch (const std::exception &e) {
+        return model_fail(e);
+    }
+}
+
+}  // extern "C"

@@ -1,0 +1,106 @@
+// Llama-style decoder over the gfx950 library: the per-layer order of the
+// reference GPU runtime (run_layer, gpu_llm/mod.rs:2056-2350; run_batch_layer,
+// gpu_llm/prefill.rs:897-1061) chained through the C ABI on device buffers:
+//   embed -> per layer [RMSNorm -> Q,K,V projections -> RoPE(Q,K) -> K/V into
+//   the ColdStore-exact page pool -> attention -> O projection -> add ->
+//   RMSNorm -> gate, up -> SwiGLU -> down -> add] -> RMSNorm -> LM head ->
+//   greedy token (first index on ties).
+// A runner holds `max_batch` sequence slots.  Prefill runs one slot's prompt
+// in causal chunks of up to `chunk_tokens` (prefill_batched, mod.rs:2499-2570);
+// decode runs one token for each of slots 0..B-1, each at its own position,
+// over the paged K/V of every layer.  Weights are device BF16 buffers owned by
+// the caller, row-major [out][in] as tv_hip_matrix_multiply expects.
+#pragma once
+
+#include <cstdint>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "native.hpp"
+
+namespace mslim {
+namespace model {
+
+// The ModelSpec fields a layer uses (model_config.rs:22-42; RoPE arguments as
+// RopeKernelConfig, gpu_llm/kernels.rs:15-23).
+struct ModelSpec {
+    int layers = 0, hidden = 0, q_heads = 0, kv_heads = 0, head_dim = 0, intermediate = 0, vocab = 0;
+    float rms_eps = 1e-5f, rope_theta = 500000.0f;
+    int llama3 = 0;
+    float rope_factor = 1.0f, rope_low = 1.0f, rope_high = 2.0f, rope_original_max = 1.0f;
+    void validate() const;
+};
+
+struct LayerWeights {
+    const void *input_norm = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr;
+    const void *post_norm = nullptr, *gate = nullptr, *up = nullptr, *down = nullptr;
+};
+
+struct ModelWeights {
+    const void *embed = nullptr;  // [vocab][hidden]
+    std::vector<LayerWeights> layers;
+    const void *final_norm = nullptr;
+    const void *lm_head = nullptr;  // [vocab][hidden]; the embedding when tied
+};
+
+// GpuStep (gpu_llm/mod.rs:112-119) without the timing field.
+struct Step {
+    int32_t argmax_token = 0;
+    int64_t position = 0;  // tokens of the slot after this step
+};
+
+class DecoderRunner {
+public:
+    static constexpr int kPageTokens = 16;
+    DecoderRunner(std::shared_ptr<NativeContext> ctx, ModelSpec spec, ModelWeights weights, int max_batch,
+                  int chunk_tokens, int max_context);
+    ~DecoderRunner();
+    DecoderRunner(const DecoderRunner &) = delete;
+    DecoderRunner &operator=(const DecoderRunner &) = delete;
+
+    // Prompt of slot `seq` from position 0 (prefill_only, mod.rs:2499-2570):
+    // the greedy token after the prompt, not appended.
+    Step prefill_only(int seq, const std::vector<int32_t> &prompt);
+    // One token for each slot 0..tokens.size()-1 at that slot's position
+    // (forward_token, mod.rs:2457-2484, for a batch of sessions).
+    std::vector<Step> forward_batch(const std::vector<int32_t> &tokens);
+    // prefill_only, then greedy steps until max_new tokens or an EOS id
+    // (generate_cancellable, mod.rs:2587-2700).  Returns the generated tokens.
+    std::vector<int32_t> generate(int seq, const std::vector<int32_t> &prompt, int max_new,
+                                  const std::vector<int32_t> &eos_ids);
+    void reset(int seq);
+    // BF16 logits of the last prefill (1 row) or forward_batch (one row per
+    // slot), as raw bits.
+    std::vector<uint16_t> last_logits() const;
+    int64_t position(int seq) const { return positions_.at(seq); }
+    int max_batch() const { return max_batch_; }
+    // GpuLlm::logical_kv_sha256 (mod.rs:1981-2028) of one slot, read from the
+    // page pools.
+    std::string logical_kv_sha256(int seq) const;
+    const ModelSpec &spec() const { return spec_; }
+
+private:
+    void *alloc(size_t bytes);
+    void chunk(int seq, const int32_t *ids, int n, int64_t prior);
+    void gemm(const void *w, const void *in, void *out, int inner, int rows, int tokens);
+    void head(const uint16_t *rows_in, int rows);
+    const int32_t *table_row(int seq) const { return table_ + (int64_t)seq * pages_per_seq_; }
+
+    std::shared_ptr<NativeContext> ctx_;
+    ModelSpec spec_;
+    ModelWeights w_;
+    int max_batch_, chunk_tokens_, max_context_, pages_per_seq_, rows_cap_;
+    float scale_;
+    std::vector<int64_t> positions_;
+    std::vector<void *> owned_;
+    std::vector<void *> k_pools_, v_pools_;
+    int32_t *table_ = nullptr, *ids_ = nullptr, *pos_ = nullptr, *next_ = nullptr;
+    uint16_t *x_ = nullptr, *norm_ = nullptr, *q_ = nullptr, *k_ = nullptr, *v_ = nullptr, *qr_ = nullptr,
+             *kr_ = nullptr, *attn_ = nullptr, *proj_ = nullptr, *gate_ = nullptr, *up_ = nullptr, *act_ = nullptr,
+             *kd_ = nullptr, *vd_ = nullptr, *logits_ = nullptr;
+    int logits_rows_ = 0;
+};
+
+}  // namespace model
+}  // namespace mslim

@@ -47,7 +47,16 @@ public:
         if (!h) throw NativeError("mslim_attn_ctx_new", 0, mslim_attn_last_error());
         return std::shared_ptr<NativeContext>(new NativeContext(h));
     }
-    ~NativeContext() { mslim_attn_ctx_destroy(handle_); }
+    // A context owned elsewhere (for example by a Python caller); it is not
+    // destroyed with this object.
+    static std::shared_ptr<NativeContext> borrow(void *handle) {
+        auto c = std::shared_ptr<NativeContext>(new NativeContext(handle));
+        c->owned_ = false;
+        return c;
+    }
+    ~NativeContext() {
+        if (owned_) mslim_attn_ctx_destroy(handle_);
+    }
     NativeContext(const NativeContext &) = delete;
     NativeContext &operator=(const NativeContext &) = delete;
 
@@ -61,6 +70,7 @@ public:
 private:
     explicit NativeContext(void *h) : handle_(h) {}
     void *handle_;
+    bool owned_ = true;
     std::mutex mutex_;
 };
 

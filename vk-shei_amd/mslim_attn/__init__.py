@@ -61,8 +61,10 @@ EXPORTS = (
     "mslim_attn_backend_decode",
     "mslim_attn_rmsnorm",
     "mslim_attn_rope",
+    "mslim_attn_rope_rows",
     "mslim_attn_swiglu",
     "mslim_attn_pages_write",
+    "mslim_attn_pages_append",
     "mslim_attn_pages_gather",
     "mslim_attn_logical_kv_sha256",
     "mslim_attn_record_frame_bytes",
@@ -70,6 +72,9 @@ EXPORTS = (
     "mslim_attn_record_payloads",
     "mslim_attn_matrix_multiply",
     "mslim_attn_gemm_bf16",
+    "mslim_attn_add",
+    "mslim_attn_embed",
+    "mslim_attn_argmax",
 )
 
 RECORD_HEADER_BYTES = 104  # cold_store.rs:23
@@ -127,8 +132,10 @@ def library() -> C.CDLL:
         "mslim_attn_backend_decode": (I, [P, P, P, I, P, I, I64, I, I, I, P, C.POINTER(Timings)]),
         "mslim_attn_rmsnorm": (I, [P, P, P, P, I, I, F]),
         "mslim_attn_rope": (I, [P, P, P, I, I, I, I, F, I, F, F, F, F]),
+        "mslim_attn_rope_rows": (I, [P, P, P, I, I, I, P, F, I, F, F, F, F]),
         "mslim_attn_swiglu": (I, [P, P, P, P, SZ]),
         "mslim_attn_pages_write": (I, [P, P, P, P, I, I, I, I64, I64, P, P]),
+        "mslim_attn_pages_append": (I, [P, P, P, P, I, I, I, I, I, P, P, P]),
         "mslim_attn_pages_gather": (I, [P, P, P, I, I, I, I64, I64, P]),
         "mslim_attn_logical_kv_sha256": (I, [P, I, I64, I, I, P, P, P, I, C.c_char_p]),
         "mslim_attn_record_frame_bytes": (I64, [I]),
@@ -136,6 +143,9 @@ def library() -> C.CDLL:
         "mslim_attn_record_payloads": (I, [P, P, P, I64, I, I, I, P, I, P, P, I]),
         "mslim_attn_matrix_multiply": (I, [P, P, P, P, I, I, I]),
         "mslim_attn_gemm_bf16": (I, [P, P, P, P, I, I, I]),
+        "mslim_attn_add": (I, [P, P, P, P, SZ]),
+        "mslim_attn_embed": (I, [P, P, I, I, P, I, P, P]),
+        "mslim_attn_argmax": (I, [P, P, I, I, P]),
     }
     for name in EXPORTS:
         res, args = sigs[name]
@@ -313,6 +323,15 @@ class Context:
             int(bool(llama3_scaling)), factor, low_freq_factor, high_freq_factor,
             original_max_position))
 
+    def rope_rows(self, x, out, tokens: int, heads: int, head_dim: int, positions,
+                  theta: float, llama3_scaling: bool = False, factor: float = 1.0,
+                  low_freq_factor: float = 1.0, high_freq_factor: float = 2.0,
+                  original_max_position: float = 1.0) -> None:
+        self._check("rope_rows", self._lib.mslim_attn_rope_rows(
+            self._h, _ptr(x), _ptr(out), tokens, heads, head_dim, _ptr(positions), theta,
+            int(bool(llama3_scaling)), factor, low_freq_factor, high_freq_factor,
+            original_max_position))
+
     def swiglu(self, gate, up, out, n: int) -> None:
         self._check("swiglu", self._lib.mslim_attn_swiglu(self._h, _ptr(gate), _ptr(up),
                                                           _ptr(out), n))
@@ -323,6 +342,12 @@ class Context:
         self._check("pages_write", self._lib.mslim_attn_pages_write(
             self._h, _ptr(k_pool), _ptr(v_pool), _ptr(page_table_row), page_tokens, kv_heads,
             head_dim, first_token, tokens, _ptr(k_rows), _ptr(v_rows)))
+
+    def pages_append(self, k_pool, v_pool, page_table, pages_per_seq: int, page_tokens: int,
+                     kv_heads: int, head_dim: int, batch: int, positions, k_rows, v_rows) -> None:
+        self._check("pages_append", self._lib.mslim_attn_pages_append(
+            self._h, _ptr(k_pool), _ptr(v_pool), _ptr(page_table), pages_per_seq, page_tokens,
+            kv_heads, head_dim, batch, _ptr(positions), _ptr(k_rows), _ptr(v_rows)))
 
     def pages_gather(self, pool, page_table_row, page_tokens: int, kv_heads: int, head_dim: int,
                      first_token: int, tokens: int, rows_out) -> None:
@@ -369,6 +394,16 @@ class Context:
     def gemm_bf16(self, weight, input_dev, output_dev, inner: int, rows: int, tokens: int) -> None:
         self._check("gemm_bf16", self._lib.mslim_attn_gemm_bf16(
             self._h, _ptr(weight), _ptr(input_dev), _ptr(output_dev), inner, rows, tokens))
+
+    def add(self, a, b, out, n: int) -> None:
+        self._check("add", self._lib.mslim_attn_add(self._h, _ptr(a), _ptr(b), _ptr(out), n))
+
+    def embed(self, table, vocab: int, hidden: int, ids, tokens: int, out, bad=None) -> None:
+        self._check("embed", self._lib.mslim_attn_embed(self._h, _ptr(table), vocab, hidden, _ptr(ids),
+                                                        tokens, _ptr(out), _ptr(bad)))
+
+    def argmax(self, logits, rows: int, vocab: int, out) -> None:
+        self._check("argmax", self._lib.mslim_attn_argmax(self._h, _ptr(logits), rows, vocab, _ptr(out)))
 
     def record_payloads(self, k_pool, v_pool, pool_pages: int, page_tokens: int, kv_heads: int,
                         head_dim: int, records, count: int, k_stage, v_stage, to_staging: bool) -> None:
