@@ -243,6 +243,12 @@ int mslim_attn_argmax(void *ctx, const void *logits, int rows, int vocab, int32_
 
 /* ---- ColdStore-exact page pool --------------------------------------------- */
 
+/* The page entry points below (write, append, gather, digest) take any
+ * power-of-two page_tokens: 16 is the ColdStore-exact pool the paged decode
+ * reads, and 1 makes a pool of token-major rows, i.e. the dense layout
+ * addressed through a table (GpuRegionStore uses 1-token pages for decode
+ * appends, gpu_region_store.rs:376-384). */
+
 /* Write `tokens` token-major rows of one sequence (K and V, [tokens][kv_heads]
  * [head_dim]) into the page pool at logical positions first_token.. through
  * the device page table row `page_table` (int32 [pages]).  The device

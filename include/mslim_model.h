@@ -25,6 +25,16 @@ extern "C" {
 /* Weight tensors per layer, in the order of the `weights` array below. */
 #define MSLIM_MODEL_LAYER_TENSORS 9
 
+/* K/V layouts (mslim_model_new's kv_layout).  PAGED: the ColdStore-exact pool
+ * of 16-token head-major pages read by mslim_attn_decode_paged, as the
+ * GPU-region runtime (GpuLlm::load_with_gpu_region_native_hip,
+ * src/gpu_llm/mod.rs:299-306).  DENSE: token-major rows per slot read by
+ * mslim_attn_decode_dense, as the Workspace cache of load_dense_native_hip
+ * (mod.rs:308).  Both give bit-identical tokens, logits and K/V digests
+ * (the reference's invariant, mod.rs:2993-3048). */
+#define MSLIM_MODEL_KV_PAGED 0
+#define MSLIM_MODEL_KV_DENSE 1
+
 /* ModelSpec fields a layer uses (src/model_config.rs:22-42) and the RoPE
  * arguments of RopeKernelConfig (src/gpu_llm/kernels.rs:15-23). */
 typedef struct {
@@ -44,11 +54,12 @@ const char *mslim_model_last_error(void);
  *   [kv_heads*head_dim][hidden], o [hidden][q_heads*head_dim], post norm
  *   [hidden], gate and up [intermediate][hidden], down [hidden][intermediate].
  * max_batch <= 64 slots, chunk_tokens <= 512 prompt tokens per causal chunk,
- * max_context tokens per slot.  The runner allocates its K/V page pools and
- * activations on the context's device.  Replaces GpuLlm::load_dense_native_hip
- * (src/gpu_llm/mod.rs:308) for weights already on the device. */
+ * max_context tokens per slot, kv_layout MSLIM_MODEL_KV_*.  The runner
+ * allocates its K/V pools and activations on the context's device.  Replaces
+ * GpuLlm::load_dense_native_hip / load_with_gpu_region_native_hip
+ * (src/gpu_llm/mod.rs:299-308) for weights already on the device. */
 void *mslim_model_new(void *attn_ctx, const mslim_model_spec *spec, const void *const *weights,
-                      int max_batch, int chunk_tokens, int max_context);
+                      int max_batch, int chunk_tokens, int max_context, int kv_layout);
 void mslim_model_destroy(void *model);
 
 /* Prompt of slot `seq` from position 0; *next_token = greedy token after the

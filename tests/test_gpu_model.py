@@ -176,7 +176,7 @@ def _margin(bits):
 
 
 def _check_token(got, want_bits, label):
-    want = int(oracle.argmax_bf16(want_bits, 1, SPEC.vocab)[0])
+    want = int(oracle.argmax_bf16(want_bits, 1, want_bits.size)[0])
     if _margin(want_bits) > 2 * MODEL_LOGIT_MAX_ABS:
         assert got == want, f"{label}: token {got} != oracle {want}"
 
@@ -278,3 +278,84 @@ def test_runner_rejects_bad_requests(tiny_model):
         model.forward_batch([1, 2, 3, 4])
     with pytest.raises(MslimAttnError, match="capacity"):
         model.generate([1] * 78, 5)
+
+
+def test_runner_dense_and_paged_are_bit_identical(ctx, tiny_model):
+    # the reference's invariant (gpu_llm/mod.rs:2993-3048): the ColdStore-exact
+    # route and the dense route give the same tokens, logits and K/V digest
+    from mslim_attn.model import Model, ModelSpec
+
+    w, paged = tiny_model
+    dev = {k: to_torch(v) for k, v in w.items()}
+    spec = ModelSpec(SPEC.layers, SPEC.hidden, SPEC.q_heads, SPEC.kv_heads, SPEC.head_dim,
+                     SPEC.intermediate, SPEC.vocab, SPEC.rms_eps, SPEC.rope_theta)
+    dense = Model(ctx, spec, dev, max_batch=3, chunk_tokens=16, max_context=80, kv_layout="dense")
+    try:
+        rng = np.random.default_rng(77)
+        prompts = [list(rng.integers(0, SPEC.vocab, n)) for n in (41, 3, 17)]
+        toks = []
+        for seq, prompt in enumerate(prompts):
+            a, b = paged.prefill_only(seq, prompt), dense.prefill_only(seq, prompt)
+            assert a == b and np.array_equal(paged.logits(), dense.logits()), seq
+            toks.append(a)
+        for step in range(5):
+            a, b = paged.forward_batch(toks), dense.forward_batch(toks)
+            assert a == b and np.array_equal(paged.logits(), dense.logits()), step
+            toks = a
+        for seq in range(3):
+            assert paged.logical_kv_sha256(seq) == dense.logical_kv_sha256(seq)
+    finally:
+        dense.close()
+
+
+def test_runner_llama3_8b_width_reduced_depth(ctx):
+    # The cfg5 decoder at full width (hidden 4096, 32/8 heads of 128, FFN
+    # 14336, vocab 128256, weights N(0, 0.02)) and reduced depth (2 layers)
+    # against the CPU decoder oracle: two ragged prompts, then batched greedy
+    # steps.  Weights come from torch's seeded device generator, rounded to
+    # BF16 (round-to-nearest-even, as write_bf16 for finite values).
+    from mslim_attn.model import Model, ModelSpec
+
+    spec = Spec(layers=2, hidden=4096, q_heads=32, kv_heads=8, head_dim=128, intermediate=14336, vocab=128256)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(5)
+
+    def normal(shape, scale):
+        return (torch.randn(shape, generator=gen, device="cuda") * scale).to(torch.bfloat16).view(torch.int16)
+
+    def norm(n):
+        return (1.0 + 0.1 * torch.randn(n, generator=gen, device="cuda")).to(torch.bfloat16).view(torch.int16)
+
+    qd, kvd = spec.q_heads * spec.head_dim, spec.kv_heads * spec.head_dim
+    shapes = {"q": (qd, spec.hidden), "k": (kvd, spec.hidden), "v": (kvd, spec.hidden), "o": (spec.hidden, qd),
+              "gate": (spec.intermediate, spec.hidden), "up": (spec.intermediate, spec.hidden),
+              "down": (spec.hidden, spec.intermediate)}
+    dev = {"embed": normal((spec.vocab, spec.hidden), 1.0), "final_norm": norm(spec.hidden),
+           "lm_head": normal((spec.vocab, spec.hidden), 0.02)}
+    for l in range(spec.layers):
+        for name in ("input_norm", "q", "k", "v", "o", "post_norm", "gate", "up", "down"):
+            dev[f"layers.{l}.{name}"] = norm(spec.hidden) if name.endswith("norm") else normal(shapes[name], 0.02)
+    torch.cuda.synchronize()
+    host = {k: from_torch(v).reshape(v.shape) for k, v in dev.items()}
+    model = Model(ctx, ModelSpec(spec.layers, spec.hidden, spec.q_heads, spec.kv_heads, spec.head_dim,
+                                 spec.intermediate, spec.vocab), dev, max_batch=2, chunk_tokens=16, max_context=64)
+    try:
+        ref = DecoderOracle(spec, host)
+        prompts = [[11, 5000, 99999, 128255, 7], [3, 64000, 1]]
+        toks = []
+        for seq, prompt in enumerate(prompts):
+            got = model.prefill_only(seq, prompt)
+            want_logits, _ = ref.prefill(seq, prompt)
+            _check_logits(model.logits()[0], want_logits, f"prefill {seq}")
+            _check_token(got, want_logits, f"prefill {seq}")
+            toks.append(got)
+        for step in range(2):
+            nxt = model.forward_batch(toks)
+            logits = model.logits()
+            for seq in range(2):
+                want_logits, _ = ref.step(seq, toks[seq])
+                _check_logits(logits[seq], want_logits, f"step {step} slot {seq}")
+                _check_token(nxt[seq], want_logits, f"step {step} slot {seq}")
+            toks = nxt
+    finally:
+        model.close()

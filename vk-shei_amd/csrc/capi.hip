@@ -609,7 +609,7 @@ int mslim_attn_pages_write(void *ctx, void *k_pool, void *v_pool, const int32_t 
     g_error.clear();
     if (!ctx || !k_pool || !v_pool || !page_table || !k_rows || !v_rows || tokens < 1 ||
         first_token < 0 || kv_heads < 1 || head_dim < 8 || head_dim % 8 || !is_pow2(page_tokens) ||
-        page_tokens < 16)
+        page_tokens > (1 << 20))
         return fail("invalid page write arguments");
     Context &c = *ctx_of(ctx);
     Lock lock(c);
@@ -627,7 +627,7 @@ int mslim_attn_pages_append(void *ctx, void *k_pool, void *v_pool, const int32_t
     g_error.clear();
     if (!ctx || !k_pool || !v_pool || !page_table || !positions || !k_rows || !v_rows || batch < 1 ||
         pages_per_seq < 1 || kv_heads < 1 || head_dim < 8 || head_dim % 8 || !is_pow2(page_tokens) ||
-        page_tokens < 16)
+        page_tokens > (1 << 20))
         return fail("invalid page append arguments");
     Context &c = *ctx_of(ctx);
     Lock lock(c);
@@ -644,7 +644,7 @@ int mslim_attn_pages_gather(void *ctx, const void *pool, const int32_t *page_tab
                             void *rows_out) {
     g_error.clear();
     if (!ctx || !pool || !page_table || !rows_out || tokens < 1 || first_token < 0 || kv_heads < 1 ||
-        head_dim < 8 || head_dim % 8 || !is_pow2(page_tokens) || page_tokens < 16)
+        head_dim < 8 || head_dim % 8 || !is_pow2(page_tokens) || page_tokens > (1 << 20))
         return fail("invalid page gather arguments");
     Context &c = *ctx_of(ctx);
     Lock lock(c);
@@ -662,8 +662,8 @@ int mslim_attn_logical_kv_sha256(void *ctx, int layers, int64_t tokens, int kv_h
     if (!ctx || layers < 1 || tokens < 0 || kv_heads < 1 || head_dim < 8 || head_dim % 8 || !keys ||
         !values || !hex_out)
         return fail("invalid logical K/V digest arguments");
-    if (page_tables && (!is_pow2(page_tokens) || page_tokens < 16))
-        return fail("paged digest needs page_tokens a power of two >= 16");
+    if (page_tables && (!is_pow2(page_tokens) || page_tokens > (1 << 20)))
+        return fail("paged digest needs page_tokens a power of two");
     Context &c = *ctx_of(ctx);
     Lock lock(c);
     mslim::Sha256 sha;

@@ -25,8 +25,8 @@ void ModelSpec::validate() const {
 }
 
 DecoderRunner::DecoderRunner(std::shared_ptr<NativeContext> ctx, ModelSpec spec, ModelWeights weights,
-                             int max_batch, int chunk_tokens, int max_context)
-    : ctx_(std::move(ctx)), spec_(spec), w_(std::move(weights)), max_batch_(max_batch),
+                             int max_batch, int chunk_tokens, int max_context, KvLayout layout)
+    : ctx_(std::move(ctx)), spec_(spec), w_(std::move(weights)), layout_(layout), max_batch_(max_batch),
       chunk_tokens_(chunk_tokens), max_context_(max_context) {
     ensure(ctx_ != nullptr, "no device context");
     spec_.validate();
@@ -38,7 +38,11 @@ DecoderRunner::DecoderRunner(std::shared_ptr<NativeContext> ctx, ModelSpec spec,
     ensure(max_batch_ >= 1 && max_batch_ <= MSLIM_ATTN_MAX_BATCH, "max_batch must be 1..=64");
     ensure(chunk_tokens_ >= 1 && chunk_tokens_ <= 512, "prefill chunk must be 1..=512 tokens");
     ensure(max_context_ >= 1 && max_context_ <= (1 << 24), "max_context must be 1..=16777216 tokens");
-    pages_per_seq_ = (max_context_ + kPageTokens - 1) / kPageTokens;
+    ensure(layout_ == KvLayout::Paged || layout_ == KvLayout::Dense, "unknown K/V layout");
+    // The dense layout is a pool of one-token pages (token-major rows) under
+    // the identity table: slot s, token t -> row s * max_context + t.
+    page_tokens_ = layout_ == KvLayout::Dense ? 1 : kPageTokens;
+    pages_per_seq_ = (max_context_ + page_tokens_ - 1) / page_tokens_;
     rows_cap_ = std::max(max_batch_, chunk_tokens_);
     scale_ = (float)(1.0 / std::sqrt((double)spec_.head_dim));
     positions_.assign(max_batch_, 0);
@@ -47,15 +51,17 @@ DecoderRunner::DecoderRunner(std::shared_ptr<NativeContext> ctx, ModelSpec spec,
     const size_t pool_pages = (size_t)max_batch_ * pages_per_seq_;
     try {
         for (int l = 0; l < spec_.layers; ++l) {
-            k_pools_.push_back(alloc(pool_pages * kPageTokens * kvd * 2));
-            v_pools_.push_back(alloc(pool_pages * kPageTokens * kvd * 2));
+            k_pools_.push_back(alloc(pool_pages * page_tokens_ * kvd * 2));
+            v_pools_.push_back(alloc(pool_pages * page_tokens_ * kvd * 2));
         }
-        // Slot s, logical page p -> physical page p * max_batch + s: the
-        // slots interleave in the pool, so every read goes through the table.
+        // Paged: slot s, logical page p -> physical page p * max_batch + s, so
+        // the slots interleave in the pool and every read goes through the
+        // table.  Dense: the identity.
         std::vector<int32_t> table(pool_pages);
         for (int s = 0; s < max_batch_; ++s)
             for (int p = 0; p < pages_per_seq_; ++p)
-                table[(size_t)s * pages_per_seq_ + p] = (int32_t)((size_t)p * max_batch_ + s);
+                table[(size_t)s * pages_per_seq_ + p] =
+                    (int32_t)(layout_ == KvLayout::Dense ? (size_t)s * pages_per_seq_ + p : (size_t)p * max_batch_ + s);
         table_ = static_cast<int32_t *>(alloc(table.size() * 4));
         ctx_->check("upload page table", mslim_attn_buf_write(ctx_->handle(), table_, 0,
                                                               reinterpret_cast<const uint8_t *>(table.data()),
@@ -76,8 +82,10 @@ DecoderRunner::DecoderRunner(std::shared_ptr<NativeContext> ctx, ModelSpec spec,
         gate_ = static_cast<uint16_t *>(alloc(r * spec_.intermediate * 2));
         up_ = static_cast<uint16_t *>(alloc(r * spec_.intermediate * 2));
         act_ = static_cast<uint16_t *>(alloc(r * spec_.intermediate * 2));
-        kd_ = static_cast<uint16_t *>(alloc((size_t)max_context_ * kvd * 2));
-        vd_ = static_cast<uint16_t *>(alloc((size_t)max_context_ * kvd * 2));
+        if (layout_ == KvLayout::Paged) {
+            kd_ = static_cast<uint16_t *>(alloc((size_t)max_context_ * kvd * 2));
+            vd_ = static_cast<uint16_t *>(alloc((size_t)max_context_ * kvd * 2));
+        }
         logits_ = static_cast<uint16_t *>(alloc((size_t)max_batch_ * spec_.vocab * 2));
     } catch (...) {
         for (void *p : owned_) mslim_attn_buf_free(ctx_->handle(), p);
@@ -131,10 +139,13 @@ void DecoderRunner::chunk(int seq, const int32_t *ids, int n, int64_t prior) {
         ctx_->check("key RoPE", mslim_attn_rope(h, k_, kr_, n, s.kv_heads, s.head_dim, (int)prior, s.rope_theta,
                                                 s.llama3, s.rope_factor, s.rope_low, s.rope_high,
                                                 s.rope_original_max));
-        ctx_->check("page write", mslim_attn_pages_write(h, k_pools_[l], v_pools_[l], table_row(seq), kPageTokens,
+        ctx_->check("page write", mslim_attn_pages_write(h, k_pools_[l], v_pools_[l], table_row(seq), page_tokens_,
                                                          s.kv_heads, s.head_dim, prior, n, kr_, v_));
         const void *keys = kr_, *values = v_;
-        if (prior > 0) {
+        if (layout_ == KvLayout::Dense) {
+            keys = dense_rows(k_pools_[l], seq);
+            values = dense_rows(v_pools_[l], seq);
+        } else if (prior > 0) {
             // Earlier chunks live only in the pages: gather the slot's whole
             // history token-major for the causal kernel.
             ctx_->check("gather keys", mslim_attn_pages_gather(h, k_pools_[l], table_row(seq), kPageTokens,
@@ -209,11 +220,16 @@ std::vector<Step> DecoderRunner::forward_batch(const std::vector<int32_t> &token
                                                      s.llama3, s.rope_factor, s.rope_low, s.rope_high,
                                                      s.rope_original_max));
         ctx_->check("page append", mslim_attn_pages_append(h, k_pools_[l], v_pools_[l], table_, pages_per_seq_,
-                                                           kPageTokens, s.kv_heads, s.head_dim, b, pos_, kr_, v_));
-        ctx_->check("paged attention",
-                    mslim_attn_decode_paged(h, qr_, k_pools_[l], v_pools_[l], attn_, b, lens.data(), table_,
-                                            pages_per_seq_, kPageTokens, s.q_heads, s.kv_heads, s.head_dim,
-                                            scale_, 0));
+                                                           page_tokens_, s.kv_heads, s.head_dim, b, pos_, kr_, v_));
+        if (layout_ == KvLayout::Dense)
+            ctx_->check("dense attention",
+                        mslim_attn_decode_dense(h, qr_, k_pools_[l], v_pools_[l], attn_, b, lens.data(), max_context_,
+                                                s.q_heads, s.kv_heads, s.head_dim, scale_, 0));
+        else
+            ctx_->check("paged attention",
+                        mslim_attn_decode_paged(h, qr_, k_pools_[l], v_pools_[l], attn_, b, lens.data(), table_,
+                                                pages_per_seq_, kPageTokens, s.q_heads, s.kv_heads, s.head_dim,
+                                                scale_, 0));
         gemm(w.o, attn_, proj_, qd, s.hidden, b);
         ctx_->check("attention residual", mslim_attn_add(h, x_, proj_, x_, (size_t)b * s.hidden));
         ctx_->check("post norm", mslim_attn_rmsnorm(h, x_, w.post_norm, norm_, b, s.hidden, s.rms_eps));
@@ -271,11 +287,17 @@ std::string DecoderRunner::logical_kv_sha256(int seq) const {
     ensure(seq >= 0 && seq < max_batch_, "sequence slot out of range");
     std::vector<const int32_t *> tables(spec_.layers, table_row(seq));
     std::vector<const void *> keys(k_pools_.begin(), k_pools_.end()), values(v_pools_.begin(), v_pools_.end());
+    const bool dense = layout_ == KvLayout::Dense;
+    if (dense)
+        for (int l = 0; l < spec_.layers; ++l) {
+            keys[l] = dense_rows(k_pools_[l], seq);
+            values[l] = dense_rows(v_pools_[l], seq);
+        }
     char hex[65] = {0};
     ctx_->check("logical K/V digest",
                 mslim_attn_logical_kv_sha256(ctx_->handle(), spec_.layers, positions_[seq], spec_.kv_heads,
-                                             spec_.head_dim, keys.data(), values.data(), tables.data(),
-                                             kPageTokens, hex));
+                                             spec_.head_dim, keys.data(), values.data(),
+                                             dense ? nullptr : tables.data(), dense ? 0 : kPageTokens, hex));
     return std::string(hex);
 }
 
@@ -309,10 +331,11 @@ extern "C" {
 const char *mslim_model_last_error(void) { return g_model_error.c_str(); }
 
 void *mslim_model_new(void *attn_ctx, const mslim_model_spec *spec, const void *const *weights, int max_batch,
-                      int chunk_tokens, int max_context) {
+                      int chunk_tokens, int max_context, int kv_layout) {
     g_model_error.clear();
     try {
         mslim::ensure(attn_ctx && spec && weights, "null model arguments");
+        mslim::ensure(kv_layout == MSLIM_MODEL_KV_PAGED || kv_layout == MSLIM_MODEL_KV_DENSE, "unknown K/V layout");
         mslim::model::ModelSpec s;
         s.layers = spec->layers;
         s.hidden = spec->hidden;
@@ -349,7 +372,8 @@ void *mslim_model_new(void *attn_ctx, const mslim_model_spec *spec, const void *
         }
         auto handle = std::make_unique<ModelHandle>();
         handle->runner = std::make_unique<mslim::model::DecoderRunner>(
-            mslim::NativeContext::borrow(attn_ctx), s, std::move(w), max_batch, chunk_tokens, max_context);
+            mslim::NativeContext::borrow(attn_ctx), s, std::move(w), max_batch, chunk_tokens, max_context,
+            static_cast<mslim::model::KvLayout>(kv_layout));
         return handle.release();
     } catch (const std::exception &e) {
         model_fail(e);

@@ -8,7 +8,7 @@
 // A runner holds `max_batch` sequence slots.  Prefill runs one slot's prompt
 // in causal chunks of up to `chunk_tokens` (prefill_batched, mod.rs:2499-2570);
 // decode runs one token for each of slots 0..B-1, each at its own position,
-// over the paged K/V of every layer.  Weights are device BF16 buffers owned by
+// over every layer's K/V in the chosen layout.  Weights are device BF16 buffers owned by
 // the caller, row-major [out][in] as tv_hip_matrix_multiply expects.
 #pragma once
 
@@ -50,11 +50,19 @@ struct Step {
     int64_t position = 0;  // tokens of the slot after this step
 };
 
+// Where a runner keeps K/V: the ColdStore-exact pool of 16-token head-major
+// pages behind a page table (the GPU-region route, load_with_gpu_region_
+// native_hip, gpu_llm/mod.rs:299-306), or dense token-major rows per slot
+// (the Workspace cache of load_dense_native_hip, mod.rs:308).  The two give
+// bit-identical tokens and logits, the reference's invariant of
+// mod.rs:2993-3048.
+enum class KvLayout { Paged = 0, Dense = 1 };
+
 class DecoderRunner {
 public:
     static constexpr int kPageTokens = 16;
     DecoderRunner(std::shared_ptr<NativeContext> ctx, ModelSpec spec, ModelWeights weights, int max_batch,
-                  int chunk_tokens, int max_context);
+                  int chunk_tokens, int max_context, KvLayout layout = KvLayout::Paged);
     ~DecoderRunner();
     DecoderRunner(const DecoderRunner &) = delete;
     DecoderRunner &operator=(const DecoderRunner &) = delete;
@@ -76,7 +84,7 @@ public:
     int64_t position(int seq) const { return positions_.at(seq); }
     int max_batch() const { return max_batch_; }
     // GpuLlm::logical_kv_sha256 (mod.rs:1981-2028) of one slot, read from the
-    // page pools.
+    // K/V pools.
     std::string logical_kv_sha256(int seq) const;
     const ModelSpec &spec() const { return spec_; }
 
@@ -86,11 +94,16 @@ private:
     void gemm(const void *w, const void *in, void *out, int inner, int rows, int tokens);
     void head(const uint16_t *rows_in, int rows);
     const int32_t *table_row(int seq) const { return table_ + (int64_t)seq * pages_per_seq_; }
+    // Dense layout: token-major rows of slot `seq` in a layer pool.
+    const uint16_t *dense_rows(const void *pool, int seq) const {
+        return static_cast<const uint16_t *>(pool) + (size_t)seq * max_context_ * spec_.kv_heads * spec_.head_dim;
+    }
 
     std::shared_ptr<NativeContext> ctx_;
     ModelSpec spec_;
     ModelWeights w_;
-    int max_batch_, chunk_tokens_, max_context_, pages_per_seq_, rows_cap_;
+    KvLayout layout_;
+    int max_batch_, chunk_tokens_, max_context_, page_tokens_, pages_per_seq_, rows_cap_;
     float scale_;
     std::vector<int64_t> positions_;
     std::vector<void *> owned_;

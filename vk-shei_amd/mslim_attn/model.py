@@ -30,6 +30,9 @@ MODEL_EXPORTS = (
 
 LAYER_TENSORS = ("input_norm", "q", "k", "v", "o", "post_norm", "gate", "up", "down")
 
+# MSLIM_MODEL_KV_PAGED / MSLIM_MODEL_KV_DENSE
+KV_LAYOUTS = {"paged": 0, "dense": 1}
+
 
 class Spec(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("layers", "hidden", "q_heads", "kv_heads", "head_dim",
@@ -79,7 +82,7 @@ def host_library() -> C.CDLL:
     P, I, I64, PI32 = C.c_void_p, C.c_int, C.c_int64, C.POINTER(C.c_int32)
     sigs = {
         "mslim_model_last_error": (C.c_char_p, []),
-        "mslim_model_new": (P, [P, C.POINTER(Spec), C.POINTER(C.c_void_p), I, I, I]),
+        "mslim_model_new": (P, [P, C.POINTER(Spec), C.POINTER(C.c_void_p), I, I, I, I]),
         "mslim_model_destroy": (None, [P]),
         "mslim_model_prefill": (I, [P, I, PI32, I, PI32]),
         "mslim_model_forward_batch": (I, [P, PI32, I, PI32]),
@@ -103,7 +106,9 @@ def _ids(values: Sequence[int]):
 
 
 class Model:
-    """A decoder runner with `max_batch` sequence slots on a Context.
+    """A decoder runner with `max_batch` sequence slots on a Context; K/V in
+    the ColdStore-exact paged pool ("paged") or dense token-major rows
+    ("dense").
 
     `weights` maps "embed", "final_norm", "lm_head" and per layer l the names
     of LAYER_TENSORS ("layers.{l}.q", ...) to contiguous device BF16 tensors
@@ -112,7 +117,7 @@ class Model:
     """
 
     def __init__(self, ctx: Context, spec: ModelSpec, weights: dict, max_batch: int = 1,
-                 chunk_tokens: int = 128, max_context: int = 1024):
+                 chunk_tokens: int = 128, max_context: int = 1024, kv_layout: str = "paged"):
         lib = host_library()
         names = ["embed", "final_norm", "lm_head"] + [
             f"layers.{l}.{t}" for l in range(spec.layers) for t in LAYER_TENSORS]
@@ -125,8 +130,10 @@ class Model:
         self._spec_struct = spec.as_struct()
         self._ctx = ctx
         self._lib = lib
+        if kv_layout not in KV_LAYOUTS:
+            raise ValueError(f"kv_layout must be one of {sorted(KV_LAYOUTS)}")
         self._h = lib.mslim_model_new(ctx.handle, C.byref(self._spec_struct), arr, max_batch,
-                                      chunk_tokens, max_context)
+                                      chunk_tokens, max_context, KV_LAYOUTS[kv_layout])
         if not self._h:
             raise MslimAttnError("mslim_model_new", -1, self._error())
         self.max_batch = max_batch
