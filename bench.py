@@ -31,12 +31,21 @@ Before each timed loop a short device sleep is queued behind the final
 synchronize so that the first timed launch does not wait on host launch
 latency; every timed call is then back-to-back device work.
 
-`--kernel decode|prefill|copy` runs only that workload (warmup + steps, no
-CPU baseline) for counter collection: `copy` is a plain 1 GiB device copy
-whose FETCH_SIZE / WRITE_SIZE readings calibrate the byte counters.
+The full decoder of BASELINE.json configs[4] (Llama-3-8B shape, 32 layers,
+random N(0, 0.02) BF16 weights, batch 8, seeded 4,096-token prompts, 128
+greedy steps) runs through the C++ decoder runner with K/V in the
+ColdStore-exact page pool and is reported under "decoder": prefill and
+decode tokens/s and the decode step's HBM roofline, plus a check that the
+dense K/V layout yields the same tokens and K/V digest.  Its CPU baseline is
+the oracle decoder on one host core, one layer timed and scaled to 32.
+
+`--kernel decode|prefill|copy|decoder` runs only that workload (no CPU
+baseline for the kernels) for counter collection: `copy` is a plain 1 GiB
+device copy whose FETCH_SIZE / WRITE_SIZE readings calibrate the byte
+counters.
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--cpu-seconds 10]
-                       [--kernel all|decode|prefill|copy]
+                       [--kernel all|decode|prefill|copy|decoder] [--decoder-steps 128]
 """
 import argparse
 import json
@@ -230,6 +239,168 @@ def cpu_model() -> str:
     return "unknown"
 
 
+# BASELINE cfg5: Llama-3-8B-shaped decoder, weights N(0, 0.02) BF16, greedy
+# decode of 128 steps at batch 8 after seeded 4,096-token prompts.
+DEC_LAYERS, DEC_HIDDEN, DEC_QH, DEC_KVH, DEC_D = 32, 4096, 32, 8, 128
+DEC_FFN, DEC_VOCAB, DEC_BATCH, DEC_PROMPT, DEC_STEPS = 14336, 128256, 8, 4096, 128
+DEC_CHUNK = 512
+
+
+def decoder_weights(torch, seed: int) -> dict:
+    """Random-init cfg5 weights on the device: projections, embedding and LM
+    head N(0, 0.02), RMSNorm weights 1 + N(0, 0.1^2), rounded to BF16."""
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+
+    def normal(shape, scale):
+        return (torch.randn(shape, generator=gen, device="cuda") * scale).to(torch.bfloat16).view(torch.int16)
+
+    def norm():
+        return (1.0 + 0.1 * torch.randn(DEC_HIDDEN, generator=gen, device="cuda")).to(torch.bfloat16).view(torch.int16)
+
+    qd, kvd = DEC_QH * DEC_D, DEC_KVH * DEC_D
+    shapes = {"q": (qd, DEC_HIDDEN), "k": (kvd, DEC_HIDDEN), "v": (kvd, DEC_HIDDEN), "o": (DEC_HIDDEN, qd),
+              "gate": (DEC_FFN, DEC_HIDDEN), "up": (DEC_FFN, DEC_HIDDEN), "down": (DEC_HIDDEN, DEC_FFN)}
+    w = {"embed": normal((DEC_VOCAB, DEC_HIDDEN), 0.02), "final_norm": norm(),
+         "lm_head": normal((DEC_VOCAB, DEC_HIDDEN), 0.02)}
+    for l in range(DEC_LAYERS):
+        for name in ("input_norm", "q", "k", "v", "o", "post_norm", "gate", "up", "down"):
+            w[f"layers.{l}.{name}"] = norm() if name.endswith("norm") else normal(shapes[name], 0.02)
+    return w
+
+
+def decoder_step_bytes(contexts) -> int:
+    """Algorithmic HBM bytes of one batched decode step: every weight read
+    once (all layers, LM head, one embedding row per sequence) plus each
+    sequence's K and V history read once per layer; activations are
+    negligible (< 0.1 %)."""
+    qd, kvd = DEC_QH * DEC_D, DEC_KVH * DEC_D
+    layer = (qd * DEC_HIDDEN * 2 + kvd * DEC_HIDDEN * 2 + 3 * DEC_FFN * DEC_HIDDEN + 2 * DEC_HIDDEN) * 2
+    head = DEC_VOCAB * DEC_HIDDEN * 2 + DEC_HIDDEN * 2 + len(contexts) * DEC_HIDDEN * 2
+    kv = sum(contexts) * kvd * 2 * 2 * DEC_LAYERS
+    return DEC_LAYERS * layer + head + kv
+
+
+def cpu_decoder_baseline(host_layer: dict, host_head: dict, seconds: float):
+    """The oracle's decoder layer (oracle/decoder.py: the reference layer
+    order over the pinned stage restatements) on one host core: one decode
+    token of layer 0 at position DEC_PROMPT timed, and the final norm + LM
+    head timed, then scaled to the 32-layer model."""
+    import numpy as np
+
+    import oracle
+    from oracle.decoder import DecoderOracle, Session, Spec
+
+    spec = Spec(layers=1, hidden=DEC_HIDDEN, q_heads=DEC_QH, kv_heads=DEC_KVH, head_dim=DEC_D,
+                intermediate=DEC_FFN, vocab=DEC_VOCAB)
+    ref = DecoderOracle(spec, {**host_layer, **host_head})
+    rng = np.random.default_rng(5)
+    kvd = DEC_KVH * DEC_D
+    hist = [oracle.write_bf16(rng.standard_normal(DEC_PROMPT * kvd, dtype=np.float32)).reshape(DEC_PROMPT, kvd)
+            for _ in range(2)]
+    x = host_head["embed_row"]
+    layer_s, runs = 0.0, 0
+    start = time.perf_counter()
+    while True:
+        sess = Session([hist[0]], [hist[1]])
+        t0 = time.perf_counter()
+        y = ref._layer(0, x, 1, DEC_PROMPT, sess)
+        layer_s += time.perf_counter() - t0
+        runs += 1
+        if time.perf_counter() - start >= seconds / 2:
+            break
+    t0 = time.perf_counter()
+    ref.logits(y.reshape(1, DEC_HIDDEN))
+    head_s = time.perf_counter() - t0
+    token_s = DEC_LAYERS * layer_s / runs + head_s
+    return {
+        "value": round(1.0 / token_s, 5),
+        "unit": "tokens/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"{runs} decode tokens through one full-width layer at position {DEC_PROMPT} "
+                   f"({layer_s / runs:.3f} s each) and one final norm + LM head ({head_s:.3f} s) of the "
+                   f"oracle decoder; extrapolated to {DEC_LAYERS} layers at batch 1"),
+    }
+
+
+def decoder_leg(torch, ctx, args, np):
+    """cfg5 through the C++ decoder runner (libmslim_host): batch-8 prefill of
+    seeded 4,096-token prompts in 512-token causal chunks, then `steps`
+    batched greedy decode steps over the ColdStore-exact paged K/V.  The same
+    run on the dense K/V layout must give the same tokens."""
+    from mslim_attn.model import Model, ModelSpec
+
+    log("bench: cfg5 decoder weights on device")
+    weights = decoder_weights(torch, seed=0x38423031)
+    spec = ModelSpec(DEC_LAYERS, DEC_HIDDEN, DEC_QH, DEC_KVH, DEC_D, DEC_FFN, DEC_VOCAB, 1e-5, 500000.0)
+    prompts = np.random.default_rng(20261202).integers(0, DEC_VOCAB, (DEC_BATCH, DEC_PROMPT))
+    steps = args.decoder_steps
+    runs = {}
+    for layout in ("paged", "dense"):
+        model = Model(ctx, spec, weights, max_batch=DEC_BATCH, chunk_tokens=DEC_CHUNK,
+                      max_context=DEC_PROMPT + steps, kv_layout=layout)
+        # untimed warm-up: one short prompt and one step (hipBLASLt plans)
+        model.prefill_only(0, list(prompts[0, :DEC_CHUNK + 1]))
+        model.forward_batch([0] * DEC_BATCH)
+        torch.cuda.synchronize()
+        log(f"bench: cfg5 prefill ({layout})")
+        t0 = time.perf_counter()
+        first = [model.prefill_only(b, list(prompts[b])) for b in range(DEC_BATCH)]
+        torch.cuda.synchronize()
+        prefill_s = time.perf_counter() - t0
+        log(f"bench: cfg5 {steps} decode steps ({layout})")
+        tokens, generated = first, [first]
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            tokens = model.forward_batch(tokens)
+            generated.append(tokens)
+        decode_s = time.perf_counter() - t0
+        runs[layout] = {"prefill_s": prefill_s, "decode_s": decode_s, "tokens": generated,
+                        "digest": model.logical_kv_sha256(0)}
+        model.close()
+    p = runs["paged"]
+    contexts = [DEC_PROMPT + i for i in range(steps)]
+    step_bytes = sum(decoder_step_bytes([c] * DEC_BATCH) for c in contexts) / steps
+    step_ms = p["decode_s"] / steps * 1e3
+    achieved = step_bytes / (step_ms * 1e-3) / 1e9
+    result = {
+        "workload": (f"BASELINE cfg5: Llama-3-8B-shaped decoder ({DEC_LAYERS} layers, hidden {DEC_HIDDEN}, "
+                     f"{DEC_QH}/{DEC_KVH} heads, d={DEC_D}, FFN {DEC_FFN}, vocab {DEC_VOCAB}), random N(0,0.02) "
+                     f"BF16 weights, batch {DEC_BATCH} seeded {DEC_PROMPT}-token prompts, {steps} greedy steps, "
+                     f"K/V in the ColdStore-exact 16-token page pool"),
+        "decode_tokens_per_s": round(DEC_BATCH * steps / p["decode_s"], 1),
+        "decode_ms_per_step": round(step_ms, 3),
+        "prefill_tokens_per_s": round(DEC_BATCH * DEC_PROMPT / p["prefill_s"], 1),
+        "prefill_s": round(p["prefill_s"], 3),
+        "timing": "host wall clock around whole calls (each call ends in a blocking read of the greedy tokens)",
+        "decode_roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBPS, 4),
+            "traffic": None,
+            "bytes_per_step": int(step_bytes),
+            "note": "algorithmic bytes per batched step (all weights + K/V histories) / wall time per step",
+        },
+        "paged_equals_dense_tokens": p["tokens"] == runs["dense"]["tokens"],
+        "paged_equals_dense_kv_sha256": p["digest"] == runs["dense"]["digest"],
+        "dense_decode_tokens_per_s": round(DEC_BATCH * steps / runs["dense"]["decode_s"], 1),
+    }
+    if args.cpu_seconds > 0:
+        log("bench: cfg5 CPU baseline (oracle decoder layer on one host core)")
+
+        def host(t):
+            return t.cpu().numpy().view(np.uint16).reshape(tuple(t.shape))
+
+        layer0 = {k: host(v) for k, v in weights.items() if k.startswith("layers.0.")}
+        head = {"final_norm": host(weights["final_norm"]), "lm_head": host(weights["lm_head"]),
+                "embed": host(weights["embed"][:1]), "embed_row": host(weights["embed"][int(prompts[0, 0])])}
+        result["cpu_baseline"] = cpu_decoder_baseline(layer0, head, args.cpu_seconds)
+    del weights
+    return result
+
+
 QUEUE_FILL_CYCLES = 2_000_000  # device sleep ahead of a timed loop (about 1 ms)
 COPY_BYTES = 1 << 30             # calibration copy: 1 GiB read + 1 GiB written
 
@@ -286,8 +457,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="CPU baseline budget per leg (0 skips the CPU baseline)")
-    ap.add_argument("--kernel", choices=("all", "decode", "prefill", "copy"), default="all",
+    ap.add_argument("--kernel", choices=("all", "decode", "prefill", "copy", "decoder"), default="all",
                     help="run one workload only, for counter collection")
+    ap.add_argument("--decoder-steps", type=int, default=DEC_STEPS,
+                    help="greedy steps of the cfg5 decoder leg (0 skips the leg)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
@@ -308,6 +481,10 @@ def main() -> int:
         return copy_only(torch, args)
     ctx = mslim_attn.Context()
     ctx.use_torch_stream()
+    if args.kernel == "decoder":
+        print(json.dumps(decoder_leg(torch, ctx, args, np)), flush=True)
+        ctx.close()
+        return 0
 
     log("bench: generating cfg4 inputs on device")
     gen = torch.Generator(device="cuda").manual_seed(0x4D534C49)
@@ -421,6 +598,8 @@ def main() -> int:
     traffic = measured_traffic("decode_paged_cfg4")
     pre_traffic = measured_traffic("prefill_causal_s8192")
 
+    decoder = decoder_leg(torch, ctx, args, np) if args.decoder_steps > 0 else None
+
     cpu = None
     if args.cpu_seconds > 0:
         log("bench: CPU baseline (oracle on host cores)")
@@ -495,11 +674,14 @@ def main() -> int:
         "decode_after_prefill_ms": round(dec_after_prefill, 5),
         "decode_dense_gbps": round(dense_gbps, 2),
         "paged_equals_dense": paged_equals_dense,
+        "decoder": decoder,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
     ctx.close()
-    return 0 if paged_equals_dense else 1
+    ok = paged_equals_dense and (decoder is None or (decoder["paged_equals_dense_tokens"]
+                                                     and decoder["paged_equals_dense_kv_sha256"]))
+    return 0 if ok else 1
 
 
 if __name__ == "__main__":
