@@ -366,9 +366,35 @@ int mslim_attn_matrix_multiply(void *ctx, const void *weight, const uint8_t *inp
 /* The same product on device buffers (input [tokens][inner], output
  * [tokens][rows]), stream-ordered: the form the device-resident layer
  * (norm -> QKV -> RoPE -> attention -> O -> SwiGLU -> down) chains without
- * host round trips.  output must not alias input or weight. */
+ * host round trips.  output must not alias input or weight.  Decode batches
+ * (tokens <= 16, inner a multiple of 32, input and weight 16-byte aligned)
+ * run on the library's MFMA kernel that streams the weights once, the role
+ * of the reference's decode GEMVs (llm_gemv_bf16 / reuse-8, gpu_llm.cl:38-68,
+ * :553-596); larger products go to hipBLASLt.  Both accumulate in fp32 in
+ * their own order: results agree within the rounding of the f64 product. */
 int mslim_attn_gemm_bf16(void *ctx, const void *weight, const void *input, void *output, int inner,
                          int rows, int tokens);
+
+/* output = BF16(residual + BF16(input . weight^T)): the O and down
+ * projections with the residual add of run_layer (gpu_llm/mod.rs:2056-2350;
+ * llm_add, gpu_llm.cl:214-222) fused.  Bit-identical to mslim_attn_gemm_bf16
+ * followed by mslim_attn_add.  output may equal residual. */
+int mslim_attn_gemm_bf16_add(void *ctx, const void *weight, const void *input, const void *residual,
+                             void *output, int inner, int rows, int tokens);
+
+/* output = SwiGLU(BF16(input . gate^T), BF16(input . up^T)) over
+ * [tokens][rows]: llm_fused_swiglu_bf16 (gpu_llm.cl:797-834,
+ * project_swiglu8 prefill.rs:247).  Bit-identical to two mslim_attn_gemm_bf16
+ * calls followed by mslim_attn_swiglu. */
+int mslim_attn_gemm_swiglu(void *ctx, const void *gate_weight, const void *up_weight, const void *input,
+                           void *output, int inner, int rows, int tokens);
+
+/* The Q, K and V projections of one input in one call: llm_fused_qkv_bf16
+ * (gpu_llm.cl:740-796, project_fused_qkv gpu_resources.rs:406-440).
+ * Bit-identical to three mslim_attn_gemm_bf16 calls. */
+int mslim_attn_gemm_qkv(void *ctx, const void *q_weight, const void *k_weight, const void *v_weight,
+                        const void *input, void *q_out, void *k_out, void *v_out, int inner, int q_rows,
+                        int kv_rows, int tokens);
 
 #ifdef __cplusplus
 }

@@ -85,3 +85,69 @@ def test_matrix_multiply_rejects_bad_arguments(ctx):
             ctx.matrix_multiply(wd, x, 0, 8, 1)
     finally:
         ctx.buf_free(wd)
+
+
+def dev_bits(bits):
+    return torch.from_numpy(np.ascontiguousarray(bits, np.uint16).view(np.int16).copy()).cuda()
+
+
+def host_bits(t):
+    return t.cpu().numpy().view(np.uint16).reshape(-1)
+
+
+@pytest.mark.parametrize("tokens", [1, 2, 7, 8, 15, 16, 17])
+@pytest.mark.parametrize("inner,rows", [(4096, 1000), (14336, 72), (64, 17)])
+def test_decode_batch_product_within_bound(ctx, inner, rows, tokens):
+    # tokens <= 16 with inner % 32 == 0 run the MFMA decode kernel (ragged row
+    # tiles, padded token columns); 17 takes hipBLASLt; same bound for both
+    rng = np.random.default_rng(inner * 31 + rows + tokens)
+    w, x = bf16(rng, rows * inner, 0.02), bf16(rng, tokens * inner)
+    out = torch.empty(tokens * rows, dtype=torch.int16, device="cuda")
+    ctx.gemm_bf16(dev_bits(w), dev_bits(x), out, inner, rows, tokens)
+    torch.cuda.synchronize()
+    assert within_bound(host_bits(out), w, x, inner, rows, tokens)
+
+
+def test_unaligned_inner_uses_library_path(ctx):
+    rng = np.random.default_rng(9)
+    inner, rows, tokens = 4104, 300, 4
+    w, x = bf16(rng, rows * inner, 0.02), bf16(rng, tokens * inner)
+    out = torch.empty(tokens * rows, dtype=torch.int16, device="cuda")
+    ctx.gemm_bf16(dev_bits(w), dev_bits(x), out, inner, rows, tokens)
+    torch.cuda.synchronize()
+    assert within_bound(host_bits(out), w, x, inner, rows, tokens)
+
+
+@pytest.mark.parametrize("tokens", [1, 8, 16, 17, 40])
+def test_fused_projections_equal_unfused(ctx, tokens):
+    # the fused entries are the unfused product followed by the elementwise
+    # kernel, bit for bit, on both sides of the decode-kernel token limit
+    rng = np.random.default_rng(tokens)
+    inner, qr, kvr, inter = 512, 256, 64, 704
+    x = dev_bits(bf16(rng, tokens * inner))
+    wq, wk, wv = (dev_bits(bf16(rng, r * inner, 0.05)) for r in (qr, kvr, kvr))
+    wg, wu = dev_bits(bf16(rng, inter * inner, 0.05)), dev_bits(bf16(rng, inter * inner, 0.05))
+    wo = dev_bits(bf16(rng, inner * qr, 0.05))
+    empty = lambda n: torch.empty(tokens * n, dtype=torch.int16, device="cuda")  # noqa: E731
+    q, k, v = empty(qr), empty(kvr), empty(kvr)
+    ctx.gemm_qkv(wq, wk, wv, x, q, k, v, inner, qr, kvr, tokens)
+    q2, k2, v2 = empty(qr), empty(kvr), empty(kvr)
+    ctx.gemm_bf16(wq, x, q2, inner, qr, tokens)
+    ctx.gemm_bf16(wk, x, k2, inner, kvr, tokens)
+    ctx.gemm_bf16(wv, x, v2, inner, kvr, tokens)
+    act, g, u, act2 = empty(inter), empty(inter), empty(inter), empty(inter)
+    ctx.gemm_swiglu(wg, wu, x, act, inner, inter, tokens)
+    ctx.gemm_bf16(wg, x, g, inner, inter, tokens)
+    ctx.gemm_bf16(wu, x, u, inner, inter, tokens)
+    ctx.swiglu(g, u, act2, tokens * inter)
+    # O projection with the residual, in place and out of place
+    resid = dev_bits(bf16(rng, tokens * inner, 2.0))
+    in_place, added, prod, added2 = resid.clone(), empty(inner), empty(inner), empty(inner)
+    ctx.gemm_bf16_add(wo, q, resid, added, qr, inner, tokens)
+    ctx.gemm_bf16_add(wo, q, in_place, in_place, qr, inner, tokens)
+    ctx.gemm_bf16(wo, q, prod, qr, inner, tokens)
+    ctx.add(resid, prod, added2, tokens * inner)
+    torch.cuda.synchronize()
+    assert torch.equal(q, q2) and torch.equal(k, k2) and torch.equal(v, v2)
+    assert torch.equal(act, act2)
+    assert torch.equal(added, added2) and torch.equal(in_place, added2)

@@ -52,12 +52,15 @@ struct Context {
     mslim::GemmState *gemm = nullptr;  // hipBLASLt handle and plans, created on first use
     void *gemm_in = nullptr, *gemm_out = nullptr;  // device staging of matrix_multiply
     size_t gemm_in_bytes = 0, gemm_out_bytes = 0;
+    void *fuse_tmp = nullptr;  // products of the fused entries above the skinny token limit
+    size_t fuse_tmp_bytes = 0;
 
     ~Context() {
         if (stream) (void)hipStreamSynchronize(stream);
         mslim::gemm_state_destroy(gemm);
         if (gemm_in) (void)hipFree(gemm_in);
         if (gemm_out) (void)hipFree(gemm_out);
+        if (fuse_tmp) (void)hipFree(fuse_tmp);
         if (workspace) (void)hipFree(workspace);
         if (counters) (void)hipFree(counters);
         if (staging) (void)hipFree(staging);
@@ -779,6 +782,24 @@ int mslim_attn_record_payloads(void *ctx, void *k_pool, void *v_pool, int64_t po
     return check_hip(mslim::launch_record_payloads(l, direction == 0, c.stream), "record payload launch");
 }
 
+// One product on the context's stream: the MFMA decode kernel for up to 16
+// aligned tokens, hipBLASLt otherwise.
+static int project(Context &c, const void *weight, const void *input, void *output, int inner, int rows,
+                   int tokens) {
+    if (mslim::skinny_supported(inner, tokens, input, weight)) {
+        const mslim::SkinnyMatrix m{static_cast<const uint16_t *>(weight), static_cast<uint16_t *>(output), rows};
+        return check_hip(mslim::launch_skinny_gemm(&m, 1, static_cast<const uint16_t *>(input), inner, tokens,
+                                                   c.stream),
+                         "decode projection launch")
+                   ? 404
+                   : 0;
+    }
+    std::string err;
+    if (int code = mslim::gemm_bf16(c.gemm, weight, input, output, inner, rows, tokens, c.stream, err))
+        return fail(err, code);
+    return 0;
+}
+
 // tv_hip_matrix_multiply's argument limits (hipblaslt_bridge.cpp:207-210).
 static bool gemm_args_ok(const void *ctx, const void *w, const void *in, const void *out, int inner, int rows,
                          int tokens) {
@@ -798,9 +819,7 @@ int mslim_attn_matrix_multiply(void *ctx, const void *weight, const uint8_t *inp
     if (grow_device(c, &c.gemm_out, &c.gemm_out_bytes, outsize, "hipMalloc BF16 output")) return 401;
     if (check_hip(hipMemcpyAsync(c.gemm_in, input, insize, hipMemcpyHostToDevice, c.stream), "BF16 matrix input H2D"))
         return 402;
-    std::string err;
-    if (int code = mslim::gemm_bf16(c.gemm, weight, c.gemm_in, c.gemm_out, inner, rows, tokens, c.stream, err))
-        return fail(err, code);
+    if (int rc = project(c, weight, c.gemm_in, c.gemm_out, inner, rows, tokens)) return rc;
     if (check_hip(hipMemcpyAsync(output, c.gemm_out, outsize, hipMemcpyDeviceToHost, c.stream),
                   "BF16 matrix output D2H"))
         return 405;
@@ -815,10 +834,90 @@ int mslim_attn_gemm_bf16(void *ctx, const void *weight, const void *input, void 
     if (output == input || output == weight) return fail("GEMM output must not alias its inputs");
     Context &c = *ctx_of(ctx);
     Lock lock(c);
-    std::string err;
-    if (int code = mslim::gemm_bf16(c.gemm, weight, input, output, inner, rows, tokens, c.stream, err))
-        return fail(err, code);
-    return 0;
+    return project(c, weight, input, output, inner, rows, tokens);
+}
+
+int mslim_attn_gemm_bf16_add(void *ctx, const void *weight, const void *input, const void *residual,
+                             void *output, int inner, int rows, int tokens) {
+    g_error.clear();
+    if (!gemm_args_ok(ctx, weight, input, output, inner, rows, tokens) || !residual)
+        return fail("invalid BF16 matrix dimensions/arguments");
+    if (output == input || output == weight || residual == input)
+        return fail("GEMM output must not alias its inputs");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    const auto *w = static_cast<const uint16_t *>(weight);
+    const auto *x = static_cast<const uint16_t *>(input);
+    if (mslim::skinny_supported(inner, tokens, input, weight)) {
+        const mslim::SkinnyMatrix m{w, static_cast<uint16_t *>(output), rows};
+        return check_hip(mslim::launch_skinny_gemm_add(m, static_cast<const uint16_t *>(residual), x, inner,
+                                                       tokens, c.stream),
+                         "decode projection launch")
+                   ? 404
+                   : 0;
+    }
+    const size_t n = (size_t)rows * tokens;
+    if (grow_device(c, &c.fuse_tmp, &c.fuse_tmp_bytes, n * 2, "hipMalloc projection scratch")) return 400;
+    if (int rc = project(c, weight, input, c.fuse_tmp, inner, rows, tokens)) return rc;
+    return check_hip(mslim::launch_add(static_cast<const uint16_t *>(residual),
+                                       static_cast<const uint16_t *>(c.fuse_tmp), static_cast<uint16_t *>(output),
+                                       n, c.stream),
+                     "residual add launch");
+}
+
+int mslim_attn_gemm_swiglu(void *ctx, const void *gate_weight, const void *up_weight, const void *input,
+                           void *output, int inner, int rows, int tokens) {
+    g_error.clear();
+    if (!gemm_args_ok(ctx, gate_weight, input, output, inner, rows, tokens) || !up_weight)
+        return fail("invalid BF16 matrix dimensions/arguments");
+    if (output == input || output == gate_weight || output == up_weight)
+        return fail("GEMM output must not alias its inputs");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    const auto *x = static_cast<const uint16_t *>(input);
+    if (mslim::skinny_supported(inner, tokens, input, gate_weight, up_weight)) {
+        return check_hip(mslim::launch_skinny_swiglu(static_cast<const uint16_t *>(gate_weight),
+                                                     static_cast<const uint16_t *>(up_weight),
+                                                     static_cast<uint16_t *>(output), rows, x, inner, tokens,
+                                                     c.stream),
+                         "decode projection launch")
+                   ? 404
+                   : 0;
+    }
+    const size_t n = (size_t)rows * tokens;
+    if (grow_device(c, &c.fuse_tmp, &c.fuse_tmp_bytes, n * 4, "hipMalloc projection scratch")) return 400;
+    uint16_t *gate = static_cast<uint16_t *>(c.fuse_tmp), *up = gate + n;
+    if (int rc = project(c, gate_weight, input, gate, inner, rows, tokens)) return rc;
+    if (int rc = project(c, up_weight, input, up, inner, rows, tokens)) return rc;
+    return check_hip(mslim::launch_swiglu(gate, up, static_cast<uint16_t *>(output), n, c.stream),
+                     "SwiGLU launch");
+}
+
+int mslim_attn_gemm_qkv(void *ctx, const void *q_weight, const void *k_weight, const void *v_weight,
+                        const void *input, void *q_out, void *k_out, void *v_out, int inner, int q_rows,
+                        int kv_rows, int tokens) {
+    g_error.clear();
+    if (!gemm_args_ok(ctx, q_weight, input, q_out, inner, q_rows, tokens) ||
+        !gemm_args_ok(ctx, k_weight, input, k_out, inner, kv_rows, tokens) ||
+        !gemm_args_ok(ctx, v_weight, input, v_out, inner, kv_rows, tokens))
+        return fail("invalid BF16 matrix dimensions/arguments");
+    if (q_out == input || k_out == input || v_out == input) return fail("GEMM output must not alias its inputs");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    if (mslim::skinny_supported(inner, tokens, input, q_weight, k_weight, v_weight)) {
+        const mslim::SkinnyMatrix m[3] = {
+            {static_cast<const uint16_t *>(q_weight), static_cast<uint16_t *>(q_out), q_rows},
+            {static_cast<const uint16_t *>(k_weight), static_cast<uint16_t *>(k_out), kv_rows},
+            {static_cast<const uint16_t *>(v_weight), static_cast<uint16_t *>(v_out), kv_rows}};
+        return check_hip(mslim::launch_skinny_gemm(m, 3, static_cast<const uint16_t *>(input), inner, tokens,
+                                                   c.stream),
+                         "decode projection launch")
+                   ? 404
+                   : 0;
+    }
+    if (int rc = project(c, q_weight, input, q_out, inner, q_rows, tokens)) return rc;
+    if (int rc = project(c, k_weight, input, k_out, inner, kv_rows, tokens)) return rc;
+    return project(c, v_weight, input, v_out, inner, kv_rows, tokens);
 }
 
 }  // extern "C"

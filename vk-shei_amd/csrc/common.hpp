@@ -30,6 +30,16 @@ __device__ __forceinline__ uint16_t write_bf16(float value) {
 
 __device__ __forceinline__ float round_bf16(float value) { return read_bf16(write_bf16(value)); }
 
+// llm_swiglu's arithmetic (gpu_llm.cl:225-237) on BF16 gate and up values:
+// BF16(BF16(g / (1 + e^-g)) * u), e^-g evaluated in double and rounded once,
+// every other step correctly rounded in f32.
+__device__ __forceinline__ uint16_t swiglu_bf16(uint16_t gate, uint16_t up) {
+    const float g = read_bf16(gate);
+    const float e = (float)exp(-(double)g);
+    const float activated = __fdiv_rn(g, __fadd_rn(1.0f, e));
+    return write_bf16(__fmul_rn(round_bf16(activated), read_bf16(up)));
+}
+
 // IEEE binary16 -> f32, exact for every encoding (subnormals, inf, NaN
 // payloads) through the hardware conversion.
 __device__ __forceinline__ float half_to_float(uint16_t bits) {

@@ -45,6 +45,69 @@ __global__ __launch_bounds__(128) void rmsnorm_kernel(const uint16_t *in, const 
     }
 }
 
+// The same RMSNorm with the row and the weights staged in LDS by 16-byte
+// loads, all issued before the first wait, and the output written back by
+// 16-byte stores.  Lane `tid` still sums elements tid, tid+128, ... in order
+// and the tree is unchanged, so the result is bit-identical to rmsnorm_kernel;
+// what changes is that the row no longer arrives as 32 dependent 2-byte loads
+// per lane.  hidden % 8 == 0 and hidden <= kRmsStagedMax; dynamic LDS
+// 4 * hidden bytes.
+constexpr int kRmsStagedMax = 8192;  // 32 KiB of dynamic LDS
+constexpr int kRmsLoadsInFlight = 4;
+
+__global__ __launch_bounds__(128) void rmsnorm_staged_kernel(const uint16_t *in, const uint16_t *w,
+                                                             uint16_t *out, int hidden, float eps) {
+    extern __shared__ uint4 staged[];
+    __shared__ float partials[128];
+    uint16_t *row = reinterpret_cast<uint16_t *>(staged);
+    const uint16_t *wt = row + hidden;
+    const int tid = threadIdx.x;
+    const int chunks = hidden / 8;
+    const uint4 *src = reinterpret_cast<const uint4 *>(in + (int64_t)blockIdx.x * hidden);
+    const uint4 *wsrc = reinterpret_cast<const uint4 *>(w);
+    for (int base = tid; base < chunks; base += 128 * kRmsLoadsInFlight) {
+        uint4 a[kRmsLoadsInFlight], b[kRmsLoadsInFlight];
+#pragma unroll
+        for (int u = 0; u < kRmsLoadsInFlight; ++u) {
+            const int c = base + u * 128;
+            if (c < chunks) {
+                a[u] = src[c];
+                b[u] = wsrc[c];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kRmsLoadsInFlight; ++u) {
+            const int c = base + u * 128;
+            if (c < chunks) {
+                staged[c] = a[u];
+                staged[chunks + c] = b[u];
+            }
+        }
+    }
+    __syncthreads();
+    float s = 0.0f;
+    for (int i = tid; i < hidden; i += 128) {
+        const float v = read_bf16(row[i]);
+        s = __fmaf_rn(v, v, s);
+    }
+    partials[tid] = s;
+    __syncthreads();
+    for (int stride = 64; stride > 0; stride >>= 1) {
+        if (tid < stride) partials[tid] = __fadd_rn(partials[tid], partials[tid + stride]);
+        __syncthreads();
+    }
+    const float mean = __fdiv_rn(partials[0], (float)hidden);
+    const float factor = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, eps)));
+    // each lane rewrites only the elements it read, so in place is safe
+    for (int i = tid; i < hidden; i += 128) {
+        const uint16_t normalized = write_bf16(__fmul_rn(read_bf16(row[i]), factor));
+        row[i] = write_bf16(__fmul_rn(read_bf16(normalized), read_bf16(wt[i])));
+    }
+    __syncthreads();
+    uint4 *dst = reinterpret_cast<uint4 *>(out + (int64_t)blockIdx.x * hidden);
+    for (int c = tid; c < chunks; c += 128) dst[c] = staged[c];
+}
+
 // Inverse frequency of rotary dimension pair `fd` (kernels.rs:51-66,
 // gpu_llm.cl:123-138), f32 arithmetic with once-rounded log and exp.
 __device__ float rope_inverse_frequency(int fd, int head_dim, float theta, int llama3, float factor,
@@ -104,10 +167,7 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t *gate, const
                                                      uint16_t *out, int64_t n) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    const float g = read_bf16(gate[i]);
-    const float e = (float)exp(-(double)g);
-    const float activated = __fdiv_rn(g, __fadd_rn(1.0f, e));
-    out[i] = write_bf16(__fmul_rn(round_bf16(activated), read_bf16(up[i])));
+    out[i] = swiglu_bf16(gate[i], up[i]);
 }
 
 // Residual add with one BF16 rounding (llm_add, gpu_llm.cl:214-222).
@@ -133,29 +193,61 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint16_t *table, const
 }
 
 // Greedy token of each row of BF16 logits (llm_argmax, gpu_llm.cl:239-270),
-// one workgroup of 256 per row.  Every lane starts from (-inf, index 0) and
-// takes a value that is greater, or equal with a lower index: NaN never wins,
-// the first index wins ties, and a row with nothing above -inf gives 0.  The
-// result is the same for any lane count.
-__global__ __launch_bounds__(256) void argmax_kernel(const uint16_t *logits, int rows, int vocab, int32_t *out) {
-    __shared__ float values[256];
-    __shared__ int indices[256];
+// one workgroup of 1024 lanes per row.  Every lane starts from (-inf, index 0)
+// and takes a value that is greater, or equal with a lower index: NaN never
+// wins, the first index wins ties, and a row with nothing above -inf gives 0.
+// That rule makes the result independent of how elements are split over
+// lanes, so VEC lanes read 8 logits per 16-byte load (rows 16-byte aligned,
+// vocab % 8 == 0), four loads in flight.
+constexpr int kArgmaxThreads = 1024;
+
+__device__ __forceinline__ void argmax_take(float x, int i, float &best, int &index) {
+    if (x > best || (x == best && i < index)) {
+        best = x;
+        index = i;
+    }
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const uint16_t *logits, int rows, int vocab,
+                                                                int32_t *out) {
+    __shared__ float values[kArgmaxThreads];
+    __shared__ int indices[kArgmaxThreads];
     const int row = blockIdx.x;
     const int tid = threadIdx.x;
     const uint16_t *l = logits + (int64_t)row * vocab;
     float best = -INFINITY;
     int index = 0;
-    for (int i = tid; i < vocab; i += 256) {
-        const float x = read_bf16(l[i]);
-        if (x > best || (x == best && i < index)) {
-            best = x;
-            index = i;
+    if (VEC) {
+        const uint4 *l4 = reinterpret_cast<const uint4 *>(l);
+        const int chunks = vocab / 8;
+        constexpr int U = 4;
+        for (int base = tid; base < chunks; base += kArgmaxThreads * U) {
+            uint4 v[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int c = base + u * kArgmaxThreads;
+                if (c < chunks) v[u] = l4[c];
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int c = base + u * kArgmaxThreads;
+                if (c >= chunks) break;
+                const uint32_t words[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    argmax_take(read_bf16((uint16_t)(words[k] & 0xffffu)), c * 8 + 2 * k, best, index);
+                    argmax_take(read_bf16((uint16_t)(words[k] >> 16)), c * 8 + 2 * k + 1, best, index);
+                }
+            }
         }
+    } else {
+        for (int i = tid; i < vocab; i += kArgmaxThreads) argmax_take(read_bf16(l[i]), i, best, index);
     }
     values[tid] = best;
     indices[tid] = index;
     __syncthreads();
-    for (int stride = 128; stride > 0; stride >>= 1) {
+    for (int stride = kArgmaxThreads / 2; stride > 0; stride >>= 1) {
         if (tid < stride) {
             const float ov = values[tid + stride];
             const int oi = indices[tid + stride];
@@ -173,8 +265,14 @@ __global__ __launch_bounds__(256) void argmax_kernel(const uint16_t *logits, int
 
 hipError_t launch_rmsnorm(const uint16_t *in, const uint16_t *w, uint16_t *out, int tokens,
                           int hidden, float eps, hipStream_t stream) {
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)tokens), dim3(128), 0, stream, in, w, out, hidden,
-                       eps);
+    const bool aligned = ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(w) |
+                           reinterpret_cast<uintptr_t>(out)) & 15) == 0;
+    if (aligned && hidden % 8 == 0 && hidden <= kRmsStagedMax)
+        hipLaunchKernelGGL(rmsnorm_staged_kernel, dim3((unsigned)tokens), dim3(128), (size_t)hidden * 4, stream,
+                           in, w, out, hidden, eps);
+    else
+        hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)tokens), dim3(128), 0, stream, in, w, out, hidden,
+                           eps);
     return hipGetLastError();
 }
 
@@ -209,7 +307,12 @@ hipError_t launch_embed(const uint16_t *table, const int32_t *ids, int tokens, i
 }
 
 hipError_t launch_argmax(const uint16_t *logits, int rows, int vocab, int32_t *out, hipStream_t stream) {
-    hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)rows), dim3(256), 0, stream, logits, rows, vocab, out);
+    if (vocab % 8 == 0 && (reinterpret_cast<uintptr_t>(logits) & 15) == 0)
+        hipLaunchKernelGGL(argmax_kernel<true>, dim3((unsigned)rows), dim3(kArgmaxThreads), 0, stream, logits, rows,
+                           vocab, out);
+    else
+        hipLaunchKernelGGL(argmax_kernel<false>, dim3((unsigned)rows), dim3(kArgmaxThreads), 0, stream, logits, rows,
+                           vocab, out);
     return hipGetLastError();
 }
 

@@ -128,6 +128,25 @@ void gemm_state_destroy(GemmState *state);
 int gemm_bf16(GemmState *&state, const void *weight, const void *input, void *output, int inner, int rows,
               int tokens, hipStream_t stream, std::string &err);
 
+// Decode-batch projections on MFMA (tokens <= kSkinnyMaxTokens, inner a
+// multiple of 32, x and weights 16-byte aligned): out[t][r] =
+// BF16(sum_k x[t][k] w[r][k]) for up to three matrices in one launch, or with
+// a residual-add or SwiGLU epilogue equal to the unfused elementwise kernels.
+constexpr int kSkinnyMaxTokens = 16;
+struct SkinnyMatrix {
+    const uint16_t *w;  // [rows][inner]
+    uint16_t *out;      // [tokens][rows]
+    int rows;
+};
+bool skinny_supported(int inner, int tokens, const void *x, const void *w0, const void *w1 = nullptr,
+                      const void *w2 = nullptr);
+hipError_t launch_skinny_gemm(const SkinnyMatrix *m, int count, const uint16_t *x, int inner, int tokens,
+                              hipStream_t stream);
+hipError_t launch_skinny_gemm_add(const SkinnyMatrix &m, const uint16_t *resid, const uint16_t *x, int inner,
+                                  int tokens, hipStream_t stream);
+hipError_t launch_skinny_swiglu(const uint16_t *w_gate, const uint16_t *w_up, uint16_t *out, int rows,
+                                const uint16_t *x, int inner, int tokens, hipStream_t stream);
+
 hipError_t launch_pages_write(uint16_t *k_pool, uint16_t *v_pool, const int32_t *page_table,
                               int page_tokens, int kv_heads, int head_dim, int64_t first_token,
                               int64_t tokens, const uint16_t *k_rows, const uint16_t *v_rows,

@@ -78,9 +78,6 @@ DecoderRunner::DecoderRunner(std::shared_ptr<NativeContext> ctx, ModelSpec spec,
         k_ = static_cast<uint16_t *>(alloc(r * kvd * 2));
         kr_ = static_cast<uint16_t *>(alloc(r * kvd * 2));
         v_ = static_cast<uint16_t *>(alloc(r * kvd * 2));
-        proj_ = static_cast<uint16_t *>(alloc(r * spec_.hidden * 2));
-        gate_ = static_cast<uint16_t *>(alloc(r * spec_.intermediate * 2));
-        up_ = static_cast<uint16_t *>(alloc(r * spec_.intermediate * 2));
         act_ = static_cast<uint16_t *>(alloc(r * spec_.intermediate * 2));
         if (layout_ == KvLayout::Paged) {
             kd_ = static_cast<uint16_t *>(alloc((size_t)max_context_ * kvd * 2));
@@ -130,9 +127,7 @@ void DecoderRunner::chunk(int seq, const int32_t *ids, int n, int64_t prior) {
     for (int l = 0; l < s.layers; ++l) {
         const LayerWeights &w = w_.layers[l];
         ctx_->check("input norm", mslim_attn_rmsnorm(h, x_, w.input_norm, norm_, n, s.hidden, s.rms_eps));
-        gemm(w.q, norm_, q_, s.hidden, qd, n);
-        gemm(w.k, norm_, k_, s.hidden, kvd, n);
-        gemm(w.v, norm_, v_, s.hidden, kvd, n);
+        ctx_->check("QKV projection", mslim_attn_gemm_qkv(h, w.q, w.k, w.v, norm_, q_, k_, v_, s.hidden, qd, kvd, n));
         ctx_->check("query RoPE", mslim_attn_rope(h, q_, qr_, n, s.q_heads, s.head_dim, (int)prior, s.rope_theta,
                                                   s.llama3, s.rope_factor, s.rope_low, s.rope_high,
                                                   s.rope_original_max));
@@ -157,15 +152,21 @@ void DecoderRunner::chunk(int seq, const int32_t *ids, int n, int64_t prior) {
         }
         ctx_->check("causal attention", mslim_attn_prefill_causal(h, qr_, keys, values, attn_, n, (int)prior,
                                                                   s.q_heads, s.kv_heads, s.head_dim, scale_));
-        gemm(w.o, attn_, proj_, qd, s.hidden, n);
-        ctx_->check("attention residual", mslim_attn_add(h, x_, proj_, x_, (size_t)n * s.hidden));
-        ctx_->check("post norm", mslim_attn_rmsnorm(h, x_, w.post_norm, norm_, n, s.hidden, s.rms_eps));
-        gemm(w.gate, norm_, gate_, s.hidden, s.intermediate, n);
-        gemm(w.up, norm_, up_, s.hidden, s.intermediate, n);
-        ctx_->check("swiglu", mslim_attn_swiglu(h, gate_, up_, act_, (size_t)n * s.intermediate));
-        gemm(w.down, act_, proj_, s.intermediate, s.hidden, n);
-        ctx_->check("mlp residual", mslim_attn_add(h, x_, proj_, x_, (size_t)n * s.hidden));
+        mlp(w, n);
     }
+}
+
+// O projection + residual, post norm, gate/up + SwiGLU, down + residual over
+// `n` rows of x_ (attention output in attn_).
+void DecoderRunner::mlp(const LayerWeights &w, int n) {
+    void *h = ctx_->handle();
+    const ModelSpec &s = spec_;
+    const int qd = s.q_heads * s.head_dim;
+    ctx_->check("O projection + residual", mslim_attn_gemm_bf16_add(h, w.o, attn_, x_, x_, qd, s.hidden, n));
+    ctx_->check("post norm", mslim_attn_rmsnorm(h, x_, w.post_norm, norm_, n, s.hidden, s.rms_eps));
+    ctx_->check("gate/up + SwiGLU", mslim_attn_gemm_swiglu(h, w.gate, w.up, norm_, act_, s.hidden, s.intermediate, n));
+    ctx_->check("down projection + residual",
+                mslim_attn_gemm_bf16_add(h, w.down, act_, x_, x_, s.intermediate, s.hidden, n));
 }
 
 Step DecoderRunner::prefill_only(int seq, const std::vector<int32_t> &prompt) {
@@ -210,9 +211,7 @@ std::vector<Step> DecoderRunner::forward_batch(const std::vector<int32_t> &token
     for (int l = 0; l < s.layers; ++l) {
         const LayerWeights &w = w_.layers[l];
         ctx_->check("input norm", mslim_attn_rmsnorm(h, x_, w.input_norm, norm_, b, s.hidden, s.rms_eps));
-        gemm(w.q, norm_, q_, s.hidden, qd, b);
-        gemm(w.k, norm_, k_, s.hidden, kvd, b);
-        gemm(w.v, norm_, v_, s.hidden, kvd, b);
+        ctx_->check("QKV projection", mslim_attn_gemm_qkv(h, w.q, w.k, w.v, norm_, q_, k_, v_, s.hidden, qd, kvd, b));
         ctx_->check("query RoPE", mslim_attn_rope_rows(h, q_, qr_, b, s.q_heads, s.head_dim, pos_, s.rope_theta,
                                                        s.llama3, s.rope_factor, s.rope_low, s.rope_high,
                                                        s.rope_original_max));
@@ -230,14 +229,7 @@ std::vector<Step> DecoderRunner::forward_batch(const std::vector<int32_t> &token
                         mslim_attn_decode_paged(h, qr_, k_pools_[l], v_pools_[l], attn_, b, lens.data(), table_,
                                                 pages_per_seq_, kPageTokens, s.q_heads, s.kv_heads, s.head_dim,
                                                 scale_, 0));
-        gemm(w.o, attn_, proj_, qd, s.hidden, b);
-        ctx_->check("attention residual", mslim_attn_add(h, x_, proj_, x_, (size_t)b * s.hidden));
-        ctx_->check("post norm", mslim_attn_rmsnorm(h, x_, w.post_norm, norm_, b, s.hidden, s.rms_eps));
-        gemm(w.gate, norm_, gate_, s.hidden, s.intermediate, b);
-        gemm(w.up, norm_, up_, s.hidden, s.intermediate, b);
-        ctx_->check("swiglu", mslim_attn_swiglu(h, gate_, up_, act_, (size_t)b * s.intermediate));
-        gemm(w.down, act_, proj_, s.intermediate, s.hidden, b);
-        ctx_->check("mlp residual", mslim_attn_add(h, x_, proj_, x_, (size_t)b * s.hidden));
+        mlp(w, b);
     }
     head(x_, b);
     std::vector<int32_t> next(b);

@@ -93,6 +93,7 @@ private:
     void chunk(int seq, const int32_t *ids, int n, int64_t prior);
     void gemm(const void *w, const void *in, void *out, int inner, int rows, int tokens);
     void head(const uint16_t *rows_in, int rows);
+    void mlp(const LayerWeights &w, int n);
     const int32_t *table_row(int seq) const { return table_ + (int64_t)seq * pages_per_seq_; }
     // Dense layout: token-major rows of slot `seq` in a layer pool.
     const uint16_t *dense_rows(const void *pool, int seq) const {
@@ -110,7 +111,7 @@ private:
     std::vector<void *> k_pools_, v_pools_;
     int32_t *table_ = nullptr, *ids_ = nullptr, *pos_ = nullptr, *next_ = nullptr;
     uint16_t *x_ = nullptr, *norm_ = nullptr, *q_ = nullptr, *k_ = nullptr, *v_ = nullptr, *qr_ = nullptr,
-             *kr_ = nullptr, *attn_ = nullptr, *proj_ = nullptr, *gate_ = nullptr, *up_ = nullptr, *act_ = nullptr,
+             *kr_ = nullptr, *attn_ = nullptr, *act_ = nullptr,
              *kd_ = nullptr, *vd_ = nullptr, *logits_ = nullptr;
     int logits_rows_ = 0;
 };

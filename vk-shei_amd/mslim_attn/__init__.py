@@ -72,6 +72,9 @@ EXPORTS = (
     "mslim_attn_record_payloads",
     "mslim_attn_matrix_multiply",
     "mslim_attn_gemm_bf16",
+    "mslim_attn_gemm_bf16_add",
+    "mslim_attn_gemm_swiglu",
+    "mslim_attn_gemm_qkv",
     "mslim_attn_add",
     "mslim_attn_embed",
     "mslim_attn_argmax",
@@ -143,6 +146,9 @@ def library() -> C.CDLL:
         "mslim_attn_record_payloads": (I, [P, P, P, I64, I, I, I, P, I, P, P, I]),
         "mslim_attn_matrix_multiply": (I, [P, P, P, P, I, I, I]),
         "mslim_attn_gemm_bf16": (I, [P, P, P, P, I, I, I]),
+        "mslim_attn_gemm_bf16_add": (I, [P, P, P, P, P, I, I, I]),
+        "mslim_attn_gemm_swiglu": (I, [P, P, P, P, P, I, I, I]),
+        "mslim_attn_gemm_qkv": (I, [P, P, P, P, P, P, P, P, I, I, I, I]),
         "mslim_attn_add": (I, [P, P, P, P, SZ]),
         "mslim_attn_embed": (I, [P, P, I, I, P, I, P, P]),
         "mslim_attn_argmax": (I, [P, P, I, I, P]),
@@ -394,6 +400,23 @@ class Context:
     def gemm_bf16(self, weight, input_dev, output_dev, inner: int, rows: int, tokens: int) -> None:
         self._check("gemm_bf16", self._lib.mslim_attn_gemm_bf16(
             self._h, _ptr(weight), _ptr(input_dev), _ptr(output_dev), inner, rows, tokens))
+
+    def gemm_bf16_add(self, weight, input_dev, residual, output_dev, inner: int, rows: int,
+                      tokens: int) -> None:
+        self._check("gemm_bf16_add", self._lib.mslim_attn_gemm_bf16_add(
+            self._h, _ptr(weight), _ptr(input_dev), _ptr(residual), _ptr(output_dev), inner, rows, tokens))
+
+    def gemm_swiglu(self, gate_weight, up_weight, input_dev, output_dev, inner: int, rows: int,
+                    tokens: int) -> None:
+        self._check("gemm_swiglu", self._lib.mslim_attn_gemm_swiglu(
+            self._h, _ptr(gate_weight), _ptr(up_weight), _ptr(input_dev), _ptr(output_dev), inner, rows,
+            tokens))
+
+    def gemm_qkv(self, q_weight, k_weight, v_weight, input_dev, q_out, k_out, v_out, inner: int,
+                 q_rows: int, kv_rows: int, tokens: int) -> None:
+        self._check("gemm_qkv", self._lib.mslim_attn_gemm_qkv(
+            self._h, _ptr(q_weight), _ptr(k_weight), _ptr(v_weight), _ptr(input_dev), _ptr(q_out),
+            _ptr(k_out), _ptr(v_out), inner, q_rows, kv_rows, tokens))
 
     def add(self, a, b, out, n: int) -> None:
         self._check("add", self._lib.mslim_attn_add(self._h, _ptr(a), _ptr(b), _ptr(out), n))
