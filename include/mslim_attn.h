@@ -269,6 +269,20 @@ int mslim_attn_pages_append(void *ctx, void *k_pool, void *v_pool, const int32_t
                             int batch, const int32_t *positions, const void *k_rows,
                             const void *v_rows);
 
+/* One decode step's RoPE and K/V append in a single launch: Q rows
+ * ([batch][q_heads][head_dim]) rotated to q_out, K rows rotated and written
+ * with the V rows ([batch][kv_heads][head_dim]) to logical position
+ * positions[b] of sequence b through page-table row b.  Equal, bit for bit, to
+ * mslim_attn_rope_rows on Q and on K followed by mslim_attn_pages_append of
+ * the rotated K and V.  The reference runs the two llm_rope launches and the
+ * K/V copies of run_layer separately (gpu_llm/mod.rs:2094-2136). */
+int mslim_attn_rope_append(void *ctx, const void *q, const void *k, const void *v, void *q_out,
+                           void *k_pool, void *v_pool, const int32_t *page_table, int pages_per_seq,
+                           int page_tokens, int batch, const int32_t *positions, int q_heads,
+                           int kv_heads, int head_dim, float theta, int llama3_scaling, float factor,
+                           float low_freq_factor, float high_freq_factor,
+                           float original_max_position);
+
 /* Gather `tokens` logical positions [first_token, first_token+tokens) of one
  * sequence from a page pool into token-major rows [tokens][kv_heads][head_dim].
  * The device counterpart of GpuRegionStore::read_keys / read_values

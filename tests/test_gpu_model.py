@@ -147,6 +147,29 @@ def test_pages_append_matches_pages_write(ctx):
     assert torch.equal(k_c, k_a) and torch.equal(v_c, v_a)
 
 
+@pytest.mark.parametrize("page_tokens,llama3", [(16, False), (16, True), (1, False)])
+def test_rope_append_equals_rope_then_append(ctx, page_tokens, llama3):
+    rng = np.random.default_rng(page_tokens + 2 * llama3)
+    qh, kvh, d, batch = 8, 2, 128, 5
+    pps = 96 // page_tokens
+    pool_pages = batch * pps
+    table = _dev_i32(rng.permutation(pool_pages).astype(np.int32).reshape(batch, pps))
+    positions = _dev_i32([0, 17, 95, 96, 40])  # 96 is past the slot: Q rotates, K/V not written
+    params = (8.0, 1.0, 4.0, 8192.0) if llama3 else (1.0, 1.0, 2.0, 1.0)
+    q, k, v = (to_torch(normal_bf16(rng, (batch, h, d))) for h in (qh, kvh, kvh))
+    shape = (pool_pages, kvh, page_tokens, d)
+    k_a, v_a = (to_torch(normal_bf16(rng, shape)) for _ in range(2))
+    k_b, v_b = k_a.clone(), v_a.clone()
+    q_a, q_b, k_r = torch.empty_like(q), torch.empty_like(q), torch.empty_like(k)
+    ctx.rope_append(q, k, v, q_a, k_a, v_a, table, pps, page_tokens, batch, positions, qh, kvh, d, 500000.0,
+                    llama3, *params)
+    ctx.rope_rows(q, q_b, batch, qh, d, positions, 500000.0, llama3, *params)
+    ctx.rope_rows(k, k_r, batch, kvh, d, positions, 500000.0, llama3, *params)
+    ctx.pages_append(k_b, v_b, table, pps, page_tokens, kvh, d, batch, positions, k_r, v)
+    torch.cuda.synchronize()
+    assert torch.equal(q_a, q_b) and torch.equal(k_a, k_b) and torch.equal(v_a, v_b)
+
+
 # ---- decoder runner ------------------------------------------------------------
 
 SPEC = Spec(layers=2, hidden=256, q_heads=8, kv_heads=2, head_dim=64, intermediate=512, vocab=1000)

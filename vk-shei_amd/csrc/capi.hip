@@ -642,6 +642,47 @@ int mslim_attn_pages_append(void *ctx, void *k_pool, void *v_pool, const int32_t
                      "page append launch");
 }
 
+int mslim_attn_rope_append(void *ctx, const void *q, const void *k, const void *v, void *q_out, void *k_pool,
+                           void *v_pool, const int32_t *page_table, int pages_per_seq, int page_tokens, int batch,
+                           const int32_t *positions, int q_heads, int kv_heads, int head_dim, float theta,
+                           int llama3_scaling, float factor, float low_freq_factor, float high_freq_factor,
+                           float original_max_position) {
+    g_error.clear();
+    if (!ctx || !q || !k || !v || !q_out || !k_pool || !v_pool || !page_table || !positions || batch < 1 ||
+        pages_per_seq < 1 || q_heads < 1 || kv_heads < 1 || head_dim < 8 || head_dim % 8 ||
+        !is_pow2(page_tokens) || page_tokens > (1 << 20) || !(theta > 0.0f) || !std::isfinite(theta))
+        return fail("invalid RoPE append arguments");
+    if (q_out == q) return fail("RoPE output must not alias its input");
+    if (llama3_scaling && (!(factor > 0.0f) || !(high_freq_factor > low_freq_factor) ||
+                           !(low_freq_factor > 0.0f) || !(original_max_position > 0.0f)))
+        return fail("invalid llama3 RoPE scaling parameters");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    mslim::RopeAppendArgs a{};
+    a.q = static_cast<const uint16_t *>(q);
+    a.k = static_cast<const uint16_t *>(k);
+    a.v = static_cast<const uint16_t *>(v);
+    a.q_out = static_cast<uint16_t *>(q_out);
+    a.k_pool = static_cast<uint16_t *>(k_pool);
+    a.v_pool = static_cast<uint16_t *>(v_pool);
+    a.page_table = page_table;
+    a.positions = positions;
+    a.pages_per_seq = pages_per_seq;
+    a.shift = 0;
+    while ((1 << a.shift) < page_tokens) ++a.shift;
+    a.batch = batch;
+    a.q_heads = q_heads;
+    a.kv_heads = kv_heads;
+    a.head_dim = head_dim;
+    a.theta = theta;
+    a.llama3 = llama3_scaling;
+    a.factor = factor;
+    a.low = low_freq_factor;
+    a.high = high_freq_factor;
+    a.original_max = original_max_position;
+    return check_hip(mslim::launch_rope_append(a, c.stream), "RoPE append launch");
+}
+
 int mslim_attn_pages_gather(void *ctx, const void *pool, const int32_t *page_table, int page_tokens,
                             int kv_heads, int head_dim, int64_t first_token, int64_t tokens,
                             void *rows_out) {

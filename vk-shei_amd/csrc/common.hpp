@@ -30,6 +30,14 @@ __device__ __forceinline__ uint16_t write_bf16(float value) {
 
 __device__ __forceinline__ float round_bf16(float value) { return read_bf16(write_bf16(value)); }
 
+// Row (in head_dim units) of logical token `token`, kv head `head`, in a pool
+// of pages [page][kv_heads][1 << shift][head_dim] under page-table row `table`.
+__device__ __forceinline__ int64_t page_row(const int32_t *table, int shift, int kv_heads, int head,
+                                           int64_t token) {
+    const int64_t page = table[token >> shift];
+    return ((page * kv_heads + head) << shift) + (token & ((1 << shift) - 1));
+}
+
 // llm_swiglu's arithmetic (gpu_llm.cl:225-237) on BF16 gate and up values:
 // BF16(BF16(g / (1 + e^-g)) * u), e^-g evaluated in double and rounded once,
 // every other step correctly rounded in f32.

@@ -85,10 +85,20 @@ __global__ __launch_bounds__(128) void rmsnorm_staged_kernel(const uint16_t *in,
         }
     }
     __syncthreads();
+    // The lane's elements are read from LDS eight at a time ahead of the FMA
+    // chain, which still runs over them in ascending order.
+    constexpr int kBatch = 8;
     float s = 0.0f;
-    for (int i = tid; i < hidden; i += 128) {
-        const float v = read_bf16(row[i]);
-        s = __fmaf_rn(v, v, s);
+    for (int base = tid; base < hidden; base += 128 * kBatch) {
+        float v[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int i = base + 128 * u;
+            v[u] = i < hidden ? read_bf16(row[i]) : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u)
+            if (base + 128 * u < hidden) s = __fmaf_rn(v[u], v[u], s);
     }
     partials[tid] = s;
     __syncthreads();
@@ -99,9 +109,21 @@ __global__ __launch_bounds__(128) void rmsnorm_staged_kernel(const uint16_t *in,
     const float mean = __fdiv_rn(partials[0], (float)hidden);
     const float factor = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, eps)));
     // each lane rewrites only the elements it read, so in place is safe
-    for (int i = tid; i < hidden; i += 128) {
-        const uint16_t normalized = write_bf16(__fmul_rn(read_bf16(row[i]), factor));
-        row[i] = write_bf16(__fmul_rn(read_bf16(normalized), read_bf16(wt[i])));
+    for (int base = tid; base < hidden; base += 128 * kBatch) {
+        uint16_t xv[kBatch], wv[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int i = base + 128 * u;
+            xv[u] = i < hidden ? row[i] : 0;
+            wv[u] = i < hidden ? wt[i] : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int i = base + 128 * u;
+            if (i >= hidden) continue;
+            const uint16_t normalized = write_bf16(__fmul_rn(read_bf16(xv[u]), factor));
+            row[i] = write_bf16(__fmul_rn(read_bf16(normalized), read_bf16(wv[u])));
+        }
     }
     __syncthreads();
     uint4 *dst = reinterpret_cast<uint4 *>(out + (int64_t)blockIdx.x * hidden);
@@ -131,10 +153,29 @@ __device__ float rope_inverse_frequency(int fd, int head_dim, float theta, int l
     return inv;
 }
 
-// llm_rope / llm_prefill_rope (gpu_llm.cl:102-146, :412-456): one lane per
-// element, rotate-half partner, c and s rounded to BF16.  Row t sits at
-// position start + t, or at positions[t] when a position array is given (one
-// decode row per sequence of a batch).
+// One rotated element of llm_rope / llm_prefill_rope (gpu_llm.cl:102-146,
+// :412-456): element d of head `head` of a token row [heads][head_dim] at
+// `position`, rotate-half partner, c and s rounded to BF16.
+__device__ __forceinline__ uint16_t rope_element(const uint16_t *token_row, int head, int d, int head_dim,
+                                                 int64_t position, float theta, int llama3, float factor,
+                                                 float low, float high, float original_max) {
+    const int half = head_dim / 2;
+    const uint16_t *h = token_row + (int64_t)head * head_dim;
+    const float partner = read_bf16(h[d < half ? d + half : d - half]);
+    const float rotated = d < half ? -partner : partner;
+    const int fd = (d % half) * 2;
+    const float inv = rope_inverse_frequency(fd, head_dim, theta, llama3, factor, low, high, original_max);
+    const float phase = __fmul_rn((float)position, inv);
+    const float cs = round_bf16((float)cos((double)phase));
+    const float sn = round_bf16((float)sin((double)phase));
+    const float left = round_bf16(__fmul_rn(read_bf16(h[d]), cs));
+    const float right = round_bf16(__fmul_rn(rotated, sn));
+    return write_bf16(__fadd_rn(left, right));
+}
+
+// One lane per element.  Row t sits at position start + t, or at
+// positions[t] when a position array is given (one decode row per sequence
+// of a batch).
 __global__ __launch_bounds__(256) void rope_kernel(const uint16_t *in, uint16_t *out, int64_t total,
                                                    int heads, int head_dim, int start,
                                                    const int32_t *positions, float theta,
@@ -145,21 +186,45 @@ __global__ __launch_bounds__(256) void rope_kernel(const uint16_t *in, uint16_t 
     const int64_t elements = (int64_t)heads * head_dim;
     const int64_t token = i / elements;
     const int in_token = (int)(i % elements);
-    const int head = in_token / head_dim;
-    const int d = in_token % head_dim;
-    const int half = head_dim / 2;
-    const int64_t src = token * elements + (int64_t)head * head_dim + (d < half ? d + half : d - half);
-    const float partner = read_bf16(in[src]);
-    const float rotated = d < half ? -partner : partner;
-    const int fd = (d % half) * 2;
-    const float inv = rope_inverse_frequency(fd, head_dim, theta, llama3, factor, low, high, original_max);
     const int64_t position = positions ? (int64_t)positions[token] : start + token;
-    const float phase = __fmul_rn((float)position, inv);
-    const float cs = round_bf16((float)cos((double)phase));
-    const float sn = round_bf16((float)sin((double)phase));
-    const float left = round_bf16(__fmul_rn(read_bf16(in[i]), cs));
-    const float right = round_bf16(__fmul_rn(rotated, sn));
-    out[i] = write_bf16(__fadd_rn(left, right));
+    out[i] = rope_element(in + token * elements, in_token / head_dim, in_token % head_dim, head_dim, position,
+                          theta, llama3, factor, low, high, original_max);
+}
+
+// A decode step's RoPE and K/V append in one launch, each sequence b at
+// positions[b]: rotated Q rows to q_out; rotated K and the V rows straight
+// into the page pool through page-table row b.  Lanes [0, nq) rotate Q
+// elements, [nq, nq + nk) rotate K elements, the rest copy V 16 bytes at a
+// time.  Equal to rope_kernel on Q and on K followed by pages_append.
+__global__ __launch_bounds__(256) void rope_append_kernel(RopeAppendArgs a) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t nq = (int64_t)a.batch * a.q_heads * a.head_dim;
+    const int64_t nk = (int64_t)a.batch * a.kv_heads * a.head_dim;
+    const int64_t nv = nk / 8;
+    if (i >= nq + nk + nv) return;
+    if (i < nq) {
+        const int64_t elements = (int64_t)a.q_heads * a.head_dim;
+        const int b = (int)(i / elements), e = (int)(i % elements);
+        a.q_out[i] = rope_element(a.q + b * elements, e / a.head_dim, e % a.head_dim, a.head_dim, a.positions[b],
+                                  a.theta, a.llama3, a.factor, a.low, a.high, a.original_max);
+        return;
+    }
+    const int64_t kvd = (int64_t)a.kv_heads * a.head_dim;
+    const int64_t j = i - nq;
+    const int b = (int)((j < nk ? j : (j - nk) * 8) / kvd);
+    const int64_t position = a.positions[b];
+    if (position < 0 || position >= ((int64_t)a.pages_per_seq << a.shift)) return;
+    const int32_t *table = a.page_table + (int64_t)b * a.pages_per_seq;
+    if (j < nk) {
+        const int e = (int)(j % kvd), head = e / a.head_dim, d = e % a.head_dim;
+        a.k_pool[page_row(table, a.shift, a.kv_heads, head, position) * a.head_dim + d] =
+            rope_element(a.k + b * kvd, head, d, a.head_dim, position, a.theta, a.llama3, a.factor, a.low, a.high,
+                         a.original_max);
+    } else {
+        const int e = (int)(((j - nk) * 8) % kvd), head = e / a.head_dim, d = e % a.head_dim;
+        *reinterpret_cast<uint4 *>(a.v_pool + page_row(table, a.shift, a.kv_heads, head, position) * a.head_dim +
+                                   d) = *reinterpret_cast<const uint4 *>(a.v + b * kvd + e);
+    }
 }
 
 // llm_swiglu (gpu_llm.cl:225-237): BF16(BF16(g / (1 + e^-g)) * u).
@@ -283,6 +348,13 @@ hipError_t launch_rope(const uint16_t *in, uint16_t *out, int tokens, int heads,
     const unsigned blocks = (unsigned)((total + 255) / 256);
     hipLaunchKernelGGL(rope_kernel, dim3(blocks), dim3(256), 0, stream, in, out, total, heads, head_dim,
                        start, positions, theta, llama3, factor, low, high, original_max);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_append(const RopeAppendArgs &a, hipStream_t stream) {
+    const int64_t nk = (int64_t)a.batch * a.kv_heads * a.head_dim;
+    const int64_t total = (int64_t)a.batch * a.q_heads * a.head_dim + nk + nk / 8;
+    hipLaunchKernelGGL(rope_append_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 

@@ -76,6 +76,20 @@ hipError_t launch_rmsnorm(const uint16_t *in, const uint16_t *w, uint16_t *out, 
 hipError_t launch_rope(const uint16_t *in, uint16_t *out, int tokens, int heads, int head_dim,
                        int start, const int32_t *positions, float theta, int llama3, float factor,
                        float low, float high, float original_max, hipStream_t stream);
+// A decode step's RoPE of Q and K and the append of rotated K and V to the
+// page pool, one token per sequence at positions[b] (device int32).
+struct RopeAppendArgs {
+    const uint16_t *q, *k, *v;  // [batch][heads][head_dim] rows
+    uint16_t *q_out, *k_pool, *v_pool;
+    const int32_t *page_table;  // [batch][pages_per_seq]
+    const int32_t *positions;   // [batch]
+    int pages_per_seq, shift;   // page_tokens = 1 << shift
+    int batch, q_heads, kv_heads, head_dim;
+    float theta;
+    int llama3;
+    float factor, low, high, original_max;
+};
+hipError_t launch_rope_append(const RopeAppendArgs &a, hipStream_t stream);
 hipError_t launch_swiglu(const uint16_t *gate, const uint16_t *up, uint16_t *out, size_t n,
                          hipStream_t stream);
 hipError_t launch_add(const uint16_t *a, const uint16_t *b, uint16_t *out, size_t n, hipStream_t stream);

@@ -14,11 +14,6 @@ namespace mslim {
 
 namespace {
 
-__device__ __forceinline__ int64_t page_row(const int32_t *table, int shift, int kv_heads, int head,
-                                           int64_t token) {
-    const int64_t page = table[token >> shift];
-    return ((page * kv_heads + head) << shift) + (token & ((1 << shift) - 1));
-}
 
 __global__ __launch_bounds__(256) void pages_write_kernel(uint16_t *k_pool, uint16_t *v_pool,
                                                           const int32_t *table, int shift,

@@ -24,8 +24,22 @@ namespace mslim {
 
 namespace {
 
+// Tuning knobs, fixed at build time: MFMA steps per load batch, wavefronts
+// per workgroup (0: 16 below 1024 row tiles, 8 above), and whether weight
+// loads are non-temporal (streamed once, kept out of the way of the token
+// vectors in L2).
+#ifndef MSLIM_SKINNY_UNROLL
+#define MSLIM_SKINNY_UNROLL 4
+#endif
+#ifndef MSLIM_SKINNY_WAVES
+#define MSLIM_SKINNY_WAVES 0
+#endif
+#ifndef MSLIM_SKINNY_NONTEMPORAL
+#define MSLIM_SKINNY_NONTEMPORAL 0
+#endif
+
 constexpr int kTileRows = 16;
-constexpr int kUnroll = 4;
+constexpr int kUnroll = MSLIM_SKINNY_UNROLL;
 constexpr int kMaxSegments = 3;
 
 enum Epilogue { kPlain = 0, kAdd = 1, kSwiglu = 2 };
@@ -43,6 +57,14 @@ struct SkinnyArgs {
 };
 
 __device__ __forceinline__ bf16x8_t load8(const uint16_t *p) { return *reinterpret_cast<const bf16x8_t *>(p); }
+
+__device__ __forceinline__ bf16x8_t load_weights(const uint16_t *p) {
+#if MSLIM_SKINNY_NONTEMPORAL
+    return __builtin_nontemporal_load(reinterpret_cast<const bf16x8_t *>(p));
+#else
+    return load8(p);
+#endif
+}
 
 template <int WAVES, int EPI>
 __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(SkinnyArgs a) {
@@ -72,8 +94,8 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(SkinnyArgs a) {
         for (int u = 0; u < kUnroll; ++u) {
             const int k = k0 + u * 32;
             const bool in = k < a.inner;
-            wa[u] = in ? load8(wp + k) : zero;
-            if (EPI == kSwiglu) wu[u] = in ? load8(up + k) : zero;
+            wa[u] = in ? load_weights(wp + k) : zero;
+            if (EPI == kSwiglu) wu[u] = in ? load_weights(up + k) : zero;
             xb[u] = in && live ? load8(xp + k) : zero;
         }
 #pragma unroll
@@ -120,10 +142,13 @@ hipError_t launch(SkinnyArgs &a, hipStream_t stream) {
     }
     // Few row tiles get more wavefronts each, so that enough weight loads are
     // in flight to cover HBM latency.
-    if (tiles < 1024)
+    const int waves = MSLIM_SKINNY_WAVES ? MSLIM_SKINNY_WAVES : tiles < 1024 ? 16 : 8;
+    if (waves == 16)
         hipLaunchKernelGGL((skinny_kernel<16, EPI>), dim3((unsigned)tiles), dim3(16 * 64), 0, stream, a);
-    else
+    else if (waves == 8)
         hipLaunchKernelGGL((skinny_kernel<8, EPI>), dim3((unsigned)tiles), dim3(8 * 64), 0, stream, a);
+    else
+        hipLaunchKernelGGL((skinny_kernel<4, EPI>), dim3((unsigned)tiles), dim3(4 * 64), 0, stream, a);
     return hipGetLastError();
 }
 

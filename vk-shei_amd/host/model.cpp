@@ -212,14 +212,10 @@ std::vector<Step> DecoderRunner::forward_batch(const std::vector<int32_t> &token
         const LayerWeights &w = w_.layers[l];
         ctx_->check("input norm", mslim_attn_rmsnorm(h, x_, w.input_norm, norm_, b, s.hidden, s.rms_eps));
         ctx_->check("QKV projection", mslim_attn_gemm_qkv(h, w.q, w.k, w.v, norm_, q_, k_, v_, s.hidden, qd, kvd, b));
-        ctx_->check("query RoPE", mslim_attn_rope_rows(h, q_, qr_, b, s.q_heads, s.head_dim, pos_, s.rope_theta,
-                                                       s.llama3, s.rope_factor, s.rope_low, s.rope_high,
-                                                       s.rope_original_max));
-        ctx_->check("key RoPE", mslim_attn_rope_rows(h, k_, kr_, b, s.kv_heads, s.head_dim, pos_, s.rope_theta,
-                                                     s.llama3, s.rope_factor, s.rope_low, s.rope_high,
-                                                     s.rope_original_max));
-        ctx_->check("page append", mslim_attn_pages_append(h, k_pools_[l], v_pools_[l], table_, pages_per_seq_,
-                                                           page_tokens_, s.kv_heads, s.head_dim, b, pos_, kr_, v_));
+        ctx_->check("RoPE + K/V append",
+                    mslim_attn_rope_append(h, q_, k_, v_, qr_, k_pools_[l], v_pools_[l], table_, pages_per_seq_,
+                                           page_tokens_, b, pos_, s.q_heads, s.kv_heads, s.head_dim, s.rope_theta,
+                                           s.llama3, s.rope_factor, s.rope_low, s.rope_high, s.rope_original_max));
         if (layout_ == KvLayout::Dense)
             ctx_->check("dense attention",
                         mslim_attn_decode_dense(h, qr_, k_pools_[l], v_pools_[l], attn_, b, lens.data(), max_context_,

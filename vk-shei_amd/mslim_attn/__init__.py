@@ -65,6 +65,7 @@ EXPORTS = (
     "mslim_attn_swiglu",
     "mslim_attn_pages_write",
     "mslim_attn_pages_append",
+    "mslim_attn_rope_append",
     "mslim_attn_pages_gather",
     "mslim_attn_logical_kv_sha256",
     "mslim_attn_record_frame_bytes",
@@ -139,6 +140,7 @@ def library() -> C.CDLL:
         "mslim_attn_swiglu": (I, [P, P, P, P, SZ]),
         "mslim_attn_pages_write": (I, [P, P, P, P, I, I, I, I64, I64, P, P]),
         "mslim_attn_pages_append": (I, [P, P, P, P, I, I, I, I, I, P, P, P]),
+        "mslim_attn_rope_append": (I, [P, P, P, P, P, P, P, P, I, I, I, P, I, I, I, F, I, F, F, F, F]),
         "mslim_attn_pages_gather": (I, [P, P, P, I, I, I, I64, I64, P]),
         "mslim_attn_logical_kv_sha256": (I, [P, I, I64, I, I, P, P, P, I, C.c_char_p]),
         "mslim_attn_record_frame_bytes": (I64, [I]),
@@ -354,6 +356,16 @@ class Context:
         self._check("pages_append", self._lib.mslim_attn_pages_append(
             self._h, _ptr(k_pool), _ptr(v_pool), _ptr(page_table), pages_per_seq, page_tokens,
             kv_heads, head_dim, batch, _ptr(positions), _ptr(k_rows), _ptr(v_rows)))
+
+    def rope_append(self, q, k, v, q_out, k_pool, v_pool, page_table, pages_per_seq: int,
+                    page_tokens: int, batch: int, positions, q_heads: int, kv_heads: int, head_dim: int,
+                    theta: float, llama3_scaling: bool = False, factor: float = 1.0,
+                    low_freq_factor: float = 1.0, high_freq_factor: float = 2.0,
+                    original_max_position: float = 1.0) -> None:
+        self._check("rope_append", self._lib.mslim_attn_rope_append(
+            self._h, _ptr(q), _ptr(k), _ptr(v), _ptr(q_out), _ptr(k_pool), _ptr(v_pool), _ptr(page_table),
+            pages_per_seq, page_tokens, batch, _ptr(positions), q_heads, kv_heads, head_dim, theta,
+            int(bool(llama3_scaling)), factor, low_freq_factor, high_freq_factor, original_max_position))
 
     def pages_gather(self, pool, page_table_row, page_tokens: int, kv_heads: int, head_dim: int,
                      first_token: int, tokens: int, rows_out) -> None:
