@@ -11,7 +11,7 @@ from _data import from_torch, normal_bf16, to_torch
 pytestmark = pytest.mark.gpu
 
 
-# 4096 / 8192 / 4104 take the LDS-staged kernel; 100, 130 and 14336 the direct one
+# 4096 and 8192 take the LDS-staged kernel; 4104, 100, 130 and 14336 the direct one
 @pytest.mark.parametrize("tokens,hidden", [(1, 4096), (3, 4096), (8, 4096), (2, 8192), (5, 4104), (2, 100),
                                            (4, 130), (1, 14336)])
 def test_rmsnorm_bit_exact(ctx, tokens, hidden):

@@ -50,10 +50,11 @@ __global__ __launch_bounds__(128) void rmsnorm_kernel(const uint16_t *in, const 
 // 16-byte stores.  Lane `tid` still sums elements tid, tid+128, ... in order
 // and the tree is unchanged, so the result is bit-identical to rmsnorm_kernel;
 // what changes is that the row no longer arrives as 32 dependent 2-byte loads
-// per lane.  hidden % 8 == 0 and hidden <= kRmsStagedMax; dynamic LDS
-// 4 * hidden bytes.
+// per lane.  hidden % (128 * kRmsBatch) == 0 and hidden <= kRmsStagedMax;
+// dynamic LDS 4 * hidden bytes.
 constexpr int kRmsStagedMax = 8192;  // 32 KiB of dynamic LDS
 constexpr int kRmsLoadsInFlight = 4;
+constexpr int kRmsBatch = 8;
 
 __global__ __launch_bounds__(128) void rmsnorm_staged_kernel(const uint16_t *in, const uint16_t *w,
                                                              uint16_t *out, int hidden, float eps) {
@@ -85,20 +86,16 @@ __global__ __launch_bounds__(128) void rmsnorm_staged_kernel(const uint16_t *in,
         }
     }
     __syncthreads();
-    // The lane's elements are read from LDS eight at a time ahead of the FMA
-    // chain, which still runs over them in ascending order.
-    constexpr int kBatch = 8;
+    // hidden % (128 * kBatch) == 0: each lane's elements are read from LDS
+    // eight at a time, with no bounds test between the reads, ahead of the
+    // FMA chain, which still runs over them in ascending order.
     float s = 0.0f;
-    for (int base = tid; base < hidden; base += 128 * kBatch) {
-        float v[kBatch];
+    for (int base = tid; base < hidden; base += 128 * kRmsBatch) {
+        float v[kRmsBatch];
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-            const int i = base + 128 * u;
-            v[u] = i < hidden ? read_bf16(row[i]) : 0.0f;
-        }
+        for (int u = 0; u < kRmsBatch; ++u) v[u] = read_bf16(row[base + 128 * u]);
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u)
-            if (base + 128 * u < hidden) s = __fmaf_rn(v[u], v[u], s);
+        for (int u = 0; u < kRmsBatch; ++u) s = __fmaf_rn(v[u], v[u], s);
     }
     partials[tid] = s;
     __syncthreads();
@@ -109,20 +106,17 @@ __global__ __launch_bounds__(128) void rmsnorm_staged_kernel(const uint16_t *in,
     const float mean = __fdiv_rn(partials[0], (float)hidden);
     const float factor = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, eps)));
     // each lane rewrites only the elements it read, so in place is safe
-    for (int base = tid; base < hidden; base += 128 * kBatch) {
-        uint16_t xv[kBatch], wv[kBatch];
+    for (int base = tid; base < hidden; base += 128 * kRmsBatch) {
+        uint16_t xv[kRmsBatch], wv[kRmsBatch];
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-            const int i = base + 128 * u;
-            xv[u] = i < hidden ? row[i] : 0;
-            wv[u] = i < hidden ? wt[i] : 0;
+        for (int u = 0; u < kRmsBatch; ++u) {
+            xv[u] = row[base + 128 * u];
+            wv[u] = wt[base + 128 * u];
         }
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-            const int i = base + 128 * u;
-            if (i >= hidden) continue;
+        for (int u = 0; u < kRmsBatch; ++u) {
             const uint16_t normalized = write_bf16(__fmul_rn(read_bf16(xv[u]), factor));
-            row[i] = write_bf16(__fmul_rn(read_bf16(normalized), read_bf16(wv[u])));
+            row[base + 128 * u] = write_bf16(__fmul_rn(read_bf16(normalized), read_bf16(wv[u])));
         }
     }
     __syncthreads();
@@ -332,7 +326,7 @@ hipError_t launch_rmsnorm(const uint16_t *in, const uint16_t *w, uint16_t *out, 
                           int hidden, float eps, hipStream_t stream) {
     const bool aligned = ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(w) |
                            reinterpret_cast<uintptr_t>(out)) & 15) == 0;
-    if (aligned && hidden % 8 == 0 && hidden <= kRmsStagedMax)
+    if (aligned && hidden % (128 * kRmsBatch) == 0 && hidden <= kRmsStagedMax)
         hipLaunchKernelGGL(rmsnorm_staged_kernel, dim3((unsigned)tokens), dim3(128), (size_t)hidden * 4, stream,
                            in, w, out, hidden, eps);
     else
