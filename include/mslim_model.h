@@ -84,6 +84,15 @@ int mslim_model_reset(void *model, int seq);
 /* BF16 bits of the last logits: 1 row after prefill, one per slot after a
  * batch step (GpuStep::logits, mod.rs:116-118). */
 int mslim_model_logits(void *model, uint16_t *out, size_t capacity, int *rows);
+/* PrefillSettings JSON (calibration_profile.rs:21-27: batch_tokens,
+ * weight_reuse_tokens, attention) of the runner (GpuLlm::prefill_settings,
+ * mod.rs:594-600); fails if it does not fit in `capacity` bytes. */
+int mslim_model_prefill_settings(void *model, char *json_out, size_t capacity);
+/* Validate and install PrefillSettings JSON while every slot is empty
+ * (GpuLlm::set_calibration_prefill_settings, mod.rs:602-632): batch_tokens
+ * becomes the prompt chunk (1 when null), up to the chunk_tokens the runner
+ * was created with; experimental attention modes are rejected. */
+int mslim_model_set_prefill_settings(void *model, const char *json);
 /* GpuLlm::logical_kv_sha256 (mod.rs:1981-2028) of slot `seq`, hex with NUL. */
 int mslim_model_logical_kv_sha256(void *model, int seq, char *hex_out);
 

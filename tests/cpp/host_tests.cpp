@@ -128,6 +128,52 @@ TEST(config_ids_and_json_form) {
         expect_throw<Error>([&] { AttentionKernelConfig::from_json(bad); });
 }
 
+TEST(prefill_settings_legacy_profile_retains_reference_and_id) {
+    // tests/tiled_attention_policy.rs:5-12
+    const PrefillSettings s = PrefillSettings::from_json(R"({"batch_tokens":64,"weight_reuse_tokens":8})");
+    CHECK(s.attention == AttentionKernelConfig{});
+    CHECK(s.id() == "batch-64-reuse-8");
+    s.validate();
+    CHECK(s.chunk_tokens() == 64);
+}
+
+TEST(prefill_settings_exact_calibration_cannot_promote_online_contract) {
+    // tests/tiled_attention_policy.rs:13-25
+    PrefillSettings s;
+    s.batch_tokens = 64;
+    s.weight_reuse_tokens = 8;
+    s.attention.mode = AttentionKernelMode::OnlineExperimental;
+    expect_throw<Error>([&] { s.validate(); });
+    s.attention.mode = AttentionKernelMode::StrictTiled;
+    s.validate();
+    CHECK(s.id() != "batch-64-reuse-8");
+    CHECK(s.id() == "batch-64-reuse-8-stricttiled-q1-k64-wg64-s1");
+}
+
+TEST(prefill_settings_bounds_and_json_rules) {
+    // calibration_profile.rs:21-54: batch 1..=512 or sequential, reuse in
+    // {1, 8, 16, 32}; serde: reuse required, batch optional, no unknown fields
+    PrefillSettings s = PrefillSettings::from_json(R"({"batch_tokens":null,"weight_reuse_tokens":1})");
+    CHECK(!s.batch_tokens && s.id() == "batch-sequential-reuse-1" && s.chunk_tokens() == 1);
+    s.validate();
+    s = PrefillSettings::from_json(R"({"weight_reuse_tokens":32,"batch_tokens":512})");
+    s.validate();
+    for (size_t bad : {(size_t)0, (size_t)513}) {
+        s.batch_tokens = bad;
+        CHECK(expect_throw<Error>([&] { s.validate(); }) == "prefill batch must be 1..=512");
+    }
+    s.batch_tokens = 16;
+    s.weight_reuse_tokens = 4;
+    CHECK(expect_throw<Error>([&] { s.validate(); }) == "prefill reuse must be 1,8,16,32");
+    const PrefillSettings nested = PrefillSettings::from_json(
+        R"({"weight_reuse_tokens":16,"attention":{"mode":"strict_tiled","block_keys":128}})");
+    CHECK(nested.attention.mode == AttentionKernelMode::StrictTiled && nested.attention.block_keys == 128);
+    for (const char *bad : {R"({"batch_tokens":64})", R"({"weight_reuse_tokens":8,"fast":true})",
+                            R"({"weight_reuse_tokens":-8})", R"({"weight_reuse_tokens":8,"attention":{"mode":"x"}})",
+                            R"([])"})
+        expect_throw<Error>([&] { PrefillSettings::from_json(bad); });
+}
+
 TEST(config_split_tokens_for_the_decode_kernel) {
     AttentionKernelConfig c;
     CHECK(c.decode_split_tokens(32768) == 0);  // library choice

@@ -382,3 +382,45 @@ def test_runner_llama3_8b_width_reduced_depth(ctx):
             toks = nxt
     finally:
         model.close()
+
+
+def test_runner_prefill_settings(tiny_model):
+    # GpuLlm::prefill_settings / set_calibration_prefill_settings: the prompt
+    # chunk follows batch_tokens; tuning needs empty slots; experimental
+    # attention and chunks above the built capacity are refused
+    from mslim_attn import MslimAttnError
+
+    w, model = tiny_model
+    for seq in range(3):
+        model.reset(seq)
+    base = model.prefill_settings()
+    assert base["batch_tokens"] == 16 and base["weight_reuse_tokens"] == 8
+    assert base["attention"]["mode"] == "reference"
+    ref = DecoderOracle(SPEC, w)
+    prompt = list(np.random.default_rng(5).integers(0, SPEC.vocab, 37))
+    try:
+        model.set_prefill_settings({"batch_tokens": 8, "weight_reuse_tokens": 8})
+        assert model.prefill_settings()["batch_tokens"] == 8
+        got = model.prefill_only(0, prompt)  # five causal chunks of <= 8 tokens
+        want_logits, _ = ref.prefill(0, prompt)
+        _check_logits(model.logits()[0], want_logits, "prefill in chunks of 8")
+        _check_token(got, want_logits, "prefill in chunks of 8")
+        with pytest.raises(MslimAttnError, match="empty session"):
+            model.set_prefill_settings({"batch_tokens": 4, "weight_reuse_tokens": 8})
+        model.reset(0)
+        with pytest.raises(MslimAttnError, match="chunk this runner"):
+            model.set_prefill_settings({"batch_tokens": 32, "weight_reuse_tokens": 8})
+        with pytest.raises(MslimAttnError, match="experimental"):
+            model.set_prefill_settings({"batch_tokens": 8, "weight_reuse_tokens": 8,
+                                        "attention": {"mode": "online_experimental"}})
+        with pytest.raises(MslimAttnError, match="reuse"):
+            model.set_prefill_settings({"batch_tokens": 8, "weight_reuse_tokens": 4})
+        model.set_prefill_settings({"batch_tokens": None, "weight_reuse_tokens": 1})
+        got = model.prefill_only(0, prompt[:5])  # sequential: one token per chunk
+        want_logits, _ = ref.prefill(0, prompt[:5])
+        _check_logits(model.logits()[0], want_logits, "sequential prefill")
+    finally:
+        for seq in range(3):
+            model.reset(seq)
+        model.set_prefill_settings(base)
+    assert model.prefill_settings() == base

@@ -148,4 +148,55 @@ int AttentionKernelConfig::decode_split_tokens(size_t history) const {
     return (int)((per + 63) / 64 * 64);
 }
 
+// calibration_profile.rs:21-27 with serde's rules for this struct.
+PrefillSettings PrefillSettings::from_json(const std::string &text) {
+    return from_value(json::parse(text));
+}
+
+PrefillSettings PrefillSettings::from_value(const json::Value &value) {
+    ensure(value.kind == json::Value::Kind::Object, "invalid type: expected struct PrefillSettings");
+    PrefillSettings p;
+    bool have_reuse = false;
+    for (const auto &m : value.members) {
+        const std::string &k = m.first;
+        const json::Value &v = m.second;
+        if (k == "batch_tokens") {
+            if (v.kind == json::Value::Kind::Null) p.batch_tokens.reset();
+            else p.batch_tokens = (size_t)v.as_usize(k);
+        } else if (k == "weight_reuse_tokens") {
+            p.weight_reuse_tokens = (size_t)v.as_usize(k);
+            have_reuse = true;
+        } else if (k == "attention") {
+            p.attention = AttentionKernelConfig::from_value(v);
+        } else {
+            throw Error("unknown field `" + k +
+                        "`, expected one of `batch_tokens`, `weight_reuse_tokens`, `attention`");
+        }
+    }
+    ensure(have_reuse, "missing field `weight_reuse_tokens`");
+    return p;
+}
+
+// calibration_profile.rs:29-40
+void PrefillSettings::validate() const {
+    attention.validate_activation(false);
+    ensure(!batch_tokens || (*batch_tokens >= 1 && *batch_tokens <= 512), "prefill batch must be 1..=512");
+    ensure(weight_reuse_tokens == 1 || weight_reuse_tokens == 8 || weight_reuse_tokens == 16 ||
+               weight_reuse_tokens == 32,
+           "prefill reuse must be 1,8,16,32");
+}
+
+std::string PrefillSettings::to_json() const {
+    return std::string("{\"batch_tokens\":") + (batch_tokens ? std::to_string(*batch_tokens) : std::string("null")) +
+           ",\"weight_reuse_tokens\":" + std::to_string(weight_reuse_tokens) + ",\"attention\":" +
+           attention.to_json() + "}";
+}
+
+// calibration_profile.rs:41-54
+std::string PrefillSettings::id() const {
+    const std::string base = "batch-" + (batch_tokens ? std::to_string(*batch_tokens) : std::string("sequential")) +
+                             "-reuse-" + std::to_string(weight_reuse_tokens);
+    return attention == AttentionKernelConfig{} ? base : base + "-" + attention.id();
+}
+
 }  // namespace mslim

@@ -51,4 +51,31 @@ struct AttentionKernelConfig {
 
 const char *mode_json_name(AttentionKernelMode mode);
 
+// The prefill knobs a calibration profile may carry (calibration_profile.rs:
+// 21-54): prompt tokens per causal chunk (none = one token at a time), GEMV
+// weight reuse, and a bit-exact attention configuration.  On gfx950 the
+// decoder runner's chunk is batch_tokens; weight reuse has no counterpart
+// (a chunk's projections read each weight once whatever the reuse) and is
+// kept for the profile identity.  The profile registry and its transactions
+// stay with the caller.
+struct PrefillSettings {
+    std::optional<size_t> batch_tokens;
+    size_t weight_reuse_tokens = 0;
+    AttentionKernelConfig attention;
+
+    bool operator==(const PrefillSettings &o) const {
+        return batch_tokens == o.batch_tokens && weight_reuse_tokens == o.weight_reuse_tokens &&
+               attention == o.attention;
+    }
+    // serde(deny_unknown_fields): `weight_reuse_tokens` required,
+    // `batch_tokens` may be absent or null, `attention` defaults.
+    static PrefillSettings from_json(const std::string &text);
+    static PrefillSettings from_value(const json::Value &value);
+    void validate() const;   // :29-40
+    std::string id() const;  // :41-54
+    std::string to_json() const;
+    // Prompt tokens per runner chunk: batch_tokens, or 1 when sequential.
+    int chunk_tokens() const { return batch_tokens ? (int)*batch_tokens : 1; }
+};
+
 }  // namespace mslim

@@ -44,6 +44,10 @@ DecoderRunner::DecoderRunner(std::shared_ptr<NativeContext> ctx, ModelSpec spec,
     page_tokens_ = layout_ == KvLayout::Dense ? 1 : kPageTokens;
     pages_per_seq_ = (max_context_ + page_tokens_ - 1) / page_tokens_;
     rows_cap_ = std::max(max_batch_, chunk_tokens_);
+    // set_batch_prefill_tokens (mod.rs:742-760): a batch of 8 or more reads
+    // each weight once for 8 tokens or more.
+    settings_.batch_tokens = (size_t)chunk_tokens_;
+    settings_.weight_reuse_tokens = chunk_tokens_ >= 8 ? 8 : 1;
     scale_ = (float)(1.0 / std::sqrt((double)spec_.head_dim));
     positions_.assign(max_batch_, 0);
 
@@ -258,6 +262,14 @@ std::vector<int32_t> DecoderRunner::generate(int seq, const std::vector<int32_t>
     return generated;
 }
 
+void DecoderRunner::set_calibration_prefill_settings(const PrefillSettings &settings) {
+    settings.validate();
+    for (int64_t p : positions_) ensure(p == 0, "prefill tuning requires a healthy, empty session");
+    ensure(settings.chunk_tokens() <= rows_cap_, "prefill batch exceeds the chunk this runner was built for");
+    chunk_tokens_ = settings.chunk_tokens();
+    settings_ = settings;
+}
+
 void DecoderRunner::reset(int seq) {
     ensure(seq >= 0 && seq < max_batch_, "sequence slot out of range");
     positions_[seq] = 0;
@@ -440,6 +452,30 @@ int mslim_model_logits(void *model, uint16_t *out, size_t capacity, int *rows) {
         mslim::ensure(l.size() <= capacity, "logits buffer too small");
         std::memcpy(out, l.data(), l.size() * 2);
         *rows = (int)(l.size() / r.spec().vocab);
+        return 0;
+    } catch (const std::exception &e) {
+        return model_fail(e);
+    }
+}
+
+int mslim_model_prefill_settings(void *model, char *json_out, size_t capacity) {
+    g_model_error.clear();
+    try {
+        mslim::ensure(json_out != nullptr, "null settings buffer");
+        const std::string text = runner_of(model).prefill_settings().to_json();
+        mslim::ensure(text.size() < capacity, "settings buffer too small");
+        std::memcpy(json_out, text.c_str(), text.size() + 1);
+        return 0;
+    } catch (const std::exception &e) {
+        return model_fail(e);
+    }
+}
+
+int mslim_model_set_prefill_settings(void *model, const char *json) {
+    g_model_error.clear();
+    try {
+        mslim::ensure(json != nullptr, "null settings");
+        runner_of(model).set_calibration_prefill_settings(mslim::PrefillSettings::from_json(json));
         return 0;
     } catch (const std::exception &e) {
         return model_fail(e);

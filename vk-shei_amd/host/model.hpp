@@ -17,6 +17,7 @@
 #include <string>
 #include <vector>
 
+#include "attention_kernel.hpp"
 #include "native.hpp"
 
 namespace mslim {
@@ -87,6 +88,13 @@ public:
     // K/V pools.
     std::string logical_kv_sha256(int seq) const;
     const ModelSpec &spec() const { return spec_; }
+    // GpuLlm::prefill_settings / set_calibration_prefill_settings
+    // (gpu_llm/mod.rs:594-632): the prompt chunk is batch_tokens (1 when
+    // sequential); new settings are validated and installed only while every
+    // slot is empty, and the chunk may not exceed the one the runner was
+    // built for.
+    PrefillSettings prefill_settings() const { return settings_; }
+    void set_calibration_prefill_settings(const PrefillSettings &settings);
 
 private:
     void *alloc(size_t bytes);
@@ -106,6 +114,7 @@ private:
     KvLayout layout_;
     int max_batch_, chunk_tokens_, max_context_, page_tokens_, pages_per_seq_, rows_cap_;
     float scale_;
+    PrefillSettings settings_;
     std::vector<int64_t> positions_;
     std::vector<void *> owned_;
     std::vector<void *> k_pools_, v_pools_;

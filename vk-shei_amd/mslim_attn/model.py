@@ -26,6 +26,8 @@ MODEL_EXPORTS = (
     "mslim_model_reset",
     "mslim_model_logits",
     "mslim_model_logical_kv_sha256",
+    "mslim_model_prefill_settings",
+    "mslim_model_set_prefill_settings",
 )
 
 LAYER_TENSORS = ("input_norm", "q", "k", "v", "o", "post_norm", "gate", "up", "down")
@@ -91,6 +93,8 @@ def host_library() -> C.CDLL:
         "mslim_model_reset": (I, [P, I]),
         "mslim_model_logits": (I, [P, C.POINTER(C.c_uint16), C.c_size_t, C.POINTER(I)]),
         "mslim_model_logical_kv_sha256": (I, [P, I, C.c_char_p]),
+        "mslim_model_prefill_settings": (I, [P, C.c_char_p, C.c_size_t]),
+        "mslim_model_set_prefill_settings": (I, [P, C.c_char_p]),
     }
     for name in MODEL_EXPORTS:
         res, args = sigs[name]
@@ -195,6 +199,18 @@ class Model:
         self._check("logits", self._lib.mslim_model_logits(
             self._h, buf.ctypes.data_as(C.POINTER(C.c_uint16)), cap, C.byref(rows)))
         return buf[:rows.value * self.spec.vocab].reshape(rows.value, self.spec.vocab)
+
+    def prefill_settings(self) -> dict:
+        """PrefillSettings (batch_tokens, weight_reuse_tokens, attention)."""
+        import json
+        out = C.create_string_buffer(1024)
+        self._check("prefill_settings", self._lib.mslim_model_prefill_settings(self._h, out, 1024))
+        return json.loads(out.value.decode())
+
+    def set_prefill_settings(self, settings: dict) -> None:
+        import json
+        self._check("set_prefill_settings", self._lib.mslim_model_set_prefill_settings(
+            self._h, json.dumps(settings).encode()))
 
     def logical_kv_sha256(self, seq: int) -> str:
         out = C.create_string_buffer(65)
