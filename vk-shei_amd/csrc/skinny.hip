@@ -10,7 +10,9 @@
 // WAVES-th block of 32*kUnroll inputs and runs v_mfma_f32_16x16x32_bf16 with
 // the weights as A (16 rows x 32 inputs, one 16-byte load per lane) and the
 // tokens as B (32 inputs x 16 tokens, padded with zeros), kUnroll loads in
-// flight per operand.  The WAVES partial 16x16 tiles are summed in LDS in
+// flight per operand.  When the token rows fit (<= 8 tokens of <= 4096
+// inputs) the workgroup stages them in LDS first: the per-k-step B loads cost
+// a quarter of the streaming rate when they go to L2.  The WAVES partial 16x16 tiles are summed in LDS in
 // fixed wave order, so results do not depend on timing.  Epilogues:
 //   plain   out = BF16(acc)
 //   add     out = BF16(resid + BF16(acc))           (llm_add after the product)
@@ -19,6 +21,8 @@
 // bit.  Up to three matrices with separate outputs share one launch (Q, K, V).
 #include "common.hpp"
 #include "kernels.hpp"
+
+#include <algorithm>
 
 namespace mslim {
 
@@ -37,6 +41,18 @@ namespace {
 #ifndef MSLIM_SKINNY_NONTEMPORAL
 #define MSLIM_SKINNY_NONTEMPORAL 0
 #endif
+// Token vectors staged in LDS when they fit (1) or read per k-step (0).
+#ifndef MSLIM_SKINNY_XLDS
+#define MSLIM_SKINNY_XLDS 1
+#endif
+// Two-deep register ring of load batches (1) or load-then-use (0).
+#ifndef MSLIM_SKINNY_RING
+#define MSLIM_SKINNY_RING 0
+#endif
+// Workgroups in a launch (0: one per row tile).
+#ifndef MSLIM_SKINNY_GRID
+#define MSLIM_SKINNY_GRID 0
+#endif
 
 constexpr int kTileRows = 16;
 constexpr int kUnroll = MSLIM_SKINNY_UNROLL;
@@ -50,6 +66,7 @@ struct SkinnyArgs {
     int rows[kMaxSegments];
     int first_tile[kMaxSegments];
     int segments;
+    int tiles;
     const uint16_t *x;       // [tokens][inner]
     const uint16_t *w_up;    // swiglu: up weights beside w[0] (gate)
     const uint16_t *resid;   // add: [tokens][rows[0]], may equal out[0]
@@ -66,15 +83,44 @@ __device__ __forceinline__ bf16x8_t load_weights(const uint16_t *p) {
 #endif
 }
 
-template <int WAVES, int EPI>
+// Token vectors staged in LDS (XLDS): up to kStageTokens rows of up to
+// kStageInner inputs, each row padded by 16 bytes so that the 16 token rows
+// of a B fragment read fall in different banks.
+constexpr int kStageTokens = 8;
+constexpr int kStageInner = 4096;
+constexpr int kStageStride = kStageInner + 8;
+
+template <int WAVES, int EPI, bool XLDS>
 __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(SkinnyArgs a) {
-    __shared__ floatx4_t partial[EPI == kSwiglu ? 2 : 1][WAVES][64];
+    // One LDS region holds the staged token rows during the k loop and the
+    // wavefronts' partial tiles after it, so two workgroups fit on a CU.
+    constexpr int kPartialBytes = (EPI == kSwiglu ? 2 : 1) * WAVES * 64 * 16;
+    constexpr int kStageBytes = XLDS ? kStageTokens * kStageStride * 2 : 0;
+    __shared__ __align__(16) unsigned char lds[kPartialBytes > kStageBytes ? kPartialBytes : kStageBytes];
+    auto partial = reinterpret_cast<floatx4_t(*)[WAVES][64]>(lds);
+    uint16_t *xs = reinterpret_cast<uint16_t *>(lds);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // Workgroups loop over row tiles (tile, tile + grid, ...), so a launch
+    // with fewer workgroups than tiles keeps each one streaming longer.
+    for (int tile = blockIdx.x; tile < a.tiles; tile += gridDim.x) {
+    if (tile != (int)blockIdx.x) __syncthreads();  // the LDS of the last tile has been read
+    if (XLDS) {
+        // The B operand (token rows) is the same for every row tile: read it
+        // once per workgroup with 16-byte loads instead of once per k-step
+        // per wavefront.
+        const int chunks = a.inner / 8;
+        for (int i = threadIdx.x; i < a.tokens * chunks; i += WAVES * 64) {
+            const int t = i / chunks, c = i % chunks;
+            *reinterpret_cast<uint4 *>(xs + t * kStageStride + c * 8) =
+                *reinterpret_cast<const uint4 *>(a.x + (int64_t)t * a.inner + c * 8);
+        }
+        __syncthreads();
+    }
     int seg = 0;
-    if (a.segments > 1 && (int)blockIdx.x >= a.first_tile[1]) seg = 1;
-    if (a.segments > 2 && (int)blockIdx.x >= a.first_tile[2]) seg = 2;
+    if (a.segments > 1 && tile >= a.first_tile[1]) seg = 1;
+    if (a.segments > 2 && tile >= a.first_tile[2]) seg = 2;
     const int rows = a.rows[seg];
-    const int r0 = ((int)blockIdx.x - a.first_tile[seg]) * kTileRows;
+    const int r0 = (tile - a.first_tile[seg]) * kTileRows;
     // A operand: lane l holds row r0 + l%16, inputs 8*(l/16) .. +7 of each
     // 32-input block; B operand: token l%16, the same inputs.  Rows past the
     // end re-read the last row and are not written.
@@ -85,36 +131,64 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(SkinnyArgs a) {
     const uint16_t *wp = a.w[seg] + (int64_t)row * a.inner + kq;
     const uint16_t *up = EPI == kSwiglu ? a.w_up + (int64_t)row * a.inner + kq : nullptr;
     const uint16_t *xp = a.x + (int64_t)(live ? tok : 0) * a.inner + kq;
+    const uint16_t *xl = xs + (live ? tok : 0) * kStageStride + kq;
     floatx4_t acc = {0.0f, 0.0f, 0.0f, 0.0f}, acc_up = {0.0f, 0.0f, 0.0f, 0.0f};
     const bf16x8_t zero = {};
     // inner % 32 == 0: a block that starts inside the row ends inside it.
-    for (int k0 = wave * 32 * kUnroll; k0 < a.inner; k0 += WAVES * 32 * kUnroll) {
+    struct Batch {
         bf16x8_t wa[kUnroll], wu[kUnroll], xb[kUnroll];
+    };
+    auto load_batch = [&](Batch &bt, int k0) {
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
             const int k = k0 + u * 32;
             const bool in = k < a.inner;
-            wa[u] = in ? load_weights(wp + k) : zero;
-            if (EPI == kSwiglu) wu[u] = in ? load_weights(up + k) : zero;
-            xb[u] = in && live ? load8(xp + k) : zero;
+            bt.wa[u] = in ? load_weights(wp + k) : zero;
+            if (EPI == kSwiglu) bt.wu[u] = in ? load_weights(up + k) : zero;
+            if (XLDS) bt.xb[u] = in && live ? *reinterpret_cast<const bf16x8_t *>(xl + k) : zero;
+            else bt.xb[u] = in && live ? load8(xp + k) : zero;
         }
+    };
+    auto use_batch = [&](const Batch &bt) {
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[u], xb[u], acc, 0, 0, 0);
-            if (EPI == kSwiglu) acc_up = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wu[u], xb[u], acc_up, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bt.wa[u], bt.xb[u], acc, 0, 0, 0);
+            if (EPI == kSwiglu) acc_up = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bt.wu[u], bt.xb[u], acc_up, 0, 0, 0);
         }
+    };
+    const int step = WAVES * 32 * kUnroll;
+#if MSLIM_SKINNY_RING
+    // Two batches in registers: the next one's loads are in flight while the
+    // current one feeds the MFMAs.
+    Batch ring[2];
+    int k0 = wave * 32 * kUnroll;
+    if (k0 < a.inner) load_batch(ring[0], k0);
+    for (; k0 < a.inner; k0 += 2 * step) {
+        if (k0 + step < a.inner) load_batch(ring[1], k0 + step);
+        use_batch(ring[0]);
+        if (k0 + step >= a.inner) break;
+        if (k0 + 2 * step < a.inner) load_batch(ring[0], k0 + 2 * step);
+        use_batch(ring[1]);
     }
+#else
+    for (int k0 = wave * 32 * kUnroll; k0 < a.inner; k0 += step) {
+        Batch bt;
+        load_batch(bt, k0);
+        use_batch(bt);
+    }
+#endif
+    if (XLDS) __syncthreads();  // every wavefront is done with the staged rows
     partial[0][wave][lane] = acc;
     if (EPI == kSwiglu) partial[EPI == kSwiglu ? 1 : 0][wave][lane] = acc_up;
     __syncthreads();
-    if (wave != 0) return;
+    if (wave != 0) continue;
     floatx4_t sum = partial[0][0][lane], sum_up = partial[EPI == kSwiglu ? 1 : 0][0][lane];
     for (int w = 1; w < WAVES; ++w) {
         sum += partial[0][w][lane];
         if (EPI == kSwiglu) sum_up += partial[EPI == kSwiglu ? 1 : 0][w][lane];
     }
     // D layout: lane l holds rows 4*(l/16) + j, token l%16.
-    if (!live) return;
+    if (!live) continue;
     uint16_t *out = a.out[seg] + (int64_t)tok * rows;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -129,12 +203,13 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(SkinnyArgs a) {
             out[r] = swiglu_bf16(y, write_bf16(sum_up[j]));
         }
     }
+    }
 }
 
 int tiles_of(int rows) { return (rows + kTileRows - 1) / kTileRows; }
 
-template <int EPI>
-hipError_t launch(SkinnyArgs &a, hipStream_t stream) {
+template <int EPI, bool XLDS>
+hipError_t launch_with(SkinnyArgs &a, hipStream_t stream) {
     int tiles = 0;
     for (int s = 0; s < a.segments; ++s) {
         a.first_tile[s] = tiles;
@@ -142,14 +217,26 @@ hipError_t launch(SkinnyArgs &a, hipStream_t stream) {
     }
     // Few row tiles get more wavefronts each, so that enough weight loads are
     // in flight to cover HBM latency.
-    const int waves = MSLIM_SKINNY_WAVES ? MSLIM_SKINNY_WAVES : tiles < 1024 ? 16 : 8;
+    a.tiles = tiles;
+    // Measured per shape at 8 tokens (weights cycled through more memory
+    // than the Infinity Cache holds): 8 wavefronts for the gate/up pair,
+    // for inputs too wide to stage and for many row tiles; 16 for the rest.
+    const int waves = MSLIM_SKINNY_WAVES ? MSLIM_SKINNY_WAVES
+                      : (EPI == kSwiglu || a.inner > kStageInner || tiles >= 1024) ? 8 : 16;
+    const unsigned grid = (unsigned)(MSLIM_SKINNY_GRID ? std::min(tiles, MSLIM_SKINNY_GRID) : tiles);
     if (waves == 16)
-        hipLaunchKernelGGL((skinny_kernel<16, EPI>), dim3((unsigned)tiles), dim3(16 * 64), 0, stream, a);
+        hipLaunchKernelGGL((skinny_kernel<16, EPI, XLDS>), dim3(grid), dim3(16 * 64), 0, stream, a);
     else if (waves == 8)
-        hipLaunchKernelGGL((skinny_kernel<8, EPI>), dim3((unsigned)tiles), dim3(8 * 64), 0, stream, a);
+        hipLaunchKernelGGL((skinny_kernel<8, EPI, XLDS>), dim3(grid), dim3(8 * 64), 0, stream, a);
     else
-        hipLaunchKernelGGL((skinny_kernel<4, EPI>), dim3((unsigned)tiles), dim3(4 * 64), 0, stream, a);
+        hipLaunchKernelGGL((skinny_kernel<4, EPI, XLDS>), dim3(grid), dim3(4 * 64), 0, stream, a);
     return hipGetLastError();
+}
+
+template <int EPI>
+hipError_t launch(SkinnyArgs &a, hipStream_t stream) {
+    if (MSLIM_SKINNY_XLDS && a.tokens <= kStageTokens && a.inner <= kStageInner) return launch_with<EPI, true>(a, stream);
+    return launch_with<EPI, false>(a, stream);
 }
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
