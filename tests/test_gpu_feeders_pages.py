@@ -40,7 +40,7 @@ def test_rope_bit_exact(ctx, llama3, start):
 
 def test_rope_other_head_dims(ctx):
     rng = np.random.default_rng(1)
-    for d in (64, 80, 256):
+    for d in (64, 80, 256, 1024):  # 1024: the per-element kernel (head_dim > 512)
         xb = normal_bf16(rng, (5, 4, d))
         out = torch.empty((5, 4, d), dtype=torch.int16, device="cuda")
         ctx.rope(to_torch(xb), out, 5, 4, d, 123, 10000.0)

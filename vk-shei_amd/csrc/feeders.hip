@@ -185,6 +185,41 @@ __global__ __launch_bounds__(256) void rope_kernel(const uint16_t *in, uint16_t 
                           theta, llama3, factor, low, high, original_max);
 }
 
+// The same rotation with one workgroup per token row: the row's c and s
+// (one pair per rotary dimension pair, head_dim / 2 <= 256) are computed once
+// into LDS and shared by all heads, instead of once per element.  Each value
+// is computed exactly as rope_element computes it, so the output is
+// bit-identical.
+__global__ __launch_bounds__(256) void rope_token_kernel(const uint16_t *in, uint16_t *out, int heads,
+                                                         int head_dim, int start, const int32_t *positions,
+                                                         float theta, int llama3, float factor, float low,
+                                                         float high, float original_max) {
+    __shared__ float cs[256], sn[256];
+    const int64_t token = blockIdx.x;
+    const int half = head_dim / 2;
+    const int64_t position = positions ? (int64_t)positions[token] : start + token;
+    for (int f = threadIdx.x; f < half; f += blockDim.x) {
+        const float inv = rope_inverse_frequency(2 * f, head_dim, theta, llama3, factor, low, high, original_max);
+        const float phase = __fmul_rn((float)position, inv);
+        cs[f] = round_bf16((float)cos((double)phase));
+        sn[f] = round_bf16((float)sin((double)phase));
+    }
+    __syncthreads();
+    const int elements = heads * head_dim;
+    const uint16_t *row = in + token * elements;
+    uint16_t *dst = out + token * elements;
+    for (int e = threadIdx.x; e < elements; e += blockDim.x) {
+        const int d = e % head_dim;
+        const int h0 = e - d;
+        const float partner = read_bf16(row[h0 + (d < half ? d + half : d - half)]);
+        const float rotated = d < half ? -partner : partner;
+        const int f = d % half;
+        const float left = round_bf16(__fmul_rn(read_bf16(row[e]), cs[f]));
+        const float right = round_bf16(__fmul_rn(rotated, sn[f]));
+        dst[e] = write_bf16(__fadd_rn(left, right));
+    }
+}
+
 // A decode step's RoPE and K/V append in one launch, each sequence b at
 // positions[b]: rotated Q rows to q_out; rotated K and the V rows straight
 // into the page pool through page-table row b.  Lanes [0, nq) rotate Q
@@ -338,6 +373,11 @@ hipError_t launch_rmsnorm(const uint16_t *in, const uint16_t *w, uint16_t *out, 
 hipError_t launch_rope(const uint16_t *in, uint16_t *out, int tokens, int heads, int head_dim,
                        int start, const int32_t *positions, float theta, int llama3, float factor,
                        float low, float high, float original_max, hipStream_t stream) {
+    if (head_dim <= 512) {
+        hipLaunchKernelGGL(rope_token_kernel, dim3((unsigned)tokens), dim3(256), 0, stream, in, out, heads,
+                           head_dim, start, positions, theta, llama3, factor, low, high, original_max);
+        return hipGetLastError();
+    }
     const int64_t total = (int64_t)tokens * heads * head_dim;
     const unsigned blocks = (unsigned)((total + 255) / 256);
     hipLaunchKernelGGL(rope_kernel, dim3(blocks), dim3(256), 0, stream, in, out, total, heads, head_dim,
