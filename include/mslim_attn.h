@@ -34,6 +34,10 @@
  *            head-major ColdStore page payload (cold_store.rs:480-483,
  *            gpu_region_store.rs:386-390); page_table[b][i] is the pool page
  *            holding tokens [i*page_tokens, (i+1)*page_tokens) of sequence b.
+ *            The table is device memory and is not validated: every entry a
+ *            call reaches must name a page of the pool, as the reference's
+ *            region store guarantees for its own table
+ *            (gpu_region_store.rs:113-116, :486-489).
  */
 #ifndef MSLIM_ATTN_H
 #define MSLIM_ATTN_H
