@@ -18,10 +18,13 @@
 //     contiguous bytes of one K row as its A operand, so no K byte passes
 //     through LDS;
 //   * the online softmax max / sum run on 64-lane butterflies;
-//   * P.V accumulates in fp32 on the VALU from 128-bit V loads (16 lanes per
-//     256-byte row for D = 128), with P broadcast through a 2 KB LDS tile;
+//   * P.V runs on the same MFMA: V arrives in 128-bit loads (16 lanes per
+//     256-byte row for D = 128) and is staged transposed through a per-
+//     wavefront LDS slab as the B operand, with P taken straight from the
+//     S^T accumulator as the A operand;
 //   * the four wavefronts merge in LDS; the partitions of one (sequence, kv
-//     head) are merged in fixed partition order by a second, small launch.
+//     head) are merged in fixed partition order by the workgroup that
+//     finishes last (or, built with MSLIM_DECODE_FUSED=0, by a second launch).
 // Partitions are fixed by logical token index, and the paged and dense
 // variants differ only in how a 16-token block's base address is formed, so
 // both produce bit-identical outputs (the reference's dense == ColdStore
@@ -30,6 +33,7 @@
 #include "kernels.hpp"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace mslim {
 
@@ -109,12 +113,16 @@ __device__ __forceinline__ uint32_t pair_bf16(uint32_t hi_src, uint32_t lo_src, 
     return __builtin_amdgcn_perm(hi_src, lo_src, sel);
 }
 
-// Relaxed agent-scope atomics: coherent across the XCDs' L2 caches.
-__device__ __forceinline__ void store_coherent(float *p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Relaxed agent-scope atomics on float pairs (8-byte aligned): coherent
+// across the XCDs' L2 caches.
+__device__ __forceinline__ void store_coherent2(float *p, float x, float y) {
+    const uint64_t w = (uint64_t)__float_as_uint(x) | ((uint64_t)__float_as_uint(y) << 32);
+    __hip_atomic_store(reinterpret_cast<uint64_t *>(p), w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ float load_coherent(const float *p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ float2 load_coherent2(const float *p) {
+    const uint64_t w = __hip_atomic_load(reinterpret_cast<const uint64_t *>(p), __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+    return make_float2(__uint_as_float((uint32_t)w), __uint_as_float((uint32_t)(w >> 32)));
 }
 
 template <int D, int G>
@@ -355,14 +363,9 @@ __global__ __launch_bounds__(64 * kWaves, 2) void decode_kernel(DeviceArgs a) {
             // device-coherent level, so no cache writeback is needed before
             // the counter below publishes them.
             float *pa = a.partial_acc + (part + g) * D + d;
-            store_coherent(pa + 0, ov.x);
-            store_coherent(pa + 1, ov.y);
-            store_coherent(pa + 2, ov.z);
-            store_coherent(pa + 3, ov.w);
-            if (d == 0) {
-                store_coherent(a.partial_ml + (part + g) * 2, m);
-                store_coherent(a.partial_ml + (part + g) * 2 + 1, l);
-            }
+            store_coherent2(pa, ov.x, ov.y);
+            store_coherent2(pa + 2, ov.z, ov.w);
+            if (d == 0) store_coherent2(a.partial_ml + (part + g) * 2, m, l);
         } else {
             *reinterpret_cast<float4 *>(a.partial_acc + (part + g) * D + d) = ov;
             if (d == 0) *reinterpret_cast<float2 *>(a.partial_ml + (part + g) * 2) = make_float2(m, l);
@@ -406,20 +409,7 @@ __device__ __forceinline__ void merge_splits(const DeviceArgs &a, int b, int kvh
         const int d = (it % (D / 4)) * 4;
         float m = -INFINITY, l = 0.0f;
         float4 ov = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-#pragma unroll 8
-        for (int s = 0; s < nsplit; ++s) {
-            const int64_t idx = ((int64_t)(s0 + s) * a.kv_heads + kvh) * G + g;
-            float2 ml;
-            float4 x;
-            if (coherent) {
-                ml = make_float2(load_coherent(a.partial_ml + idx * 2), load_coherent(a.partial_ml + idx * 2 + 1));
-                const float *pa = a.partial_acc + idx * D + d;
-                x = make_float4(load_coherent(pa), load_coherent(pa + 1), load_coherent(pa + 2),
-                                load_coherent(pa + 3));
-            } else {
-                ml = *reinterpret_cast<const float2 *>(a.partial_ml + idx * 2);
-                x = *reinterpret_cast<const float4 *>(a.partial_acc + idx * D + d);
-            }
+        auto fold = [&](float2 ml, float4 x) {
             const float m_new = fmaxf(m, ml.x);
             const float wo = __builtin_amdgcn_exp2f((m - m_new) * c);
             const float wn = __builtin_amdgcn_exp2f((ml.x - m_new) * c);
@@ -427,6 +417,40 @@ __device__ __forceinline__ void merge_splits(const DeviceArgs &a, int b, int kvh
             ov.x = fmaf(ov.x, wo, x.x * wn); ov.y = fmaf(ov.y, wo, x.y * wn);
             ov.z = fmaf(ov.z, wo, x.z * wn); ov.w = fmaf(ov.w, wo, x.w * wn);
             m = m_new;
+        };
+        auto index = [&](int s) { return ((int64_t)(s0 + s) * a.kv_heads + kvh) * G + g; };
+        if (coherent) {
+            // The merge ends the call, so all loads of a batch of K
+            // partitions go out before its first fold (3K pair loads, one
+            // round trip); indices past the last partition repeat it and are
+            // not folded.
+            auto batches = [&](auto kb) {
+                constexpr int K = decltype(kb)::value;
+                for (int sb = 0; sb < nsplit; sb += K) {
+                    float2 ml[K], x0[K], x1[K];
+#pragma unroll
+                    for (int j = 0; j < K; ++j) {
+                        const int64_t idx = index(min(sb + j, nsplit - 1));
+                        const float *pa = a.partial_acc + idx * D + d;
+                        ml[j] = load_coherent2(a.partial_ml + idx * 2);
+                        x0[j] = load_coherent2(pa);
+                        x1[j] = load_coherent2(pa + 2);
+                    }
+#pragma unroll
+                    for (int j = 0; j < K; ++j) {
+                        if (sb + j < nsplit) fold(ml[j], make_float4(x0[j].x, x0[j].y, x1[j].x, x1[j].y));
+                    }
+                }
+            };
+            if (nsplit <= 8) batches(std::integral_constant<int, 8>{});
+            else batches(std::integral_constant<int, 16>{});
+        } else {
+#pragma unroll 8
+            for (int s = 0; s < nsplit; ++s) {
+                const int64_t idx = index(s);
+                fold(*reinterpret_cast<const float2 *>(a.partial_ml + idx * 2),
+                     *reinterpret_cast<const float4 *>(a.partial_acc + idx * D + d));
+            }
         }
         uint2 packed;
         packed.x = pack_bf16x2(ov.x / l, ov.y / l);
