@@ -11,7 +11,10 @@ the one the targets are quoted on):
 One step = one paged decode pass + one causal prefill pass.  The timed
 region runs the K decode passes back to back and then the K prefill passes,
 with events on the launch stream around each phase.  Inputs are resident in
-HBM before timing starts.  A decode launched directly after a prefill is
+HBM before timing starts.  The decode passes cycle through four distinct
+layer caches (2.1 GB of K/V pages, eight times the 256 MB Infinity Cache), as
+a model's decode walks its layers, so no pass finds the previous pass's bytes
+in a cache.  A decode launched directly after a prefill is
 timed separately and reported as `decode_after_prefill_ms`.
 
 `value` is the decode's achieved HBM bandwidth (algorithmic K+V+Q+O bytes /
@@ -65,6 +68,7 @@ PEAK_BF16_TFLOPS = 2500.0   # MI355X dense BF16 MFMA, published
 B, T, QH, KVH, D = 4, 32768, 64, 8, 128
 PAGE_TOKENS, HOT_WINDOW = 16, 4096
 S_PREFILL = 8192
+DECODE_LAYERS = 4  # distinct layer caches the timed decode cycles through
 
 
 def decode_bytes() -> int:
@@ -492,10 +496,15 @@ def main() -> int:
     def randn(shape):
         return torch.randn(shape, generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
 
-    k_dense = randn((B, T, KVH, D))
-    v_dense = randn((B, T, KVH, D))
+    # Layer l: dense K/V [B][T][KVH][D] and the same bytes in a page pool
+    # with its own seeded page table.  Layer 0 also feeds the seal and the
+    # CPU baseline.
+    layers = []
+    for l in range(DECODE_LAYERS):
+        kd, vd = randn((B, T, KVH, D)), randn((B, T, KVH, D))
+        layers.append((kd, vd) + build_page_pool(ctx, torch, kd, vd, seed=20261201 + l))
+    k_dense, v_dense, k_pool, v_pool = layers[0][:4]
     q_dec = randn((B, QH, D))
-    k_pool, v_pool, table, pages_per_seq = build_page_pool(ctx, torch, k_dense, v_dense, seed=20261201)
     out_dec = torch.empty_like(q_dec)
     out_dense = torch.empty_like(q_dec)
     q_pre = randn((S_PREFILL, QH, D))
@@ -504,9 +513,19 @@ def main() -> int:
     out_pre = torch.empty_like(q_pre)
     lens = [T] * B
 
-    def decode():
-        ctx.decode_paged(q_dec, k_pool, v_pool, out_dec, lens, table, pages_per_seq, PAGE_TOKENS,
-                         QH, KVH, D)
+    turn = [0]
+
+    def decode(layer=None):
+        l = turn[0] % DECODE_LAYERS if layer is None else layer
+        turn[0] += 1
+        _, _, kp, vp, table, pages_per_seq = layers[l]
+        ctx.decode_paged(q_dec, kp, vp, out_dec, lens, table, pages_per_seq, PAGE_TOKENS, QH, KVH, D)
+
+    def decode_dense(layer=None):
+        l = turn[0] % DECODE_LAYERS if layer is None else layer
+        turn[0] += 1
+        kd, vd = layers[l][:2]
+        ctx.decode_dense(q_dec, kd, vd, out_dense, lens, QH, KVH, D, seq_stride_tokens=T)
 
     def prefill():
         ctx.prefill_causal(q_pre, k_pre, v_pre, out_pre, S_PREFILL, 0, QH, KVH, D)
@@ -514,11 +533,14 @@ def main() -> int:
     if args.kernel != "all":
         return one_workload(torch, ctx, decode if args.kernel == "decode" else prefill, args)
 
-    # The paged ColdStore-exact decode must equal the dense decode bit for bit.
-    decode()
-    ctx.decode_dense(q_dec, k_dense, v_dense, out_dense, lens, QH, KVH, D, seq_stride_tokens=T)
-    torch.cuda.synchronize()
-    paged_equals_dense = bool(torch.equal(out_dec, out_dense))
+    # The paged ColdStore-exact decode must equal the dense decode bit for
+    # bit, on every layer.
+    paged_equals_dense = True
+    for l in range(DECODE_LAYERS):
+        decode(l)
+        decode_dense(l)
+        torch.cuda.synchronize()
+        paged_equals_dense &= bool(torch.equal(out_dec, out_dense))
 
     log(f"bench: warmup {args.warmup} steps")
     for _ in range(args.warmup):
@@ -562,15 +584,15 @@ def main() -> int:
     torch.cuda.synchronize()
     dec_after_prefill = sum(a.elapsed_time(b) for a, b in pairs) / args.steps
 
-    # dense decode on the same data, for reference
+    # dense decode over the same layers, for reference
     for _ in range(3):
-        ctx.decode_dense(q_dec, k_dense, v_dense, out_dense, lens, QH, KVH, D, seq_stride_tokens=T)
+        decode_dense()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda._sleep(QUEUE_FILL_CYCLES)
     e0.record()
     for _ in range(args.steps):
-        ctx.decode_dense(q_dec, k_dense, v_dense, out_dense, lens, QH, KVH, D, seq_stride_tokens=T)
+        decode_dense()
     e1.record()
     torch.cuda.synchronize()
     dense_ms = e0.elapsed_time(e1) / args.steps

@@ -113,6 +113,20 @@ __device__ __forceinline__ uint32_t pair_bf16(uint32_t hi_src, uint32_t lo_src, 
     return __builtin_amdgcn_perm(hi_src, lo_src, sel);
 }
 
+// K and V bytes are read exactly once per call, so they are loaded
+// non-temporally: the stream does not allocate in L2 or the Infinity Cache.
+// Over four distinct cfg4 caches cycled call after call (2.1 GB, nothing
+// reusable between calls) this measured 87.3 us per call against 95.6 us
+// with ordinary loads.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ bf16x8_t stream_bf16x8(const uint16_t *p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const bf16x8_t *>(p));
+}
+__device__ __forceinline__ uint4 stream_u4(const uint16_t *p) {
+    const u32x4_t t = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
+    return make_uint4(t.x, t.y, t.z, t.w);
+}
+
 // Relaxed agent-scope atomics on float pairs (8-byte aligned): coherent
 // across the XCDs' L2 caches.
 __device__ __forceinline__ void store_coherent2(float *p, float x, float y) {
@@ -193,7 +207,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void decode_kernel(DeviceArgs a) {
             const int row = min(t0 + blk * 16 + row16, last) - bt;
             const uint16_t *p = block_base<D, PAGED>(a, a.k, b, kvh, bt) + row * rs + grp * 8;
 #pragma unroll
-            for (int j = 0; j < KS; ++j) r.k[blk][j] = *reinterpret_cast<const bf16x8_t *>(p + j * 32);
+            for (int j = 0; j < KS; ++j) r.k[blk][j] = stream_bf16x8(p + j * 32);
         }
         const uint16_t *vb0 = block_base<D, PAGED>(a, a.v, b, kvh, min(t0, last & ~15));
         const uint16_t *vb1 = block_base<D, PAGED>(a, a.v, b, kvh, min(t0 + 16, last & ~15));
@@ -203,7 +217,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void decode_kernel(DeviceArgs a) {
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int row = min(t0 + vh * NV + i, last) - bt;
-            r.v[i] = *reinterpret_cast<const uint4 *>(vb + row * rs + vc * 8);
+            r.v[i] = stream_u4(vb + row * rs + vc * 8);
         }
     };
 
