@@ -664,8 +664,8 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(dec_gbps / PEAK_HBM_GBPS, 4),
             "traffic": traffic,
-            "kernel": "decode_kernel<128,8,paged,2,fused> (one launch; the last workgroup of each "
-                      f"(sequence, kv head) merges the splits), algorithmic bytes {decode_bytes()} per launch",
+            "kernel": "decode_kernel<128,8,paged,2,fused,non-temporal> (one launch; the last workgroup of "
+                      f"each (sequence, kv head) merges the splits), algorithmic bytes {decode_bytes()} per launch",
         },
         "prefill": {
             "value": round(pre_tflops, 2),

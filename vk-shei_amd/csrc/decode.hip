@@ -113,18 +113,28 @@ __device__ __forceinline__ uint32_t pair_bf16(uint32_t hi_src, uint32_t lo_src, 
     return __builtin_amdgcn_perm(hi_src, lo_src, sel);
 }
 
-// K and V bytes are read exactly once per call, so they are loaded
-// non-temporally: the stream does not allocate in L2 or the Infinity Cache.
-// Over four distinct cfg4 caches cycled call after call (2.1 GB, nothing
-// reusable between calls) this measured 87.3 us per call against 95.6 us
-// with ordinary loads.
+// K and V bytes are read exactly once per call.  A call that streams at least
+// the 256 MB Infinity Cache loads them non-temporally (NT), so the stream
+// does not allocate in L2 or the Infinity Cache; smaller calls use ordinary
+// loads.  Measured over distinct caches cycled call after call (nothing
+// reusable between calls), non-temporal against ordinary: 537 MB (cfg4)
+// 87.9 vs 96.0 us, 268 MB 48.0 vs 51.4 us, 134-138 MB equal or up to 1.7 us
+// slower (the cfg5 decoder's 8 x 4,224 tokens), 67 MB 0.5 us slower.
+constexpr int64_t kNonTemporalBytes = 256ll << 20;
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ bf16x8_t stream_bf16x8(const uint16_t *p) {
-    return __builtin_nontemporal_load(reinterpret_cast<const bf16x8_t *>(p));
+template <bool NT>
+__device__ __forceinline__ bf16x8_t kv_load8(const uint16_t *p) {
+    if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const bf16x8_t *>(p));
+    else return *reinterpret_cast<const bf16x8_t *>(p);
 }
-__device__ __forceinline__ uint4 stream_u4(const uint16_t *p) {
-    const u32x4_t t = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
-    return make_uint4(t.x, t.y, t.z, t.w);
+template <bool NT>
+__device__ __forceinline__ uint4 kv_load4(const uint16_t *p) {
+    if constexpr (NT) {
+        const u32x4_t t = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
+        return make_uint4(t.x, t.y, t.z, t.w);
+    } else {
+        return *reinterpret_cast<const uint4 *>(p);
+    }
 }
 
 // Relaxed agent-scope atomics on float pairs (8-byte aligned): coherent
@@ -143,7 +153,7 @@ template <int D, int G>
 __device__ __forceinline__ void merge_splits(const DeviceArgs &a, int b, int kvh, int tid, int nthreads,
                                              bool coherent);
 
-template <int D, int G, bool PAGED, int DEPTH, bool FUSED>
+template <int D, int G, bool PAGED, int DEPTH, bool FUSED, bool NT>
 __global__ __launch_bounds__(64 * kWaves, 2) void decode_kernel(DeviceArgs a) {
     constexpr int KS = D / 32;        // Q.K MFMA k-steps per 16-token block
     constexpr int LPR = D / 8;        // lanes per V row (8 BF16 per lane)
@@ -207,7 +217,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void decode_kernel(DeviceArgs a) {
             const int row = min(t0 + blk * 16 + row16, last) - bt;
             const uint16_t *p = block_base<D, PAGED>(a, a.k, b, kvh, bt) + row * rs + grp * 8;
 #pragma unroll
-            for (int j = 0; j < KS; ++j) r.k[blk][j] = stream_bf16x8(p + j * 32);
+            for (int j = 0; j < KS; ++j) r.k[blk][j] = kv_load8<NT>(p + j * 32);
         }
         const uint16_t *vb0 = block_base<D, PAGED>(a, a.v, b, kvh, min(t0, last & ~15));
         const uint16_t *vb1 = block_base<D, PAGED>(a, a.v, b, kvh, min(t0 + 16, last & ~15));
@@ -217,7 +227,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void decode_kernel(DeviceArgs a) {
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int row = min(t0 + vh * NV + i, last) - bt;
-            r.v[i] = stream_u4(vb + row * rs + vc * 8);
+            r.v[i] = kv_load4<NT>(vb + row * rs + vc * 8);
         }
     };
 
@@ -553,16 +563,20 @@ __global__ __launch_bounds__(64) void decode_generic_kernel(DeviceArgs a, int D)
 #endif
 
 template <int D, int G>
-hipError_t launch_fast(const DeviceArgs &a, bool paged, int total_splits, bool merge,
+hipError_t launch_fast(const DeviceArgs &a, bool paged, bool nt, int total_splits, bool merge,
                        hipStream_t stream) {
     const dim3 grid((unsigned)(total_splits * a.kv_heads));
     constexpr bool F = MSLIM_DECODE_FUSED != 0;
-    if (paged)
-        hipLaunchKernelGGL((decode_kernel<D, G, true, MSLIM_DECODE_DEPTH, F>), grid, dim3(64 * kWaves), 0,
-                           stream, a);
+    constexpr int DP = MSLIM_DECODE_DEPTH;
+    const dim3 block(64 * kWaves);
+    if (paged && nt)
+        hipLaunchKernelGGL((decode_kernel<D, G, true, DP, F, true>), grid, block, 0, stream, a);
+    else if (paged)
+        hipLaunchKernelGGL((decode_kernel<D, G, true, DP, F, false>), grid, block, 0, stream, a);
+    else if (nt)
+        hipLaunchKernelGGL((decode_kernel<D, G, false, DP, F, true>), grid, block, 0, stream, a);
     else
-        hipLaunchKernelGGL((decode_kernel<D, G, false, MSLIM_DECODE_DEPTH, F>), grid, dim3(64 * kWaves), 0,
-                           stream, a);
+        hipLaunchKernelGGL((decode_kernel<D, G, false, DP, F, false>), grid, block, 0, stream, a);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess || !merge || F) return err;
     hipLaunchKernelGGL((decode_merge_kernel<D, G>), dim3((unsigned)(a.batch * a.kv_heads)), dim3(256), 0,
@@ -606,7 +620,9 @@ hipError_t launch_decode(const DecodeLaunch &l, hipStream_t stream) {
     a.scale_log2e = l.scale * kLog2e;
     int total = 0;
     bool merge = false;
+    int64_t kv_tokens = 0;
     for (int i = 0; i < l.batch; ++i) {
+        kv_tokens += l.seq_len[i];
         a.seq_len[i] = l.seq_len[i];
         a.split_begin[i] = total;
         const int n = decode_splits(l.seq_len[i], l.split_tokens);
@@ -615,6 +631,7 @@ hipError_t launch_decode(const DecodeLaunch &l, hipStream_t stream) {
     }
     a.split_begin[l.batch] = total;
     const int group = l.q_heads / l.kv_heads;
+    const bool nt = kv_tokens * l.kv_heads * l.head_dim * 2 * 2 >= kNonTemporalBytes;
     if (!decode_fast_path(l.head_dim, group)) {
         const dim3 grid((unsigned)(l.batch * l.q_heads));
         if (l.paged)
@@ -624,7 +641,7 @@ hipError_t launch_decode(const DecodeLaunch &l, hipStream_t stream) {
         return hipGetLastError();
     }
 #define MSLIM_DECODE_CASE(DD, GG) \
-    if (l.head_dim == DD && group == GG) return launch_fast<DD, GG>(a, l.paged, total, merge, stream);
+    if (l.head_dim == DD && group == GG) return launch_fast<DD, GG>(a, l.paged, nt, total, merge, stream);
     MSLIM_DECODE_CASE(128, 16)
     MSLIM_DECODE_CASE(128, 8)
     MSLIM_DECODE_CASE(128, 4)
