@@ -108,11 +108,23 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(SkinnyArgs a) {
         // The B operand (token rows) is the same for every row tile: read it
         // once per workgroup with 16-byte loads instead of once per k-step
         // per wavefront.
+        // All of a thread's loads go out before its first LDS write (a
+        // load-wait-write loop costs one L2 round trip per 16 bytes); past
+        // the last chunk the index is clamped in bounds and not written.
+        constexpr int kPerThread = kStageTokens * kStageInner / 8 / (WAVES * 64);
         const int chunks = a.inner / 8;
-        for (int i = threadIdx.x; i < a.tokens * chunks; i += WAVES * 64) {
-            const int t = i / chunks, c = i % chunks;
-            *reinterpret_cast<uint4 *>(xs + t * kStageStride + c * 8) =
-                *reinterpret_cast<const uint4 *>(a.x + (int64_t)t * a.inner + c * 8);
+        const int total = a.tokens * chunks;
+        bf16x8_t v[kPerThread];
+#pragma unroll
+        for (int k = 0; k < kPerThread; ++k) {
+            const int i = min((int)threadIdx.x + k * WAVES * 64, total - 1);
+            v[k] = load8(a.x + (int64_t)(i / chunks) * a.inner + (i % chunks) * 8);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the writes
+#pragma unroll
+        for (int k = 0; k < kPerThread; ++k) {
+            const int i = (int)threadIdx.x + k * WAVES * 64;
+            if (i < total) *reinterpret_cast<bf16x8_t *>(xs + (i / chunks) * kStageStride + (i % chunks) * 8) = v[k];
         }
         __syncthreads();
     }
