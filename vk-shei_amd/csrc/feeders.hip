@@ -53,7 +53,6 @@ __global__ __launch_bounds__(128) void rmsnorm_kernel(const uint16_t *in, const 
 // per lane.  hidden % (128 * kRmsBatch) == 0 and hidden <= kRmsStagedMax;
 // dynamic LDS 4 * hidden bytes.
 constexpr int kRmsStagedMax = 8192;  // 32 KiB of dynamic LDS
-constexpr int kRmsLoadsInFlight = 4;
 constexpr int kRmsBatch = 8;
 
 __global__ __launch_bounds__(128) void rmsnorm_staged_kernel(const uint16_t *in, const uint16_t *w,
@@ -66,23 +65,24 @@ __global__ __launch_bounds__(128) void rmsnorm_staged_kernel(const uint16_t *in,
     const int chunks = hidden / 8;
     const uint4 *src = reinterpret_cast<const uint4 *>(in + (int64_t)blockIdx.x * hidden);
     const uint4 *wsrc = reinterpret_cast<const uint4 *>(w);
-    for (int base = tid; base < chunks; base += 128 * kRmsLoadsInFlight) {
-        uint4 a[kRmsLoadsInFlight], b[kRmsLoadsInFlight];
+    // Every load of the lane goes out before its first LDS write (the
+    // compiler otherwise pairs each load with its write and waits between
+    // them); chunks past the row are clamped in bounds and not written.
+    constexpr int kPer = kRmsStagedMax / 8 / 128;
+    bf16x8_t xa[kPer], wa[kPer];
 #pragma unroll
-        for (int u = 0; u < kRmsLoadsInFlight; ++u) {
-            const int c = base + u * 128;
-            if (c < chunks) {
-                a[u] = src[c];
-                b[u] = wsrc[c];
-            }
-        }
+    for (int k = 0; k < kPer; ++k) {
+        const int c = min(tid + 128 * k, chunks - 1);
+        xa[k] = *reinterpret_cast<const bf16x8_t *>(src + c);
+        wa[k] = *reinterpret_cast<const bf16x8_t *>(wsrc + c);
+    }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int u = 0; u < kRmsLoadsInFlight; ++u) {
-            const int c = base + u * 128;
-            if (c < chunks) {
-                staged[c] = a[u];
-                staged[chunks + c] = b[u];
-            }
+    for (int k = 0; k < kPer; ++k) {
+        const int c = tid + 128 * k;
+        if (c < chunks) {
+            reinterpret_cast<bf16x8_t *>(staged)[c] = xa[k];
+            reinterpret_cast<bf16x8_t *>(staged)[chunks + c] = wa[k];
         }
     }
     __syncthreads();
