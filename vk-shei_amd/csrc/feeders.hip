@@ -208,15 +208,47 @@ __global__ __launch_bounds__(256) void rope_token_kernel(const uint16_t *in, uin
     const int elements = heads * head_dim;
     const uint16_t *row = in + token * elements;
     uint16_t *dst = out + token * elements;
+    auto rotate = [&](float x, float partner, int d) {
+        const float rotated = d < half ? -partner : partner;
+        const int f = d % half;
+        const float left = round_bf16(__fmul_rn(x, cs[f]));
+        const float right = round_bf16(__fmul_rn(rotated, sn[f]));
+        return write_bf16(__fadd_rn(left, right));
+    };
+    if (head_dim % 16 == 0 && (((uintptr_t)row | (uintptr_t)dst) & 15) == 0) {
+        // 16-byte chunks of 8 elements (half % 8 == 0: a chunk and its
+        // rotate-half partner chunk each lie in one half of a head); every
+        // lane's loads of a batch go out before its first use.
+        constexpr int kBatch = 4;
+        const int chunks = elements / 8;
+        for (int c0 = threadIdx.x; c0 < chunks; c0 += kBatch * blockDim.x) {
+            uint4 x[kBatch], p[kBatch];
+#pragma unroll
+            for (int k = 0; k < kBatch; ++k) {
+                const int e = min(c0 + k * (int)blockDim.x, chunks - 1) * 8;
+                const int d = e % head_dim;
+                x[k] = *reinterpret_cast<const uint4 *>(row + e);
+                p[k] = *reinterpret_cast<const uint4 *>(row + e - d + (d < half ? d + half : d - half));
+            }
+#pragma unroll
+            for (int k = 0; k < kBatch; ++k) {
+                const int c = c0 + k * (int)blockDim.x;
+                if (c >= chunks) continue;
+                const int d = (c * 8) % head_dim;
+                const uint16_t *xs = reinterpret_cast<const uint16_t *>(&x[k]);
+                const uint16_t *ps = reinterpret_cast<const uint16_t *>(&p[k]);
+                uint16_t r[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) r[j] = rotate(read_bf16(xs[j]), read_bf16(ps[j]), d + j);
+                *reinterpret_cast<uint4 *>(dst + c * 8) = *reinterpret_cast<const uint4 *>(r);
+            }
+        }
+        return;
+    }
     for (int e = threadIdx.x; e < elements; e += blockDim.x) {
         const int d = e % head_dim;
         const int h0 = e - d;
-        const float partner = read_bf16(row[h0 + (d < half ? d + half : d - half)]);
-        const float rotated = d < half ? -partner : partner;
-        const int f = d % half;
-        const float left = round_bf16(__fmul_rn(read_bf16(row[e]), cs[f]));
-        const float right = round_bf16(__fmul_rn(rotated, sn[f]));
-        dst[e] = write_bf16(__fadd_rn(left, right));
+        dst[e] = rotate(read_bf16(row[e]), read_bf16(row[h0 + (d < half ? d + half : d - half)]), d);
     }
 }
 
