@@ -39,13 +39,27 @@ def test_rope_bit_exact(ctx, llama3, start):
 
 
 def test_rope_other_head_dims(ctx):
+    # 64, 80, 256: 16-byte chunks; 72 (half not a multiple of 8): one element
+    # per lane; 1024: the per-element kernel (head_dim > 512)
     rng = np.random.default_rng(1)
-    for d in (64, 80, 256, 1024):  # 1024: the per-element kernel (head_dim > 512)
+    for d in (64, 72, 80, 256, 1024):
         xb = normal_bf16(rng, (5, 4, d))
         out = torch.empty((5, 4, d), dtype=torch.int16, device="cuda")
         ctx.rope(to_torch(xb), out, 5, 4, d, 123, 10000.0)
         torch.cuda.synchronize()
         assert np.array_equal(from_torch(out).reshape(-1), oracle.rope_gpu(xb, 5, 4, d, 123, 10000.0))
+
+
+def test_rope_unaligned_rows_take_the_element_path(ctx):
+    # an output one element past a 16-byte boundary cannot take 16-byte chunks
+    rng = np.random.default_rng(2)
+    tokens, heads, d = 3, 8, 128
+    xb = normal_bf16(rng, (tokens, heads, d))
+    buf = torch.empty(tokens * heads * d + 1, dtype=torch.int16, device="cuda")
+    out = buf[1:]
+    ctx.rope(to_torch(xb), out, tokens, heads, d, 77, 500000.0)
+    torch.cuda.synchronize()
+    assert np.array_equal(from_torch(out).reshape(-1), oracle.rope_gpu(xb, tokens, heads, d, 77, 500000.0))
 
 
 def test_swiglu_bit_exact(ctx):
