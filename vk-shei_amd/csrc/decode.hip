@@ -33,6 +33,7 @@
 #include "kernels.hpp"
 
 #include <algorithm>
+#include <cstdint>
 #include <type_traits>
 
 namespace mslim {
@@ -587,15 +588,50 @@ hipError_t launch_fast(const DeviceArgs &a, bool paged, bool nt, int total_split
 }  // namespace
 
 int decode_auto_split_tokens(const int32_t *seq_lens, int batch, int kv_heads) {
-    // About one workgroup per CU (256 on MI355X): long partitions keep each
-    // workgroup's load pipeline full and measured fastest at the BASELINE
-    // shapes (4096 tokens per partition for 4 x 32k x 8 kv heads).  Multiple
-    // of 256, between 256 and 16384 tokens.
+    // Start from about one workgroup per CU (256 on MI355X): S1 = tokens *
+    // kv_heads / 256, a multiple of 256 in [256, 16384].  Long partitions keep
+    // each workgroup's load pipeline full, and for equal lengths S1 is the
+    // measured best (4,096 tokens for 4 x 32k x 8 kv heads).  Ragged lengths
+    // leave many short remainder partitions beside full ones, and the call
+    // waits for the busiest CU.  All of a call's workgroups (up to two per CU)
+    // start together, and workgroup i shares a CU with workgroup i + 256, so
+    // each split size from S1 down to S1 / 2 (multiples of 256, at most 512
+    // workgroups) is scored by its busiest CU: the sum of its workgroups'
+    // tokens plus kWorkgroupCost per workgroup.  The smallest score wins;
+    // ties keep the larger split.  Measured over ragged batches (cfg3-like
+    // 32 x U[512, 8192] and others), this picks within 4.5% of the best split
+    // of a sweep, where S1 alone was up to 33% slower.
+    constexpr int kCus = 256;
+    constexpr int64_t kMaxResident = 512;
+    constexpr int64_t kWorkgroupCost = 128;  // tokens' worth of fixed cost
     int64_t total = 0;
     for (int i = 0; i < batch; ++i) total += seq_lens[i];
-    int64_t per = (total * kv_heads + 255) / 256;
+    int64_t per = (total * kv_heads + kCus - 1) / kCus;
     per = (per + 255) / 256 * 256;
-    return (int)std::min<int64_t>(16384, std::max<int64_t>(256, per));
+    const int s1 = (int)std::min<int64_t>(16384, std::max<int64_t>(256, per));
+    int best_split = s1;
+    int64_t best_load = INT64_MAX;
+    int64_t load[kCus];
+    for (int s = s1; s >= std::max(256, s1 / 2); s -= 256) {
+        int64_t workgroups = 0;
+        for (int b = 0; b < batch; ++b) workgroups += (int64_t)decode_splits(seq_lens[b], s) * kv_heads;
+        if (workgroups > kMaxResident && s != s1) continue;
+        std::fill(load, load + kCus, (int64_t)0);
+        int64_t wg = 0;
+        for (int b = 0; b < batch; ++b) {
+            const int n = decode_splits(seq_lens[b], s);
+            for (int sp = 0; sp < n; ++sp) {
+                const int64_t part = std::min<int64_t>(s, (int64_t)seq_lens[b] - (int64_t)sp * s) + kWorkgroupCost;
+                for (int h = 0; h < kv_heads; ++h) load[(wg++) % kCus] += part;
+            }
+        }
+        const int64_t busiest = *std::max_element(load, load + kCus);
+        if (busiest < best_load) {
+            best_load = busiest;
+            best_split = s;
+        }
+    }
+    return best_split;
 }
 
 bool decode_fast_path(int head_dim, int group) {

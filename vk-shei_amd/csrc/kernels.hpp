@@ -36,8 +36,9 @@ struct DecodeLaunch {
 inline int decode_splits(int tokens, int split_tokens) {
     return (tokens + split_tokens - 1) / split_tokens;
 }
-// Library choice of split_tokens for a batch: about one workgroup per CU,
-// 256..16384 tokens per split.
+// Library choice of split_tokens for a batch: about one workgroup per CU for
+// equal lengths, smaller for ragged lengths when that evens out the busiest
+// CU's load; a multiple of 256 in 256..16384.
 int decode_auto_split_tokens(const int32_t *seq_lens, int batch, int kv_heads);
 // True when the MFMA fast path covers this geometry.
 bool decode_fast_path(int head_dim, int group);
