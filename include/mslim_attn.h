@@ -128,6 +128,16 @@ int mslim_attn_decode_dense(void *ctx, const void *q, const void *k, const void 
                             int64_t seq_stride_tokens, int q_heads, int kv_heads,
                             int head_dim, float scale, int split_tokens);
 
+/* The split_tokens that split_tokens = 0 picks for this batch: about one
+ * workgroup per CU for equal lengths, a smaller split for ragged lengths
+ * when that evens out the busiest CU's load; a multiple of 256 in
+ * [256, 16384].  A function of the lengths and kv_heads only, so the dense
+ * and paged entry points pick the same partitions.  Host only (no context,
+ * no device work); -1 on invalid arguments.  No counterpart in the
+ * reference, whose split count is a config field (attention_kernel.rs:
+ * 16-40, splits 1..64). */
+int mslim_attn_decode_auto_split(const int32_t *seq_lens, int batch, int kv_heads);
+
 /* The same decode over the ColdStore-exact paged layout.  Replaces
  * attention_gpu_region (gpu_resources.rs:883-1063: llm_attention_qk/softmax +
  * llm_lod_pv_stage/finish, gpu_llm.cl:280-322) at epsilon = 0, with K and V

@@ -79,3 +79,45 @@ def test_host_library_exports_the_model_runner():
     model.host_library()
     lib = ctypes.CDLL(model.HOST_LIB_PATH)
     assert [n for n in declared if not hasattr(lib, n)] == []
+
+
+def _one_per_cu_split(lens, kv_heads):
+    per = -(-sum(lens) * kv_heads // 256)
+    return min(16384, max(256, -(-per // 256) * 256))
+
+
+def test_auto_split_choices():
+    # host-only policy of split_tokens = 0 (mslim_attn_decode_auto_split)
+    import numpy as np
+    from mslim_attn import auto_split
+    # equal lengths keep about one workgroup per CU: cfg4 (256 workgroups), cfg5
+    assert auto_split([32768] * 4, 8) == 4096
+    assert auto_split([4224] * 8, 8) == 1280
+    # ragged lengths take the split that evens out the busiest CU; both were
+    # measured faster on MI355X than the one-per-CU split (126.6 vs 154 us and
+    # 101.7 vs 149 us)
+    cfg3 = np.random.default_rng(20261203).integers(512, 8193, size=32).tolist()
+    assert auto_split(cfg3, 8) == 3328 and _one_per_cu_split(cfg3, 8) == 4608
+    skew = np.random.default_rng(17).integers(1024, 32769, size=8).tolist()
+    assert auto_split(skew, 8) == 2304
+
+
+def test_auto_split_invariants():
+    import numpy as np
+    from mslim_attn import auto_split, split_count
+    for seed in range(40):
+        rng = np.random.default_rng(seed)
+        lens = rng.integers(1, 65537, size=int(rng.integers(1, 65))).tolist()
+        kvh = int(rng.choice([1, 2, 4, 8, 16]))
+        s, s1 = auto_split(lens, kvh), _one_per_cu_split(lens, kvh)
+        assert s % 256 == 0 and 256 <= s <= s1 and s >= s1 // 2 - 255
+        if s != s1:
+            assert sum(split_count(t, s) for t in lens) * kvh <= 512
+        assert auto_split(list(reversed(lens)), kvh) % 256 == 0
+
+
+def test_auto_split_rejects_bad_batches():
+    from mslim_attn import MslimAttnError, auto_split
+    for lens, kvh in (([], 8), ([0], 8), ([5] * 65, 8), ([5], 0)):
+        with pytest.raises(MslimAttnError, match="code=-1"):
+            auto_split(lens, kvh)

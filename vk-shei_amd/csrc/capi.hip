@@ -339,6 +339,15 @@ int mslim_attn_buf_write(void *ctx, void *buffer, size_t offset, const uint8_t *
     return check_hip(hipStreamSynchronize(c.stream), "hipStreamSynchronize write");
 }
 
+int mslim_attn_decode_auto_split(const int32_t *seq_lens, int batch, int kv_heads) {
+    g_error.clear();
+    if (!seq_lens || batch < 1 || batch > MSLIM_ATTN_MAX_BATCH || kv_heads < 1)
+        return fail("decode batch must be 1..64 with host seq_lens and kv_heads >= 1");
+    for (int i = 0; i < batch; ++i)
+        if (seq_lens[i] < 1) return fail("decode seq_lens must be >= 1");
+    return mslim::decode_auto_split_tokens(seq_lens, batch, kv_heads);
+}
+
 int mslim_attn_decode_dense(void *ctx, const void *q, const void *k, const void *v, void *out,
                             int batch, const int32_t *seq_lens, int64_t seq_stride_tokens,
                             int q_heads, int kv_heads, int head_dim, float scale,

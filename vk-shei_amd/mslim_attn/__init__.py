@@ -54,6 +54,7 @@ EXPORTS = (
     "mslim_attn_buf_free",
     "mslim_attn_buf_read",
     "mslim_attn_buf_write",
+    "mslim_attn_decode_auto_split",
     "mslim_attn_decode_dense",
     "mslim_attn_decode_paged",
     "mslim_attn_prefill_causal",
@@ -129,6 +130,7 @@ def library() -> C.CDLL:
         "mslim_attn_buf_free": (I, [P, P]),
         "mslim_attn_buf_read": (I, [P, P, SZ, P, SZ]),
         "mslim_attn_buf_write": (I, [P, P, SZ, P, SZ]),
+        "mslim_attn_decode_auto_split": (I, [C.POINTER(C.c_int32), I, I]),
         "mslim_attn_decode_dense": (I, [P, P, P, P, P, I, PI32, I64, I, I, I, F, I]),
         "mslim_attn_decode_paged": (I, [P, P, P, P, P, I, PI32, P, I, I, I, I, I, F, I]),
         "mslim_attn_prefill_causal": (I, [P, P, P, P, P, I, I, I, I, I, F]),
@@ -454,3 +456,13 @@ def _host_ptr(a) -> int:
 
 def split_count(tokens: int, split_tokens: int) -> int:
     return math.ceil(tokens / split_tokens)
+
+
+def auto_split(seq_lens: Sequence[int], kv_heads: int) -> int:
+    """The split_tokens that split_tokens = 0 picks for this batch (host only)."""
+    lib = library()
+    arr = (C.c_int32 * len(seq_lens))(*[int(t) for t in seq_lens])
+    out = lib.mslim_attn_decode_auto_split(arr, len(seq_lens), kv_heads)
+    if out < 0:
+        raise MslimAttnError("decode_auto_split", out, lib.mslim_attn_last_error().decode())
+    return out
