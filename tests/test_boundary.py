@@ -93,11 +93,12 @@ def test_auto_split_choices():
     # equal lengths keep about one workgroup per CU: cfg4 (256 workgroups), cfg5
     assert auto_split([32768] * 4, 8) == 4096
     assert auto_split([4224] * 8, 8) == 1280
-    # ragged lengths take the split that evens out the busiest CU; both were
-    # measured faster on MI355X than the one-per-CU split (126.6 vs 154 us and
-    # 101.7 vs 149 us)
+    # ragged lengths take the split that evens out the busiest CU when the
+    # last partitions launch after the full ones, longest first; both were
+    # measured faster on MI355X than the one-per-CU split (116.7 vs 154 us and
+    # 101.6 vs 149 us)
     cfg3 = np.random.default_rng(20261203).integers(512, 8193, size=32).tolist()
-    assert auto_split(cfg3, 8) == 3328 and _one_per_cu_split(cfg3, 8) == 4608
+    assert auto_split(cfg3, 8) == 2304 and _one_per_cu_split(cfg3, 8) == 4608
     skew = np.random.default_rng(17).integers(1024, 32769, size=8).tolist()
     assert auto_split(skew, 8) == 2304
 
@@ -110,9 +111,11 @@ def test_auto_split_invariants():
         lens = rng.integers(1, 65537, size=int(rng.integers(1, 65))).tolist()
         kvh = int(rng.choice([1, 2, 4, 8, 16]))
         s, s1 = auto_split(lens, kvh), _one_per_cu_split(lens, kvh)
-        assert s % 256 == 0 and 256 <= s <= s1 and s >= s1 // 2 - 255
+        assert s % 256 == 0 and 256 <= s <= s1 and s >= s1 // 4 - 255
         if s != s1:
-            assert sum(split_count(t, s) for t in lens) * kvh <= 512
+            assert sum(split_count(t, s) for t in lens) * kvh <= 2048
+        if len(set(lens)) == 1:
+            assert s == s1
         assert auto_split(list(reversed(lens)), kvh) % 256 == 0
 
 

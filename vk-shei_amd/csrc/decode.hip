@@ -33,6 +33,9 @@
 #include "kernels.hpp"
 
 #include <algorithm>
+#include <utility>
+#include <vector>
+#include <queue>
 #include <cstdint>
 #include <type_traits>
 
@@ -42,6 +45,11 @@ namespace {
 
 #ifndef MSLIM_DECODE_WAVES
 #define MSLIM_DECODE_WAVES 4
+#endif
+// 1: full partitions launch first, last partitions after them, longest first
+// (the order the automatic split models); 0: sequence order.
+#ifndef MSLIM_DECODE_LPT
+#define MSLIM_DECODE_LPT 1
 #endif
 constexpr int kWaves = MSLIM_DECODE_WAVES;
 constexpr int kTile = 32;
@@ -60,6 +68,11 @@ struct DeviceArgs {
     float scale_log2e;
     int seq_len[kMaxBatch];
     int split_begin[kMaxBatch + 1];
+    // Launch order of the partitions: every sequence's partitions but its
+    // last, in sequence order (full_begin: prefix counts), then the last
+    // partitions, longest first (last_order: sequence indices).
+    int full_begin[kMaxBatch + 1];
+    int16_t last_order[kMaxBatch];
 };
 
 // Base of the 16-token block starting at logical token t0 (a multiple of 16).
@@ -83,11 +96,13 @@ __device__ __forceinline__ int row_stride(const DeviceArgs &a) {
     else return a.kv_heads * D;
 }
 
+#if !MSLIM_DECODE_LPT
 __device__ __forceinline__ int sequence_of(const DeviceArgs &a, int sg) {
     int b = 0;
     while (b + 1 < a.batch && a.split_begin[b + 1] <= sg) ++b;
     return b;
 }
+#endif
 
 // Ordering point for LDS traffic inside one wavefront: a wavefront's LDS
 // operations execute in order, so only the compiler must not move them.
@@ -175,8 +190,24 @@ __global__ __launch_bounds__(64 * kWaves, 2) void decode_kernel(DeviceArgs a) {
     const int grp = lane >> 4;
     const int kvh = blockIdx.x % a.kv_heads;
     const int sg = blockIdx.x / a.kv_heads;
+#if MSLIM_DECODE_LPT
+    // Full partitions launch first and the shorter last partitions after
+    // them, longest first: when a launch has more workgroups than fit at
+    // once, the dispatcher hands the short ones to the CUs that free up.
+    // The partition's logical index (split_begin[b] + split) is unchanged.
+    int b = 0, split = 0;
+    const int full_total = a.full_begin[a.batch];
+    if (sg < full_total) {
+        while (b + 1 < a.batch && a.full_begin[b + 1] <= sg) ++b;
+        split = sg - a.full_begin[b];
+    } else {
+        b = a.last_order[sg - full_total];
+        split = a.split_begin[b + 1] - a.split_begin[b] - 1;
+    }
+#else
     const int b = sequence_of(a, sg);
     const int split = sg - a.split_begin[b];
+#endif
     const int nsplit = a.split_begin[b + 1] - a.split_begin[b];
     const int seq_len = a.seq_len[b];
     const int begin = split * a.split_tokens;
@@ -361,7 +392,9 @@ __global__ __launch_bounds__(64 * kWaves, 2) void decode_kernel(DeviceArgs a) {
     // Combine the four wavefronts in fixed order: thread -> (head, 4 dims).
     constexpr int ITEMS = G * D / 4;
     const bool final_write = nsplit == 1;
-    const int64_t part = ((int64_t)sg * a.kv_heads + kvh) * G;
+    // Partials are stored by logical partition index, the order the merge
+    // reads them in, whatever the launch order.
+    const int64_t part = ((int64_t)(a.split_begin[b] + split) * a.kv_heads + kvh) * G;
     for (int it = tid; it < ITEMS; it += 64 * kWaves) {
         const int g = it / (D / 4);
         const int d = (it % (D / 4)) * 4;
@@ -588,43 +621,69 @@ hipError_t launch_fast(const DeviceArgs &a, bool paged, bool nt, int total_split
 }  // namespace
 
 int decode_auto_split_tokens(const int32_t *seq_lens, int batch, int kv_heads) {
-    // Start from about one workgroup per CU (256 on MI355X): S1 = tokens *
-    // kv_heads / 256, a multiple of 256 in [256, 16384].  Long partitions keep
-    // each workgroup's load pipeline full, and for equal lengths S1 is the
-    // measured best (4,096 tokens for 4 x 32k x 8 kv heads).  Ragged lengths
-    // leave many short remainder partitions beside full ones, and the call
-    // waits for the busiest CU.  All of a call's workgroups (up to two per CU)
-    // start together, and workgroup i shares a CU with workgroup i + 256, so
-    // each split size from S1 down to S1 / 2 (multiples of 256, at most 512
-    // workgroups) is scored by its busiest CU: the sum of its workgroups'
-    // tokens plus kWorkgroupCost per workgroup.  The smallest score wins;
-    // ties keep the larger split.  Measured over ragged batches (cfg3-like
-    // 32 x U[512, 8192] and others), this picks within 4.5% of the best split
-    // of a sweep, where S1 alone was up to 33% slower.
+    // S1 = tokens * kv_heads / 256, a multiple of 256 in [256, 16384]: about
+    // one workgroup per CU (256 on MI355X).  For equal lengths that is the
+    // measured best (4,096 tokens for 4 x 32k x 8 kv heads, 1,280 for
+    // 8 x 4,224), and it is returned as is.
+    //
+    // Ragged lengths leave short last partitions beside full ones.  The
+    // kernel launches the full partitions first and the last ones longest
+    // first; workgroups i and i + 256 start together on one CU, and each later
+    // workgroup starts on the CU that frees a slot first.  Two workgroups on a
+    // CU measured no faster together than one, so a CU finishes when its
+    // total work is done.  Each candidate split from S1 down to S1 / 4 (at
+    // most 2,048 workgroups) is scored by the busiest CU under that dispatch
+    // (greedy: each later workgroup to the least-loaded CU), counting
+    // kWorkgroupCost tokens of fixed cost per workgroup; the lowest score
+    // wins, ties keep the larger split.  On five measured batch shapes
+    // (ragged and equal) this picks the fastest split of the sweep.
     constexpr int kCus = 256;
-    constexpr int64_t kMaxResident = 512;
-    constexpr int64_t kWorkgroupCost = 128;  // tokens' worth of fixed cost
+    constexpr int64_t kWorkgroupCost = 256;
+    constexpr int64_t kMaxWorkgroups = 2048;
     int64_t total = 0;
-    for (int i = 0; i < batch; ++i) total += seq_lens[i];
+    bool uniform = true;
+    for (int i = 0; i < batch; ++i) {
+        total += seq_lens[i];
+        uniform &= seq_lens[i] == seq_lens[0];
+    }
     int64_t per = (total * kv_heads + kCus - 1) / kCus;
     per = (per + 255) / 256 * 256;
     const int s1 = (int)std::min<int64_t>(16384, std::max<int64_t>(256, per));
+    if (uniform) return s1;
+    const int step = std::max(256, s1 / 16 / 256 * 256);
     int best_split = s1;
     int64_t best_load = INT64_MAX;
     int64_t load[kCus];
-    for (int s = s1; s >= std::max(256, s1 / 2); s -= 256) {
+    int last_len[kMaxBatch];
+    for (int s = s1; s >= std::max(256, s1 / 4); s -= step) {
         int64_t workgroups = 0;
         for (int b = 0; b < batch; ++b) workgroups += (int64_t)decode_splits(seq_lens[b], s) * kv_heads;
-        if (workgroups > kMaxResident && s != s1) continue;
+        if (workgroups > kMaxWorkgroups && s != s1) continue;
+        for (int b = 0; b < batch; ++b) last_len[b] = seq_lens[b] - (decode_splits(seq_lens[b], s) - 1) * s;
+        std::sort(last_len, last_len + batch, [](int x, int y) { return x > y; });
         std::fill(load, load + kCus, (int64_t)0);
+        std::priority_queue<std::pair<int64_t, int>, std::vector<std::pair<int64_t, int>>,
+                            std::greater<std::pair<int64_t, int>>> free_first;
         int64_t wg = 0;
-        for (int b = 0; b < batch; ++b) {
-            const int n = decode_splits(seq_lens[b], s);
-            for (int sp = 0; sp < n; ++sp) {
-                const int64_t part = std::min<int64_t>(s, (int64_t)seq_lens[b] - (int64_t)sp * s) + kWorkgroupCost;
-                for (int h = 0; h < kv_heads; ++h) load[(wg++) % kCus] += part;
+        auto place = [&](int64_t tokens) {
+            const int64_t work = tokens + kWorkgroupCost;
+            if (wg < 2 * kCus) {
+                load[wg % kCus] += work;
+                if (wg == 2 * kCus - 1)
+                    for (int c = 0; c < kCus; ++c) free_first.push({load[c], c});
+            } else {
+                auto [l, c] = free_first.top();
+                free_first.pop();
+                load[c] = l + work;
+                free_first.push({load[c], c});
             }
-        }
+            ++wg;
+        };
+        for (int b = 0; b < batch; ++b)
+            for (int sp = 0; sp + 1 < decode_splits(seq_lens[b], s); ++sp)
+                for (int h = 0; h < kv_heads; ++h) place(s);
+        for (int b = 0; b < batch; ++b)
+            for (int h = 0; h < kv_heads; ++h) place(last_len[b]);
         const int64_t busiest = *std::max_element(load, load + kCus);
         if (busiest < best_load) {
             best_load = busiest;
@@ -666,6 +725,18 @@ hipError_t launch_decode(const DecodeLaunch &l, hipStream_t stream) {
         total += n;
     }
     a.split_begin[l.batch] = total;
+    int full = 0;
+    for (int i = 0; i < l.batch; ++i) {
+        a.full_begin[i] = full;
+        full += a.split_begin[i + 1] - a.split_begin[i] - 1;
+        a.last_order[i] = (int16_t)i;
+    }
+    a.full_begin[l.batch] = full;
+    auto last_len = [&](int i) {
+        return l.seq_len[i] - (a.split_begin[i + 1] - a.split_begin[i] - 1) * l.split_tokens;
+    };
+    std::stable_sort(a.last_order, a.last_order + l.batch,
+                     [&](int16_t x, int16_t y) { return last_len(x) > last_len(y); });
     const int group = l.q_heads / l.kv_heads;
     const bool nt = kv_tokens * l.kv_heads * l.head_dim * 2 * 2 >= kNonTemporalBytes;
     if (!decode_fast_path(l.head_dim, group)) {
