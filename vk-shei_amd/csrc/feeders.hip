@@ -18,6 +18,22 @@ namespace mslim {
 
 namespace {
 
+// Tree over the 128 lane sums of an RMSNorm row, pairs (t, t + stride) for
+// stride 64 .. 1 (gpu_llm.cl:72-98): the first level crosses the two
+// wavefronts through LDS, the rest are shuffles inside wavefront 0, whose lane
+// 0 ends with the same sum and leaves it in partials[0].
+__device__ __forceinline__ void rms_tree(float *partials, float s, int tid) {
+    if (tid >= 64) partials[tid] = s;
+    __syncthreads();
+    if (tid < 64) {
+        float t = __fadd_rn(s, partials[tid + 64]);
+#pragma unroll
+        for (int stride = 32; stride > 0; stride >>= 1) t = __fadd_rn(t, __shfl_down(t, stride, 64));
+        if (tid == 0) partials[0] = t;
+    }
+    __syncthreads();
+}
+
 // llm_rmsnorm / llm_prefill_norm (gpu_llm.cl:72-98, :378-408): one workgroup
 // of 128 lanes per token, strided FMA sum of squares, 64..1 tree.
 __global__ __launch_bounds__(128) void rmsnorm_kernel(const uint16_t *in, const uint16_t *w,
@@ -31,12 +47,7 @@ __global__ __launch_bounds__(128) void rmsnorm_kernel(const uint16_t *in, const 
         const float v = read_bf16(row[i]);
         s = __fmaf_rn(v, v, s);
     }
-    partials[tid] = s;
-    __syncthreads();
-    for (int stride = 64; stride > 0; stride >>= 1) {
-        if (tid < stride) partials[tid] = __fadd_rn(partials[tid], partials[tid + stride]);
-        __syncthreads();
-    }
+    rms_tree(partials, s, tid);
     const float mean = __fdiv_rn(partials[0], (float)hidden);
     const float factor = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, eps)));
     for (int i = tid; i < hidden; i += 128) {
@@ -97,12 +108,7 @@ __global__ __launch_bounds__(128) void rmsnorm_staged_kernel(const uint16_t *in,
 #pragma unroll
         for (int u = 0; u < kRmsBatch; ++u) s = __fmaf_rn(v[u], v[u], s);
     }
-    partials[tid] = s;
-    __syncthreads();
-    for (int stride = 64; stride > 0; stride >>= 1) {
-        if (tid < stride) partials[tid] = __fadd_rn(partials[tid], partials[tid + stride]);
-        __syncthreads();
-    }
+    rms_tree(partials, s, tid);
     const float mean = __fdiv_rn(partials[0], (float)hidden);
     const float factor = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, eps)));
     // each lane rewrites only the elements it read, so in place is safe
