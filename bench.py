@@ -434,6 +434,105 @@ def timed_calls(torch, fn, steps: int) -> float:
     return e0.elapsed_time(e1) / steps
 
 
+def other_configs_leg(torch, ctx, np, steps: int) -> dict:
+    """BASELINE cfg1-cfg3 at their own shapes, informational (the headline
+    line is cfg4).  cfg1: dense decode, B=1, T=1,024, 32/8 heads.  cfg2:
+    RoPE (theta 5e5, rotate-half) of Q and K at positions 0..2,047, then the
+    causal prefill of 2,048 tokens, 32/8 heads.  cfg3: 32 sessions with
+    lengths U[512, 8192] (seeded), 16-token pages under seeded random page
+    tables, four distinct layer pools cycled; paged == dense is checked bit
+    for bit on the first."""
+    import mslim_attn
+
+    gen = torch.Generator(device="cuda").manual_seed(0x43464733)
+
+    def randn(shape):
+        return torch.randn(shape, generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+
+    qh, kvh, d = 32, 8, 128
+    out = {}
+    # cfg1
+    k1, v1, q1 = randn((1, 1024, kvh, d)), randn((1, 1024, kvh, d)), randn((1, qh, d))
+    o1 = torch.empty_like(q1)
+    f1 = lambda: ctx.decode_dense(q1, k1, v1, o1, [1024], qh, kvh, d)
+    for _ in range(5):
+        f1()
+    ms1 = timed_calls(torch, f1, steps)
+    bytes1 = 1024 * kvh * d * 2 * 2 + qh * d * 2 * 2
+    out["cfg1_dense_decode"] = {"us": round(ms1 * 1e3, 2), "gbps": round(bytes1 / (ms1 * 1e-3) / 1e9, 1),
+                                "bytes": bytes1, "note": "B=1, T=1,024: launch-bound (0.53 us at the HBM peak)"}
+    # cfg2
+    s2 = 2048
+    q2, k2, v2 = randn((s2, qh, d)), randn((s2, kvh, d)), randn((s2, kvh, d))
+    q2r, k2r, o2 = torch.empty_like(q2), torch.empty_like(k2), torch.empty_like(q2)
+
+    def rope2():
+        ctx.rope(q2, q2r, s2, qh, d, 0, 500000.0)
+        ctx.rope(k2, k2r, s2, kvh, d, 0, 500000.0)
+
+    f2 = lambda: ctx.prefill_causal(q2r, k2r, v2, o2, s2, 0, qh, kvh, d)
+    rope2()
+    for _ in range(PREFILL_WARM):
+        f2()
+    ms2 = timed_calls(torch, f2, steps)
+    ms2r = timed_calls(torch, rope2, steps)
+    flops2 = 2 * d * qh * s2 * (s2 + 1)
+    out["cfg2_prefill"] = {"us": round(ms2 * 1e3, 2), "tflops": round(flops2 / (ms2 * 1e-3) / 1e12, 1),
+                           "flop": flops2, "rope_qk_us": round(ms2r * 1e3, 2),
+                           "note": "256 workgroups (64 rows x 4 heads each), one per CU, of 1 to 32 "
+                                   "causal key tiles: the launch lasts as long as the longest, so the "
+                                   "chip is about half busy"}
+    # cfg3
+    lens = np.random.default_rng(20261203).integers(512, 8193, size=32).tolist()
+    nb = len(lens)
+    pps = max(-(-t // PAGE_TOKENS) for t in lens)
+    npages = sum(-(-t // PAGE_TOKENS) for t in lens)
+    tmax = pps * PAGE_TOKENS
+    q3 = randn((nb, qh, d))
+    layers = []
+    for layer in range(DECODE_LAYERS):
+        kd, vd = randn((nb, tmax, kvh, d)), randn((nb, tmax, kvh, d))
+        perm = np.random.default_rng(1000 + layer).permutation(npages).astype(np.int32)
+        table = np.zeros((nb, pps), np.int32)
+        o = 0
+        for b, t in enumerate(lens):
+            n = -(-t // PAGE_TOKENS)
+            table[b, :n] = perm[o:o + n]
+            o += n
+        table_t = torch.from_numpy(table).cuda()
+        kp = torch.empty((npages, kvh, PAGE_TOKENS, d), dtype=torch.int16, device="cuda")
+        vp = torch.empty_like(kp)
+        for b, t in enumerate(lens):
+            ctx.pages_write(kp, vp, table_t[b], PAGE_TOKENS, kvh, d, 0, t, kd[b], vd[b])
+        layers.append((kp, vp, table_t, kd if layer == 0 else None, vd if layer == 0 else None))
+        del kd, vd
+    o3, o3d = torch.empty_like(q3), torch.empty_like(q3)
+    kp, vp, tab, kd, vd = layers[0]
+    ctx.decode_paged(q3, kp, vp, o3, lens, tab, pps, PAGE_TOKENS, qh, kvh, d)
+    ctx.decode_dense(q3, kd, vd, o3d, lens, qh, kvh, d, seq_stride_tokens=tmax)
+    torch.cuda.synchronize()
+    equal = bool(torch.equal(o3, o3d))
+    it = [0]
+
+    def f3():
+        kp, vp, tab = layers[it[0] % DECODE_LAYERS][:3]
+        it[0] += 1
+        ctx.decode_paged(q3, kp, vp, o3, lens, tab, pps, PAGE_TOKENS, qh, kvh, d)
+
+    for _ in range(2 * DECODE_LAYERS):
+        f3()
+    ms3 = timed_calls(torch, f3, steps)
+    bytes3 = sum(lens) * kvh * d * 2 * 2 + nb * qh * d * 2 * 2
+    out["cfg3_paged_ragged_decode"] = {
+        "us": round(ms3 * 1e3, 2), "gbps": round(bytes3 / (ms3 * 1e-3) / 1e9, 1),
+        "frac_of_hbm_peak": round(bytes3 / (ms3 * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4), "bytes": bytes3,
+        "tokens": int(sum(lens)), "auto_split_tokens": mslim_attn.auto_split(lens, kvh),
+        "paged_equals_dense": equal}
+    if not equal:
+        raise SystemExit("cfg3: paged decode differs from dense decode")
+    return out
+
+
 def one_workload(torch, ctx, fn, args) -> int:
     for _ in range(args.warmup):
         fn()
@@ -629,6 +728,9 @@ def main() -> int:
     traffic = measured_traffic("decode_paged_cfg4")
     pre_traffic = measured_traffic("prefill_causal_s8192")
 
+    log("bench: cfg1-cfg3 at their own shapes")
+    others = other_configs_leg(torch, ctx, np, args.steps)
+
     decoder = decoder_leg(torch, ctx, args, np) if args.decoder_steps > 0 else None
 
     cpu = None
@@ -705,6 +807,7 @@ def main() -> int:
         "decode_after_prefill_ms": round(dec_after_prefill, 5),
         "decode_dense_gbps": round(dense_gbps, 2),
         "paged_equals_dense": paged_equals_dense,
+        "other_configs": others,
         "decoder": decoder,
         "cpu_baseline": cpu,
     }
