@@ -204,11 +204,14 @@ __global__ __launch_bounds__(256) void rope_token_kernel(const uint16_t *in, uin
     const int64_t token = blockIdx.x;
     const int half = head_dim / 2;
     const int64_t position = positions ? (int64_t)positions[token] : start + token;
-    for (int f = threadIdx.x; f < half; f += blockDim.x) {
+    // Lanes [0, half) compute c and lanes [half, 2 * half) compute s, so the
+    // table costs one trigonometric evaluation per lane, not two.
+    for (int t = threadIdx.x; t < 2 * half; t += blockDim.x) {
+        const int f = t % half;
         const float inv = rope_inverse_frequency(2 * f, head_dim, theta, llama3, factor, low, high, original_max);
         const float phase = __fmul_rn((float)position, inv);
-        cs[f] = round_bf16((float)cos((double)phase));
-        sn[f] = round_bf16((float)sin((double)phase));
+        if (t < half) cs[f] = round_bf16((float)cos((double)phase));
+        else sn[f] = round_bf16((float)sin((double)phase));
     }
     __syncthreads();
     const int elements = heads * head_dim;
