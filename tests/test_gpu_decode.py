@@ -97,6 +97,32 @@ def test_decode_ragged_batch_dense(ctx):
         assert max_abs_bf16(got[b], ref) <= TOL, b
 
 
+def test_decode_ragged_partition_order(ctx):
+    # The kernel launches every sequence's full partitions first and the last
+    # partitions after them, longest first; partials are stored by logical
+    # partition index.  Sequences of one partition, of a 1-token last
+    # partition and of many partitions, in an order unrelated to their
+    # lengths: dense against the oracle, paged == dense bit for bit, for a
+    # fixed split and the automatic one.
+    rng = np.random.default_rng(11)
+    qh, kvh, d, stride = 32, 8, 128, 5000
+    lens = [1, 256, 257, 5000, 100, 3000, 511, 2048, 4097]
+    qb = normal_bf16(rng, (len(lens), qh, d))
+    kb = normal_bf16(rng, (len(lens), stride, kvh, d))
+    vb = normal_bf16(rng, (len(lens), stride, kvh, d))
+    q, k, v = to_torch(qb), to_torch(kb), to_torch(vb)
+    k_pool, v_pool, table_t, pps, _ = _paged_pool(ctx, k, v, lens, stride, 16, seed=5)
+    for split in (256, 0):
+        got = _decode(ctx, qb, kb, vb, lens, qh, kvh, d, split=split, stride=stride).reshape(len(lens), -1)
+        for b, t in enumerate(lens):
+            ref = _oracle_decode(qb[b], kb[b, :t], vb[b, :t], qh, kvh, d)
+            assert max_abs_bf16(got[b], ref) <= TOL, (split, b)
+        paged = torch.empty_like(q)
+        ctx.decode_paged(q, k_pool, v_pool, paged, lens, table_t, pps, 16, qh, kvh, d, split_tokens=split)
+        torch.cuda.synchronize()
+        assert np.array_equal(from_torch(paged).reshape(len(lens), -1), got), split
+
+
 def _paged_pool(ctx, k, v, lens, stride, page_tokens, seed):
     """Scatter dense [B][stride][KVH][D] K/V into a randomly permuted page pool
     with the product's page writer; returns (k_pool, v_pool, table, pages_per_seq)."""
