@@ -88,6 +88,23 @@ int mslim_attn_get_device_info(void *ctx, mslim_attn_device_info *out);
  * single queue (gpu_resources.rs:122-123); callers that share a stream with
  * other libraries need to name it. */
 int mslim_attn_ctx_set_stream(void *ctx, void *hip_stream);
+/* A context's decode workspace and split counters serve one stream at a
+ * time: mslim_attn_ctx_set_stream waits for the work queued on the old
+ * stream before it switches, and one context must not be driven from two
+ * host threads on two streams at once. */
+
+/* Context options.  No reference counterpart (the OpenCL engine has no merge
+ * choice); for tests and callers that want the two-launch merge.
+ *   MSLIM_ATTN_OPT_DECODE_MERGE: how split-KV decode partials are merged --
+ *     MSLIM_ATTN_DECODE_MERGE_FUSED (default): the last workgroup of each
+ *     (sequence, kv head) merges them inside the decode launch;
+ *     MSLIM_ATTN_DECODE_MERGE_SEPARATE: a merge launch follows the decode
+ *     launch.  Both merge in fixed partition order and give the same bits.
+ * Returns -1 for an unknown option or value. */
+#define MSLIM_ATTN_OPT_DECODE_MERGE 1
+#define MSLIM_ATTN_DECODE_MERGE_FUSED 0
+#define MSLIM_ATTN_DECODE_MERGE_SEPARATE 1
+int mslim_attn_ctx_set_option(void *ctx, int option, int64_t value);
 
 /* queue.finish() equivalent (gpu_llm/mod.rs:1998-2001). */
 int mslim_attn_synchronize(void *ctx);
@@ -131,7 +148,8 @@ int mslim_attn_decode_dense(void *ctx, const void *q, const void *k, const void 
 /* The split_tokens that split_tokens = 0 picks for this batch: about one
  * workgroup per CU for equal lengths, a smaller split for ragged lengths
  * when that evens out the busiest CU's load; a multiple of 256 in
- * [256, 16384].  A function of the lengths and kv_heads only, so the dense
+ * [256, 16384], or 128 for a batch too small to give each of the 256 CUs
+ * 256 tokens (tokens x kv_heads <= 32,768).  A function of the lengths and kv_heads only, so the dense
  * and paged entry points pick the same partitions.  Host only (no context,
  * no device work); -1 on invalid arguments.  No counterpart in the
  * reference, whose split count is a config field (attention_kernel.rs:

@@ -54,6 +54,8 @@ def _load() -> C.CDLL:
         "orc_rope_cpu": (None, [P, I, I, I, F]),
         "orc_swiglu": (None, [P, P, SZ, P]),
         "orc_matmul_bf16": (None, [P, P, I, I, I, P]),
+        "orc_matvec_cpu": (None, [P, P, I, I, P]),
+        "orc_argmax_total_last": (C.c_int32, [P, I]),
         "orc_add_bf16": (None, [P, P, SZ, P]),
         "orc_argmax_bf16": (None, [P, I, I, P]),
         "orc_softmax": (None, [P, I]),
@@ -262,6 +264,23 @@ def matmul_bf16(w_bits, in_bits, inner: int, rows: int, tokens: int) -> np.ndarr
     out = np.empty(tokens * rows, np.uint16)
     lib().orc_matmul_bf16(_p(w), _p(x), inner, rows, tokens, _p(out))
     return out
+
+
+def matvec_cpu(w_bits, x, rows: int, cols: int) -> np.ndarray:
+    """native_cpu_adapter.rs:129-150: f32 [rows], each a left-to-right f32 sum
+    of BF16 weight x f32 input products (no FMA), rounded to BF16."""
+    w = np.ascontiguousarray(w_bits, np.uint16)
+    x = np.ascontiguousarray(x, np.float32)
+    assert w.size == rows * cols and x.size == cols
+    out = np.empty(rows, np.float32)
+    lib().orc_matvec_cpu(_p(w), _p(x), rows, cols, _p(out))
+    return out
+
+
+def argmax_total_last(logits) -> int:
+    """native_cpu_adapter.rs:577-582: the last maximum under f32 total order."""
+    x = np.ascontiguousarray(logits, np.float32).reshape(-1)
+    return int(lib().orc_argmax_total_last(_p(x), x.size))
 
 
 # ---- Integrity -----------------------------------------------------------

@@ -1,7 +1,15 @@
-"""CPU decoder forward -- TEST INFRASTRUCTURE ONLY (see the package header).
+"""CPU decoder forwards -- TEST INFRASTRUCTURE ONLY (see the package header).
 
-The layer order of the reference GPU runtime, restated from its stage
-functions (each pinned in oracle.h):
+Two restatements of the reference decoder:
+
+* DecoderOracle: the GPU runtime's form (below), the arithmetic the HIP runner
+  reproduces stage for stage;
+* CpuDecoderOracle: the reference's own CPU decoder, NativeCpuDecoder::
+  forward_token (src/native_cpu_adapter.rs:486-590), one token at a time --
+  the path the north star judges against.
+
+DecoderOracle: the layer order of the reference GPU runtime, restated from its
+stage functions (each pinned in oracle.h):
   run_layer, src/gpu_llm/mod.rs:2056-2350 (one decode token) and
   run_batch_layer, src/gpu_llm/prefill.rs:897-1061 (a prompt chunk):
     x = embed(ids)                                    llm_embed  gpu_llm.cl:24-33
@@ -15,11 +23,21 @@ functions (each pinned in oracle.h):
       h = rmsnorm(x, post_norm)
       x = x + swiglu(h.Wg^T, h.Wu^T).Wd^T             llm_swiglu :225-237
     logits = rmsnorm(x_last, final_norm).Wlm^T; token = argmax  llm_argmax :239-270
-pin: the composition is checked in tests/test_oracle.py against closed forms
-that a wrong wiring breaks: with every projection zero the residual stream is
-the embedding and the logits are lm_head . rmsnorm(embedding); a one-token
-prompt attends only to itself, so its attention output is V of the mapped
-kv head exactly.
+pin (both decoders): tests/test_oracle.py checks the composition against
+closed forms that a wrong wiring breaks:
+  * every projection zero: the residual stream is the embedding and the logits
+    are lm_head . rmsnorm(embedding);
+  * a one-token prompt attends only to itself, so its attention output is V
+    of the mapped kv head exactly;
+  * MLP wiring: with input_norm zero the attention block adds exactly zero,
+    and with an all-ones embedding and post_norm the MLP of a one-entry gate
+    (2) and up (-1) projection gives x[0] = 1 + BF16(BF16(silu(2)) * -1) =
+    -0.7578125 exactly; a swapped gate/up gives 0.4609375, swapped norms give
+    1.0 or a nonzero attention term, a dropped residual gives -1.7578125;
+  * RoPE positions: with k = e_0 the cached key of the token at position p is
+    (BF16(cos p), ..., BF16(sin p), ...) for prompt and decode positions
+    alike, so a position offset fails;
+and the two decoders agree within the model tolerance of tests/_data.py.
 """
 from __future__ import annotations
 
@@ -28,8 +46,9 @@ from typing import Dict, List
 
 import numpy as np
 
-from . import (add_bf16, argmax_bf16, embed_rows, gpu_reference_attention, matmul_bf16,
-               rmsnorm_gpu, rope_gpu, swiglu)
+from . import (add_bf16, argmax_bf16, argmax_total_last, dense_attention_bf16, embed_rows,
+               gpu_reference_attention, matmul_bf16, matvec_cpu, read_bf16, rms_norm_cpu,
+               rmsnorm_gpu, rope_cpu, rope_gpu, round_bf16, swiglu, write_bf16)
 
 LAYER_TENSORS = ("input_norm", "q", "k", "v", "o", "post_norm", "gate", "up", "down")
 
@@ -131,6 +150,89 @@ class DecoderOracle:
         x = self.hidden_rows(seq, [token])
         lg = self.logits(x)
         return lg[0], int(argmax_bf16(lg, 1, self.s.vocab)[0])
+
+
+class CpuDecoderOracle:
+    """NativeCpuDecoder::forward_token (src/native_cpu_adapter.rs:486-590),
+    the reference's CPU decoder, one token per call:
+
+      state = embedding row (f32 of BF16)                     :498-503
+      per layer:
+        n = rms_norm(state, input_norm)                       :194-204
+        q, k, v = matvec(W, n), each output BF16              :129-150, :510-530
+        q, k = apply_rope(q|k, position)  (CPU angle form)    :206-221, :531-532
+        K/V += BF16(k), BF16(v)                               :458-484
+        a = dense_attention_bf16(q, K, V)  (hot dense route)  :253-307, :362-377
+        state = BF16(state + matvec(Wo, a))                   :187-192, :535-541
+        n = rms_norm(state, post_norm)
+        act = BF16(BF16(g / (1 + exp(-g))) * u)               :559-566
+        state = BF16(state + matvec(Wd, act))                 :567-573
+      logits = matvec(lm_head, rms_norm(state, final_norm))   :577-581
+      token = last maximum under f32 total order              :582-587
+
+    Weights: the same dict of BF16 bit arrays as DecoderOracle.  RoPE has no
+    llama3 scaling in this path (apply_rope takes theta only).  Logits are
+    f32 arrays holding BF16 values."""
+
+    def __init__(self, spec: Spec, weights: Dict[str, np.ndarray]):
+        self.s = spec
+        self.w = weights
+        self.sessions: Dict[int, Session] = {}
+        self.rope_shift = 0  # planted-mistake switch, as in DecoderOracle
+        self._norms = {}
+        self.last_hidden = None
+
+    def reset(self, seq: int) -> None:
+        kvd = self.s.kv_heads * self.s.head_dim
+        self.sessions[seq] = Session([np.zeros((0, kvd), np.uint16) for _ in range(self.s.layers)],
+                                     [np.zeros((0, kvd), np.uint16) for _ in range(self.s.layers)])
+
+    def _vector(self, name: str) -> np.ndarray:
+        if name not in self._norms:
+            self._norms[name] = read_bf16(self.w[name]).astype(np.float32)
+        return self._norms[name]
+
+    def forward_token(self, seq: int, token: int) -> tuple:
+        """(logits f32 [vocab], next token) after appending `token`."""
+        s, w = self.s, self.w
+        if seq not in self.sessions:
+            self.reset(seq)
+        sess = self.sessions[seq]
+        qd, kvd = s.q_heads * s.head_dim, s.kv_heads * s.head_dim
+        position = sess.tokens + self.rope_shift
+        state = read_bf16(np.asarray(w["embed"]).reshape(-1, s.hidden)[int(token)]).astype(np.float32)
+        for l in range(s.layers):
+            g = lambda name: w[f"layers.{l}.{name}"]  # noqa: E731
+            n = rms_norm_cpu(state, self._vector(f"layers.{l}.input_norm"), s.rms_eps)
+            q = matvec_cpu(g("q"), n, qd, s.hidden)
+            k = matvec_cpu(g("k"), n, kvd, s.hidden)
+            v = matvec_cpu(g("v"), n, kvd, s.hidden)
+            q = rope_cpu(q, s.q_heads, s.head_dim, position, s.rope_theta)
+            k = rope_cpu(k, s.kv_heads, s.head_dim, position, s.rope_theta)
+            sess.keys[l] = np.concatenate([sess.keys[l], write_bf16(k).reshape(1, kvd)])
+            sess.values[l] = np.concatenate([sess.values[l], write_bf16(v).reshape(1, kvd)])
+            a = dense_attention_bf16(q, sess.keys[l], sess.values[l], s.q_heads, s.kv_heads, s.head_dim)
+            state = round_bf16(state + matvec_cpu(g("o"), a, s.hidden, qd))
+            n = rms_norm_cpu(state, self._vector(f"layers.{l}.post_norm"), s.rms_eps)
+            gate = matvec_cpu(g("gate"), n, s.intermediate, s.hidden)
+            up = matvec_cpu(g("up"), n, s.intermediate, s.hidden)
+            act = read_bf16(swiglu(write_bf16(gate), write_bf16(up))).astype(np.float32)
+            state = round_bf16(state + matvec_cpu(g("down"), act, s.hidden, s.intermediate))
+        self.last_hidden = state  # the final residual row, for closed-form checks
+        final = rms_norm_cpu(state, self._vector("final_norm"), s.rms_eps)
+        logits = matvec_cpu(w["lm_head"], final, s.vocab, s.hidden)
+        return logits, argmax_total_last(logits)
+
+    def prefill(self, seq: int, prompt) -> tuple:
+        """(logits, greedy token) after the prompt, token by token; the slot restarts."""
+        self.reset(seq)
+        out = None
+        for t in prompt:
+            out = self.forward_token(seq, int(t))
+        return out
+
+    def step(self, seq: int, token: int) -> tuple:
+        return self.forward_token(seq, token)
 
 
 def random_weights(spec: Spec, rng: np.random.Generator, scale: float = 0.08) -> Dict[str, np.ndarray]:

@@ -389,7 +389,10 @@ void orc_argmax_bf16(const uint16_t *logits, int rows, int vocab, int32_t *out) 
  * one rounding at the end.  pin: identity weight reproduces the input bit for
  * bit, linearity in the weight, f64 brute force on small shapes. */
 void orc_matmul_bf16(const uint16_t *w, const uint16_t *in, int inner, int rows, int tokens, uint16_t *out) {
+    /* Outputs are independent: rows split over OpenMP threads, each sum in
+     * ascending i as before. */
     for (int t = 0; t < tokens; ++t)
+#pragma omp parallel for schedule(static)
         for (int r = 0; r < rows; ++r) {
             float acc = 0.0f;
             const uint16_t *wr = w + (size_t)r * inner;
@@ -397,6 +400,33 @@ void orc_matmul_bf16(const uint16_t *w, const uint16_t *in, int inner, int rows,
             for (int i = 0; i < inner; ++i) acc = fmaf(orc_read_bf16(wr[i]), orc_read_bf16(xt[i]), acc);
             out[(size_t)t * rows + r] = orc_write_bf16(acc);
         }
+}
+
+void orc_matvec_cpu(const uint16_t *w, const float *x, int rows, int cols, float *out) {
+#pragma omp parallel for schedule(static)
+    for (int r = 0; r < rows; ++r) {
+        const uint16_t *wr = w + (size_t)r * cols;
+        float sum = -0.0f;
+        for (int i = 0; i < cols; ++i) {
+            const float product = orc_read_bf16(wr[i]) * x[i];
+            sum += product;
+        }
+        out[r] = round_bf16(sum);
+    }
+}
+
+/* IEEE total order key of an f32 (Rust's f32::total_cmp). */
+static int32_t total_key(float x) {
+    int32_t bits;
+    memcpy(&bits, &x, 4);
+    return bits ^ (int32_t)(((uint32_t)(bits >> 31)) >> 1);
+}
+
+int32_t orc_argmax_total_last(const float *logits, int n) {
+    int32_t index = 0;
+    for (int i = 1; i < n; ++i)
+        if (total_key(logits[i]) >= total_key(logits[index])) index = i;
+    return n > 0 ? index : -1;
 }
 
 /* ---- Integrity primitives ----------------------------------------------- */

@@ -133,6 +133,25 @@ void orc_argmax_bf16(const uint16_t *logits, int rows, int vocab, int32_t *out);
  * fp32 accumulation (fma, ascending i), one rounding. */
 void orc_matmul_bf16(const uint16_t *w, const uint16_t *in, int inner, int rows, int tokens, uint16_t *out);
 
+/* native_cpu_adapter.rs:129-150 NativeWeightArchive::matvec of the reference
+ * CPU decoder: out[r] = BF16(sum_i w[r][i] * x[i]) with every product rounded
+ * to f32 and summed left to right from -0.0 (no FMA), x in f32.  Rows are
+ * independent (the reference runs them in parallel with rayon), so they are
+ * split over OpenMP threads; each row's sum order is unchanged.
+ * pin: the sequence order of the sum ([2^25, 1, -2^25, 1] -> 1, not 2 or 0),
+ * no FMA (a product that an FMA would keep unrounded), BF16 rounding of the
+ * sum, and f64 brute force within one rounding on random rows. */
+void orc_matvec_cpu(const uint16_t *w, const float *x, int rows, int cols, float *out);
+
+/* native_cpu_adapter.rs:577-582: the reference CPU decoder's greedy token,
+ * `max_by(|a, b| a.total_cmp(b))` over the f32 logits: the LAST index among
+ * equal maxima, under IEEE total order (-NaN < -inf < ... < -0 < +0 < ... <
+ * +inf < +NaN).  The GPU argmax (orc_argmax_bf16, gpu_llm.cl:239-270) takes
+ * the FIRST index on ties and never picks NaN.
+ * pin: ties resolve to the last index, -0 < +0, +NaN above +inf, -NaN below
+ * -inf; distinct values agree with numpy.argmax. */
+int32_t orc_argmax_total_last(const float *logits, int n);
+
 /* ---- Integrity primitives ----------------------------------------------- */
 /* cold_store.rs:909-922 FNV-1a-64 over concatenated parts.
  * pin: published vectors ("" -> cbf29ce484222325, "a" -> af63dc4c8601ec8c). */

@@ -101,6 +101,11 @@ def test_auto_split_choices():
     assert auto_split(cfg3, 8) == 2304 and _one_per_cu_split(cfg3, 8) == 4608
     skew = np.random.default_rng(17).integers(1024, 32769, size=8).tolist()
     assert auto_split(skew, 8) == 2304
+    # batches too small to give each CU 256 tokens take 128-token splits:
+    # cfg1 (B = 1, T = 1,024, 8 kv heads) and short decode contexts
+    assert auto_split([1024], 8) == 128
+    assert auto_split([300, 17, 3000], 8) == 128
+    assert auto_split([4096, 4096], 8) == 256
 
 
 def test_auto_split_invariants():
@@ -111,12 +116,16 @@ def test_auto_split_invariants():
         lens = rng.integers(1, 65537, size=int(rng.integers(1, 65))).tolist()
         kvh = int(rng.choice([1, 2, 4, 8, 16]))
         s, s1 = auto_split(lens, kvh), _one_per_cu_split(lens, kvh)
+        if sum(lens) * kvh <= 128 * 256:
+            assert s == 128
+            continue
         assert s % 256 == 0 and 256 <= s <= s1 and s >= s1 // 4 - 255
         if s != s1:
             assert sum(split_count(t, s) for t in lens) * kvh <= 2048
         if len(set(lens)) == 1:
             assert s == s1
         assert auto_split(list(reversed(lens)), kvh) % 256 == 0
+    assert auto_split([1] * 64, 1) == 128
 
 
 def test_auto_split_rejects_bad_batches():

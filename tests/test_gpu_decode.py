@@ -254,3 +254,149 @@ def test_decode_rejects_bad_arguments(ctx):
         ctx.decode_paged(q, k, k, out, [64], table, 4, 24, 8, 8, 128)
     with pytest.raises(mslim_attn.MslimAttnError, match="shorter"):
         ctx.decode_paged(q, k, k, out, [65], table, 4, 16, 8, 8, 128)
+
+
+def _merge_modes(ctx, fn):
+    """fn() under the fused last-workgroup merge and under the separate merge
+    launch; returns both outputs (host bits) and restores the default."""
+    outs = []
+    try:
+        for separate in (False, True):
+            ctx.set_decode_merge(separate)
+            outs.append(fn())
+    finally:
+        ctx.set_decode_merge(False)
+    return outs
+
+
+def test_decode_merge_modes_bitwise_ragged(ctx):
+    # The fused merge (last workgroup of each (sequence, kv head), partials
+    # published with release / acquire on the split counter) and the
+    # two-launch merge read the same partials in the same fixed order.
+    rng = np.random.default_rng(31)
+    qh, kvh, d, stride = 32, 8, 128, 6000
+    lens = [1, 300, 6000, 257, 4096, 1023, 2, 5555]
+    qb = normal_bf16(rng, (len(lens), qh, d))
+    kb = normal_bf16(rng, (len(lens), stride, kvh, d))
+    vb = normal_bf16(rng, (len(lens), stride, kvh, d))
+    q, k, v = to_torch(qb), to_torch(kb), to_torch(vb)
+    k_pool, v_pool, table_t, pps, _ = _paged_pool(ctx, k, v, lens, stride, 16, seed=8)
+    for split in (64, 256, 0):
+        def dense():
+            out = torch.empty_like(q)
+            ctx.decode_dense(q, k, v, out, lens, qh, kvh, d, seq_stride_tokens=stride, split_tokens=split)
+            torch.cuda.synchronize()
+            return from_torch(out)
+
+        def paged():
+            out = torch.empty_like(q)
+            ctx.decode_paged(q, k_pool, v_pool, out, lens, table_t, pps, 16, qh, kvh, d, split_tokens=split)
+            torch.cuda.synchronize()
+            return from_torch(out)
+
+        fused_d, separate_d = _merge_modes(ctx, dense)
+        fused_p, separate_p = _merge_modes(ctx, paged)
+        assert np.array_equal(fused_d, separate_d), split
+        assert np.array_equal(fused_p, separate_p), split
+        assert np.array_equal(fused_d, fused_p), split
+        got = fused_d.reshape(len(lens), -1)
+        for b in (0, 2, 7):
+            t = lens[b]
+            assert max_abs_bf16(got[b], _oracle_decode(qb[b], kb[b, :t], vb[b, :t], qh, kvh, d)) <= TOL, (split, b)
+
+
+def _cfg4_hot_cold_pool(k, v, lens, hot_window, page_tokens, seed, ctx):
+    """cfg4's layout: per sequence the cold pages are a seeded random
+    permutation of pool slots and the most recent `hot_window` tokens one
+    contiguous run of slots after them."""
+    batch, t_max, kvh, d = k.shape
+    pages = t_max // page_tokens
+    hot = hot_window // page_tokens
+    cold = pages - hot
+    rng = np.random.default_rng(seed)
+    cold_slots = rng.permutation(batch * cold).astype(np.int32)
+    table = np.zeros((batch, pages), np.int32)
+    for b in range(batch):
+        table[b, :cold] = cold_slots[b * cold:(b + 1) * cold]
+        table[b, cold:] = batch * cold + b * hot + np.arange(hot, dtype=np.int32)
+    table_t = torch.from_numpy(table).cuda()
+    k_pool = torch.empty((batch * pages, kvh, page_tokens, d), dtype=torch.int16, device="cuda")
+    v_pool = torch.empty_like(k_pool)
+    for b in range(batch):
+        ctx.pages_write(k_pool, v_pool, table_t[b], page_tokens, kvh, d, 0, lens[b], k[b, :lens[b]].contiguous(),
+                        v[b, :lens[b]].contiguous())
+    torch.cuda.synchronize()
+    return k_pool, v_pool, table_t, pages
+
+
+def test_decode_cfg4_hot_window_cold_pages_against_oracle(ctx):
+    # BASELINE config 4 as configured: B=4, T=32,768, 64/8/128, a 4,096-token
+    # contiguous hot window plus cold 16-token pages in a seeded random
+    # permutation.  paged == dense bit for bit under both merge modes; two
+    # sequences in full against the CPU oracle.
+    qh, kvh, d, t, batch = 64, 8, 128, 32768, 4
+    gen = torch.Generator(device="cuda").manual_seed(44)
+    k = torch.randn((batch, t, kvh, d), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    v = torch.randn((batch, t, kvh, d), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    q = torch.randn((batch, qh, d), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    lens = [t] * batch
+    k_pool, v_pool, table_t, pps = _cfg4_hot_cold_pool(k, v, lens, 4096, 16, 20261201, ctx)
+
+    def paged():
+        out = torch.empty_like(q)
+        ctx.decode_paged(q, k_pool, v_pool, out, lens, table_t, pps, 16, qh, kvh, d)
+        torch.cuda.synchronize()
+        return from_torch(out)
+
+    dense = torch.empty_like(q)
+    ctx.decode_dense(q, k, v, dense, lens, qh, kvh, d, seq_stride_tokens=t)
+    torch.cuda.synchronize()
+    fused, separate = _merge_modes(ctx, paged)
+    assert np.array_equal(fused, from_torch(dense))
+    assert np.array_equal(fused, separate)
+    got = fused.reshape(batch, -1)
+    for b in (1, 2):
+        ref = _oracle_decode(from_torch(q[b]), from_torch(k[b]), from_torch(v[b]), qh, kvh, d)
+        assert max_abs_bf16(got[b], ref) <= TOL, b
+
+
+def test_decode_stream_switch_between_ragged_split_decodes(ctx):
+    # One context's split workspace and counters serve one stream at a time:
+    # a ragged split decode queued on stream A, then a switch to stream B and
+    # a second ragged split decode there.  The switch waits for A, so both
+    # outputs equal the same calls made on one stream.
+    rng = np.random.default_rng(41)
+    qh, kvh, d, stride = 32, 8, 128, 8192
+    lens_a = [8192, 700, 5000, 3]
+    lens_b = [2048, 8000, 1]
+    qa, qb = normal_bf16(rng, (len(lens_a), qh, d)), normal_bf16(rng, (len(lens_b), qh, d))
+    ka = to_torch(normal_bf16(rng, (len(lens_a), stride, kvh, d)))
+    va = to_torch(normal_bf16(rng, (len(lens_a), stride, kvh, d)))
+    kb = ka[:len(lens_b)].flip(0).contiguous()
+    vb = va[:len(lens_b)].flip(0).contiguous()
+    qa_t, qb_t = to_torch(qa), to_torch(qb)
+    want_a, want_b = torch.empty_like(qa_t), torch.empty_like(qb_t)
+    ctx.decode_dense(qa_t, ka, va, want_a, lens_a, qh, kvh, d, seq_stride_tokens=stride, split_tokens=256)
+    ctx.decode_dense(qb_t, kb, vb, want_b, lens_b, qh, kvh, d, seq_stride_tokens=stride, split_tokens=256)
+    torch.cuda.synchronize()
+    s_a, s_b = torch.cuda.Stream(), torch.cuda.Stream()
+    out_a, out_b = torch.empty_like(qa_t), torch.empty_like(qb_t)
+    try:
+        ctx.set_stream(s_a.cuda_stream)
+        ctx.decode_dense(qa_t, ka, va, out_a, lens_a, qh, kvh, d, seq_stride_tokens=stride, split_tokens=256)
+        ctx.set_stream(s_b.cuda_stream)
+        ctx.decode_dense(qb_t, kb, vb, out_b, lens_b, qh, kvh, d, seq_stride_tokens=stride, split_tokens=256)
+        ctx.synchronize()
+    finally:
+        ctx.use_torch_stream()
+    torch.cuda.synchronize()
+    assert torch.equal(out_a, want_a)
+    assert torch.equal(out_b, want_b)
+
+
+def test_decode_option_rejects_unknown_values(ctx):
+    import mslim_attn
+    with pytest.raises(mslim_attn.MslimAttnError, match="merge mode"):
+        ctx.set_option(mslim_attn.OPT_DECODE_MERGE, 2)
+    with pytest.raises(mslim_attn.MslimAttnError, match="unknown context option"):
+        ctx.set_option(99, 0)

@@ -42,6 +42,8 @@ struct Context {
     size_t workspace_bytes = 0;
     int *counters = nullptr;        // decode split counters, zero between launches
     size_t counter_bytes = 0;
+    bool counters_dirty = false;    // a decode launch failed: clear before the next
+    bool separate_merge = false;    // MSLIM_ATTN_OPT_DECODE_MERGE
     void *staging = nullptr;       // device, digest serialisation
     size_t staging_bytes = 0;
     void *host_staging = nullptr;  // pinned host, digest readback
@@ -113,7 +115,8 @@ struct Lock {
     std::lock_guard<std::mutex> guard;
 };
 
-int decode_common(Context &c, mslim::DecodeLaunch &l, const int32_t *seq_lens, int split_tokens) {
+// Argument checks and the split choice shared by every decode entry point.
+int decode_prepare(mslim::DecodeLaunch &l, const int32_t *seq_lens, int split_tokens) {
     if (l.batch < 1 || l.batch > MSLIM_ATTN_MAX_BATCH || !seq_lens)
         return fail("decode batch must be 1..64 with host seq_lens");
     if (!valid_geometry(l.q_heads, l.kv_heads, l.head_dim))
@@ -130,16 +133,24 @@ int decode_common(Context &c, mslim::DecodeLaunch &l, const int32_t *seq_lens, i
         return fail("split_tokens must be 0 or a positive multiple of 64");
     l.split_tokens = split_tokens ? split_tokens
                                   : mslim::decode_auto_split_tokens(seq_lens, l.batch, l.kv_heads);
+    return 0;
+}
+
+// Partials at `base`: the (m, l) pairs, then the accumulators.
+void decode_place_partials(mslim::DecodeLaunch &l, void *base) {
     int64_t splits = 0;
-    for (int i = 0; i < l.batch; ++i) splits += mslim::decode_splits(seq_lens[i], l.split_tokens);
-    const int group = l.q_heads / l.kv_heads;
-    const size_t ml_bytes = (size_t)splits * l.kv_heads * group * 2 * sizeof(float);
-    const size_t acc_bytes = (size_t)splits * l.kv_heads * group * l.head_dim * sizeof(float);
-    if (int rc = grow_device(c, &c.workspace, &c.workspace_bytes, ml_bytes + acc_bytes,
+    for (int i = 0; i < l.batch; ++i) splits += mslim::decode_splits(l.seq_len[i], l.split_tokens);
+    const size_t ml_bytes = (size_t)splits * l.kv_heads * (l.q_heads / l.kv_heads) * 2 * sizeof(float);
+    l.partial_ml = static_cast<float *>(base);
+    l.partial_acc = reinterpret_cast<float *>(static_cast<char *>(base) + ml_bytes);
+}
+
+int decode_common(Context &c, mslim::DecodeLaunch &l, const int32_t *seq_lens, int split_tokens) {
+    if (int rc = decode_prepare(l, seq_lens, split_tokens)) return rc;
+    if (int rc = grow_device(c, &c.workspace, &c.workspace_bytes, mslim::decode_partial_bytes(l),
                              "hipMalloc decode split workspace"))
         return rc;
-    l.partial_ml = static_cast<float *>(c.workspace);
-    l.partial_acc = reinterpret_cast<float *>(static_cast<char *>(c.workspace) + ml_bytes);
+    decode_place_partials(l, c.workspace);
     // One split counter per (sequence, kv head); the kernel leaves them at
     // zero, so they are cleared only when the buffer is (re)allocated.
     const size_t ctr_bytes = (size_t)MSLIM_ATTN_MAX_BATCH * l.kv_heads * sizeof(int);
@@ -148,11 +159,22 @@ int decode_common(Context &c, mslim::DecodeLaunch &l, const int32_t *seq_lens, i
         if (int rc = grow_device(c, &mem, &c.counter_bytes, ctr_bytes, "hipMalloc decode split counters"))
             return rc;
         c.counters = static_cast<int *>(mem);
-        if (int rc = check_hip(hipMemsetAsync(c.counters, 0, ctr_bytes, c.stream), "hipMemset split counters"))
+        c.counters_dirty = true;
+    }
+    // A fill kernel, not hipMemsetAsync: the call may be under graph capture.
+    if (c.counters_dirty) {
+        if (int rc = check_hip(mslim::launch_zero_i32(c.counters, (int)(c.counter_bytes / sizeof(int)), c.stream),
+                               "clear split counters"))
             return rc;
+        c.counters_dirty = false;
     }
     l.counters = c.counters;
-    return check_hip(mslim::launch_decode(l, c.stream), "decode attention launch");
+    l.separate_merge = c.separate_merge;
+    const int rc = check_hip(mslim::launch_decode(l, c.stream), "decode attention launch");
+    // A launch that failed may have left counts behind: clear them before
+    // the next fused merge relies on them.
+    if (rc) c.counters_dirty = true;
+    return rc;
 }
 
 
@@ -264,8 +286,28 @@ int mslim_attn_ctx_set_stream(void *ctx, void *hip_stream) {
     if (!ctx) return fail("null context");
     Context &c = *ctx_of(ctx);
     Lock lock(c);
+    // The context's workspace and split counters serve one stream at a time:
+    // work queued on the old stream finishes before any call on the new one.
+    if (int rc = check_hip(hipStreamSynchronize(c.stream), "hipStreamSynchronize before stream switch"))
+        return rc;
     c.stream = static_cast<hipStream_t>(hip_stream);
     return 0;
+}
+
+int mslim_attn_ctx_set_option(void *ctx, int option, int64_t value) {
+    g_error.clear();
+    if (!ctx) return fail("null context");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    switch (option) {
+    case MSLIM_ATTN_OPT_DECODE_MERGE:
+        if (value != MSLIM_ATTN_DECODE_MERGE_FUSED && value != MSLIM_ATTN_DECODE_MERGE_SEPARATE)
+            return fail("decode merge mode must be 0 (fused) or 1 (separate launch)");
+        c.separate_merge = value == MSLIM_ATTN_DECODE_MERGE_SEPARATE;
+        return 0;
+    default:
+        return fail("unknown context option");
+    }
 }
 
 int mslim_attn_synchronize(void *ctx) {
@@ -374,13 +416,12 @@ int mslim_attn_decode_dense(void *ctx, const void *q, const void *k, const void 
     return decode_common(c, l, seq_lens, split_tokens);
 }
 
-int mslim_attn_decode_paged(void *ctx, const void *q, const void *k_pool, const void *v_pool,
-                            void *out, int batch, const int32_t *seq_lens,
-                            const int32_t *page_table, int pages_per_seq, int page_tokens,
-                            int q_heads, int kv_heads, int head_dim, float scale,
-                            int split_tokens) {
-    g_error.clear();
-    if (!ctx) return fail("null context");
+}  // extern "C"
+
+namespace {
+int paged_launch_args(mslim::DecodeLaunch &l, const void *q, const void *k_pool, const void *v_pool, void *out,
+                      int batch, const int32_t *seq_lens, const int32_t *page_table, int pages_per_seq,
+                      int page_tokens, int q_heads, int kv_heads, int head_dim, float scale) {
     if (!page_table) return fail("paged decode needs a device page table");
     if (!is_pow2(page_tokens) || page_tokens < 16 || page_tokens > 4096)
         return fail("page_tokens must be a power of two in 16..4096");
@@ -389,9 +430,7 @@ int mslim_attn_decode_paged(void *ctx, const void *q, const void *k_pool, const 
             if ((int64_t)pages_per_seq * page_tokens < seq_lens[i])
                 return fail("paged decode: page table row shorter than the sequence");
     }
-    Context &c = *ctx_of(ctx);
-    Lock lock(c);
-    mslim::DecodeLaunch l{};
+    l = mslim::DecodeLaunch{};
     l.q = static_cast<const uint16_t *>(q);
     l.k = static_cast<const uint16_t *>(k_pool);
     l.v = static_cast<const uint16_t *>(v_pool);
@@ -402,6 +441,25 @@ int mslim_attn_decode_paged(void *ctx, const void *q, const void *k_pool, const 
     l.page_table = page_table;
     l.pages_per_seq = pages_per_seq;
     l.page_tokens = page_tokens;
+    return 0;
+}
+}  // namespace
+
+extern "C" {
+
+int mslim_attn_decode_paged(void *ctx, const void *q, const void *k_pool, const void *v_pool,
+                            void *out, int batch, const int32_t *seq_lens,
+                            const int32_t *page_table, int pages_per_seq, int page_tokens,
+                            int q_heads, int kv_heads, int head_dim, float scale,
+                            int split_tokens) {
+    g_error.clear();
+    if (!ctx) return fail("null context");
+    mslim::DecodeLaunch l;
+    if (int rc = paged_launch_args(l, q, k_pool, v_pool, out, batch, seq_lens, page_table, pages_per_seq,
+                                   page_tokens, q_heads, kv_heads, head_dim, scale))
+        return rc;
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
     return decode_common(c, l, seq_lens, split_tokens);
 }
 

@@ -24,7 +24,8 @@
 //     S^T accumulator as the A operand;
 //   * the four wavefronts merge in LDS; the partitions of one (sequence, kv
 //     head) are merged in fixed partition order by the workgroup that
-//     finishes last (or, built with MSLIM_DECODE_FUSED=0, by a second launch).
+//     finishes last (or, when the context asks for it, by a second launch;
+//     both orders give the same bits).
 // Partitions are fixed by logical token index, and the paged and dense
 // variants differ only in how a 16-token block's base address is formed, so
 // both produce bit-identical outputs (the reference's dense == ColdStore
@@ -35,7 +36,6 @@
 #include <algorithm>
 #include <utility>
 #include <vector>
-#include <queue>
 #include <cstdint>
 #include <type_traits>
 
@@ -43,15 +43,11 @@ namespace mslim {
 
 namespace {
 
-#ifndef MSLIM_DECODE_WAVES
-#define MSLIM_DECODE_WAVES 4
-#endif
-// 1: full partitions launch first, last partitions after them, longest first
-// (the order the automatic split models); 0: sequence order.
-#ifndef MSLIM_DECODE_LPT
-#define MSLIM_DECODE_LPT 1
-#endif
-constexpr int kWaves = MSLIM_DECODE_WAVES;
+// Four wavefronts per workgroup and a ring of two tiles per wavefront: eight
+// wavefronts, a three-deep ring and 2,048-token splits were each measured
+// slower at cfg4 (rotating layer caches).
+constexpr int kWaves = 4;
+constexpr int kDepth = 2;
 constexpr int kTile = 32;
 
 struct DeviceArgs {
@@ -95,14 +91,6 @@ __device__ __forceinline__ int row_stride(const DeviceArgs &a) {
     if constexpr (PAGED) return D;
     else return a.kv_heads * D;
 }
-
-#if !MSLIM_DECODE_LPT
-__device__ __forceinline__ int sequence_of(const DeviceArgs &a, int sg) {
-    int b = 0;
-    while (b + 1 < a.batch && a.split_begin[b + 1] <= sg) ++b;
-    return b;
-}
-#endif
 
 // Ordering point for LDS traffic inside one wavefront: a wavefront's LDS
 // operations execute in order, so only the compiler must not move them.
@@ -169,8 +157,9 @@ template <int D, int G>
 __device__ __forceinline__ void merge_splits(const DeviceArgs &a, int b, int kvh, int tid, int nthreads,
                                              bool coherent);
 
-template <int D, int G, bool PAGED, int DEPTH, bool FUSED, bool NT>
+template <int D, int G, bool PAGED, bool FUSED, bool NT>
 __global__ __launch_bounds__(64 * kWaves, 2) void decode_kernel(DeviceArgs a) {
+    constexpr int DEPTH = kDepth;
     constexpr int KS = D / 32;        // Q.K MFMA k-steps per 16-token block
     constexpr int LPR = D / 8;        // lanes per V row (8 BF16 per lane)
     constexpr int RPI = 64 / LPR;     // V rows per load instruction
@@ -190,7 +179,6 @@ __global__ __launch_bounds__(64 * kWaves, 2) void decode_kernel(DeviceArgs a) {
     const int grp = lane >> 4;
     const int kvh = blockIdx.x % a.kv_heads;
     const int sg = blockIdx.x / a.kv_heads;
-#if MSLIM_DECODE_LPT
     // Full partitions launch first and the shorter last partitions after
     // them, longest first: when a launch has more workgroups than fit at
     // once, the dispatcher hands the short ones to the CUs that free up.
@@ -204,10 +192,6 @@ __global__ __launch_bounds__(64 * kWaves, 2) void decode_kernel(DeviceArgs a) {
         b = a.last_order[sg - full_total];
         split = a.split_begin[b + 1] - a.split_begin[b] - 1;
     }
-#else
-    const int b = sequence_of(a, sg);
-    const int split = sg - a.split_begin[b];
-#endif
     const int nsplit = a.split_begin[b + 1] - a.split_begin[b];
     const int seq_len = a.seq_len[b];
     const int begin = split * a.split_tokens;
@@ -317,15 +301,17 @@ __global__ __launch_bounds__(64 * kWaves, 2) void decode_kernel(DeviceArgs a) {
         // P as the A operand of O = P.V: row = head row16, k-slot j of lane
         // group grp = token (j < 4 ? 4*grp + j : 16 + 4*grp + j - 4), which is
         // exactly where the S^T accumulator left it.
+        // The row sum adds the same BF16-rounded p that the P.V MFMA
+        // multiplies, so O / l is a convex combination of V rows.
         bf16x8_t pa;
         float psum = 0.0f;
 #pragma unroll
         for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float p = __builtin_amdgcn_exp2f(fmaf(s[blk][i], c, -mc));
-                psum += p;
-                pa[blk * 4 + i] = (__bf16)p;
+                const __bf16 p = (__bf16)__builtin_amdgcn_exp2f(fmaf(s[blk][i], c, -mc));
+                psum += (float)p;
+                pa[blk * 4 + i] = p;
             }
         l_run = l_run * alpha + psum;
         m_run = m_new;
@@ -417,9 +403,8 @@ __global__ __launch_bounds__(64 * kWaves, 2) void decode_kernel(DeviceArgs a) {
             packed.y = pack_bf16x2(ov.z / l, ov.w / l);
             *reinterpret_cast<uint2 *>(a.out + ((int64_t)b * a.q_heads + qh0 + g) * D + d) = packed;
         } else if constexpr (FUSED) {
-            // Agent-scope atomic stores are written through to the
-            // device-coherent level, so no cache writeback is needed before
-            // the counter below publishes them.
+            // Agent-scope atomic stores: the merging workgroup may run on
+            // another XCD.
             float *pa = a.partial_acc + (part + g) * D + d;
             store_coherent2(pa, ov.x, ov.y);
             store_coherent2(pa + 2, ov.z, ov.w);
@@ -431,9 +416,23 @@ __global__ __launch_bounds__(64 * kWaves, 2) void decode_kernel(DeviceArgs a) {
     }
     if constexpr (FUSED) {
         if (final_write) return;
-        // Every store of this workgroup has completed before thread 0 counts
-        // the split; the workgroup that finishes a (sequence, kv head) last
-        // merges its partitions in fixed order, as decode_merge_kernel does.
+        // Publication of the partials, ordered at the ISA level: the
+        // partials were written with agent-scope atomic stores, which gfx950
+        // issues write-through to the device coherence point (sc1), and every
+        // thread waits for its own stores to complete (s_waitcnt vmcnt(0))
+        // before the barrier, so they are visible to every XCD before thread
+        // 0 counts the split.  The merging workgroup reads them with
+        // agent-scope atomic loads, which bypass the XCD-local L2 (sc1).  The
+        // language-level release / acquire on the counter gives the same
+        // order but adds an L2 write-back and invalidate per workgroup:
+        // measured on cfg4 / cfg3 / the cfg5 decoder shape, 98.8 / 149 / 40
+        // us with release / acquire on thread 0's RMW, 119 / 254 / 60 us with
+        // a release fence in every thread, against 90.0 / 124 / 34 us here.
+        // The separate merge launch (MSLIM_ATTN_OPT_DECODE_MERGE), ordered by
+        // the kernel boundary, measured 92.4 / 122 / 36 us and gives the same
+        // bits.  The workgroup that takes the count to nsplit - 1 merges the
+        // partitions in fixed order, as decode_merge_kernel does, and resets
+        // the counter for the next call.
         __builtin_amdgcn_s_waitcnt(0);
         __shared__ int last;
         __syncthreads();
@@ -589,40 +588,60 @@ __global__ __launch_bounds__(64) void decode_generic_kernel(DeviceArgs a, int D)
     }
 }
 
-#ifndef MSLIM_DECODE_DEPTH
-#define MSLIM_DECODE_DEPTH 2
-#endif
-#ifndef MSLIM_DECODE_FUSED
-#define MSLIM_DECODE_FUSED 1
-#endif
-
-template <int D, int G>
-hipError_t launch_fast(const DeviceArgs &a, bool paged, bool nt, int total_splits, bool merge,
-                       hipStream_t stream) {
-    const dim3 grid((unsigned)(total_splits * a.kv_heads));
-    constexpr bool F = MSLIM_DECODE_FUSED != 0;
-    constexpr int DP = MSLIM_DECODE_DEPTH;
+template <int D, int G, bool FUSED>
+void launch_variant(const DeviceArgs &a, bool paged, bool nt, dim3 grid, hipStream_t stream) {
     const dim3 block(64 * kWaves);
     if (paged && nt)
-        hipLaunchKernelGGL((decode_kernel<D, G, true, DP, F, true>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((decode_kernel<D, G, true, FUSED, true>), grid, block, 0, stream, a);
     else if (paged)
-        hipLaunchKernelGGL((decode_kernel<D, G, true, DP, F, false>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((decode_kernel<D, G, true, FUSED, false>), grid, block, 0, stream, a);
     else if (nt)
-        hipLaunchKernelGGL((decode_kernel<D, G, false, DP, F, true>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((decode_kernel<D, G, false, FUSED, true>), grid, block, 0, stream, a);
     else
-        hipLaunchKernelGGL((decode_kernel<D, G, false, DP, F, false>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((decode_kernel<D, G, false, FUSED, false>), grid, block, 0, stream, a);
+}
+
+// fused: the last split workgroup of each (sequence, kv head) merges; else a
+// decode_merge_kernel launch follows when any sequence has several splits.
+template <int D, int G>
+hipError_t launch_fast(const DeviceArgs &a, bool paged, bool nt, int total_splits, bool merge, bool fused,
+                       hipStream_t stream) {
+    const dim3 grid((unsigned)(total_splits * a.kv_heads));
+    if (fused)
+        launch_variant<D, G, true>(a, paged, nt, grid, stream);
+    else
+        launch_variant<D, G, false>(a, paged, nt, grid, stream);
     hipError_t err = hipGetLastError();
-    if (err != hipSuccess || !merge || F) return err;
+    if (err != hipSuccess || !merge || fused) return err;
     hipLaunchKernelGGL((decode_merge_kernel<D, G>), dim3((unsigned)(a.batch * a.kv_heads)), dim3(256), 0,
                        stream, a);
     return hipGetLastError();
 }
 
+__global__ __launch_bounds__(256) void zero_i32_kernel(int *p, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) p[i] = 0;
+}
+
 }  // namespace
 
+hipError_t launch_zero_i32(int *p, int n, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(zero_i32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, p, n);
+    return hipGetLastError();
+}
+
+size_t decode_partial_bytes(const DecodeLaunch &l) {
+    int64_t splits = 0;
+    for (int i = 0; i < l.batch; ++i) splits += decode_splits(l.seq_len[i], l.split_tokens);
+    const int group = l.q_heads / l.kv_heads;
+    return (size_t)splits * l.kv_heads * group * (l.head_dim + 2) * sizeof(float);
+}
+
 int decode_auto_split_tokens(const int32_t *seq_lens, int batch, int kv_heads) {
-    // S1 = tokens * kv_heads / 256, a multiple of 256 in [256, 16384]: about
-    // one workgroup per CU (256 on MI355X).  For equal lengths that is the
+    // S1 = tokens * kv_heads / 256, a multiple of 256 in [256, 16384] (128
+    // for batches too small to fill the CUs): about one workgroup per CU (256
+    // on MI355X).  For equal lengths that is the
     // measured best (4,096 tokens for 4 x 32k x 8 kv heads, 1,280 for
     // 8 x 4,224), and it is returned as is.
     //
@@ -647,6 +666,11 @@ int decode_auto_split_tokens(const int32_t *seq_lens, int batch, int kv_heads) {
         uniform &= seq_lens[i] == seq_lens[0];
     }
     int64_t per = (total * kv_heads + kCus - 1) / kCus;
+    // A batch too small to give every CU 256 tokens (under 64k tokens x kv
+    // heads) takes 128-token splits: one tile per wavefront, 0.9 us faster
+    // than 256 at cfg1 (B = 1, T = 1,024, 8 kv heads), while 64-token splits
+    // leave half of each workgroup idle and measured slower.
+    if (per <= 128) return 128;
     per = (per + 255) / 256 * 256;
     const int s1 = (int)std::min<int64_t>(16384, std::max<int64_t>(256, per));
     if (uniform) return s1;
@@ -662,20 +686,25 @@ int decode_auto_split_tokens(const int32_t *seq_lens, int batch, int kv_heads) {
         for (int b = 0; b < batch; ++b) last_len[b] = seq_lens[b] - (decode_splits(seq_lens[b], s) - 1) * s;
         std::sort(last_len, last_len + batch, [](int x, int y) { return x > y; });
         std::fill(load, load + kCus, (int64_t)0);
-        std::priority_queue<std::pair<int64_t, int>, std::vector<std::pair<int64_t, int>>,
-                            std::greater<std::pair<int64_t, int>>> free_first;
+        // Min-heap of (load, CU) in a fixed array: the choice allocates
+        // nothing, so the allocation-free entry point can make it too.
+        std::pair<int64_t, int> free_first[kCus];
+        const auto later = std::greater<std::pair<int64_t, int>>();
         int64_t wg = 0;
         auto place = [&](int64_t tokens) {
             const int64_t work = tokens + kWorkgroupCost;
             if (wg < 2 * kCus) {
                 load[wg % kCus] += work;
-                if (wg == 2 * kCus - 1)
-                    for (int c = 0; c < kCus; ++c) free_first.push({load[c], c});
+                if (wg == 2 * kCus - 1) {
+                    for (int c = 0; c < kCus; ++c) free_first[c] = {load[c], c};
+                    std::make_heap(free_first, free_first + kCus, later);
+                }
             } else {
-                auto [l, c] = free_first.top();
-                free_first.pop();
-                load[c] = l + work;
-                free_first.push({load[c], c});
+                std::pop_heap(free_first, free_first + kCus, later);
+                auto &top = free_first[kCus - 1];
+                load[top.second] = top.first + work;
+                top.first = load[top.second];
+                std::push_heap(free_first, free_first + kCus, later);
             }
             ++wg;
         };
@@ -748,7 +777,8 @@ hipError_t launch_decode(const DecodeLaunch &l, hipStream_t stream) {
         return hipGetLastError();
     }
 #define MSLIM_DECODE_CASE(DD, GG) \
-    if (l.head_dim == DD && group == GG) return launch_fast<DD, GG>(a, l.paged, nt, total, merge, stream);
+    if (l.head_dim == DD && group == GG) \
+        return launch_fast<DD, GG>(a, l.paged, nt, total, merge, !l.separate_merge, stream);
     MSLIM_DECODE_CASE(128, 16)
     MSLIM_DECODE_CASE(128, 8)
     MSLIM_DECODE_CASE(128, 4)

@@ -30,6 +30,10 @@ struct DecodeLaunch {
     int seq_len[kMaxBatch];
     int split_begin[kMaxBatch + 1];
     bool paged;
+    // false: the last split workgroup of each (sequence, kv head) merges the
+    // partials (counters needed); true: a merge launch follows the decode
+    // launch (counters unused).  Both give the same bits.
+    bool separate_merge;
 };
 
 // Number of split partitions of a sequence of `tokens` tokens.
@@ -38,11 +42,15 @@ inline int decode_splits(int tokens, int split_tokens) {
 }
 // Library choice of split_tokens for a batch: about one workgroup per CU for
 // equal lengths, smaller for ragged lengths when that evens out the busiest
-// CU's load; a multiple of 256 in 256..16384.
+// CU's load; a multiple of 256 in 256..16384, or 128 for tiny batches.
 int decode_auto_split_tokens(const int32_t *seq_lens, int batch, int kv_heads);
 // True when the MFMA fast path covers this geometry.
 bool decode_fast_path(int head_dim, int group);
 hipError_t launch_decode(const DecodeLaunch &a, hipStream_t stream);
+// Split-partial bytes a decode launch of this shape needs.
+size_t decode_partial_bytes(const DecodeLaunch &l);
+// n int32 zeros at p (a fill kernel: safe under graph capture).
+hipError_t launch_zero_i32(int *p, int n, hipStream_t stream);
 
 struct PrefillLaunch {
     const uint16_t *q, *k, *v;

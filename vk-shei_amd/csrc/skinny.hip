@@ -28,34 +28,12 @@ namespace mslim {
 
 namespace {
 
-// Tuning knobs, fixed at build time: MFMA steps per load batch, wavefronts
-// per workgroup (0: 16 below 1024 row tiles, 8 above), and whether weight
-// loads are non-temporal (streamed once, kept out of the way of the token
-// vectors in L2).
-#ifndef MSLIM_SKINNY_UNROLL
-#define MSLIM_SKINNY_UNROLL 4
-#endif
-#ifndef MSLIM_SKINNY_WAVES
-#define MSLIM_SKINNY_WAVES 0
-#endif
-#ifndef MSLIM_SKINNY_NONTEMPORAL
-#define MSLIM_SKINNY_NONTEMPORAL 0
-#endif
-// Token vectors staged in LDS when they fit (1) or read per k-step (0).
-#ifndef MSLIM_SKINNY_XLDS
-#define MSLIM_SKINNY_XLDS 1
-#endif
-// Two-deep register ring of load batches (1) or load-then-use (0).
-#ifndef MSLIM_SKINNY_RING
-#define MSLIM_SKINNY_RING 0
-#endif
-// Workgroups in a launch (0: one per row tile).
-#ifndef MSLIM_SKINNY_GRID
-#define MSLIM_SKINNY_GRID 0
-#endif
-
 constexpr int kTileRows = 16;
-constexpr int kUnroll = MSLIM_SKINNY_UNROLL;
+// MFMA steps per load batch: kUnroll 16-byte weight loads in flight per lane
+// before the first MFMA of the batch.  Unroll 8, a two-deep register ring of
+// batches, a persistent grid and non-temporal weight loads each measured no
+// faster (non-temporal loads cost 10-30%).
+constexpr int kUnroll = 4;
 constexpr int kMaxSegments = 3;
 
 enum Epilogue { kPlain = 0, kAdd = 1, kSwiglu = 2 };
@@ -75,13 +53,6 @@ struct SkinnyArgs {
 
 __device__ __forceinline__ bf16x8_t load8(const uint16_t *p) { return *reinterpret_cast<const bf16x8_t *>(p); }
 
-__device__ __forceinline__ bf16x8_t load_weights(const uint16_t *p) {
-#if MSLIM_SKINNY_NONTEMPORAL
-    return __builtin_nontemporal_load(reinterpret_cast<const bf16x8_t *>(p));
-#else
-    return load8(p);
-#endif
-}
 
 // Token vectors staged in LDS (XLDS): up to kStageTokens rows of up to
 // kStageInner inputs, each row padded by 16 bytes so that the 16 token rows
@@ -100,10 +71,7 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(SkinnyArgs a) {
     auto partial = reinterpret_cast<floatx4_t(*)[WAVES][64]>(lds);
     uint16_t *xs = reinterpret_cast<uint16_t *>(lds);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    // Workgroups loop over row tiles (tile, tile + grid, ...), so a launch
-    // with fewer workgroups than tiles keeps each one streaming longer.
-    for (int tile = blockIdx.x; tile < a.tiles; tile += gridDim.x) {
-    if (tile != (int)blockIdx.x) __syncthreads();  // the LDS of the last tile has been read
+    const int tile = blockIdx.x;  // one workgroup per 16-row tile
     if (XLDS) {
         // The B operand (token rows) is the same for every row tile: read it
         // once per workgroup with 16-byte loads instead of once per k-step
@@ -155,8 +123,8 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(SkinnyArgs a) {
         for (int u = 0; u < kUnroll; ++u) {
             const int k = k0 + u * 32;
             const bool in = k < a.inner;
-            bt.wa[u] = in ? load_weights(wp + k) : zero;
-            if (EPI == kSwiglu) bt.wu[u] = in ? load_weights(up + k) : zero;
+            bt.wa[u] = in ? load8(wp + k) : zero;
+            if (EPI == kSwiglu) bt.wu[u] = in ? load8(up + k) : zero;
             if (XLDS) bt.xb[u] = in && live ? *reinterpret_cast<const bf16x8_t *>(xl + k) : zero;
             else bt.xb[u] = in && live ? load8(xp + k) : zero;
         }
@@ -169,38 +137,23 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(SkinnyArgs a) {
         }
     };
     const int step = WAVES * 32 * kUnroll;
-#if MSLIM_SKINNY_RING
-    // Two batches in registers: the next one's loads are in flight while the
-    // current one feeds the MFMAs.
-    Batch ring[2];
-    int k0 = wave * 32 * kUnroll;
-    if (k0 < a.inner) load_batch(ring[0], k0);
-    for (; k0 < a.inner; k0 += 2 * step) {
-        if (k0 + step < a.inner) load_batch(ring[1], k0 + step);
-        use_batch(ring[0]);
-        if (k0 + step >= a.inner) break;
-        if (k0 + 2 * step < a.inner) load_batch(ring[0], k0 + 2 * step);
-        use_batch(ring[1]);
-    }
-#else
     for (int k0 = wave * 32 * kUnroll; k0 < a.inner; k0 += step) {
         Batch bt;
         load_batch(bt, k0);
         use_batch(bt);
     }
-#endif
     if (XLDS) __syncthreads();  // every wavefront is done with the staged rows
     partial[0][wave][lane] = acc;
     if (EPI == kSwiglu) partial[EPI == kSwiglu ? 1 : 0][wave][lane] = acc_up;
     __syncthreads();
-    if (wave != 0) continue;
+    if (wave != 0) return;
     floatx4_t sum = partial[0][0][lane], sum_up = partial[EPI == kSwiglu ? 1 : 0][0][lane];
     for (int w = 1; w < WAVES; ++w) {
         sum += partial[0][w][lane];
         if (EPI == kSwiglu) sum_up += partial[EPI == kSwiglu ? 1 : 0][w][lane];
     }
     // D layout: lane l holds rows 4*(l/16) + j, token l%16.
-    if (!live) continue;
+    if (!live) return;
     uint16_t *out = a.out[seg] + (int64_t)tok * rows;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -214,7 +167,6 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(SkinnyArgs a) {
         } else {
             out[r] = swiglu_bf16(y, write_bf16(sum_up[j]));
         }
-    }
     }
 }
 
@@ -233,21 +185,18 @@ hipError_t launch_with(SkinnyArgs &a, hipStream_t stream) {
     // Measured per shape at 8 tokens (weights cycled through more memory
     // than the Infinity Cache holds): 8 wavefronts for the gate/up pair,
     // for inputs too wide to stage and for many row tiles; 16 for the rest.
-    const int waves = MSLIM_SKINNY_WAVES ? MSLIM_SKINNY_WAVES
-                      : (EPI == kSwiglu || a.inner > kStageInner || tiles >= 1024) ? 8 : 16;
-    const unsigned grid = (unsigned)(MSLIM_SKINNY_GRID ? std::min(tiles, MSLIM_SKINNY_GRID) : tiles);
+    const int waves = (EPI == kSwiglu || a.inner > kStageInner || tiles >= 1024) ? 8 : 16;
+    const unsigned grid = (unsigned)tiles;
     if (waves == 16)
         hipLaunchKernelGGL((skinny_kernel<16, EPI, XLDS>), dim3(grid), dim3(16 * 64), 0, stream, a);
-    else if (waves == 8)
-        hipLaunchKernelGGL((skinny_kernel<8, EPI, XLDS>), dim3(grid), dim3(8 * 64), 0, stream, a);
     else
-        hipLaunchKernelGGL((skinny_kernel<4, EPI, XLDS>), dim3(grid), dim3(4 * 64), 0, stream, a);
+        hipLaunchKernelGGL((skinny_kernel<8, EPI, XLDS>), dim3(grid), dim3(8 * 64), 0, stream, a);
     return hipGetLastError();
 }
 
 template <int EPI>
 hipError_t launch(SkinnyArgs &a, hipStream_t stream) {
-    if (MSLIM_SKINNY_XLDS && a.tokens <= kStageTokens && a.inner <= kStageInner) return launch_with<EPI, true>(a, stream);
+    if (a.tokens <= kStageTokens && a.inner <= kStageInner) return launch_with<EPI, true>(a, stream);
     return launch_with<EPI, false>(a, stream);
 }
 

@@ -21,6 +21,8 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmslim_attn.so")
 
 MAX_BATCH = 64
+OPT_DECODE_MERGE = 1                        # mslim_attn_ctx_set_option options
+DECODE_MERGE_FUSED, DECODE_MERGE_SEPARATE = 0, 1
 FORMAT_BF16, FORMAT_F16, FORMAT_F32 = 1, 2, 3  # gpu_backend.rs:258-262
 ERR_NONFINITE = -2
 
@@ -48,6 +50,7 @@ EXPORTS = (
     "mslim_attn_ctx_destroy",
     "mslim_attn_get_device_info",
     "mslim_attn_ctx_set_stream",
+    "mslim_attn_ctx_set_option",
     "mslim_attn_synchronize",
     "mslim_attn_buf_alloc",
     "mslim_attn_buf_upload",
@@ -124,6 +127,7 @@ def library() -> C.CDLL:
         "mslim_attn_ctx_destroy": (None, [P]),
         "mslim_attn_get_device_info": (I, [P, C.POINTER(DeviceInfo)]),
         "mslim_attn_ctx_set_stream": (I, [P, P]),
+        "mslim_attn_ctx_set_option": (I, [P, I, I64]),
         "mslim_attn_synchronize": (I, [P]),
         "mslim_attn_buf_alloc": (P, [P, SZ]),
         "mslim_attn_buf_upload": (P, [P, P, SZ]),
@@ -228,6 +232,14 @@ class Context:
     def set_stream(self, stream: Optional[int]) -> None:
         """Run on HIP stream `stream` (0 or None is the null stream)."""
         self._check("set_stream", self._lib.mslim_attn_ctx_set_stream(self._h, stream or None))
+
+    def set_option(self, option: int, value: int) -> None:
+        self._check("set_option", self._lib.mslim_attn_ctx_set_option(self._h, option, value))
+
+    def set_decode_merge(self, separate: bool) -> None:
+        """Merge decode split partials in a second launch (True) or in the
+        last workgroup of each (sequence, kv head) (False, the default)."""
+        self.set_option(OPT_DECODE_MERGE, DECODE_MERGE_SEPARATE if separate else DECODE_MERGE_FUSED)
 
     def use_torch_stream(self) -> None:
         import torch
