@@ -169,6 +169,25 @@ int mslim_attn_decode_paged(void *ctx, const void *q, const void *k_pool,
                             int pages_per_seq, int page_tokens, int q_heads,
                             int kv_heads, int head_dim, float scale, int split_tokens);
 
+/* mslim_attn_decode_paged without any allocation.  No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * split partials live in a fixed 16 MiB device array of the library (one per
+ * GPU, held until the process ends) instead of the context workspace, and the
+ * partitions are merged by a second launch, so no counter has to start at
+ * zero.  Same arguments and the same output bits as mslim_attn_decode_paged
+ * with the same split_tokens.  A call whose partials exceed 16 MiB
+ * (splits x kv_heads x group x (head_dim + 2) x 4 bytes) fails with -1 and
+ * names the size.  Every call on one GPU shares the array, whichever context
+ * makes it: calls that overlap on one GPU (two streams or two host threads)
+ * race and give wrong results. */
+int mslim_attn_decode_paged_noalloc(void *ctx, const void *q, const void *k_pool,
+                                    const void *v_pool, void *out, int batch,
+                                    const int32_t *seq_lens, const int32_t *page_table,
+                                    int pages_per_seq, int page_tokens, int q_heads,
+                                    int kv_heads, int head_dim, float scale,
+                                    int split_tokens);
+
 /* Causal GQA attention for a chunk of `queries` new tokens after `prior`
  * cached tokens: row i attends keys 0..prior+i.  K/V hold prior+queries
  * tokens, token-major.  Replaces BatchKernels::attention (prefill.rs:363-435:

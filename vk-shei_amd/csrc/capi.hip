@@ -463,6 +463,35 @@ int mslim_attn_decode_paged(void *ctx, const void *q, const void *k_pool, const 
     return decode_common(c, l, seq_lens, split_tokens);
 }
 
+int mslim_attn_decode_paged_noalloc(void *ctx, const void *q, const void *k_pool, const void *v_pool,
+                                    void *out, int batch, const int32_t *seq_lens,
+                                    const int32_t *page_table, int pages_per_seq, int page_tokens,
+                                    int q_heads, int kv_heads, int head_dim, float scale,
+                                    int split_tokens) {
+    g_error.clear();
+    if (!ctx) return fail("null context");
+    mslim::DecodeLaunch l;
+    if (int rc = paged_launch_args(l, q, k_pool, v_pool, out, batch, seq_lens, page_table, pages_per_seq,
+                                   page_tokens, q_heads, kv_heads, head_dim, scale))
+        return rc;
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    if (int rc = decode_prepare(l, seq_lens, split_tokens)) return rc;
+    const size_t need = mslim::decode_partial_bytes(l);
+    if (need > mslim::kDecodeStaticBytes)
+        return fail("allocation-free decode: split partials need " + std::to_string(need) +
+                    " bytes, above the fixed " + std::to_string(mslim::kDecodeStaticBytes) +
+                    "-byte scratch; use a larger split_tokens or mslim_attn_decode_paged");
+    float *scratch = nullptr;
+    if (int rc = check_hip(mslim::decode_static_scratch(c.device, &scratch), "hipGetSymbolAddress decode scratch"))
+        return rc;
+    decode_place_partials(l, scratch);
+    // The merge runs as its own launch, so no counter has to start at zero.
+    l.counters = nullptr;
+    l.separate_merge = true;
+    return check_hip(mslim::launch_decode(l, c.stream), "decode attention launch");
+}
+
 int mslim_attn_prefill_causal(void *ctx, const void *q, const void *k, const void *v, void *out,
                               int queries, int prior, int q_heads, int kv_heads, int head_dim,
                               float scale) {

@@ -34,6 +34,7 @@
 #include "kernels.hpp"
 
 #include <algorithm>
+#include <mutex>
 #include <utility>
 #include <vector>
 #include <cstdint>
@@ -623,7 +624,29 @@ __global__ __launch_bounds__(256) void zero_i32_kernel(int *p, int n) {
     if (i < n) p[i] = 0;
 }
 
+// Split partials of the allocation-free decode entry point (16 MiB, the
+// reference's decode scratch bound, attention_kernel.rs:124-139).  Host code
+// never passes `scratch` itself to a kernel: its device address comes from
+// hipGetSymbolAddress, per device.
+static __device__ __align__(256) unsigned char scratch[kDecodeStaticBytes];
+
 }  // namespace
+
+hipError_t decode_static_scratch(int device, float **ptr) {
+    static std::mutex lock;
+    static void *address[kMaxDevices] = {};
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> guard(lock);
+    if (!address[device]) {
+        void *p = nullptr;
+        const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (err != hipSuccess) return err;
+        if (!p) return hipErrorInvalidSymbol;
+        address[device] = p;
+    }
+    *ptr = static_cast<float *>(address[device]);
+    return hipSuccess;
+}
 
 hipError_t launch_zero_i32(int *p, int n, hipStream_t stream) {
     if (n <= 0) return hipSuccess;

@@ -49,6 +49,13 @@ bool decode_fast_path(int head_dim, int group);
 hipError_t launch_decode(const DecodeLaunch &a, hipStream_t stream);
 // Split-partial bytes a decode launch of this shape needs.
 size_t decode_partial_bytes(const DecodeLaunch &l);
+// A file-scope device array of kDecodeStaticBytes that the allocation-free
+// decode entry point uses for its split partials.  decode_static_scratch
+// returns its address on the current device (hipGetSymbolAddress on the first
+// call per device, cached after).  Every call on one device shares it.
+constexpr size_t kDecodeStaticBytes = (size_t)16 << 20;
+constexpr int kMaxDevices = 64;
+hipError_t decode_static_scratch(int device, float **ptr);
 // n int32 zeros at p (a fill kernel: safe under graph capture).
 hipError_t launch_zero_i32(int *p, int n, hipStream_t stream);
 

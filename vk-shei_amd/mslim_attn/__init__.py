@@ -23,6 +23,7 @@ LIB_PATH = os.path.join(_HERE, "libmslim_attn.so")
 MAX_BATCH = 64
 OPT_DECODE_MERGE = 1                        # mslim_attn_ctx_set_option options
 DECODE_MERGE_FUSED, DECODE_MERGE_SEPARATE = 0, 1
+DECODE_STATIC_SCRATCH_BYTES = 16 << 20      # mslim_attn_decode_paged_noalloc partials bound
 FORMAT_BF16, FORMAT_F16, FORMAT_F32 = 1, 2, 3  # gpu_backend.rs:258-262
 ERR_NONFINITE = -2
 
@@ -60,6 +61,7 @@ EXPORTS = (
     "mslim_attn_decode_auto_split",
     "mslim_attn_decode_dense",
     "mslim_attn_decode_paged",
+    "mslim_attn_decode_paged_noalloc",
     "mslim_attn_prefill_causal",
     "mslim_attn_frames_decode",
     "mslim_attn_backend_decode",
@@ -137,6 +139,7 @@ def library() -> C.CDLL:
         "mslim_attn_decode_auto_split": (I, [C.POINTER(C.c_int32), I, I]),
         "mslim_attn_decode_dense": (I, [P, P, P, P, P, I, PI32, I64, I, I, I, F, I]),
         "mslim_attn_decode_paged": (I, [P, P, P, P, P, I, PI32, P, I, I, I, I, I, F, I]),
+        "mslim_attn_decode_paged_noalloc": (I, [P, P, P, P, P, I, PI32, P, I, I, I, I, I, F, I]),
         "mslim_attn_prefill_causal": (I, [P, P, P, P, P, I, I, I, I, I, F]),
         "mslim_attn_frames_decode": (I, [P, P, P, I, P, I, P, I64, I, I, I]),
         "mslim_attn_backend_decode": (I, [P, P, P, I, P, I, I64, I, I, I, P, C.POINTER(Timings)]),
@@ -295,6 +298,17 @@ class Context:
                      head_dim: int, scale: Optional[float] = None, split_tokens: int = 0) -> None:
         scale = default_scale(head_dim) if scale is None else scale
         self._check("decode_paged", self._lib.mslim_attn_decode_paged(
+            self._h, _ptr(q), _ptr(k_pool), _ptr(v_pool), _ptr(out), len(seq_lens),
+            _lens(seq_lens), _ptr(page_table), pages_per_seq, page_tokens, q_heads, kv_heads,
+            head_dim, scale, split_tokens))
+
+    def decode_paged_noalloc(self, q, k_pool, v_pool, out, seq_lens: Sequence[int], page_table,
+                             pages_per_seq: int, page_tokens: int, q_heads: int, kv_heads: int,
+                             head_dim: int, scale: Optional[float] = None, split_tokens: int = 0) -> None:
+        """decode_paged with its split partials in the library's fixed device
+        array: no allocation; calls that overlap on one GPU race."""
+        scale = default_scale(head_dim) if scale is None else scale
+        self._check("decode_paged_noalloc", self._lib.mslim_attn_decode_paged_noalloc(
             self._h, _ptr(q), _ptr(k_pool), _ptr(v_pool), _ptr(out), len(seq_lens),
             _lens(seq_lens), _ptr(page_table), pages_per_seq, page_tokens, q_heads, kv_heads,
             head_dim, scale, split_tokens))
