@@ -250,26 +250,16 @@ DEC_FFN, DEC_VOCAB, DEC_BATCH, DEC_PROMPT, DEC_STEPS = 14336, 128256, 8, 4096, 1
 DEC_CHUNK = 512
 
 
-def decoder_weights(torch, seed: int) -> dict:
+def decoder_weights(seed: int) -> dict:
     """Random-init cfg5 weights on the device: projections, embedding and LM
     head N(0, 0.02), RMSNorm weights 1 + N(0, 0.1^2), rounded to BF16."""
-    gen = torch.Generator(device="cuda").manual_seed(seed)
+    from mslim_attn.model import synthetic_weights
+    return synthetic_weights(decoder_spec(), seed)
 
-    def normal(shape, scale):
-        return (torch.randn(shape, generator=gen, device="cuda") * scale).to(torch.bfloat16).view(torch.int16)
 
-    def norm():
-        return (1.0 + 0.1 * torch.randn(DEC_HIDDEN, generator=gen, device="cuda")).to(torch.bfloat16).view(torch.int16)
-
-    qd, kvd = DEC_QH * DEC_D, DEC_KVH * DEC_D
-    shapes = {"q": (qd, DEC_HIDDEN), "k": (kvd, DEC_HIDDEN), "v": (kvd, DEC_HIDDEN), "o": (DEC_HIDDEN, qd),
-              "gate": (DEC_FFN, DEC_HIDDEN), "up": (DEC_FFN, DEC_HIDDEN), "down": (DEC_HIDDEN, DEC_FFN)}
-    w = {"embed": normal((DEC_VOCAB, DEC_HIDDEN), 0.02), "final_norm": norm(),
-         "lm_head": normal((DEC_VOCAB, DEC_HIDDEN), 0.02)}
-    for l in range(DEC_LAYERS):
-        for name in ("input_norm", "q", "k", "v", "o", "post_norm", "gate", "up", "down"):
-            w[f"layers.{l}.{name}"] = norm() if name.endswith("norm") else normal(shapes[name], 0.02)
-    return w
+def decoder_spec():
+    from mslim_attn.model import ModelSpec
+    return ModelSpec(DEC_LAYERS, DEC_HIDDEN, DEC_QH, DEC_KVH, DEC_D, DEC_FFN, DEC_VOCAB, 1e-5, 500000.0)
 
 
 def decoder_step_bytes(contexts) -> int:
@@ -332,11 +322,11 @@ def decoder_leg(torch, ctx, args, np):
     seeded 4,096-token prompts in 512-token causal chunks, then `steps`
     batched greedy decode steps over the ColdStore-exact paged K/V.  The same
     run on the dense K/V layout must give the same tokens."""
-    from mslim_attn.model import Model, ModelSpec
+    from mslim_attn.model import Model
 
     log("bench: cfg5 decoder weights on device")
-    weights = decoder_weights(torch, seed=0x38423031)
-    spec = ModelSpec(DEC_LAYERS, DEC_HIDDEN, DEC_QH, DEC_KVH, DEC_D, DEC_FFN, DEC_VOCAB, 1e-5, 500000.0)
+    weights = decoder_weights(seed=0x38423031)
+    spec = decoder_spec()
     prompts = np.random.default_rng(20261202).integers(0, DEC_VOCAB, (DEC_BATCH, DEC_PROMPT))
     steps = args.decoder_steps
     runs = {}

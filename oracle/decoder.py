@@ -192,8 +192,10 @@ class CpuDecoderOracle:
             self._norms[name] = read_bf16(self.w[name]).astype(np.float32)
         return self._norms[name]
 
-    def forward_token(self, seq: int, token: int) -> tuple:
-        """(logits f32 [vocab], next token) after appending `token`."""
+    def forward_token(self, seq: int, token: int, head: bool = True) -> tuple:
+        """(logits f32 [vocab], next token) after appending `token`; with
+        head=False the final norm and LM head are skipped (None, -1), for
+        prompt tokens whose logits the caller discards."""
         s, w = self.s, self.w
         if seq not in self.sessions:
             self.reset(seq)
@@ -219,6 +221,8 @@ class CpuDecoderOracle:
             act = read_bf16(swiglu(write_bf16(gate), write_bf16(up))).astype(np.float32)
             state = round_bf16(state + matvec_cpu(g("down"), act, s.hidden, s.intermediate))
         self.last_hidden = state  # the final residual row, for closed-form checks
+        if not head:
+            return None, -1
         final = rms_norm_cpu(state, self._vector("final_norm"), s.rms_eps)
         logits = matvec_cpu(w["lm_head"], final, s.vocab, s.hidden)
         return logits, argmax_total_last(logits)
@@ -226,10 +230,10 @@ class CpuDecoderOracle:
     def prefill(self, seq: int, prompt) -> tuple:
         """(logits, greedy token) after the prompt, token by token; the slot restarts."""
         self.reset(seq)
-        out = None
-        for t in prompt:
-            out = self.forward_token(seq, int(t))
-        return out
+        prompt = [int(t) for t in prompt]
+        for t in prompt[:-1]:
+            self.forward_token(seq, t, head=False)
+        return self.forward_token(seq, prompt[-1])
 
     def step(self, seq: int, token: int) -> tuple:
         return self.forward_token(seq, token)

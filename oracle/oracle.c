@@ -384,6 +384,10 @@ void orc_argmax_bf16(const uint16_t *logits, int rows, int vocab, int32_t *out) 
     }
 }
 
+/* Eight rows per step of the inner loops below: eight independent sums, each
+ * still added in ascending order, so every output is unchanged. */
+#define ORC_ROWS 8
+
 /* hipblaslt_bridge.cpp:203-233 tv_hip_matrix_multiply: out[t][r] =
  * BF16(sum_i in[t][i] * w[r][i]), products and sum in fp32 (ascending i),
  * one rounding at the end.  pin: identity weight reproduces the input bit for
@@ -391,27 +395,48 @@ void orc_argmax_bf16(const uint16_t *logits, int rows, int vocab, int32_t *out) 
 void orc_matmul_bf16(const uint16_t *w, const uint16_t *in, int inner, int rows, int tokens, uint16_t *out) {
     /* Outputs are independent: rows split over OpenMP threads, each sum in
      * ascending i as before. */
-    for (int t = 0; t < tokens; ++t)
+    const int blocks = (rows + ORC_ROWS - 1) / ORC_ROWS;
+    for (int t = 0; t < tokens; ++t) {
+        const uint16_t *xt = in + (size_t)t * inner;
 #pragma omp parallel for schedule(static)
-        for (int r = 0; r < rows; ++r) {
-            float acc = 0.0f;
-            const uint16_t *wr = w + (size_t)r * inner;
-            const uint16_t *xt = in + (size_t)t * inner;
-            for (int i = 0; i < inner; ++i) acc = fmaf(orc_read_bf16(wr[i]), orc_read_bf16(xt[i]), acc);
-            out[(size_t)t * rows + r] = orc_write_bf16(acc);
+        for (int blk = 0; blk < blocks; ++blk) {
+            const int r0 = blk * ORC_ROWS;
+            const int n = rows - r0 < ORC_ROWS ? rows - r0 : ORC_ROWS;
+            const uint16_t *wr[ORC_ROWS];
+            float acc[ORC_ROWS];
+            for (int j = 0; j < ORC_ROWS; ++j) {
+                wr[j] = w + (size_t)(r0 + (j < n ? j : 0)) * inner;
+                acc[j] = 0.0f;
+            }
+            for (int i = 0; i < inner; ++i) {
+                const float xi = orc_read_bf16(xt[i]);
+                for (int j = 0; j < ORC_ROWS; ++j) acc[j] = fmaf(orc_read_bf16(wr[j][i]), xi, acc[j]);
+            }
+            for (int j = 0; j < n; ++j) out[(size_t)t * rows + r0 + j] = orc_write_bf16(acc[j]);
         }
+    }
 }
 
 void orc_matvec_cpu(const uint16_t *w, const float *x, int rows, int cols, float *out) {
+    const int blocks = (rows + ORC_ROWS - 1) / ORC_ROWS;
 #pragma omp parallel for schedule(static)
-    for (int r = 0; r < rows; ++r) {
-        const uint16_t *wr = w + (size_t)r * cols;
-        float sum = -0.0f;
-        for (int i = 0; i < cols; ++i) {
-            const float product = orc_read_bf16(wr[i]) * x[i];
-            sum += product;
+    for (int blk = 0; blk < blocks; ++blk) {
+        const int r0 = blk * ORC_ROWS;
+        const int n = rows - r0 < ORC_ROWS ? rows - r0 : ORC_ROWS;
+        const uint16_t *wr[ORC_ROWS];
+        float sum[ORC_ROWS];
+        for (int j = 0; j < ORC_ROWS; ++j) {
+            wr[j] = w + (size_t)(r0 + (j < n ? j : 0)) * cols;
+            sum[j] = -0.0f;
         }
-        out[r] = round_bf16(sum);
+        for (int i = 0; i < cols; ++i) {
+            const float xi = x[i];
+            for (int j = 0; j < ORC_ROWS; ++j) {
+                const float product = orc_read_bf16(wr[j][i]) * xi;
+                sum[j] += product;
+            }
+        }
+        for (int j = 0; j < n; ++j) out[r0 + j] = round_bf16(sum[j]);
     }
 }
 
