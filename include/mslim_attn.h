@@ -104,6 +104,12 @@ int mslim_attn_ctx_set_stream(void *ctx, void *hip_stream);
 #define MSLIM_ATTN_OPT_DECODE_MERGE 1
 #define MSLIM_ATTN_DECODE_MERGE_FUSED 0
 #define MSLIM_ATTN_DECODE_MERGE_SEPARATE 1
+/*   MSLIM_ATTN_OPT_PREFILL_SPLIT: 1 (default) lets mslim_attn_prefill_causal
+ *     split the key range of long row blocks into chunks, merged in fixed
+ *     chunk order, when a launch has too few workgroups to keep every CU busy
+ *     (same tolerance, deterministic; the output differs from the unsplit
+ *     launch in rounding only); 0 never splits. */
+#define MSLIM_ATTN_OPT_PREFILL_SPLIT 2
 int mslim_attn_ctx_set_option(void *ctx, int option, int64_t value);
 
 /* queue.finish() equivalent (gpu_llm/mod.rs:1998-2001). */
@@ -113,6 +119,13 @@ int mslim_attn_synchronize(void *ctx);
 
 /* GpuEngine::alloc_u8 (gpu_resources.rs) equivalent; NULL on failure. */
 void *mslim_attn_buf_alloc(void *ctx, size_t bytes);
+/* Page-locked host memory (hipHostMalloc) for staging that the buffer
+ * read/write entry points move by DMA: the seal and restore staging of the
+ * ColdStore path, reused across calls.  No reference counterpart (the
+ * reference stages through ordinary Vec<u8>).  NULL on failure;
+ * mslim_attn_host_free waits for the context's stream first. */
+void *mslim_attn_host_alloc(void *ctx, size_t bytes);
+int mslim_attn_host_free(void *ctx, void *host);
 /* Replaces tv_hip_load_weight (hipblaslt_bridge.cpp:173-187,
  * native_hip.rs:104,146): allocate and copy `bytes` host bytes. */
 void *mslim_attn_buf_upload(void *ctx, const uint8_t *bytes, size_t byte_length);
@@ -197,6 +210,13 @@ int mslim_attn_decode_paged_noalloc(void *ctx, const void *q, const void *k_pool
 int mslim_attn_prefill_causal(void *ctx, const void *q, const void *k, const void *v,
                               void *out, int queries, int prior, int q_heads,
                               int kv_heads, int head_dim, float scale);
+
+/* Key tiles (64 keys each) per chunk that mslim_attn_prefill_causal splits
+ * the longest row blocks of this shape into, or 0 when the launch is not
+ * split (enough workgroups to keep every CU busy, or MSLIM_ATTN_OPT_PREFILL_
+ * SPLIT off).  A function of the shape only.  Host only (no context, no
+ * device work); -1 on invalid arguments.  No reference counterpart. */
+int mslim_attn_prefill_split_tiles(int queries, int prior, int q_heads, int kv_heads, int head_dim);
 
 /* ---- Portable backend (exact K/V frames) ------------------------------------ */
 
@@ -361,14 +381,16 @@ int mslim_attn_logical_kv_sha256(void *ctx, int layers, int64_t tokens, int kv_h
 
 /* One ColdStore record to be made from a pool page: its header fields
  * (cold_store.rs:291-309) and the pool page holding its K and V payloads in
- * rows 0..tokens-1 of every head. */
+ * rows first_row .. first_row + tokens - 1 of every head (first_row > 0 when
+ * a record starts inside a page, for example after a turn that ended there;
+ * first_row + tokens <= page_tokens). */
 typedef struct {
     uint64_t page_id;
     uint64_t token_start;
     uint32_t layer;
     uint32_t tokens;    /* 1..page_tokens */
     int32_t pool_page;  /* 0..pool_pages-1 */
-    uint32_t reserved;  /* ignored */
+    uint32_t first_row; /* pool-page row of the first token */
 } mslim_attn_page_record;
 
 #define MSLIM_ATTN_RECORD_HEADER_BYTES 104 /* cold_store.rs:23 */
@@ -391,13 +413,24 @@ int64_t mslim_attn_record_frame_bytes(int page_tokens);
  *     hashes (8 * tokens_i B) | zeros | footer (56 B, the slot's last bytes).
  * Record i's file bytes are slot[0 .. 104 + 16 * tokens_i) | K payload |
  * V payload | slot footer, the payloads being the head-major
- * [kv_heads][tokens_i][head_dim] rows of pool page pool_page.  A record
- * whose tokens or pool_page is out of range gets an all-zero slot (no
- * header magic).  `tile` must divide head_dim (cold_store.rs:690-692).
- * Stream-ordered. */
+ * [kv_heads][tokens_i][head_dim] rows first_row.. of pool page pool_page.  A
+ * record whose tokens, first_row or pool_page is out of range gets an
+ * all-zero slot (no header magic).  `tile` must divide head_dim
+ * (cold_store.rs:690-692).  Stream-ordered. */
 int mslim_attn_record_frames(void *ctx, const void *k_pool, const void *v_pool, int64_t pool_pages,
                              int page_tokens, int kv_heads, int head_dim, uint32_t tile,
                              const mslim_attn_page_record *records, int count, void *frames);
+
+/* The same frames for records whose payloads sit in staging (slot i of
+ * k_stage / v_stage holds record i compacted to [kv_heads][tokens_i]
+ * [head_dim], the layout of mslim_attn_record_payloads) instead of pool
+ * pages; pool_page and first_row are not read.  Lets a restore verify a
+ * stored record on the device before any of its bytes reach the pool (the
+ * reference verifies each record before its bytes reach the GPU buffer,
+ * gpu_llm/mod.rs:1367-1398).  Stream-ordered. */
+int mslim_attn_record_frames_staged(void *ctx, const void *k_stage, const void *v_stage, int page_tokens,
+                                    int kv_heads, int head_dim, uint32_t tile,
+                                    const mslim_attn_page_record *records, int count, void *frames);
 
 /* Move the payloads of `count` records between their pool pages and
  * contiguous staging, so a batch of records crosses PCIe as one copy each
@@ -408,7 +441,8 @@ int mslim_attn_record_frames(void *ctx, const void *k_pool, const void *v_pool, 
  * the ColdStore, the device side of GpuRegionStore::append_batch,
  * gpu_region_store.rs:452-472); direction 1: staging -> pool (restoring
  * verified pages, replacing the per-chunk read_values + H2D staging of
- * gpu_resources.rs:1017-1048).  Records out of range are skipped.
+ * gpu_resources.rs:1017-1048).  Only rows first_row .. first_row + tokens_i
+ * - 1 of each pool page move.  Records out of range are skipped.
  * Stream-ordered. */
 int mslim_attn_record_payloads(void *ctx, void *k_pool, void *v_pool, int64_t pool_pages, int page_tokens,
                                int kv_heads, int head_dim, const mslim_attn_page_record *records,

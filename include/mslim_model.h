@@ -96,6 +96,42 @@ int mslim_model_set_prefill_settings(void *model, const char *json);
 /* GpuLlm::logical_kv_sha256 (mod.rs:1981-2028) of slot `seq`, hex with NUL. */
 int mslim_model_logical_kv_sha256(void *model, int seq, char *hex_out);
 
+/* ---- ColdStore-exact persistence (MSLIM_MODEL_KV_PAGED only) -------------- */
+
+/* Give empty slot `seq` the canonical ColdStore <directory>/pages-exact.kv
+ * (created, or opened with its committed records; GpuRegionConfig::
+ * cold_directory of the GPU-region runtime, gpu_llm/mod.rs:299-306).  While
+ * attached, mslim_model_prefill commits the prompt's K/V at its end
+ * (gpu_llm/prefill.rs:760-790), decode steps defer their commit, and
+ * mslim_model_flush_cold commits every token past the committed prefix
+ * (flush_deferred_cold, gpu_llm/mod.rs:1614-1699).  A prefill into a slot
+ * whose store already holds tokens fails: restore it instead. */
+int mslim_model_attach_cold_store(void *model, int seq, const char *directory);
+int mslim_model_detach_cold_store(void *model, int seq);
+int mslim_model_flush_cold(void *model, int seq);
+/* Load the store's committed prefix of `tokens` tokens (every layer must hold
+ * exactly that many) into empty slot `seq`, verifying every record on the
+ * device (header, token hashes, checksums, SHA-256) before any byte reaches
+ * the page pool; afterwards the slot continues at position `tokens`
+ * (restore_session, gpu_llm/mod.rs:1335-1451).  A corrupt or incomplete
+ * store fails and leaves the slot empty. */
+int mslim_model_restore_session(void *model, int seq, int64_t tokens);
+/* GpuRegionStore::logical_kv_sha256 (gpu_region_store.rs:341-371) of the
+ * slot's ColdStore, read from the file: equal to mslim_model_logical_kv_
+ * sha256 once every token is committed. */
+int mslim_model_cold_logical_kv_sha256(void *model, int seq, char *hex_out);
+
+/* Persistence figures of one slot (gpu_llm/mod.rs:192-208). */
+typedef struct {
+    int attached;
+    int64_t committed_tokens;
+    double prefill_seal_seconds;          /* last_prefill_cold_seal_seconds */
+    double last_commit_seconds;           /* last_deferred_cold_commit_seconds */
+    int64_t last_committed_token_layers;  /* last_deferred_cold_committed_token_layers */
+    double last_restore_seconds;
+} mslim_model_cold_info;
+int mslim_model_cold_report(void *model, int seq, mslim_model_cold_info *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -755,7 +755,11 @@ TEST(gpu_region_device_restore_detects_corruption_and_seal_rejects_nonfinite) {
         const uint8_t flipped = bytes[off] ^ 0x10;
         write_at(path, off, &flipped, 1);
         const std::vector<int32_t> other{1, 2, 0};
+        // The record is verified from its staged copy before any byte moves:
+        // a failed restore leaves the pool exactly as it was.
+        const auto k_before = dk.read(), v_before = dv.read();
         CHECK(expect_kind([&] { store.restore_to_device(*ctx, 0, pool, other); }) == Kind::InvalidData);
+        CHECK(dk.read() == k_before && dv.read() == v_before);
     }
     // A NaN in V of a fresh pool page: the seal is rejected before any commit.
     std::vector<uint8_t> v_bad = v_pool;
@@ -772,6 +776,84 @@ TEST(gpu_region_device_restore_detects_corruption_and_seal_rejects_nonfinite) {
           "GPU ColdStore V nonfinite");
     CHECK(store2.layer_tokens(0) == 0);
     CHECK(store2.storage_metrics().pages == 0);
+}
+
+TEST(gpu_region_device_seal_mid_page_multi_layer_and_restore) {
+    // Two commits of two layers, the second starting inside a pool page (a
+    // turn that ended at token 20 of 16-token pages): the records are
+    // [0,16) [16,20) | [20,32) [32,45) per layer.  The logical digest equals
+    // a host append of the same rows; a reopened store restores every layer
+    // into a different pool through seal/restore_device_layers, rows equal.
+    auto ctx = NativeContext::create();
+    const size_t kvh = 4, d = 64, P = 16, per_layer = 8, layers = 2, tokens = 45;
+    const auto g = portable::AttentionGeometry::create(8, kvh, d);
+    const size_t page_bytes = kvh * P * d * 2, token_bytes = kvh * d * 2, pool_pages = per_layer * layers;
+    std::mt19937_64 rng(77);
+    std::vector<std::vector<uint8_t>> k_rows(layers), v_rows(layers);
+    std::vector<uint8_t> k_pool(pool_pages * page_bytes, 0xEE), v_pool(pool_pages * page_bytes, 0xEE);
+    const std::vector<int32_t> order{5, 2, 7, 0};  // logical page -> page of the layer's pool slice
+    std::vector<region::LayerBlocks> lb(layers);
+    for (size_t l = 0; l < layers; ++l) {
+        k_rows[l] = finite_bf16(rng, tokens * kvh * d);
+        v_rows[l] = finite_bf16(rng, tokens * kvh * d);
+        lb[l].layer = l;
+        for (int32_t o : order) lb[l].blocks.push_back((int32_t)(l * per_layer) + o);
+        for (size_t t = 0; t < tokens; ++t)
+            for (size_t h = 0; h < kvh; ++h) {
+                const size_t dst = (size_t)lb[l].blocks[t / P] * page_bytes + (h * P + t % P) * d * 2;
+                std::memcpy(k_pool.data() + dst, k_rows[l].data() + t * token_bytes + h * d * 2, d * 2);
+                std::memcpy(v_pool.data() + dst, v_rows[l].data() + t * token_bytes + h * d * 2, d * 2);
+            }
+    }
+    DeviceVec dk(ctx, k_pool), dv(ctx, v_pool);
+    region::DevicePagePool pool;
+    pool.k_pool = dk.ptr;
+    pool.v_pool = dv.ptr;
+    pool.pool_pages = (int64_t)pool_pages;
+    pool.page_tokens = (int)P;
+    TempPath da("unused-a"), db("unused-b");
+    region::RegionConfig ca, cb;
+    ca.cold_directory = da.dir;
+    cb.cold_directory = db.dir;
+    std::string digest;
+    {
+        region::RegionStore host(g, layers, ca), dev(g, layers, cb);
+        for (size_t l = 0; l < layers; ++l) host.append_batch(l, 0, k_rows[l], v_rows[l], P);
+        region::DeviceStaging staging(*ctx);
+        dev.seal_device_layers(staging, 0, 20, pool, lb);
+        CHECK(dev.layer_tokens(0) == 20 && dev.layer_tokens(1) == 20);
+        dev.seal_device_layers(staging, 20, tokens - 20, pool, lb);
+        CHECK(dev.stats.device_sealed_pages == 8);
+        // page ids: first commit layer 0 {0, 1}, layer 1 {2, 3}; second
+        // commit layer 0 {4, 5}: page 4 starts inside its pool page
+        CHECK(dev.cold_store().metadata().at(4).geometry.layer == 0);
+        CHECK(dev.cold_store().metadata().at(4).geometry.token_start == 20);
+        CHECK(dev.cold_store().metadata().at(4).geometry.tokens == 12);
+        digest = host.logical_kv_sha256();
+        CHECK(dev.logical_kv_sha256() == digest);
+    }
+    region::RegionStore reopened(g, layers, cb);
+    CHECK(reopened.logical_kv_sha256() == digest);
+    std::vector<uint8_t> zeros(pool_pages * page_bytes, 0);
+    DeviceVec rk(ctx, zeros), rv(ctx, zeros);
+    region::DevicePagePool fresh = pool;
+    fresh.k_pool = rk.ptr;
+    fresh.v_pool = rv.ptr;
+    std::vector<region::LayerBlocks> lb2(layers);
+    for (size_t l = 0; l < layers; ++l) {
+        lb2[l].layer = l;
+        for (int32_t o : {1, 6, 3, 4}) lb2[l].blocks.push_back((int32_t)(l * per_layer) + o);
+    }
+    region::DeviceStaging staging(*ctx);
+    CHECK(reopened.restore_device_layers(staging, fresh, lb2) == 8);
+    const auto kk = rk.read(), vv = rv.read();
+    for (size_t l = 0; l < layers; ++l)
+        for (size_t t = 0; t < tokens; ++t)
+            for (size_t h = 0; h < kvh; ++h) {
+                const size_t src = (size_t)lb2[l].blocks[t / P] * page_bytes + (h * P + t % P) * d * 2;
+                CHECK(std::memcmp(kk.data() + src, k_rows[l].data() + t * token_bytes + h * d * 2, d * 2) == 0);
+                CHECK(std::memcmp(vv.data() + src, v_rows[l].data() + t * token_bytes + h * d * 2, d * 2) == 0);
+            }
 }
 
 // Four-route parity of the attention path, after the reference's adapter

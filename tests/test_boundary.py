@@ -133,3 +133,18 @@ def test_auto_split_rejects_bad_batches():
     for lens, kvh in (([], 8), ([0], 8), ([5] * 65, 8), ([5], 0)):
         with pytest.raises(MslimAttnError, match="code=-1"):
             auto_split(lens, kvh)
+
+
+def test_prefill_split_choices():
+    # host-only plan of mslim_attn_prefill_causal: chunk length in key tiles,
+    # 0 when the launch keeps every CU busy without splitting
+    from mslim_attn import MslimAttnError, prefill_split_tiles
+    assert prefill_split_tiles(8192, 0, 64, 8, 128) == 0     # cfg4: 2,048 workgroups
+    assert prefill_split_tiles(2048, 0, 32, 8, 128) == 17    # cfg2: 256 workgroups of 1..32 tiles
+    assert prefill_split_tiles(512, 3584, 32, 8, 128) == 16  # a decoder prompt chunk after 3,584 tokens
+    assert prefill_split_tiles(512, 0, 32, 8, 128) == 4
+    assert prefill_split_tiles(100, 0, 32, 8, 128) == 0
+    assert prefill_split_tiles(300, 0, 4, 2, 80) == 0        # generic kernel: never split
+    for args in ((0, 0, 32, 8, 128), (5, -1, 32, 8, 128), (5, 0, 32, 3, 128)):
+        with pytest.raises(MslimAttnError):
+            prefill_split_tiles(*args)

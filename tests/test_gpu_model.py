@@ -11,6 +11,8 @@ MODEL_LOGIT_REL2 (tests/_data.py, which states how they were set and which
 planted mistakes they reject).  Greedy tokens must agree wherever the
 oracle's top-1/top-2 margin exceeds 2 * MODEL_LOGIT_MAX_ABS.
 """
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -424,3 +426,80 @@ def test_runner_prefill_settings(tiny_model):
             model.reset(seq)
         model.set_prefill_settings(base)
     assert model.prefill_settings() == base
+
+
+def test_runner_coldstore_commit_digest_and_restore(ctx, tmp_path):
+    # ColdStore-exact persistence of the runner: the prompt is committed at
+    # the end of prefill (gpu_llm/prefill.rs:760-790), decode steps defer
+    # their commit until flush_cold (flush_deferred_cold, gpu_llm/mod.rs:
+    # 1614-1699), and the ColdStore's logical K/V digest then equals the
+    # runner's.  A fresh runner restores the slot from the directory
+    # (restore_session, mod.rs:1335-1451) and continues with bit-identical
+    # tokens and logits; a corrupted record is refused before any byte
+    # reaches the pool, and the slot stays empty.
+    from mslim_attn import MslimAttnError
+    from mslim_attn.model import Model, ModelSpec
+
+    w = random_weights(SPEC, np.random.default_rng(20261201))
+    dev = {k: to_torch(v) for k, v in w.items()}
+    spec = ModelSpec(SPEC.layers, SPEC.hidden, SPEC.q_heads, SPEC.kv_heads, SPEC.head_dim,
+                     SPEC.intermediate, SPEC.vocab, SPEC.rms_eps, SPEC.rope_theta)
+    directory = str(tmp_path / "session")
+    os.makedirs(directory)
+    prompt = list(np.random.default_rng(41).integers(0, SPEC.vocab, 37))
+    first = Model(ctx, spec, dev, max_batch=2, chunk_tokens=16, max_context=80)
+    try:
+        first.attach_cold_store(0, directory)
+        tok = first.prefill_only(0, prompt)
+        report = first.cold_report(0)
+        assert report["attached"] and report["committed_tokens"] == len(prompt)
+        assert first.cold_logical_kv_sha256(0) == first.logical_kv_sha256(0)
+        toks = [tok]
+        for _ in range(5):  # 5 deferred steps: the first ends inside a 16-token page
+            toks.append(first.forward_batch([toks[-1]])[0])
+        assert first.cold_report(0)["committed_tokens"] == len(prompt)
+        first.flush_cold(0)
+        report = first.cold_report(0)
+        assert report["committed_tokens"] == len(prompt) + 5
+        assert report["last_committed_token_layers"] == 5 * SPEC.layers
+        digest = first.logical_kv_sha256(0)
+        assert first.cold_logical_kv_sha256(0) == digest
+        # the uninterrupted continuation
+        want_next = first.forward_batch([toks[-1]])[0]
+        want_logits = first.logits()[0].copy()
+        # a prefill into a slot whose store holds a session is refused
+        with pytest.raises(MslimAttnError, match="already holds a session"):
+            first.prefill_only(0, prompt)
+    finally:
+        first.close()
+
+    second = Model(ctx, spec, dev, max_batch=1, chunk_tokens=16, max_context=80)
+    try:
+        second.attach_cold_store(0, directory)
+        assert second.cold_report(0)["committed_tokens"] == len(prompt) + 5
+        second.restore_session(0, len(prompt) + 5)
+        assert second.position(0) == len(prompt) + 5
+        assert second.logical_kv_sha256(0) == digest
+        assert second.forward_batch([toks[-1]])[0] == want_next
+        assert np.array_equal(second.logits()[0], want_logits)
+    finally:
+        second.close()
+
+    # The store opens clean (every record verified on the host); then one
+    # payload byte in the file changes underneath it.  The device
+    # verification of the staged records refuses the restore and the slot
+    # stays empty.
+    third = Model(ctx, spec, dev, max_batch=1, chunk_tokens=16, max_context=80)
+    try:
+        third.attach_cold_store(0, directory)
+        path = os.path.join(directory, "pages-exact.kv")
+        with open(path, "r+b") as f:
+            f.seek(os.path.getsize(path) // 2)
+            byte = f.read(1)
+            f.seek(-1, os.SEEK_CUR)
+            f.write(bytes([byte[0] ^ 0x08]))
+        with pytest.raises(MslimAttnError, match="device verification failed"):
+            third.restore_session(0, len(prompt) + 5)
+        assert third.position(0) == 0
+    finally:
+        third.close()

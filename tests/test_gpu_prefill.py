@@ -142,3 +142,55 @@ def test_prefill_rejects_bad_arguments(ctx):
         ctx.prefill_causal(q, k, k, out, 0, 0, 8, 8, 128)
     with pytest.raises(mslim_attn.MslimAttnError):
         ctx.prefill_causal(q, k, k, out, 4, -1, 8, 8, 128)
+
+
+# Launches too small to fill the CUs split long row blocks into chunks of key
+# tiles (merged in fixed chunk order): cfg2, the decoder's 512-token prompt
+# chunks after a long prior, ragged query counts, D = 64 and a group of 2.
+SPLIT_SHAPES = [(2048, 0, 32, 8, 128), (512, 3584, 32, 8, 128), (1000, 777, 64, 8, 128),
+                (1500, 0, 16, 2, 64), (2048, 0, 16, 8, 128), (512, 0, 32, 8, 128)]
+
+
+@pytest.mark.parametrize("queries,prior,qh,kvh,d", SPLIT_SHAPES)
+def test_prefill_split_launches(ctx, queries, prior, qh, kvh, d):
+    import mslim_attn
+    assert mslim_attn.prefill_split_tiles(queries, prior, qh, kvh, d) > 0
+    hist = prior + queries
+    gen = torch.Generator(device="cuda").manual_seed(queries + prior + qh)
+    q = torch.randn((queries, qh, d), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    k = torch.randn((hist, kvh, d), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    v = torch.randn((hist, kvh, d), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    out, again, whole = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
+    ctx.prefill_causal(q, k, v, out, queries, prior, qh, kvh, d)
+    ctx.prefill_causal(q, k, v, again, queries, prior, qh, kvh, d)
+    try:
+        ctx.set_prefill_split(False)
+        ctx.prefill_causal(q, k, v, whole, queries, prior, qh, kvh, d)
+    finally:
+        ctx.set_prefill_split(True)
+    torch.cuda.synchronize()
+    # deterministic: the merge order does not depend on which chunk ends last
+    assert torch.equal(out, again)
+    got, unsplit = from_torch(out), from_torch(whole)
+    qb, kb, vb = from_torch(q), from_torch(k), from_torch(v)
+    rng = np.random.default_rng(queries)
+    rows = sorted({0, 1, 63, 64, queries // 2, queries - 2, queries - 1} |
+                  {int(x) for x in rng.integers(0, queries, size=10)})
+    ref = _rows_reference(qb, kb, vb, rows, prior, qh, kvh, d)
+    for r in rows:
+        assert max_abs_bf16(got[r], ref[r]) <= TOL, r
+        assert max_abs_bf16(unsplit[r], ref[r]) <= TOL, r
+    # split and unsplit launches differ in rounding only
+    diff = np.abs(oracle.read_bf16(got).astype(np.float64) - oracle.read_bf16(unsplit).astype(np.float64))
+    assert float(diff.max()) <= TOL
+
+
+def test_prefill_split_plan_is_shape_only(ctx):
+    import mslim_attn
+    # cfg4's 8,192-token prefill has 2,048 workgroups: never split
+    assert mslim_attn.prefill_split_tiles(8192, 0, 64, 8, 128) == 0
+    # tiny launches have nothing to split
+    assert mslim_attn.prefill_split_tiles(100, 0, 32, 8, 128) == 0
+    assert mslim_attn.prefill_split_tiles(2048, 0, 32, 8, 128) == 17
+    with pytest.raises(mslim_attn.MslimAttnError):
+        mslim_attn.prefill_split_tiles(0, 0, 32, 8, 128)

@@ -44,6 +44,12 @@ struct Context {
     size_t counter_bytes = 0;
     bool counters_dirty = false;    // a decode launch failed: clear before the next
     bool separate_merge = false;    // MSLIM_ATTN_OPT_DECODE_MERGE
+    void *prefill_partial = nullptr;  // split prefill partials
+    size_t prefill_partial_bytes = 0;
+    void *prefill_counters = nullptr;  // split prefill chunk counters, zero between launches
+    size_t prefill_counter_bytes = 0;
+    bool prefill_counters_dirty = false;
+    bool prefill_split = true;        // MSLIM_ATTN_OPT_PREFILL_SPLIT
     void *staging = nullptr;       // device, digest serialisation
     size_t staging_bytes = 0;
     void *host_staging = nullptr;  // pinned host, digest readback
@@ -64,6 +70,8 @@ struct Context {
         if (gemm_out) (void)hipFree(gemm_out);
         if (fuse_tmp) (void)hipFree(fuse_tmp);
         if (workspace) (void)hipFree(workspace);
+        if (prefill_partial) (void)hipFree(prefill_partial);
+        if (prefill_counters) (void)hipFree(prefill_counters);
         if (counters) (void)hipFree(counters);
         if (staging) (void)hipFree(staging);
         if (host_staging) (void)hipHostFree(host_staging);
@@ -305,6 +313,10 @@ int mslim_attn_ctx_set_option(void *ctx, int option, int64_t value) {
             return fail("decode merge mode must be 0 (fused) or 1 (separate launch)");
         c.separate_merge = value == MSLIM_ATTN_DECODE_MERGE_SEPARATE;
         return 0;
+    case MSLIM_ATTN_OPT_PREFILL_SPLIT:
+        if (value != 0 && value != 1) return fail("prefill split must be 0 (never) or 1 (automatic)");
+        c.prefill_split = value == 1;
+        return 0;
     default:
         return fail("unknown context option");
     }
@@ -492,6 +504,17 @@ int mslim_attn_decode_paged_noalloc(void *ctx, const void *q, const void *k_pool
     return check_hip(mslim::launch_decode(l, c.stream), "decode attention launch");
 }
 
+int mslim_attn_prefill_split_tiles(int queries, int prior, int q_heads, int kv_heads, int head_dim) {
+    g_error.clear();
+    if (!valid_geometry(q_heads, kv_heads, head_dim) || queries < 1 || prior < 0 ||
+        (int64_t)queries + prior > INT32_MAX - 64)
+        return fail("prefill split query needs a valid geometry, queries >= 1 and prior >= 0");
+    mslim::PrefillLaunch l{};
+    l.queries = queries; l.prior = prior; l.q_heads = q_heads; l.kv_heads = kv_heads; l.head_dim = head_dim;
+    l.split_allowed = true;
+    return mslim::prefill_split_plan(l).chunk_tiles;
+}
+
 int mslim_attn_prefill_causal(void *ctx, const void *q, const void *k, const void *v, void *out,
                               int queries, int prior, int q_heads, int kv_heads, int head_dim,
                               float scale) {
@@ -512,8 +535,32 @@ int mslim_attn_prefill_causal(void *ctx, const void *q, const void *k, const voi
     l.out = static_cast<uint16_t *>(out);
     l.queries = queries; l.prior = prior; l.q_heads = q_heads; l.kv_heads = kv_heads;
     l.head_dim = head_dim; l.scale = scale;
-    if (int rc = check_hip(mslim::launch_prefill(l, c.stream), "prefill attention launch")) return rc;
-    return 0;
+    l.split_allowed = c.prefill_split;
+    const mslim::PrefillSplit plan = mslim::prefill_split_plan(l);
+    if (plan.chunk_tiles) {
+        if (int rc = grow_device(c, &c.prefill_partial, &c.prefill_partial_bytes, plan.partial_bytes,
+                                 "hipMalloc prefill split partials"))
+            return rc;
+        const size_t ctr_bytes = (size_t)plan.counters * sizeof(int);
+        if (c.prefill_counter_bytes < ctr_bytes) {
+            if (int rc = grow_device(c, &c.prefill_counters, &c.prefill_counter_bytes, ctr_bytes,
+                                     "hipMalloc prefill split counters"))
+                return rc;
+            c.prefill_counters_dirty = true;
+        }
+        if (c.prefill_counters_dirty) {
+            if (int rc = check_hip(mslim::launch_zero_i32(static_cast<int *>(c.prefill_counters),
+                                                          (int)(c.prefill_counter_bytes / sizeof(int)), c.stream),
+                                   "clear prefill split counters"))
+                return rc;
+            c.prefill_counters_dirty = false;
+        }
+        l.partial = static_cast<float *>(c.prefill_partial);
+        l.counters = static_cast<int *>(c.prefill_counters);
+    }
+    const int rc = check_hip(mslim::launch_prefill(l, c.stream), "prefill attention launch");
+    if (rc && plan.chunk_tiles) c.prefill_counters_dirty = true;
+    return rc;
 }
 
 int mslim_attn_frames_decode(void *ctx, const float *query, const void *keys, int key_format,
@@ -888,7 +935,60 @@ int mslim_attn_record_frames(void *ctx, const void *k_pool, const void *v_pool, 
     l.count = count;
     l.frames = frames;
     l.frame_bytes = mslim::record_frame_bytes(page_tokens);
+    l.staged = false;
     return check_hip(mslim::launch_record_frames(l, c.stream), "record frame launch");
+}
+
+int mslim_attn_record_frames_staged(void *ctx, const void *k_stage, const void *v_stage, int page_tokens,
+                                    int kv_heads, int head_dim, uint32_t tile,
+                                    const mslim_attn_page_record *records, int count, void *frames) {
+    g_error.clear();
+    if (!ctx || !k_stage || !v_stage || !records || !frames || count < 0)
+        return fail("invalid staged record frame arguments");
+    if (!is_pow2(page_tokens) || page_tokens > 512 || kv_heads < 1 || head_dim < 8 || head_dim % 8)
+        return fail("record frames need page_tokens a power of two <= 512, kv_heads >= 1 and "
+                    "head_dim a multiple of 8");
+    if (tile == 0 || (uint32_t)head_dim % tile) return fail("head_dim is not a multiple of tile");
+    if ((uintptr_t)k_stage % 16 || (uintptr_t)v_stage % 16 || (uintptr_t)frames % 8)
+        return fail("record frames need 16-byte aligned staging and an 8-byte aligned frame buffer");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    mslim::FramesCodecLaunch l;
+    l.k_pool = k_stage;
+    l.v_pool = v_stage;
+    l.pool_pages = count;
+    l.page_tokens = page_tokens;
+    l.kv_heads = kv_heads;
+    l.head_dim = head_dim;
+    l.tile = tile;
+    l.records = reinterpret_cast<const mslim::RecordDesc *>(records);
+    l.count = count;
+    l.frames = frames;
+    l.frame_bytes = mslim::record_frame_bytes(page_tokens);
+    l.staged = true;
+    return check_hip(mslim::launch_record_frames(l, c.stream), "staged record frame launch");
+}
+
+void *mslim_attn_host_alloc(void *ctx, size_t bytes) {
+    g_error.clear();
+    if (!ctx || !bytes) {
+        g_error = "invalid pinned host allocation";
+        return nullptr;
+    }
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    void *p = nullptr;
+    if (check_hip(hipHostMalloc(&p, bytes, hipHostMallocDefault), "hipHostMalloc staging")) return nullptr;
+    return p;
+}
+
+int mslim_attn_host_free(void *ctx, void *host) {
+    g_error.clear();
+    if (!ctx || !host) return fail("invalid pinned host buffer");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    if (int rc = check_hip(hipStreamSynchronize(c.stream), "hipStreamSynchronize before host free")) return rc;
+    return check_hip(hipHostFree(host), "hipHostFree staging");
 }
 
 int mslim_attn_record_payloads(void *ctx, void *k_pool, void *v_pool, int64_t pool_pages, int page_tokens,

@@ -11,6 +11,13 @@
 // or compares a stored record's frame with a recomputed one (verified
 // restore).  Every value is byte-identical to the host codec.
 //
+// A record's tokens are rows first_row .. first_row + tokens - 1 of its pool
+// page (a record can start inside a page when a turn ended there).  In staged
+// mode the payloads are read instead from compacted staging slots (slot i of
+// k_pool / v_pool holds record i as [heads][tokens][row], the layout
+// record_payloads writes), so a stored record can be verified before any of
+// its bytes reach the pool.
+//
 // Two launches:
 //   * token_hashes_kernel: one lane per (record, K/V, token) computes the
 //     FNV-1a-64 of that token's bytes over all heads (cold_store.rs:725-742).
@@ -53,8 +60,30 @@ __device__ __forceinline__ uint64_t fnv_chunk(uint64_t s, const u32x4_t &c) {
 }
 
 __device__ __forceinline__ bool record_valid(const RecordDesc &r, int page_tokens, int64_t pool_pages) {
-    return r.tokens >= 1 && r.tokens <= (uint32_t)page_tokens && r.pool_page >= 0 &&
+    return r.tokens >= 1 && (uint64_t)r.first_row + r.tokens <= (uint64_t)page_tokens && r.pool_page >= 0 &&
            (int64_t)r.pool_page < pool_pages;
+}
+
+// A record the frame kernels can read: in staged mode its pool page and
+// first row are not used.
+__device__ __forceinline__ bool record_ok(const FramesCodecLaunch &a, const RecordDesc &r) {
+    if (a.staged) return r.tokens >= 1 && r.tokens <= (uint32_t)a.page_tokens;
+    return record_valid(r, a.page_tokens, a.pool_pages);
+}
+
+// Row 0 of head 0 of record `rec`'s payload and the byte distance between
+// heads: inside its pool page, or in its compacted staging slot.
+struct PayloadAt {
+    const unsigned char *base;
+    int64_t head_stride;
+};
+__device__ __forceinline__ PayloadAt payload_at(const FramesCodecLaunch &a, const void *src, const RecordDesc &r,
+                                                int rec, int row_bytes) {
+    const int64_t page_bytes = (int64_t)a.kv_heads * a.page_tokens * row_bytes;
+    const unsigned char *s = static_cast<const unsigned char *>(src);
+    if (a.staged) return {s + (int64_t)rec * page_bytes, (int64_t)r.tokens * row_bytes};
+    return {s + (int64_t)r.pool_page * page_bytes + (int64_t)r.first_row * row_bytes,
+            (int64_t)a.page_tokens * row_bytes};
 }
 
 // Iterates the 16-byte chunks of one token's bytes over all heads (or of a
@@ -101,16 +130,14 @@ __global__ __launch_bounds__(256) void token_hashes_kernel(FramesCodecLaunch a) 
     const int part = rem / a.page_tokens;  // 0 = K, 1 = V
     const int token = rem - part * a.page_tokens;
     const RecordDesc r = a.records[rec];
-    if (!record_valid(r, a.page_tokens, a.pool_pages) || token >= (int)r.tokens) return;
+    if (!record_ok(a, r) || token >= (int)r.tokens) return;
 
     const int row_bytes = a.head_dim * 2;
-    const int64_t page_bytes = (int64_t)a.kv_heads * a.page_tokens * row_bytes;
-    const unsigned char *page =
-        static_cast<const unsigned char *>(part ? a.v_pool : a.k_pool) + (int64_t)r.pool_page * page_bytes;
+    const PayloadAt at = payload_at(a, part ? a.v_pool : a.k_pool, r, rec, row_bytes);
     ChunkWalk w;
-    w.head_base = page + (int64_t)token * row_bytes;
+    w.head_base = at.base + (int64_t)token * row_bytes;
     w.row = w.head_base;
-    w.head_stride = (int64_t)a.page_tokens * row_bytes;
+    w.head_stride = at.head_stride;
     w.row_bytes = row_bytes;
     w.col = 0;
     w.rows_left = 0;
@@ -309,25 +336,27 @@ __global__ __launch_bounds__(2 * kFrameThreads) void frame_kernel(FramesCodecLau
     const bool live = rec < a.count;
     RecordDesc r = {};
     if (live) r = a.records[rec];
-    const bool valid = live && record_valid(r, a.page_tokens, a.pool_pages);
+    const bool valid = live && record_ok(a, r);
     uint32_t *frame_words = reinterpret_cast<uint32_t *>(static_cast<unsigned char *>(a.frames) +
                                                          (int64_t)(live ? rec : 0) * a.frame_bytes);
     const int frame_words_n = (int)(a.frame_bytes / 4);
     const int tokens = valid ? (int)r.tokens : 0;
     const int row_bytes = a.head_dim * 2;
-    const int64_t page_bytes = (int64_t)a.kv_heads * a.page_tokens * row_bytes;
     const int64_t payload_len = (int64_t)a.kv_heads * tokens * row_bytes;
     const int64_t payload_chunks = payload_len / 16;
-    const int64_t pool_page = valid ? r.pool_page : 0;
-    const unsigned char *kpage = static_cast<const unsigned char *>(a.k_pool) + pool_page * page_bytes;
-    const unsigned char *vpage = static_cast<const unsigned char *>(a.v_pool) + pool_page * page_bytes;
+    RecordDesc rv = r;
+    if (!valid) rv = RecordDesc{0, 0, 0, 1, 0, 0};
+    const PayloadAt kat = payload_at(a, a.k_pool, rv, valid ? rec : 0, row_bytes);
+    const PayloadAt vat = payload_at(a, a.v_pool, rv, valid ? rec : 0, row_bytes);
+    const unsigned char *kpage = kat.base;
+    const unsigned char *vpage = vat.base;
 
-    // Head-major payload of `tokens` rows per head inside a pool page.
+    // Head-major payload of `tokens` rows per head.
     auto payload_walk = [&](const unsigned char *page) __attribute__((always_inline)) {
         ChunkWalk w;
         w.head_base = page;
         w.row = page;
-        w.head_stride = (int64_t)a.page_tokens * row_bytes;
+        w.head_stride = kat.head_stride;
         w.row_bytes = row_bytes;
         w.col = 0;
         w.rows_left = tokens - 1;
@@ -466,10 +495,11 @@ __global__ __launch_bounds__(256) void record_payloads_kernel(PayloadMoveLaunch 
     const RecordDesc r = a.records[rec];
     if (!record_valid(r, a.page_tokens, a.pool_pages)) return;
     const int col = (int)(c % cpr);
-    const int64_t hr = c / cpr;  // head * page_tokens + row
-    const int row = (int)(hr % a.page_tokens);
+    const int64_t hr = c / cpr;  // head * page_tokens + row of the pool page
+    const int page_row = (int)(hr % a.page_tokens);
     const int head = (int)(hr / a.page_tokens);
-    if (row >= (int)r.tokens) return;
+    const int row = page_row - (int)r.first_row;  // row of the record
+    if (row < 0 || row >= (int)r.tokens) return;
     const int64_t page_bytes = per_page * 16;
     const int64_t pool_off = (int64_t)r.pool_page * page_bytes + c * 16;
     const int64_t stage_off = (int64_t)rec * page_bytes + (((int64_t)head * r.tokens + row) * cpr + col) * 16;

@@ -64,8 +64,17 @@ struct PrefillLaunch {
     uint16_t *out;
     int queries, prior, q_heads, kv_heads, head_dim;
     float scale;
+    bool split_allowed;  // chunk long row blocks when the launch is small
+    float *partial;      // split workspace of prefill_split_plan().partial_bytes
+    int *counters;       // prefill_split_plan().counters ints, zero between launches
 };
 bool prefill_fast_path(int head_dim, int group);
+// How a launch splits its row blocks: chunk_tiles == 0 means no split.
+struct PrefillSplit {
+    int chunk_tiles = 0, max_chunks = 1, items = 0, counters = 0;
+    size_t partial_bytes = 0;
+};
+PrefillSplit prefill_split_plan(const PrefillLaunch &l);
 hipError_t launch_prefill(const PrefillLaunch &a, hipStream_t stream);
 
 // Portable-backend decode: f32 query, raw K/V frames, f32 output.
@@ -124,7 +133,7 @@ struct RecordDesc {                      // layout of mslim_attn_page_record
     uint32_t layer;
     uint32_t tokens;
     int32_t pool_page;
-    uint32_t reserved;
+    uint32_t first_row;                  // pool-page row of the record's first token
 };
 static_assert(sizeof(RecordDesc) == 32, "RecordDesc must match mslim_attn_page_record");
 struct FramesCodecLaunch {
@@ -136,6 +145,7 @@ struct FramesCodecLaunch {
     int count;
     void *frames;
     int64_t frame_bytes;
+    bool staged;  // payloads in compacted staging slots instead of pool pages
 };
 int64_t record_frame_bytes(int page_tokens);
 hipError_t launch_record_frames(const FramesCodecLaunch &a, hipStream_t stream);

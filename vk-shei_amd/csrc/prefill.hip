@@ -25,8 +25,18 @@
 //     units (exact: the final O / l uses the same stale maximum), row sums
 //     use v_dot2 on the BF16 P that feeds the MFMA;
 //   * workgroups are mapped so that each XCD works through whole kv heads,
-//     longest row blocks first, keeping those heads' K/V resident in its L2.
+//     longest row blocks first, keeping those heads' K/V resident in its L2;
+//   * a launch too small to keep every CU busy for the length of its longest
+//     row block (cfg2's 2,048 tokens: 256 workgroups of 1 to 32 key tiles;
+//     the decoder's 512-token prompt chunks: 64 workgroups) splits long row
+//     blocks into chunks of key tiles and dispatches all chunks longest
+//     first.  Chunks are counted back from the causal diagonal, so every
+//     chunk but the last sees only unmasked keys; the last workgroup of a
+//     split row block to finish merges the chunks' (m, l, O) partials in
+//     fixed chunk order, so the result does not depend on timing.
+#include <algorithm>
 #include <type_traits>
+#include <vector>
 
 #include "common.hpp"
 #include "kernels.hpp"
@@ -35,15 +45,29 @@ namespace mslim {
 
 namespace {
 
+// Split-mode work items in the kernel arguments: row block | chunk << 10 |
+// head group << 16, longest first; at most kMaxChunks chunks per row block.
+constexpr int kMaxSplitItems = 768;
+constexpr int kMaxChunks = 8;
+constexpr uint32_t kNoItem = 0xFFFFFFFFu;  // padding slot of the item table
+
 struct PrefillArgs {
     const uint16_t *q, *k, *v;
     uint16_t *out;
     int queries, prior, history;
     int q_heads, kv_heads;
     float scale_log2e;
+    // chunk_tiles > 0: split mode.  partial holds [row block key][max_chunks]
+    // [wave][MT * 8 + 1][64] float pairs (O, then (m, l)), counters one int
+    // per row block key (kv head group x row blocks), zero between launches.
+    int chunk_tiles, max_chunks, items;
+    float *partial;
+    int *counters;
+    uint32_t item[kMaxSplitItems];
 };
 
 constexpr int kBN = 64;          // keys per LDS tile
+constexpr int kCus = 256;        // MI355X compute units
 constexpr int kXcds = 8;         // MI355X accelerator complex dies
 constexpr float kLazyLog2 = 8.0f;  // rescale O only past 2^8 growth
 
@@ -112,16 +136,27 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
     const int group = a.q_heads / a.kv_heads;
     const int subgroups = group / HW;
     const int nrb = (a.queries + RW - 1) / RW;
-    const int total = nrb * a.kv_heads * subgroups;
-    const int per_xcd = (total + kXcds - 1) / kXcds;
-    const int item = (int)(blockIdx.x % kXcds) * per_xcd + (int)(blockIdx.x / kXcds);
-    if (item >= total) return;
-    const int per_head = nrb * subgroups;
-    const int kvh = item / per_head;
-    const int rank = (item % per_head) / subgroups;
-    const int sub = item % subgroups;
+    int kvh, sub, rb, chunk = 0;
+    if (a.chunk_tiles) {
+        if ((int)blockIdx.x >= a.items || a.item[blockIdx.x] == kNoItem) return;
+        const uint32_t u = a.item[blockIdx.x];
+        rb = (int)(u & 1023u);
+        chunk = (int)((u >> 10) & 63u);
+        const int hg = (int)(u >> 16);
+        kvh = hg / subgroups;
+        sub = hg % subgroups;
+    } else {
+        const int total = nrb * a.kv_heads * subgroups;
+        const int per_xcd = (total + kXcds - 1) / kXcds;
+        const int item = (int)(blockIdx.x % kXcds) * per_xcd + (int)(blockIdx.x / kXcds);
+        if (item >= total) return;
+        const int per_head = nrb * subgroups;
+        kvh = item / per_head;
+        rb = nrb - 1 - (item % per_head) / subgroups;
+        sub = item % subgroups;
+    }
     const int head = kvh * group + sub * HW + wave % HW;
-    const int r0 = (nrb - 1 - rank) * RW;
+    const int r0 = rb * RW;
     const int rw0 = r0 + (wave / HW) * 32;
     const int row = rw0 + col;
     const int row_abs = a.prior + row;
@@ -141,6 +176,15 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
     const int key_end = min(a.history, a.prior + r0 + RW);
     const int nkt = (key_end + kBN - 1) / kBN;
     const int last_key = a.history - 1;
+    // Tiles [tb, te) of this workgroup: chunk c of nchunks, counted back from
+    // the last tile (chunk 0 takes the remainder).
+    int nchunks = 1, tb = 0, te = nkt;
+    if (a.chunk_tiles) {
+        nchunks = (nkt + a.chunk_tiles - 1) / a.chunk_tiles;
+        te = nkt - (nchunks - 1 - chunk) * a.chunk_tiles;
+        tb = max(0, te - a.chunk_tiles);
+    }
+    const int ntl = te - tb;
 
     // Copy of one K/V tile: wavefront w moves chunks w, w+8, ...; lane l of
     // chunk ch lands at row RPC*ch + l/NSLOT, physical slot l % NSLOT and
@@ -301,6 +345,7 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
     // wavefront's rows are computed too: their scores are all masked, so
     // they add exactly zero.  Every iteration issues one copy batch (the
     // last tile is repeated past the end) so the wait below is exact.
+    // j counts this workgroup's tiles from 0; its key tile is tb + j.
     auto iteration = [&](int j, const uint16_t *kc, const uint16_t *vp, uint16_t *kd, uint16_t *vd)
         __attribute__((always_inline)) {
         // This wavefront's copy of tile j has landed (that of tile j+1 may
@@ -308,10 +353,10 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
         // every wavefront is past iteration j-1, which freed stage j-2.
         __builtin_amdgcn_s_waitcnt(vmcnt_lds_imm(2 * CPW));
         raw_barrier();
-        dma_tile(kd, vd, min(j + 2, nkt - 1));
+        dma_tile(kd, vd, tb + min(j + 2, ntl - 1));
         apply_rescale();
         qk(kc);
-        if (j * kBN + kBN - 1 > a.prior + rw0) mask_tile(j);
+        if ((tb + j) * kBN + kBN - 1 > a.prior + rw0) mask_tile(tb + j);
         pv_softmax(vp, Yes{}, Yes{});
     };
 
@@ -319,27 +364,27 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
     // end), tile 0 scored and turned into P.  Stage i holds tile j with
     // j % 4 == i; the loop is unrolled by four so every stage is a distinct
     // LDS object.
-    dma_tile(k0, v0, 0);
-    dma_tile(k1, v1, min(1, nkt - 1));
-    dma_tile(k2, v2, min(2, nkt - 1));
+    dma_tile(k0, v0, tb);
+    dma_tile(k1, v1, tb + min(1, ntl - 1));
+    dma_tile(k2, v2, tb + min(2, ntl - 1));
     __builtin_amdgcn_s_waitcnt(vmcnt_lds_imm(2 * 2 * CPW));
     raw_barrier();
     qk(k0);
-    if (kBN - 1 > a.prior + rw0) mask_tile(0);
+    if (tb * kBN + kBN - 1 > a.prior + rw0) mask_tile(tb);
     pv_softmax(v0, No{}, Yes{});
-    for (int j = 1; j < nkt; j += ST) {
+    for (int j = 1; j < ntl; j += ST) {
         iteration(j, k1, v0, k3, v3);
-        if (j + 1 >= nkt) break;
+        if (j + 1 >= ntl) break;
         iteration(j + 1, k2, v1, k0, v0);
-        if (j + 2 >= nkt) break;
+        if (j + 2 >= ntl) break;
         iteration(j + 2, k3, v2, k1, v1);
-        if (j + 3 >= nkt) break;
+        if (j + 3 >= ntl) break;
         iteration(j + 3, k0, v3, k2, v2);
     }
     // P.V of the last tile, from the stage that holds it.
     __builtin_amdgcn_s_waitcnt(vmcnt_lds_imm(0));
     apply_rescale();
-    const int last_stage = (nkt - 1) % ST;
+    const int last_stage = (ntl - 1) % ST;
     if (last_stage == 0) pv_softmax(v0, Yes{}, No{});
     else if (last_stage == 1) pv_softmax(v1, Yes{}, No{});
     else if (last_stage == 2) pv_softmax(v2, Yes{}, No{});
@@ -347,7 +392,8 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // no DMA may still target LDS at exit
 
     const float l = l_run + __shfl_xor(l_run, 32, 64);
-    if (row < a.queries) {
+    auto write_out = [&](const floatx16_t *acc, float lsum) __attribute__((always_inline)) {
+        if (row >= a.queries) return;
         uint16_t *op = a.out + ((int64_t)row * a.q_heads + head) * D;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
@@ -355,11 +401,106 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
             for (int r4 = 0; r4 < 4; ++r4) {
                 const int d = mt * 32 + r4 * 8 + half * 4;
                 uint2 w;
-                w.x = pack_bf16x2(o[mt][r4 * 4 + 0] / l, o[mt][r4 * 4 + 1] / l);
-                w.y = pack_bf16x2(o[mt][r4 * 4 + 2] / l, o[mt][r4 * 4 + 3] / l);
+                w.x = pack_bf16x2(acc[mt][r4 * 4 + 0] / lsum, acc[mt][r4 * 4 + 1] / lsum);
+                w.y = pack_bf16x2(acc[mt][r4 * 4 + 2] / lsum, acc[mt][r4 * 4 + 3] / lsum);
                 *reinterpret_cast<uint2 *>(op + d) = w;
             }
+    };
+    if (nchunks == 1) {
+        write_out(o, l);
+        return;
     }
+
+    // Split row block: publish this chunk's partial as float pairs in
+    // [pair][lane] order (O, then (m, l)), so every store and load covers a
+    // contiguous 512-byte run.  The stores are agent-scope atomic pairs
+    // (written through to the device coherence point), each thread waits for
+    // its own, and only then does thread 0 count the chunk; the merging
+    // workgroup reads the others with agent-scope atomic loads (the decode
+    // merge's ordering).
+    constexpr int PAIRS = MT * 8 + 1;
+    const int rbk = (kvh * subgroups + sub) * nrb + rb;
+    auto chunk_base = [&](int ch) __attribute__((always_inline)) {
+        return a.partial + ((((int64_t)rbk * a.max_chunks + ch) * WAVES + wave) * PAIRS * 64 + lane) * 2;
+    };
+    auto put2 = [](float *p, float x, float y) __attribute__((always_inline)) {
+        const uint64_t w = (uint64_t)__float_as_uint(x) | ((uint64_t)__float_as_uint(y) << 32);
+        __hip_atomic_store(reinterpret_cast<uint64_t *>(p), w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+    auto get2 = [](const float *p) __attribute__((always_inline)) {
+        const uint64_t w = __hip_atomic_load(reinterpret_cast<const uint64_t *>(p), __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+        return make_float2(__uint_as_float((uint32_t)w), __uint_as_float((uint32_t)(w >> 32)));
+    };
+    {
+        float *mine = chunk_base(chunk);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) put2(mine + (mt * 8 + r / 2) * 128, o[mt][r], o[mt][r + 1]);
+        put2(mine + (MT * 8) * 128, m_used, l);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __shared__ int last;
+    __syncthreads();
+    if (tid == 0) {
+        int *ctr = a.counters + rbk;
+        const int done = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = done == nchunks - 1;
+        if (last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!last) return;
+    // Merge in chunk order: M = the largest chunk maximum, then
+    // O = sum_c O_c 2^((m_c - M) c) and l likewise, chunk 0 first; this
+    // workgroup's own chunk enters from registers at its place in the order.
+    // M first (one batch of (m, l) loads), then the sums in chunk order; each
+    // other chunk's partial is loaded in two batches (round trips of uncached
+    // loads) and folded in.
+    float2 ml[kMaxChunks];
+#pragma unroll
+    for (int ch = 0; ch < kMaxChunks; ++ch)
+        if (ch < nchunks) ml[ch] = ch == chunk ? make_float2(m_used, l) : get2(chunk_base(ch) + (MT * 8) * 128);
+    float mmax = m_used, lsum = 0.0f;
+#pragma unroll
+    for (int ch = 0; ch < kMaxChunks; ++ch)
+        if (ch < nchunks) mmax = fmaxf(mmax, ml[ch].x);
+#pragma unroll
+    for (int ch = 0; ch < kMaxChunks; ++ch)
+        if (ch < nchunks) lsum = fmaf(ml[ch].y, __builtin_amdgcn_exp2f((ml[ch].x - mmax) * c), lsum);
+    floatx16_t acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[mt][r] = 0.0f;
+#pragma unroll 1
+    for (int ch = 0; ch < nchunks; ++ch) {
+        if (ch == chunk) {
+            const float w = __builtin_amdgcn_exp2f((m_used - mmax) * c);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[mt][r] = fmaf(o[mt][r], w, acc[mt][r]);
+            continue;
+        }
+        const float *theirs = chunk_base(ch);
+        const float w = __builtin_amdgcn_exp2f((get2(theirs + (MT * 8) * 128).x - mmax) * c);
+        constexpr int HM = MT > 1 ? MT / 2 : 1;
+#pragma unroll
+        for (int m0 = 0; m0 < MT; m0 += HM) {
+            float2 x[HM * 8];
+#pragma unroll
+            for (int e = 0; e < HM * 8; ++e) x[e] = get2(theirs + (m0 * 8 + e) * 128);
+#pragma unroll
+            for (int mh = 0; mh < HM; ++mh)
+#pragma unroll
+                for (int r = 0; r < 8; ++r) {
+                    acc[m0 + mh][2 * r] = fmaf(x[mh * 8 + r].x, w, acc[m0 + mh][2 * r]);
+                    acc[m0 + mh][2 * r + 1] = fmaf(x[mh * 8 + r].y, w, acc[m0 + mh][2 * r + 1]);
+                }
+        }
+    }
+    write_out(acc, lsum);
 }
 
 // Any-geometry fallback: one wavefront per (query row, head), 64-key tiles.
@@ -418,14 +559,68 @@ hipError_t launch_mfma(const PrefillArgs &a, hipStream_t stream) {
     const int group = a.q_heads / a.kv_heads;
     const int total = ((a.queries + RW - 1) / RW) * a.kv_heads * (group / HW);
     const int per_xcd = (total + kXcds - 1) / kXcds;
-    hipLaunchKernelGGL((prefill_mfma_kernel<D, HW>), dim3((unsigned)(per_xcd * kXcds)), dim3(512), 0, stream, a);
+    const unsigned grid = a.chunk_tiles ? (unsigned)a.items : (unsigned)(per_xcd * kXcds);
+    hipLaunchKernelGGL((prefill_mfma_kernel<D, HW>), dim3(grid), dim3(512), 0, stream, a);
     return hipGetLastError();
+}
+
+// Heads per workgroup: the largest of 8, 4, 2, 1 that divides the group.
+int heads_per_workgroup(int group) { return group % 8 == 0 ? 8 : group % 4 == 0 ? 4 : group; }
+
+// Key tiles of row block rb.
+int row_block_tiles(const PrefillLaunch &l, int rows_per_block, int rb) {
+    const int key_end = std::min(l.prior + l.queries, l.prior + (rb + 1) * rows_per_block);
+    return (key_end + kBN - 1) / kBN;
 }
 
 }  // namespace
 
 bool prefill_fast_path(int head_dim, int group) {
     return (head_dim == 64 || head_dim == 128) && (group == 1 || group == 2 || group % 4 == 0);
+}
+
+PrefillSplit prefill_split_plan(const PrefillLaunch &l) {
+    PrefillSplit p;
+    const int group = l.q_heads / l.kv_heads;
+    if (!l.split_allowed || !prefill_fast_path(l.head_dim, group)) return p;
+    const int hw = heads_per_workgroup(group);
+    const int rows = 32 * (8 / hw);
+    const int nrb = (l.queries + rows - 1) / rows;
+    const int groups = l.kv_heads * (group / hw);
+    if (nrb > 1024 || groups > 65535) return p;
+    int64_t work = 0;
+    int longest = 0;
+    for (int rb = 0; rb < nrb; ++rb) {
+        const int t = row_block_tiles(l, rows, rb);
+        work += t;
+        longest = std::max(longest, t);
+    }
+    work *= groups;
+    // One workgroup per CU (128 KiB of LDS each): a launch is balanced when
+    // its longest workgroup is close to the mean work per CU.
+    const int64_t target = (work + kCus - 1) / kCus;
+    // Every chunk but the last must end below the diagonal of its row block,
+    // whose rows span rows / 64 + 1 key tiles; a chunk also costs a prologue
+    // of three tile copies, so chunks are at least 4 tiles.
+    const int min_chunk = std::max(4, rows / kBN + 2);
+    if (longest <= target + target / 4 || longest <= min_chunk) return p;
+    int tc = (int)std::max<int64_t>(target, min_chunk);
+    for (;; ++tc) {
+        int64_t items = 0;
+        for (int rb = 0; rb < nrb; ++rb) items += (row_block_tiles(l, rows, rb) + tc - 1) / tc;
+        items *= groups;
+        if (items <= kMaxSplitItems && (longest + tc - 1) / tc <= kMaxChunks) {
+            p.items = (int)items;
+            break;
+        }
+    }
+    if (tc >= longest) return PrefillSplit{};
+    p.chunk_tiles = tc;
+    p.max_chunks = (longest + tc - 1) / tc;
+    p.counters = groups * nrb;
+    const int pairs = (l.head_dim / 32) * 8 + 1;
+    p.partial_bytes = (size_t)groups * nrb * p.max_chunks * 8 * pairs * 64 * 2 * sizeof(float);
+    return p;
 }
 
 hipError_t launch_prefill(const PrefillLaunch &l, hipStream_t stream) {
@@ -440,8 +635,60 @@ hipError_t launch_prefill(const PrefillLaunch &l, hipStream_t stream) {
                            stream, a, l.head_dim);
         return hipGetLastError();
     }
-    // Heads per workgroup: the largest of 8, 4, 2, 1 that divides the group.
-    const int hw = group % 8 == 0 ? 8 : group % 4 == 0 ? 4 : group;
+    const int hw = heads_per_workgroup(group);
+    const PrefillSplit plan = prefill_split_plan(l);
+    if (plan.chunk_tiles) {
+        if (!l.partial || !l.counters) return hipErrorInvalidValue;
+        // Items (row block, chunk, head group), longest first; the chunks of
+        // a row block are counted back from its last tile, chunk 0 taking the
+        // remainder (the kernel recomputes the same ranges).
+        const int rows = 32 * (8 / hw);
+        const int nrb = (l.queries + rows - 1) / rows;
+        const int groups = l.kv_heads * (group / hw);
+        //
+        // Workgroup L runs on XCD L % 8.  When the kv heads split evenly over
+        // the XCDs, each XCD gets the items of its own kv heads, longest
+        // first, so its L2 holds few heads' K/V (as the unsplit mapping
+        // does); otherwise one longest-first list is dealt round-robin.
+        std::vector<std::vector<std::pair<int, uint32_t>>> buckets(kXcds);
+        const bool by_head = l.kv_heads % kXcds == 0;
+        for (int hg = 0; hg < groups; ++hg)
+            for (int rb = nrb - 1; rb >= 0; --rb) {
+                const int nkt = row_block_tiles(l, rows, rb);
+                const int nc = (nkt + plan.chunk_tiles - 1) / plan.chunk_tiles;
+                for (int c = 0; c < nc; ++c) {
+                    const int size = c ? plan.chunk_tiles : nkt - (nc - 1) * plan.chunk_tiles;
+                    const int kvh = hg / (group / hw);
+                    buckets[by_head ? (kvh / (l.kv_heads / kXcds)) % kXcds : 0].push_back(
+                        {size, (uint32_t)rb | ((uint32_t)c << 10) | ((uint32_t)hg << 16)});
+                }
+            }
+        auto longest_first = [](const std::pair<int, uint32_t> &x, const std::pair<int, uint32_t> &y) {
+            return x.first > y.first;
+        };
+        size_t slots = 0;
+        if (by_head) {
+            size_t most = 0;
+            for (auto &b : buckets) {
+                std::stable_sort(b.begin(), b.end(), longest_first);
+                most = std::max(most, b.size());
+            }
+            slots = most * kXcds;
+            if (slots > (size_t)kMaxSplitItems) return hipErrorInvalidValue;
+            for (size_t j = 0; j < most; ++j)
+                for (int x = 0; x < kXcds; ++x)
+                    a.item[j * kXcds + x] = j < buckets[x].size() ? buckets[x][j].second : kNoItem;
+        } else {
+            std::stable_sort(buckets[0].begin(), buckets[0].end(), longest_first);
+            slots = buckets[0].size();
+            for (size_t i = 0; i < slots; ++i) a.item[i] = buckets[0][i].second;
+        }
+        a.chunk_tiles = plan.chunk_tiles;
+        a.max_chunks = plan.max_chunks;
+        a.items = (int)slots;
+        a.partial = l.partial;
+        a.counters = l.counters;
+    }
     if (l.head_dim == 128) {
         if (hw == 8) return launch_mfma<128, 8>(a, stream);
         if (hw == 4) return launch_mfma<128, 4>(a, stream);

@@ -1,6 +1,7 @@
 // Decoder runner over the C ABI: see model.hpp for the layer order.
 #include "model.hpp"
 
+#include <chrono>
 #include <climits>
 #include <cmath>
 #include <cstring>
@@ -54,9 +55,15 @@ DecoderRunner::DecoderRunner(std::shared_ptr<NativeContext> ctx, ModelSpec spec,
     const size_t kvd = (size_t)spec_.kv_heads * spec_.head_dim, qd = (size_t)spec_.q_heads * spec_.head_dim;
     const size_t pool_pages = (size_t)max_batch_ * pages_per_seq_;
     try {
+        // One allocation for every layer's K pages and one for V: layer l's
+        // pool is pages [l * pool_pages, (l + 1) * pool_pages), so the
+        // ColdStore seal and restore of a slot cover all layers per launch.
+        const size_t layer_bytes = pool_pages * page_tokens_ * kvd * 2;
+        k_base_ = alloc(layer_bytes * spec_.layers);
+        v_base_ = alloc(layer_bytes * spec_.layers);
         for (int l = 0; l < spec_.layers; ++l) {
-            k_pools_.push_back(alloc(pool_pages * page_tokens_ * kvd * 2));
-            v_pools_.push_back(alloc(pool_pages * page_tokens_ * kvd * 2));
+            k_pools_.push_back(static_cast<char *>(k_base_) + layer_bytes * l);
+            v_pools_.push_back(static_cast<char *>(v_base_) + layer_bytes * l);
         }
         // Paged: slot s, logical page p -> physical page p * max_batch + s, so
         // the slots interleave in the pool and every read goes through the
@@ -66,6 +73,7 @@ DecoderRunner::DecoderRunner(std::shared_ptr<NativeContext> ctx, ModelSpec spec,
             for (int p = 0; p < pages_per_seq_; ++p)
                 table[(size_t)s * pages_per_seq_ + p] =
                     (int32_t)(layout_ == KvLayout::Dense ? (size_t)s * pages_per_seq_ + p : (size_t)p * max_batch_ + s);
+        host_table_ = table;
         table_ = static_cast<int32_t *>(alloc(table.size() * 4));
         ctx_->check("upload page table", mslim_attn_buf_write(ctx_->handle(), table_, 0,
                                                               reinterpret_cast<const uint8_t *>(table.data()),
@@ -88,6 +96,8 @@ DecoderRunner::DecoderRunner(std::shared_ptr<NativeContext> ctx, ModelSpec spec,
             vd_ = static_cast<uint16_t *>(alloc((size_t)max_context_ * kvd * 2));
         }
         logits_ = static_cast<uint16_t *>(alloc((size_t)max_batch_ * spec_.vocab * 2));
+        cold_.resize(max_batch_);
+        cold_report_.assign(max_batch_, ColdReport{});
     } catch (...) {
         for (void *p : owned_) mslim_attn_buf_free(ctx_->handle(), p);
         throw;
@@ -95,6 +105,8 @@ DecoderRunner::DecoderRunner(std::shared_ptr<NativeContext> ctx, ModelSpec spec,
 }
 
 DecoderRunner::~DecoderRunner() {
+    cold_.clear();
+    staging_.reset();
     for (void *p : owned_) mslim_attn_buf_free(ctx_->handle(), p);
 }
 
@@ -178,18 +190,32 @@ Step DecoderRunner::prefill_only(int seq, const std::vector<int32_t> &prompt) {
     ensure(!prompt.empty(), "GPU prompt IDs empty");
     ensure(prompt.size() < (size_t)max_context_, "GPU context capacity not large enough for prompt");
     for (int32_t id : prompt) ensure(id >= 0 && id < spec_.vocab, "token id outside the vocabulary");
-    std::lock_guard<std::mutex> lock(ctx_->mutex());
-    positions_[seq] = 0;
-    const int n_total = (int)prompt.size();
-    for (int start = 0; start < n_total; start += chunk_tokens_) {
-        const int n = std::min(chunk_tokens_, n_total - start);
-        chunk(seq, prompt.data() + start, n, start);
-        if (start + n == n_total) head(x_ + (size_t)(n - 1) * spec_.hidden, 1);
-    }
-    positions_[seq] = n_total;
+    if (cold_[seq])
+        ensure(cold_report_[seq].committed_tokens == 0,
+               "GPU prefill into a slot whose ColdStore already holds a session; restore it or attach an empty "
+               "directory");
     int32_t next = 0;
-    ctx_->check("read greedy token", mslim_attn_buf_read(ctx_->handle(), next_, 0,
-                                                         reinterpret_cast<uint8_t *>(&next), 4));
+    const int n_total = (int)prompt.size();
+    {
+        std::lock_guard<std::mutex> lock(ctx_->mutex());
+        positions_[seq] = 0;
+        for (int start = 0; start < n_total; start += chunk_tokens_) {
+            const int n = std::min(chunk_tokens_, n_total - start);
+            chunk(seq, prompt.data() + start, n, start);
+            if (start + n == n_total) head(x_ + (size_t)(n - 1) * spec_.hidden, 1);
+        }
+        positions_[seq] = n_total;
+        ctx_->check("read greedy token", mslim_attn_buf_read(ctx_->handle(), next_, 0,
+                                                             reinterpret_cast<uint8_t *>(&next), 4));
+    }
+    if (cold_[seq]) {
+        // The prompt's K/V are committed to the canonical ColdStore at the end
+        // of prefill (gpu_llm/prefill.rs:760-790).
+        const auto t0 = std::chrono::steady_clock::now();
+        seal_slot(seq, 0, n_total);
+        cold_report_[seq].prefill_seal_seconds =
+            std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+    }
     return Step{next, n_total};
 }
 
@@ -273,6 +299,101 @@ void DecoderRunner::set_calibration_prefill_settings(const PrefillSettings &sett
 void DecoderRunner::reset(int seq) {
     ensure(seq >= 0 && seq < max_batch_, "sequence slot out of range");
     positions_[seq] = 0;
+}
+
+region::DevicePagePool DecoderRunner::all_layer_pool() const {
+    region::DevicePagePool pool;
+    pool.k_pool = k_base_;
+    pool.v_pool = v_base_;
+    pool.pool_pages = (int64_t)max_batch_ * pages_per_seq_ * spec_.layers;
+    pool.page_tokens = kPageTokens;
+    return pool;
+}
+
+std::vector<region::LayerBlocks> DecoderRunner::slot_blocks(int seq) const {
+    const int64_t per_layer = (int64_t)max_batch_ * pages_per_seq_;
+    std::vector<region::LayerBlocks> out(spec_.layers);
+    for (int l = 0; l < spec_.layers; ++l) {
+        out[l].layer = (size_t)l;
+        out[l].blocks.resize(pages_per_seq_);
+        for (int p = 0; p < pages_per_seq_; ++p)
+            out[l].blocks[p] = (int32_t)(l * per_layer + host_table_[(size_t)seq * pages_per_seq_ + p]);
+    }
+    return out;
+}
+
+// Commit tokens [from, to) of every layer of slot `seq` from the pool.
+void DecoderRunner::seal_slot(int seq, int64_t from, int64_t to) {
+    if (to <= from) return;
+    if (!staging_) staging_ = std::make_unique<region::DeviceStaging>(*ctx_);
+    cold_[seq]->seal_device_layers(*staging_, (size_t)from, (size_t)(to - from), all_layer_pool(), slot_blocks(seq));
+    cold_report_[seq].committed_tokens = to;
+}
+
+void DecoderRunner::attach_cold_store(int seq, const std::string &directory) {
+    ensure(seq >= 0 && seq < max_batch_, "sequence slot out of range");
+    ensure(layout_ == KvLayout::Paged, "the ColdStore-exact route needs the paged K/V layout");
+    ensure(positions_[seq] == 0, "attach a ColdStore to an empty slot");
+    region::RegionConfig config;
+    config.cold_directory = directory;
+    const auto g = portable::AttentionGeometry::create((size_t)spec_.q_heads, (size_t)spec_.kv_heads,
+                                                       (size_t)spec_.head_dim);
+    auto store = std::make_unique<region::RegionStore>(g, (size_t)spec_.layers, config);
+    const size_t held = store->layer_tokens(0);
+    for (int l = 1; l < spec_.layers; ++l)
+        ensure(store->layer_tokens(l) == held, "persisted ColdStore layers do not share a complete causal prefix");
+    cold_[seq] = std::move(store);
+    cold_report_[seq] = ColdReport{};
+    cold_report_[seq].attached = true;
+    cold_report_[seq].committed_tokens = (int64_t)held;
+}
+
+void DecoderRunner::detach_cold_store(int seq) {
+    ensure(seq >= 0 && seq < max_batch_, "sequence slot out of range");
+    cold_[seq].reset();
+    cold_report_[seq] = ColdReport{};
+}
+
+void DecoderRunner::flush_cold(int seq) {
+    ensure(seq >= 0 && seq < max_batch_, "sequence slot out of range");
+    ensure(cold_[seq] != nullptr, "deferred commit requires canonical ColdStore");
+    const auto t0 = std::chrono::steady_clock::now();
+    const int64_t from = cold_report_[seq].committed_tokens, to = positions_[seq];
+    ensure(from <= to, "GPU ColdStore prefill prefix missing/longer than in-flight KV");
+    seal_slot(seq, from, to);
+    cold_report_[seq].last_commit_seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+    cold_report_[seq].last_committed_token_layers = (to - from) * spec_.layers;
+}
+
+void DecoderRunner::restore_session(int seq, int64_t tokens) {
+    ensure(seq >= 0 && seq < max_batch_, "sequence slot out of range");
+    ensure(cold_[seq] != nullptr, "canonical GPU restore requires persistent LOD/ColdStore");
+    ensure(positions_[seq] == 0, "canonical GPU restore requires a fresh session");
+    ensure(tokens > 0, "canonical GPU restore prefix is empty");
+    ensure(tokens < max_context_, "canonical GPU restore must leave capacity for continuation");
+    for (int l = 0; l < spec_.layers; ++l)
+        ensure((int64_t)cold_[seq]->layer_tokens(l) == tokens,
+               "canonical GPU restore layer " + std::to_string(l) + " is not a complete causal prefix");
+    const auto t0 = std::chrono::steady_clock::now();
+    if (!staging_) staging_ = std::make_unique<region::DeviceStaging>(*ctx_);
+    // Every record is verified on the device before any byte reaches the
+    // pool; on failure the slot stays empty.
+    cold_[seq]->restore_device_layers(*staging_, all_layer_pool(), slot_blocks(seq));
+    positions_[seq] = tokens;
+    cold_report_[seq].committed_tokens = tokens;
+    cold_report_[seq].last_restore_seconds =
+        std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+}
+
+std::string DecoderRunner::cold_logical_kv_sha256(int seq) {
+    ensure(seq >= 0 && seq < max_batch_, "sequence slot out of range");
+    ensure(cold_[seq] != nullptr, "no ColdStore attached to this slot");
+    return cold_[seq]->logical_kv_sha256();
+}
+
+ColdReport DecoderRunner::cold_report(int seq) const {
+    ensure(seq >= 0 && seq < max_batch_, "sequence slot out of range");
+    return cold_report_[seq];
 }
 
 std::vector<uint16_t> DecoderRunner::last_logits() const {
@@ -476,6 +597,76 @@ int mslim_model_set_prefill_settings(void *model, const char *json) {
     try {
         mslim::ensure(json != nullptr, "null settings");
         runner_of(model).set_calibration_prefill_settings(mslim::PrefillSettings::from_json(json));
+        return 0;
+    } catch (const std::exception &e) {
+        return model_fail(e);
+    }
+}
+
+int mslim_model_attach_cold_store(void *model, int seq, const char *directory) {
+    g_model_error.clear();
+    try {
+        mslim::ensure(directory != nullptr, "null ColdStore directory");
+        runner_of(model).attach_cold_store(seq, directory);
+        return 0;
+    } catch (const std::exception &e) {
+        return model_fail(e);
+    }
+}
+
+int mslim_model_detach_cold_store(void *model, int seq) {
+    g_model_error.clear();
+    try {
+        runner_of(model).detach_cold_store(seq);
+        return 0;
+    } catch (const std::exception &e) {
+        return model_fail(e);
+    }
+}
+
+int mslim_model_flush_cold(void *model, int seq) {
+    g_model_error.clear();
+    try {
+        runner_of(model).flush_cold(seq);
+        return 0;
+    } catch (const std::exception &e) {
+        return model_fail(e);
+    }
+}
+
+int mslim_model_restore_session(void *model, int seq, int64_t tokens) {
+    g_model_error.clear();
+    try {
+        runner_of(model).restore_session(seq, tokens);
+        return 0;
+    } catch (const std::exception &e) {
+        return model_fail(e);
+    }
+}
+
+int mslim_model_cold_logical_kv_sha256(void *model, int seq, char *hex_out) {
+    g_model_error.clear();
+    try {
+        mslim::ensure(hex_out != nullptr, "null digest buffer");
+        const std::string hex = runner_of(model).cold_logical_kv_sha256(seq);
+        std::memcpy(hex_out, hex.c_str(), hex.size() + 1);
+        return 0;
+    } catch (const std::exception &e) {
+        return model_fail(e);
+    }
+}
+
+int mslim_model_cold_report(void *model, int seq, mslim_model_cold_info *out) {
+    g_model_error.clear();
+    try {
+        mslim::ensure(out != nullptr, "null report");
+        const mslim::model::ColdReport r = runner_of(model).cold_report(seq);
+        out->attached = r.attached ? 1 : 0;
+        out->committed_tokens = r.committed_tokens;
+        out->prefill_seal_seconds = r.prefill_seal_seconds;
+        out->last_commit_seconds = r.last_commit_seconds;
+        out->last_committed_token_layers = r.last_committed_token_layers;
+        out->last_restore_seconds = r.last_restore_seconds;
         return 0;
     } catch (const std::exception &e) {
         return model_fail(e);

@@ -19,6 +19,7 @@
 
 #include "attention_kernel.hpp"
 #include "native.hpp"
+#include "region_store.hpp"
 
 namespace mslim {
 namespace model {
@@ -59,6 +60,19 @@ struct Step {
 // mod.rs:2993-3048.
 enum class KvLayout { Paged = 0, Dense = 1 };
 
+// ColdStore persistence of one slot: the reference's last_prefill_cold_seal_
+// seconds, last_deferred_cold_commit_seconds and last_deferred_cold_committed_
+// token_layers (gpu_llm/mod.rs:192-208, :1696-1697) and the committed
+// length.
+struct ColdReport {
+    bool attached = false;
+    int64_t committed_tokens = 0;    // tokens of every layer in the ColdStore
+    double prefill_seal_seconds = 0.0;
+    double last_commit_seconds = 0.0;
+    int64_t last_committed_token_layers = 0;
+    double last_restore_seconds = 0.0;
+};
+
 class DecoderRunner {
 public:
     static constexpr int kPageTokens = 16;
@@ -96,9 +110,33 @@ public:
     PrefillSettings prefill_settings() const { return settings_; }
     void set_calibration_prefill_settings(const PrefillSettings &settings);
 
+    // ColdStore-exact persistence (paged layout only).  attach_cold_store
+    // gives slot `seq` a canonical ColdStore at <directory>/pages-exact.kv
+    // (the GPU-region runtime's GpuRegionConfig::cold_directory,
+    // gpu_llm/mod.rs:299-306), opening the records already there.  With a
+    // store attached, prefill_only commits the prompt's K/V at its end (the
+    // prefill seal, gpu_llm/prefill.rs:760-790) and decode steps defer their
+    // commit; flush_cold commits every token past the committed prefix (the
+    // end-of-turn flush_deferred_cold, mod.rs:1614-1699).  restore_session
+    // loads a store's committed prefix of `tokens` tokens into an empty slot
+    // after verifying every record on the device (restore_session,
+    // mod.rs:1335-1451).  The slot's ColdStore digest is
+    // cold_logical_kv_sha256 (gpu_region_store.rs:341-371).
+    void attach_cold_store(int seq, const std::string &directory);
+    void detach_cold_store(int seq);
+    void flush_cold(int seq);
+    void restore_session(int seq, int64_t tokens);
+    std::string cold_logical_kv_sha256(int seq);
+    ColdReport cold_report(int seq) const;
+
 private:
     void *alloc(size_t bytes);
     void chunk(int seq, const int32_t *ids, int n, int64_t prior);
+    // The page pool of every layer (one allocation each for K and V) and the
+    // pool pages of slot `seq` per layer, for the ColdStore device paths.
+    region::DevicePagePool all_layer_pool() const;
+    std::vector<region::LayerBlocks> slot_blocks(int seq) const;
+    void seal_slot(int seq, int64_t from, int64_t to);
     void gemm(const void *w, const void *in, void *out, int inner, int rows, int tokens);
     void head(const uint16_t *rows_in, int rows);
     void mlp(const LayerWeights &w, int n);
@@ -117,7 +155,12 @@ private:
     PrefillSettings settings_;
     std::vector<int64_t> positions_;
     std::vector<void *> owned_;
-    std::vector<void *> k_pools_, v_pools_;
+    std::vector<void *> k_pools_, v_pools_;  // layer l: k_base_ + l * layer pool bytes
+    void *k_base_ = nullptr, *v_base_ = nullptr;
+    std::vector<int32_t> host_table_;          // copy of the device page table
+    std::vector<std::unique_ptr<region::RegionStore>> cold_;
+    std::vector<ColdReport> cold_report_;
+    std::unique_ptr<region::DeviceStaging> staging_;
     int32_t *table_ = nullptr, *ids_ = nullptr, *pos_ = nullptr, *next_ = nullptr;
     uint16_t *x_ = nullptr, *norm_ = nullptr, *q_ = nullptr, *k_ = nullptr, *v_ = nullptr, *qr_ = nullptr,
              *kr_ = nullptr, *attn_ = nullptr, *act_ = nullptr,

@@ -342,148 +342,238 @@ void check_pool(const DevicePagePool &pool, const portable::AttentionGeometry &g
 
 }  // namespace
 
-void RegionStore::seal_device_pages(NativeContext &ctx, size_t layer, size_t position, const DevicePagePool &pool,
-                                    const std::vector<int32_t> &blocks, size_t count) {
+DeviceStaging::~DeviceStaging() {
+    for (void *p : {d_desc, d_frames, d_k, d_v})
+        if (p) mslim_attn_buf_free(ctx_.handle(), p);
+    for (uint8_t *p : {h_desc, h_frames, h_k, h_v})
+        if (p) mslim_attn_host_free(ctx_.handle(), p);
+}
+
+void DeviceStaging::grow(size_t &cap, size_t bytes, void **dev, uint8_t **host) {
+    if (cap >= bytes) return;
+    if (*dev) mslim_attn_buf_free(ctx_.handle(), *dev);
+    if (*host) mslim_attn_host_free(ctx_.handle(), *host);
+    *dev = nullptr;
+    *host = nullptr;
+    cap = 0;
+    *dev = mslim_attn_buf_alloc(ctx_.handle(), bytes);
+    if (!*dev) throw NativeError("allocate seal staging", -1, mslim_attn_last_error());
+    *host = static_cast<uint8_t *>(mslim_attn_host_alloc(ctx_.handle(), bytes));
+    if (!*host) throw NativeError("allocate pinned seal staging", -1, mslim_attn_last_error());
+    cap = bytes;
+}
+
+void DeviceStaging::reserve(size_t records, size_t frame_slot, size_t payload_bytes) {
+    records = std::max<size_t>(records, 1);
+    grow(desc_cap_, records * sizeof(mslim_attn_page_record), &d_desc, &h_desc);
+    grow(frames_cap_, records * frame_slot, &d_frames, &h_frames);
+    // K and V share one capacity figure; both buffers grow together.
+    if (payload_cap_ < records * payload_bytes) {
+        size_t cap_v = payload_cap_;
+        grow(payload_cap_, records * payload_bytes, &d_k, &h_k);
+        grow(cap_v, records * payload_bytes, &d_v, &h_v);
+    }
+}
+
+void RegionStore::seal_device_layers(DeviceStaging &st, size_t position, size_t count, const DevicePagePool &pool,
+                                     const std::vector<LayerBlocks> &layers, size_t max_group_bytes) {
+    NativeContext &ctx = st.ctx();
     check_pool(pool, geometry_);
-    ensure(layer < pages_.size(), "GPU LOD batch layer out of range");
-    ensure(pages_[layer].size() == position, "GPU LOD append needs sequential tokens");
     ensure(count > 0, "GPU LOD batched BF16 K/V shape mismatch");
     const size_t P = (size_t)pool.page_tokens;
-    ensure(position % P == 0, "device seal must start at a pool page boundary");
-    const size_t records = (count + P - 1) / P;
-    ensure(blocks.size() >= records, "device seal needs a pool page for every logical page");
     const size_t kvh = geometry_.kv_heads, row_bytes = geometry_.head_dim * 2;
     const size_t page_bytes = kvh * P * row_bytes;
     const uint32_t tile = geometry_.head_dim % 16 == 0 ? 16 : 1;
-    const uint64_t first_page_id = cold_.metadata().size();
-
-    std::vector<mslim_attn_page_record> descs(records);
-    for (size_t i = 0; i < records; ++i) {
-        ensure(blocks[i] >= 0 && blocks[i] < pool.pool_pages, "device seal pool page out of range");
-        descs[i].page_id = first_page_id + i;
-        descs[i].token_start = position + i * P;
-        descs[i].layer = (uint32_t)layer;
-        descs[i].tokens = (uint32_t)std::min(P, count - i * P);
-        descs[i].pool_page = blocks[i];
-        descs[i].reserved = 0;
-    }
     const int64_t slot = mslim_attn_record_frame_bytes((int)P);
-    std::vector<uint8_t> frames(records * slot), k(records * page_bytes), v(records * page_bytes);
-    {
-        std::lock_guard<std::mutex> guard(ctx.mutex());
-        DeviceBuffer d_desc(ctx, descs.data(), descs.size() * sizeof(mslim_attn_page_record));
-        DeviceBuffer d_frames(ctx, frames.size()), d_k(ctx, k.size()), d_v(ctx, v.size());
-        ctx.check("record frames",
-                  mslim_attn_record_frames(ctx.handle(), pool.k_pool, pool.v_pool, pool.pool_pages, (int)P, (int)kvh,
-                                           (int)geometry_.head_dim, tile,
-                                           static_cast<const mslim_attn_page_record *>(d_desc.ptr), (int)records,
-                                           d_frames.ptr));
-        ctx.check("record payloads",
-                  mslim_attn_record_payloads(ctx.handle(), pool.k_pool, pool.v_pool, pool.pool_pages, (int)P,
-                                             (int)kvh, (int)geometry_.head_dim,
-                                             static_cast<const mslim_attn_page_record *>(d_desc.ptr), (int)records,
-                                             d_k.ptr, d_v.ptr, 0));
-        d_frames.read(frames.data(), frames.size());
-        d_k.read(k.data(), k.size());
-        d_v.read(v.data(), v.size());
+    // Records of one layer: the first starts at position % P inside its page.
+    const size_t first_row = position % P;
+    std::vector<size_t> starts;  // token offsets of the records within [0, count)
+    for (size_t t = 0; t < count; t += (t == 0 ? P - first_row : P)) starts.push_back(t);
+    const size_t per_layer = starts.size();
+    const size_t logical0 = position / P;
+    for (const LayerBlocks &lb : layers) {
+        ensure(lb.layer < pages_.size(), "GPU LOD batch layer out of range");
+        ensure(pages_[lb.layer].size() == position, "GPU LOD append needs sequential tokens");
+        ensure(lb.blocks.size() >= logical0 + per_layer, "device seal needs a pool page for every logical page");
     }
-    // Same validation as append_batch, before anything is committed.
-    std::vector<double> maxima = value_abs_max_[layer];
-    for (size_t i = 0; i < records; ++i) {
-        const size_t n = descs[i].tokens;
-        const uint8_t *kp = k.data() + i * page_bytes;
-        const uint8_t *vp = v.data() + i * page_bytes;
-        if (layer == 0)
-            for (size_t j = 0; j < n * kvh * row_bytes; j += 2)
-                ensure(!bf16_nonfinite(load_u16(kp + j)), "GPU ColdStore K nonfinite");
-        for (size_t h = 0; h < kvh; ++h)
-            for (size_t j = 0; j < n * row_bytes; j += 2) {
-                const float x = bf16_to_f32(load_u16(vp + h * n * row_bytes + j));
-                ensure(std::isfinite(x), "GPU ColdStore V nonfinite");
-                maxima[h] = std::max(maxima[h], (double)std::fabs(x));
+    const size_t group_layers = std::max<size_t>(1, max_group_bytes / std::max<size_t>(1, per_layer * page_bytes));
+    for (size_t g0 = 0; g0 < layers.size(); g0 += group_layers) {
+        const size_t g1 = std::min(layers.size(), g0 + group_layers);
+        const size_t records = (g1 - g0) * per_layer;
+        st.reserve(records, (size_t)slot, page_bytes);
+        auto *descs = reinterpret_cast<mslim_attn_page_record *>(st.h_desc);
+        uint64_t page_id = cold_.metadata().size();
+        for (size_t li = g0; li < g1; ++li)
+            for (size_t r = 0; r < per_layer; ++r) {
+                const int32_t block = layers[li].blocks[logical0 + r];
+                ensure(block >= 0 && block < pool.pool_pages, "device seal pool page out of range");
+                const size_t t0 = starts[r];
+                const size_t t1 = r + 1 < per_layer ? starts[r + 1] : count;
+                mslim_attn_page_record &d = descs[(li - g0) * per_layer + r];
+                d.page_id = page_id++;
+                d.token_start = position + t0;
+                d.layer = (uint32_t)layers[li].layer;
+                d.tokens = (uint32_t)(t1 - t0);
+                d.pool_page = block;
+                d.first_row = (uint32_t)(r == 0 ? first_row : 0);
             }
+        {
+            std::lock_guard<std::mutex> guard(ctx.mutex());
+            void *h = ctx.handle();
+            ctx.check("upload record descriptors",
+                      mslim_attn_buf_write(h, st.d_desc, 0, st.h_desc, records * sizeof(mslim_attn_page_record)));
+            ctx.check("record frames",
+                      mslim_attn_record_frames(h, pool.k_pool, pool.v_pool, pool.pool_pages, (int)P, (int)kvh,
+                                               (int)geometry_.head_dim, tile,
+                                               static_cast<const mslim_attn_page_record *>(st.d_desc), (int)records,
+                                               st.d_frames));
+            ctx.check("record payloads",
+                      mslim_attn_record_payloads(h, pool.k_pool, pool.v_pool, pool.pool_pages, (int)P, (int)kvh,
+                                                 (int)geometry_.head_dim,
+                                                 static_cast<const mslim_attn_page_record *>(st.d_desc),
+                                                 (int)records, st.d_k, st.d_v, 0));
+            ctx.check("read record frames", mslim_attn_buf_read(h, st.d_frames, 0, st.h_frames, records * slot));
+            ctx.check("read K payloads", mslim_attn_buf_read(h, st.d_k, 0, st.h_k, records * page_bytes));
+            ctx.check("read V payloads", mslim_attn_buf_read(h, st.d_v, 0, st.h_v, records * page_bytes));
+        }
+        // Same validation as append_batch, before anything of the group is
+        // committed.
+        std::vector<std::vector<double>> maxima(g1 - g0);
+        for (size_t li = g0; li < g1; ++li) {
+            const size_t layer = layers[li].layer;
+            maxima[li - g0] = value_abs_max_[layer];
+            for (size_t r = 0; r < per_layer; ++r) {
+                const size_t i = (li - g0) * per_layer + r;
+                const size_t n = descs[i].tokens;
+                const uint8_t *kp = st.h_k + i * page_bytes;
+                const uint8_t *vp = st.h_v + i * page_bytes;
+                if (layer == 0)
+                    for (size_t j = 0; j < n * kvh * row_bytes; j += 2)
+                        ensure(!bf16_nonfinite(load_u16(kp + j)), "GPU ColdStore K nonfinite");
+                for (size_t hd = 0; hd < kvh; ++hd)
+                    for (size_t j = 0; j < n * row_bytes; j += 2) {
+                        const float x = bf16_to_f32(load_u16(vp + hd * n * row_bytes + j));
+                        ensure(std::isfinite(x), "GPU ColdStore V nonfinite");
+                        maxima[li - g0][hd] = std::max(maxima[li - g0][hd], (double)std::fabs(x));
+                    }
+            }
+        }
+        for (size_t li = g0; li < g1; ++li) {
+            const size_t layer = layers[li].layer;
+            for (size_t r = 0; r < per_layer; ++r) {
+                const size_t i = (li - g0) * per_layer + r;
+                const size_t n = descs[i].tokens;
+                const cold::PageMeta meta =
+                    cold_.append_framed(st.h_frames + i * slot, (size_t)slot, st.h_k + i * page_bytes,
+                                        st.h_v + i * page_bytes, n * kvh * row_bytes, false);
+                for (size_t offset = 0; offset < n; ++offset) pages_[layer].push_back({meta.page_id, offset});
+                stats.prefill_batched_page_tokens = std::max(stats.prefill_batched_page_tokens, n);
+            }
+            value_abs_max_[layer] = maxima[li - g0];
+            if (layer == 0) axis_tokens_ += count;
+        }
+        stats.device_sealed_pages += records;
     }
-    for (size_t i = 0; i < records; ++i) {
-        const size_t n = descs[i].tokens;
-        const uint8_t *frame = frames.data() + i * slot;
-        const cold::PageMeta meta = cold_.append_framed(frame, (size_t)slot, k.data() + i * page_bytes,
-                                                        v.data() + i * page_bytes, n * kvh * row_bytes, false);
-        for (size_t offset = 0; offset < n; ++offset) pages_[layer].push_back({meta.page_id, offset});
-        stats.prefill_batched_page_tokens = std::max(stats.prefill_batched_page_tokens, n);
-    }
-    value_abs_max_[layer] = maxima;
-    if (layer == 0) axis_tokens_ += count;
-    stats.device_sealed_pages += records;
     const cold::ColdStoreStats info = cold_.stats();
     stats.physical_cold_store_bytes = info.committed_bytes;
     stats.physical_cold_store_pages = info.pages;
 }
 
-void RegionStore::restore_to_device(NativeContext &ctx, size_t layer, const DevicePagePool &pool,
-                                    const std::vector<int32_t> &blocks) {
+size_t RegionStore::restore_device_layers(DeviceStaging &st, const DevicePagePool &pool,
+                                          const std::vector<LayerBlocks> &layers) {
+    NativeContext &ctx = st.ctx();
     check_pool(pool, geometry_);
-    ensure(layer < pages_.size(), "GPU LOD read layer missing");
     const size_t P = (size_t)pool.page_tokens;
     const size_t kvh = geometry_.kv_heads, row_bytes = geometry_.head_dim * 2;
     const size_t page_bytes = kvh * P * row_bytes;
     const uint32_t tile = geometry_.head_dim % 16 == 0 ? 16 : 1;
-    // The layer's records, in token order.
-    std::vector<uint64_t> ids;
-    for (const PageAddress &a : pages_[layer])
-        if (ids.empty() || ids.back() != a.page_id) ids.push_back(a.page_id);
-    if (ids.empty()) return;
-    const size_t records = ids.size();
     const int64_t slot = mslim_attn_record_frame_bytes((int)P);
-    std::vector<mslim_attn_page_record> descs(records);
-    std::vector<uint8_t> stored(records * slot), k(records * page_bytes, 0), v(records * page_bytes, 0);
+    // Every record of the listed layers, in token order per layer.
+    struct Item {
+        uint64_t page_id;
+        int32_t pool_page;
+    };
+    std::vector<Item> items;
+    for (const LayerBlocks &lb : layers) {
+        ensure(lb.layer < pages_.size(), "GPU LOD read layer missing");
+        uint64_t last = UINT64_MAX;
+        for (const PageAddress &a : pages_[lb.layer]) {
+            if (a.page_id == last) continue;
+            last = a.page_id;
+            const cold::PageMeta &m = cold_.metadata().at(a.page_id);
+            const size_t row = m.geometry.token_start % P;
+            ensure(row + m.geometry.tokens <= P, "a persisted record does not fit in one device pool page");
+            const size_t block = m.geometry.token_start / P;
+            ensure(block < lb.blocks.size() && lb.blocks[block] >= 0 && lb.blocks[block] < pool.pool_pages,
+                   "device restore pool page out of range");
+            items.push_back({a.page_id, lb.blocks[block]});
+        }
+    }
+    const size_t records = items.size();
+    if (records == 0) return 0;
+    st.reserve(records, (size_t)slot, page_bytes);
+    auto *descs = reinterpret_cast<mslim_attn_page_record *>(st.h_desc);
     std::vector<uint8_t> frame, key, value;
+    std::vector<uint8_t> stored(records * slot);
     for (size_t i = 0; i < records; ++i) {
-        const cold::PageMeta &m = cold_.metadata().at(ids[i]);
-        ensure(m.geometry.token_start % P == 0 && m.geometry.tokens <= P,
-               "layer pages are not aligned to the device pool pages");
-        const size_t block = m.geometry.token_start / P;
-        ensure(block < blocks.size() && blocks[block] >= 0 && blocks[block] < pool.pool_pages,
-               "device restore pool page out of range");
-        cold_.read_record_raw(ids[i], (uint32_t)P, frame, key, value);
+        const cold::PageMeta &m = cold_.metadata().at(items[i].page_id);
+        cold_.read_record_raw(items[i].page_id, (uint32_t)P, frame, key, value);
         std::memcpy(stored.data() + i * slot, frame.data(), slot);
-        std::memcpy(k.data() + i * page_bytes, key.data(), key.size());
-        std::memcpy(v.data() + i * page_bytes, value.data(), value.size());
+        std::memcpy(st.h_k + i * page_bytes, key.data(), key.size());
+        std::memcpy(st.h_v + i * page_bytes, value.data(), value.size());
         descs[i].page_id = m.page_id;
         descs[i].token_start = m.geometry.token_start;
         descs[i].layer = m.geometry.layer;
         descs[i].tokens = m.geometry.tokens;
-        descs[i].pool_page = blocks[block];
-        descs[i].reserved = 0;
+        descs[i].pool_page = items[i].pool_page;
+        descs[i].first_row = (uint32_t)(m.geometry.token_start % P);
     }
-    std::vector<uint8_t> recomputed(records * slot);
-    {
-        std::lock_guard<std::mutex> guard(ctx.mutex());
-        DeviceBuffer d_desc(ctx, descs.data(), descs.size() * sizeof(mslim_attn_page_record));
-        DeviceBuffer d_k(ctx, k.data(), k.size()), d_v(ctx, v.data(), v.size()), d_frames(ctx, recomputed.size());
-        ctx.check("record payloads",
-                  mslim_attn_record_payloads(ctx.handle(), pool.k_pool, pool.v_pool, pool.pool_pages, (int)P,
-                                             (int)kvh, (int)geometry_.head_dim,
-                                             static_cast<const mslim_attn_page_record *>(d_desc.ptr), (int)records,
-                                             d_k.ptr, d_v.ptr, 1));
-        ctx.check("record frames",
-                  mslim_attn_record_frames(ctx.handle(), pool.k_pool, pool.v_pool, pool.pool_pages, (int)P, (int)kvh,
-                                           (int)geometry_.head_dim, tile,
-                                           static_cast<const mslim_attn_page_record *>(d_desc.ptr), (int)records,
-                                           d_frames.ptr));
-        d_frames.read(recomputed.data(), recomputed.size());
-    }
-    // The stored frame must equal the one recomputed from the pool bytes:
-    // header (payload checksums), token hashes, record checksum and SHA-256.
+    std::lock_guard<std::mutex> guard(ctx.mutex());
+    void *h = ctx.handle();
+    ctx.check("upload record descriptors",
+              mslim_attn_buf_write(h, st.d_desc, 0, st.h_desc, records * sizeof(mslim_attn_page_record)));
+    ctx.check("upload K payloads", mslim_attn_buf_write(h, st.d_k, 0, st.h_k, records * page_bytes));
+    ctx.check("upload V payloads", mslim_attn_buf_write(h, st.d_v, 0, st.h_v, records * page_bytes));
+    // Frames recomputed from the staged copies, compared with the stored
+    // ones, before the payloads move into the pool.
+    ctx.check("staged record frames",
+              mslim_attn_record_frames_staged(h, st.d_k, st.d_v, (int)P, (int)kvh, (int)geometry_.head_dim, tile,
+                                              static_cast<const mslim_attn_page_record *>(st.d_desc), (int)records,
+                                              st.d_frames));
+    ctx.check("read record frames", mslim_attn_buf_read(h, st.d_frames, 0, st.h_frames, records * slot));
     for (size_t i = 0; i < records; ++i) {
         const uint8_t *want = stored.data() + i * slot;
-        const uint8_t *got = recomputed.data() + i * slot;
+        const uint8_t *got = st.h_frames + i * slot;
         const size_t prefix = cold::kHeaderLen + 16ull * descs[i].tokens;
         if (std::memcmp(want, got, prefix) != 0 ||
             std::memcmp(want + slot - cold::kFooterLen, got + slot - cold::kFooterLen, cold::kFooterLen) != 0)
             throw cold::ColdStoreError(cold::ColdStoreError::Kind::InvalidData,
                                        "device verification failed for KV page " + std::to_string(descs[i].page_id));
     }
+    ctx.check("record payloads",
+              mslim_attn_record_payloads(h, pool.k_pool, pool.v_pool, pool.pool_pages, (int)P, (int)kvh,
+                                         (int)geometry_.head_dim,
+                                         static_cast<const mslim_attn_page_record *>(st.d_desc), (int)records,
+                                         st.d_k, st.d_v, 1));
+    ctx.check("restore barrier", mslim_attn_synchronize(h));
     stats.device_restored_pages += records;
+    return records;
+}
+
+void RegionStore::seal_device_pages(NativeContext &ctx, size_t layer, size_t position, const DevicePagePool &pool,
+                                    const std::vector<int32_t> &blocks, size_t count) {
+    check_pool(pool, geometry_);
+    const size_t P = (size_t)pool.page_tokens;
+    std::vector<int32_t> logical(position / P, 0);
+    logical.insert(logical.end(), blocks.begin(), blocks.end());
+    DeviceStaging st(ctx);
+    seal_device_layers(st, position, count, pool, {LayerBlocks{layer, logical}});
+}
+
+void RegionStore::restore_to_device(NativeContext &ctx, size_t layer, const DevicePagePool &pool,
+                                    const std::vector<int32_t> &blocks) {
+    DeviceStaging st(ctx);
+    restore_device_layers(st, pool, {LayerBlocks{layer, blocks}});
 }
 
 }  // namespace region

@@ -5,11 +5,13 @@
 // the logical K/V SHA-256, with the same argument meaning and error texts.
 //
 // The device page pool adds two batch paths the reference does through the
-// host: seal_device_pages commits pages that live in the pool (the
-// end-of-turn deferred commit, gpu_llm/mod.rs:1614-1699) with the record
-// frames computed on the device, and restore_to_device loads a layer's
-// committed pages into the pool and verifies every byte on the device
-// (replacing read_values + per-chunk H2D, gpu_resources.rs:1017-1048).
+// host: seal_device_layers commits pages that live in the pool (the
+// end-of-turn deferred commit, gpu_llm/mod.rs:1614-1699, and the prefill
+// seal, gpu_llm/prefill.rs:760-790) with the record frames computed on the
+// device, and restore_device_layers verifies committed records on the
+// device and loads them into the pool (restore_session, gpu_llm/mod.rs:
+// 1335-1451, replacing read_values + per-chunk H2D, gpu_resources.rs:
+// 1017-1048).
 //
 // Not built: the positive-epsilon LOD selection (4-bit LSH axis, mass
 // certificates, micro regions); a config with epsilon > 0 is rejected.
@@ -76,6 +78,38 @@ struct DevicePagePool {
     int page_tokens = 16;
 };
 
+// Staging of the device seal and restore paths, reused across calls: device
+// buffers for record descriptors, frames and compacted payloads, and
+// page-locked host buffers that the copies move by DMA.  Grown on demand,
+// freed with the object; the context must outlive it.
+class DeviceStaging {
+public:
+    explicit DeviceStaging(NativeContext &ctx) : ctx_(ctx) {}
+    ~DeviceStaging();
+    DeviceStaging(const DeviceStaging &) = delete;
+    DeviceStaging &operator=(const DeviceStaging &) = delete;
+    NativeContext &ctx() { return ctx_; }
+    // Room for `records` records of `frame_slot` frame bytes and
+    // `payload_bytes` bytes of K (and of V) each.
+    void reserve(size_t records, size_t frame_slot, size_t payload_bytes);
+
+    void *d_desc = nullptr, *d_frames = nullptr, *d_k = nullptr, *d_v = nullptr;
+    uint8_t *h_desc = nullptr, *h_frames = nullptr, *h_k = nullptr, *h_v = nullptr;
+
+private:
+    void grow(size_t &cap, size_t bytes, void **dev, uint8_t **host);
+    NativeContext &ctx_;
+    size_t desc_cap_ = 0, frames_cap_ = 0, payload_cap_ = 0;
+};
+
+// Pool pages of one layer for the multi-layer device paths: blocks[i] is the
+// pool page that holds the sequence's logical page i (token i * page_tokens
+// onward).
+struct LayerBlocks {
+    size_t layer;
+    std::vector<int32_t> blocks;
+};
+
 class RegionStore {
 public:
     // gpu_region_store.rs:137-207: opens (and restores) or creates
@@ -110,20 +144,42 @@ public:
     std::vector<uint8_t> read_keys(size_t layer, const std::vector<size_t> &positions);
 
     // Commit tokens [position, position + count) of `layer` from the device
-    // pool as one ColdStore record per pool page.  `blocks[i]` is the pool
-    // page of the sequence's logical page position / page_tokens + i.
-    // position must equal layer_tokens(layer) and be a multiple of
-    // page_tokens.  Values are checked like append_batch (V finite on every
-    // layer, K finite on layer 0) before any record is committed.
+    // pool as one ColdStore record per pool page (or part of one).
+    // `blocks[i]` is the pool page of the sequence's logical page
+    // position / page_tokens + i.  position must equal layer_tokens(layer).
+    // Values are checked like append_batch (V finite on every layer, K
+    // finite on layer 0) before any record is committed.  One layer of
+    // seal_device_layers, with staging of its own.
     void seal_device_pages(NativeContext &ctx, size_t layer, size_t position, const DevicePagePool &pool,
                            const std::vector<int32_t> &blocks, size_t count);
     // Load every committed page of `layer` into the device pool at
-    // blocks[token_start / page_tokens] and verify each record on the device
-    // against its stored header, token hashes, checksums and SHA-256.  The
-    // layer's records must each cover one aligned pool page.  On error the
-    // pool pages written by this call hold unverified bytes.
+    // blocks[token_start / page_tokens] after verifying each record on the
+    // device against its stored header, token hashes, checksums and SHA-256;
+    // a corrupt record leaves the pool untouched.  One layer of
+    // restore_device_layers, with staging of its own.
     void restore_to_device(NativeContext &ctx, size_t layer, const DevicePagePool &pool,
                            const std::vector<int32_t> &blocks);
+
+    // Commit tokens [position, position + count) of every listed layer from
+    // the device pool in few launches: the end-of-turn deferred commit
+    // (gpu_llm/mod.rs:1614-1699) and the prefill seal (gpu_llm/prefill.rs:
+    // 760-790) of a whole model.  position must equal each layer's
+    // layer_tokens; it need not be a page boundary (the first record then
+    // starts inside its pool page).  One record per pool page or part of
+    // one, layers in order, so the file holds the records the reference's
+    // per-layer append_batch writes for 16-token pages.  Layers are staged in
+    // groups of at most `max_group_bytes` of payload; each group is checked
+    // (V finite on every layer, K finite on layer 0) before any of its
+    // records is committed, as append_batch checks each layer.
+    void seal_device_layers(DeviceStaging &staging, size_t position, size_t count, const DevicePagePool &pool,
+                            const std::vector<LayerBlocks> &layers, size_t max_group_bytes = (size_t)256 << 20);
+    // Load every committed record of the listed layers into the pool and
+    // verify each on the device (header, token hashes, checksums, SHA-256)
+    // from its staged copy BEFORE any byte reaches the pool: a corrupt store
+    // leaves the pool untouched.  Each record must lie within one pool page.
+    // Returns the number of records moved.
+    size_t restore_device_layers(DeviceStaging &staging, const DevicePagePool &pool,
+                                 const std::vector<LayerBlocks> &layers);
 
     RegionStats stats;
 

@@ -23,6 +23,7 @@ LIB_PATH = os.path.join(_HERE, "libmslim_attn.so")
 MAX_BATCH = 64
 OPT_DECODE_MERGE = 1                        # mslim_attn_ctx_set_option options
 DECODE_MERGE_FUSED, DECODE_MERGE_SEPARATE = 0, 1
+OPT_PREFILL_SPLIT = 2
 DECODE_STATIC_SCRATCH_BYTES = 16 << 20      # mslim_attn_decode_paged_noalloc partials bound
 FORMAT_BF16, FORMAT_F16, FORMAT_F32 = 1, 2, 3  # gpu_backend.rs:258-262
 ERR_NONFINITE = -2
@@ -54,6 +55,8 @@ EXPORTS = (
     "mslim_attn_ctx_set_option",
     "mslim_attn_synchronize",
     "mslim_attn_buf_alloc",
+    "mslim_attn_host_alloc",
+    "mslim_attn_host_free",
     "mslim_attn_buf_upload",
     "mslim_attn_buf_free",
     "mslim_attn_buf_read",
@@ -63,6 +66,7 @@ EXPORTS = (
     "mslim_attn_decode_paged",
     "mslim_attn_decode_paged_noalloc",
     "mslim_attn_prefill_causal",
+    "mslim_attn_prefill_split_tiles",
     "mslim_attn_frames_decode",
     "mslim_attn_backend_decode",
     "mslim_attn_rmsnorm",
@@ -76,6 +80,7 @@ EXPORTS = (
     "mslim_attn_logical_kv_sha256",
     "mslim_attn_record_frame_bytes",
     "mslim_attn_record_frames",
+    "mslim_attn_record_frames_staged",
     "mslim_attn_record_payloads",
     "mslim_attn_matrix_multiply",
     "mslim_attn_gemm_bf16",
@@ -94,7 +99,7 @@ RECORD_FOOTER_BYTES = 56   # cold_store.rs:24
 class PageRecord(C.Structure):
     """mslim_attn_page_record: header fields of one record and its pool page."""
     _fields_ = [("page_id", C.c_uint64), ("token_start", C.c_uint64), ("layer", C.c_uint32),
-                ("tokens", C.c_uint32), ("pool_page", C.c_int32), ("reserved", C.c_uint32)]
+                ("tokens", C.c_uint32), ("pool_page", C.c_int32), ("first_row", C.c_uint32)]
 
 
 class MslimAttnError(RuntimeError):
@@ -132,6 +137,8 @@ def library() -> C.CDLL:
         "mslim_attn_ctx_set_option": (I, [P, I, I64]),
         "mslim_attn_synchronize": (I, [P]),
         "mslim_attn_buf_alloc": (P, [P, SZ]),
+        "mslim_attn_host_alloc": (P, [P, SZ]),
+        "mslim_attn_host_free": (I, [P, P]),
         "mslim_attn_buf_upload": (P, [P, P, SZ]),
         "mslim_attn_buf_free": (I, [P, P]),
         "mslim_attn_buf_read": (I, [P, P, SZ, P, SZ]),
@@ -141,6 +148,7 @@ def library() -> C.CDLL:
         "mslim_attn_decode_paged": (I, [P, P, P, P, P, I, PI32, P, I, I, I, I, I, F, I]),
         "mslim_attn_decode_paged_noalloc": (I, [P, P, P, P, P, I, PI32, P, I, I, I, I, I, F, I]),
         "mslim_attn_prefill_causal": (I, [P, P, P, P, P, I, I, I, I, I, F]),
+        "mslim_attn_prefill_split_tiles": (I, [I, I, I, I, I]),
         "mslim_attn_frames_decode": (I, [P, P, P, I, P, I, P, I64, I, I, I]),
         "mslim_attn_backend_decode": (I, [P, P, P, I, P, I, I64, I, I, I, P, C.POINTER(Timings)]),
         "mslim_attn_rmsnorm": (I, [P, P, P, P, I, I, F]),
@@ -154,6 +162,7 @@ def library() -> C.CDLL:
         "mslim_attn_logical_kv_sha256": (I, [P, I, I64, I, I, P, P, P, I, C.c_char_p]),
         "mslim_attn_record_frame_bytes": (I64, [I]),
         "mslim_attn_record_frames": (I, [P, P, P, I64, I, I, I, C.c_uint32, P, I, P]),
+        "mslim_attn_record_frames_staged": (I, [P, P, P, I, I, I, C.c_uint32, P, I, P]),
         "mslim_attn_record_payloads": (I, [P, P, P, I64, I, I, I, P, I, P, P, I]),
         "mslim_attn_matrix_multiply": (I, [P, P, P, P, I, I, I]),
         "mslim_attn_gemm_bf16": (I, [P, P, P, P, I, I, I]),
@@ -243,6 +252,11 @@ class Context:
         """Merge decode split partials in a second launch (True) or in the
         last workgroup of each (sequence, kv head) (False, the default)."""
         self.set_option(OPT_DECODE_MERGE, DECODE_MERGE_SEPARATE if separate else DECODE_MERGE_FUSED)
+
+    def set_prefill_split(self, allowed: bool) -> None:
+        """Let prefill split long row blocks on small launches (True, the
+        default) or never (False)."""
+        self.set_option(OPT_PREFILL_SPLIT, 1 if allowed else 0)
 
     def use_torch_stream(self) -> None:
         import torch
@@ -491,4 +505,13 @@ def auto_split(seq_lens: Sequence[int], kv_heads: int) -> int:
     out = lib.mslim_attn_decode_auto_split(arr, len(seq_lens), kv_heads)
     if out < 0:
         raise MslimAttnError("decode_auto_split", out, lib.mslim_attn_last_error().decode())
+    return out
+
+
+def prefill_split_tiles(queries: int, prior: int, q_heads: int, kv_heads: int, head_dim: int) -> int:
+    """Key tiles per chunk of a split prefill launch of this shape (0: not split)."""
+    lib = library()
+    out = lib.mslim_attn_prefill_split_tiles(queries, prior, q_heads, kv_heads, head_dim)
+    if out < 0:
+        raise MslimAttnError("prefill_split_tiles", out, lib.mslim_attn_last_error().decode())
     return out

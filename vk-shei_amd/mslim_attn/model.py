@@ -28,7 +28,23 @@ MODEL_EXPORTS = (
     "mslim_model_logical_kv_sha256",
     "mslim_model_prefill_settings",
     "mslim_model_set_prefill_settings",
+    "mslim_model_attach_cold_store",
+    "mslim_model_detach_cold_store",
+    "mslim_model_flush_cold",
+    "mslim_model_restore_session",
+    "mslim_model_cold_logical_kv_sha256",
+    "mslim_model_cold_report",
 )
+
+
+class ColdReport(C.Structure):
+    """mslim_model_cold_report (gpu_llm/mod.rs:192-208)."""
+    _fields_ = [("attached", C.c_int), ("committed_tokens", C.c_int64), ("prefill_seal_seconds", C.c_double),
+                ("last_commit_seconds", C.c_double), ("last_committed_token_layers", C.c_int64),
+                ("last_restore_seconds", C.c_double)]
+
+    def as_dict(self) -> dict:
+        return {name: getattr(self, name) for name, _ in self._fields_}
 
 LAYER_TENSORS = ("input_norm", "q", "k", "v", "o", "post_norm", "gate", "up", "down")
 
@@ -95,6 +111,12 @@ def host_library() -> C.CDLL:
         "mslim_model_logical_kv_sha256": (I, [P, I, C.c_char_p]),
         "mslim_model_prefill_settings": (I, [P, C.c_char_p, C.c_size_t]),
         "mslim_model_set_prefill_settings": (I, [P, C.c_char_p]),
+        "mslim_model_attach_cold_store": (I, [P, I, C.c_char_p]),
+        "mslim_model_detach_cold_store": (I, [P, I]),
+        "mslim_model_flush_cold": (I, [P, I]),
+        "mslim_model_restore_session": (I, [P, I, I64]),
+        "mslim_model_cold_logical_kv_sha256": (I, [P, I, C.c_char_p]),
+        "mslim_model_cold_report": (I, [P, I, C.POINTER(ColdReport)]),
     }
     for name in MODEL_EXPORTS:
         res, args = sigs[name]
@@ -216,3 +238,60 @@ class Model:
         out = C.create_string_buffer(65)
         self._check("logical_kv_sha256", self._lib.mslim_model_logical_kv_sha256(self._h, seq, out))
         return out.value.decode()
+
+    # ---- ColdStore-exact persistence ----------------------------------------
+    def attach_cold_store(self, seq: int, directory: str) -> None:
+        self._check("attach_cold_store", self._lib.mslim_model_attach_cold_store(
+            self._h, seq, os.fsencode(directory)))
+
+    def detach_cold_store(self, seq: int) -> None:
+        self._check("detach_cold_store", self._lib.mslim_model_detach_cold_store(self._h, seq))
+
+    def flush_cold(self, seq: int) -> None:
+        """End-of-turn commit of every token past the committed prefix."""
+        self._check("flush_cold", self._lib.mslim_model_flush_cold(self._h, seq))
+
+    def restore_session(self, seq: int, tokens: int) -> None:
+        self._check("restore_session", self._lib.mslim_model_restore_session(self._h, seq, tokens))
+
+    def cold_logical_kv_sha256(self, seq: int) -> str:
+        out = C.create_string_buffer(65)
+        self._check("cold_logical_kv_sha256", self._lib.mslim_model_cold_logical_kv_sha256(self._h, seq, out))
+        return out.value.decode()
+
+    def cold_report(self, seq: int) -> dict:
+        r = ColdReport()
+        self._check("cold_report", self._lib.mslim_model_cold_report(self._h, seq, C.byref(r)))
+        return r.as_dict()
+
+
+def synthetic_weights(spec: ModelSpec, seed: int, scale: float = 0.02, embed_scale: float = 0.02,
+                      norm_spread: float = 0.1) -> dict:
+    """Random-init BF16 device weights of the runner's layout from torch's
+    seeded device generator: projections, LM head and embedding N(0, scale^2)
+    (embedding N(0, embed_scale^2)), RMSNorm weights 1 + N(0, norm_spread^2),
+    each rounded to BF16.  Generation order: embedding, final norm, LM head,
+    then every layer's LAYER_TENSORS in order, so a seed fixes every tensor.
+    Returns a dict of int16 device tensors (BF16 bits) keyed as Model expects.
+    """
+    import torch
+
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+
+    def normal(shape, sc):
+        return (torch.randn(shape, generator=gen, device="cuda") * sc).to(torch.bfloat16).view(torch.int16)
+
+    def norm():
+        return (1.0 + norm_spread * torch.randn(spec.hidden, generator=gen, device="cuda")).to(
+            torch.bfloat16).view(torch.int16)
+
+    qd, kvd = spec.q_heads * spec.head_dim, spec.kv_heads * spec.head_dim
+    shapes = {"q": (qd, spec.hidden), "k": (kvd, spec.hidden), "v": (kvd, spec.hidden), "o": (spec.hidden, qd),
+              "gate": (spec.intermediate, spec.hidden), "up": (spec.intermediate, spec.hidden),
+              "down": (spec.hidden, spec.intermediate)}
+    w = {"embed": normal((spec.vocab, spec.hidden), embed_scale), "final_norm": norm(),
+         "lm_head": normal((spec.vocab, spec.hidden), scale)}
+    for l in range(spec.layers):
+        for name in LAYER_TENSORS:
+            w[f"layers.{l}.{name}"] = norm() if name.endswith("norm") else normal(shapes[name], scale)
+    return w
