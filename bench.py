@@ -109,6 +109,21 @@ def build_page_pool(ctx, torch, k_dense, v_dense, seed: int):
     return k_pool, v_pool, table_t, pages_per_seq
 
 
+def device_peak_figures(ctx) -> dict:
+    """The dense BF16 peak computed from what the device reports, beside the
+    published figure the roofline fraction uses: CUs x peak engine clock x
+    4,096 FLOP per clock per CU (gfx950 MFMA).  The memory clock and bus
+    width are reported as read; HBM3E moves more than two transfers per
+    reported clock, so no HBM peak is derived from them."""
+    info = ctx.device_info()
+    return {
+        "name": info["name"], "arch": info["arch"], "compute_units": info["compute_units"],
+        "max_clock_mhz": info["max_clock_mhz"], "memory_clock_mhz": info["memory_clock_mhz"],
+        "memory_bus_bits": info["memory_bus_bits"],
+        "bf16_tflops": round(info["compute_units"] * info["max_clock_mhz"] * 1e6 * 4096 / 1e12, 1),
+    }
+
+
 def cpu_threads() -> int:
     return max(1, min(16, os.cpu_count() or 1))
 
@@ -317,6 +332,93 @@ def cpu_decoder_baseline(host_layer: dict, host_head: dict, seconds: float):
     }
 
 
+def cold_store_run(torch, ctx, spec, weights, model, prompts, steps: int, plain_tokens) -> dict:
+    """cfg5 again on the same runner with a ColdStore-exact store attached to
+    every slot (the GPU-region runtime's persistence, gpu_llm/mod.rs:299-306):
+    each prefill commits its prompt's K/V at its end (prefill.rs:760-790),
+    the decode steps defer their commit, and the end-of-turn flush commits
+    the turn's tokens (flush_deferred_cold, mod.rs:1614-1699).  Checks: the
+    tokens equal the run without a store; the ColdStore digest read back
+    from each file equals the runner's digest of the slot (slots 0 and the
+    last); a fresh runner restores all slots from the files
+    (restore_session, mod.rs:1335-1451) and its next batched step gives the
+    same tokens and bit-identical logits as the uninterrupted runner."""
+    import shutil
+    import tempfile
+
+    import numpy as np
+
+    from mslim_attn.model import Model
+
+    root = tempfile.mkdtemp(prefix="mslim-cfg5-cold-")
+    try:
+        dirs = []
+        for b in range(DEC_BATCH):
+            model.reset(b)
+            dirs.append(os.path.join(root, f"slot{b}"))
+            os.makedirs(dirs[-1])
+            model.attach_cold_store(b, dirs[-1])
+        torch.cuda.synchronize()
+        log("bench: cfg5 prefill with ColdStore commit (paged)")
+        t0 = time.perf_counter()
+        first = [model.prefill_only(b, list(prompts[b])) for b in range(DEC_BATCH)]
+        torch.cuda.synchronize()
+        prefill_s = time.perf_counter() - t0
+        seal_s = sum(model.cold_report(b)["prefill_seal_seconds"] for b in range(DEC_BATCH))
+        log(f"bench: cfg5 {steps} decode steps with deferred commit (paged)")
+        tokens, generated = first, [first]
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            tokens = model.forward_batch(tokens)
+            generated.append(tokens)
+        decode_s = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        for b in range(DEC_BATCH):
+            model.flush_cold(b)
+        flush_s = time.perf_counter() - t0
+        committed = [model.cold_report(b)["committed_tokens"] for b in range(DEC_BATCH)]
+        log("bench: cfg5 ColdStore digests")
+        digests_equal = all(model.cold_logical_kv_sha256(b) == model.logical_kv_sha256(b)
+                            for b in (0, DEC_BATCH - 1))
+        want_next = model.forward_batch(tokens)
+        want_logits = model.logits().copy()
+        for b in range(DEC_BATCH):  # release each file's exclusive writer
+            model.detach_cold_store(b)
+        log("bench: cfg5 restore of every slot into a fresh runner")
+        fresh = Model(ctx, spec, weights, max_batch=DEC_BATCH, chunk_tokens=DEC_CHUNK,
+                      max_context=DEC_PROMPT + steps + 1, kv_layout="paged")
+        try:
+            t0 = time.perf_counter()
+            for b in range(DEC_BATCH):
+                fresh.attach_cold_store(b, dirs[b])
+                fresh.restore_session(b, DEC_PROMPT + steps)
+            torch.cuda.synchronize()
+            restore_s = time.perf_counter() - t0
+            got_next = fresh.forward_batch(tokens)
+            restored_equal = got_next == want_next and np.array_equal(fresh.logits(), want_logits)
+        finally:
+            fresh.close()
+        file_bytes = sum(os.path.getsize(os.path.join(d, "pages-exact.kv")) for d in dirs)
+    finally:
+        shutil.rmtree(root, ignore_errors=True)
+    return {
+        "prefill_tokens_per_s": round(DEC_BATCH * DEC_PROMPT / prefill_s, 1),
+        "prefill_s": round(prefill_s, 3),
+        "prefill_seal_s": round(seal_s, 3),
+        "decode_tokens_per_s": round(DEC_BATCH * steps / decode_s, 1),
+        "decode_with_flush_tokens_per_s": round(DEC_BATCH * steps / (decode_s + flush_s), 1),
+        "flush_s": round(flush_s, 3),
+        "restore_s": round(restore_s, 3),
+        "committed_tokens_per_slot": committed[0] if len(set(committed)) == 1 else committed,
+        "coldstore_file_bytes": file_bytes,
+        "tokens_equal_run_without_store": generated == plain_tokens,
+        "cold_digest_equals_runner_digest": digests_equal,
+        "restored_next_step_identical": restored_equal,
+        "timing": ("host wall clock; prefill_s includes the end-of-prefill commit, flush_s the end-of-turn "
+                   "commit of the decode tokens of all slots, restore_s the device-verified load of all slots"),
+    }
+
+
 def decoder_leg(torch, ctx, args, np):
     """cfg5 through the C++ decoder runner (libmslim_host): batch-8 prefill of
     seeded 4,096-token prompts in 512-token causal chunks, then `steps`
@@ -332,7 +434,7 @@ def decoder_leg(torch, ctx, args, np):
     runs = {}
     for layout in ("paged", "dense"):
         model = Model(ctx, spec, weights, max_batch=DEC_BATCH, chunk_tokens=DEC_CHUNK,
-                      max_context=DEC_PROMPT + steps, kv_layout=layout)
+                      max_context=DEC_PROMPT + steps + 1, kv_layout=layout)
         # untimed warm-up: one short prompt and one step (hipBLASLt plans)
         model.prefill_only(0, list(prompts[0, :DEC_CHUNK + 1]))
         model.forward_batch([0] * DEC_BATCH)
@@ -351,6 +453,8 @@ def decoder_leg(torch, ctx, args, np):
         decode_s = time.perf_counter() - t0
         runs[layout] = {"prefill_s": prefill_s, "decode_s": decode_s, "tokens": generated,
                         "digest": model.logical_kv_sha256(0)}
+        if layout == "paged" and args.cold:
+            runs["cold"] = cold_store_run(torch, ctx, spec, weights, model, prompts, steps, generated)
         model.close()
     p = runs["paged"]
     contexts = [DEC_PROMPT + i for i in range(steps)]
@@ -381,6 +485,8 @@ def decoder_leg(torch, ctx, args, np):
         "paged_equals_dense_kv_sha256": p["digest"] == runs["dense"]["digest"],
         "dense_decode_tokens_per_s": round(DEC_BATCH * steps / runs["dense"]["decode_s"], 1),
     }
+    if "cold" in runs:
+        result["coldstore"] = runs["cold"]
     if args.cpu_seconds > 0:
         log("bench: cfg5 CPU baseline (oracle decoder layer on one host core)")
 
@@ -469,9 +575,11 @@ def other_configs_leg(torch, ctx, np, steps: int) -> dict:
     flops2 = 2 * d * qh * s2 * (s2 + 1)
     out["cfg2_prefill"] = {"us": round(ms2 * 1e3, 2), "tflops": round(flops2 / (ms2 * 1e-3) / 1e12, 1),
                            "flop": flops2, "rope_qk_us": round(ms2r * 1e3, 2),
-                           "note": "256 workgroups (64 rows x 4 heads each), one per CU, of 1 to 32 "
-                                   "causal key tiles: the launch lasts as long as the longest, so the "
-                                   "chip is about half busy"}
+                           "split_chunk_tiles": mslim_attn.prefill_split_tiles(s2, 0, qh, kvh, d),
+                           "note": "256 (64-row block, 4-head group) tiles of 1 to 32 causal key "
+                                   "tiles; the long rows split into chunks of split_chunk_tiles key "
+                                   "tiles counted back from the diagonal, spread over the 8 XCDs "
+                                   "longest first, the last chunk of a row merging the partials"}
     # cfg3
     lens = np.random.default_rng(20261203).integers(512, 8193, size=32).tolist()
     nb = len(lens)
@@ -555,6 +663,8 @@ def main() -> int:
                     help="run one workload only, for counter collection")
     ap.add_argument("--decoder-steps", type=int, default=DEC_STEPS,
                     help="greedy steps of the cfg5 decoder leg (0 skips the leg)")
+    ap.add_argument("--no-cold", dest="cold", action="store_false",
+                    help="skip the cfg5 run with ColdStore persistence")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
@@ -575,6 +685,7 @@ def main() -> int:
         return copy_only(torch, args)
     ctx = mslim_attn.Context()
     ctx.use_torch_stream()
+    device_peaks = device_peak_figures(ctx)
     if args.kernel == "decoder":
         print(json.dumps(decoder_leg(torch, ctx, args, np)), flush=True)
         ctx.close()
@@ -646,28 +757,35 @@ def main() -> int:
     # prefill phase is preceded on the same stream, with no host wait, by
     # PREFILL_WARM untimed prefills; the events bracket exactly the K timed
     # launches of each phase.
+    # An event is recorded before every launch and after the last, so each
+    # launch's duration is measured and the roofline uses the median launch
+    # (the phase averages give ms_per_step).
     mk = lambda: torch.cuda.Event(enable_timing=True)
-    start_all, mid, pre_start, end_all = mk(), mk(), mk(), mk()
+    ev_dec = [mk() for _ in range(args.steps + 1)]
+    ev_pre = [mk() for _ in range(args.steps + 1)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     torch.cuda._sleep(QUEUE_FILL_CYCLES)
-    start_all.record()
-    for _ in range(args.steps):
+    for i in range(args.steps):
+        ev_dec[i].record()
         decode()
-    mid.record()
+    ev_dec[args.steps].record()
     for _ in range(PREFILL_WARM):
         prefill()
-    pre_start.record()
-    for _ in range(args.steps):
+    for i in range(args.steps):
+        ev_pre[i].record()
         prefill()
-    end_all.record()
+    ev_pre[args.steps].record()
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0 - mid.elapsed_time(pre_start) * 1e-3  # less the warm prefills
-    dec_avg = start_all.elapsed_time(mid) / args.steps
-    pre_avg = pre_start.elapsed_time(end_all) / args.steps
+    wall = time.perf_counter() - t0 - ev_dec[args.steps].elapsed_time(ev_pre[0]) * 1e-3  # less the warm prefills
+    dec_avg = ev_dec[0].elapsed_time(ev_dec[args.steps]) / args.steps
+    pre_avg = ev_pre[0].elapsed_time(ev_pre[args.steps]) / args.steps
+    dec_med = float(np.median([ev_dec[i].elapsed_time(ev_dec[i + 1]) for i in range(args.steps)]))
+    pre_med = float(np.median([ev_pre[i].elapsed_time(ev_pre[i + 1]) for i in range(args.steps)]))
     step_ms = dec_avg + pre_avg
     log(f"bench: {args.steps} steps, {step_ms:.3f} ms/step (wall {wall * 1e3 / args.steps:.3f}), "
-        f"decode {dec_avg * 1e3:.1f} us, prefill {pre_avg * 1e3:.1f} us")
+        f"decode {dec_avg * 1e3:.1f} us (median {dec_med * 1e3:.1f}), prefill {pre_avg * 1e3:.1f} us "
+        f"(median {pre_med * 1e3:.1f})")
 
     # Informational: decode launched directly after a prefill (the prefill's
     # output is still being written back and the clock is recovering).
@@ -711,8 +829,8 @@ def main() -> int:
     seal_ms = timed_calls(torch, seal, max(3, args.steps // 4))
     seal_payload = total_pages * 2 * KVH * PAGE_TOKENS * D * 2
 
-    dec_gbps = decode_bytes() / (dec_avg * 1e-3) / 1e9
-    pre_tflops = prefill_flops() / (pre_avg * 1e-3) / 1e12
+    dec_gbps = decode_bytes() / (dec_med * 1e-3) / 1e9
+    pre_tflops = prefill_flops() / (pre_med * 1e-3) / 1e12
     dense_gbps = decode_bytes() / (dense_ms * 1e-3) / 1e9
 
     traffic = measured_traffic("decode_paged_cfg4")
@@ -765,6 +883,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(dec_gbps / PEAK_HBM_GBPS, 4),
             "traffic": traffic,
+            "timing": "median of per-launch HIP event intervals over the timed launches",
             "kernel": "decode_kernel<128,8,paged,2,fused,non-temporal> (one launch; the last workgroup of "
                       f"each (sequence, kv head) merges the splits), algorithmic bytes {decode_bytes()} per launch",
         },
@@ -779,6 +898,8 @@ def main() -> int:
                 "unit": "TFLOP/s",
                 "frac": round(pre_tflops / PEAK_BF16_TFLOPS, 4),
                 "traffic": pre_traffic,
+                "timing": "median of per-launch HIP event intervals over the timed launches",
+                "peak_from_device": device_peaks["bf16_tflops"],
                 "kernel": f"prefill_mfma_kernel<128,8>, algorithmic FLOP {prefill_flops()} per launch",
             },
         },
@@ -794,6 +915,9 @@ def main() -> int:
         "decode_tokens_per_s": round(B / (dec_avg * 1e-3), 1),
         "prefill_tokens_per_s": round(S_PREFILL / (pre_avg * 1e-3), 1),
         "decode_ms": round(dec_avg, 5),
+        "decode_ms_median": round(dec_med, 5),
+        "prefill_ms_median": round(pre_med, 5),
+        "device": device_peaks,
         "decode_after_prefill_ms": round(dec_after_prefill, 5),
         "decode_dense_gbps": round(dense_gbps, 2),
         "paged_equals_dense": paged_equals_dense,

@@ -79,6 +79,9 @@ typedef struct {
     uint64_t global_memory_bytes;
     uint64_t max_allocation_bytes;
     uint32_t lds_bytes_per_workgroup;
+    uint32_t max_clock_mhz;     /* peak engine clock (hipDeviceProp_t::clockRate) */
+    uint32_t memory_clock_mhz;  /* peak memory clock (memoryClockRate) */
+    uint32_t memory_bus_bits;   /* memory interface width (memoryBusWidth) */
 } mslim_attn_device_info;
 int mslim_attn_get_device_info(void *ctx, mslim_attn_device_info *out);
 

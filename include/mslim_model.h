@@ -79,7 +79,10 @@ int mslim_model_generate(void *model, const int32_t *prompt, int tokens, int max
 
 /* Tokens held by slot `seq`, or -1 (GpuLlm::position, mod.rs:1314). */
 int64_t mslim_model_position(void *model, int seq);
-/* Empty slot `seq` (GpuLlm::reset_session, mod.rs:1530). */
+/* Empty slot `seq` (GpuLlm::reset_session, mod.rs:1530-1577).  With a
+ * ColdStore attached, deferred tokens are committed first and the slot
+ * continues in a fresh store at <parent>/session-<pid>-<nonce> beside the old
+ * directory, which keeps the finished session for a later restore. */
 int mslim_model_reset(void *model, int seq);
 /* BF16 bits of the last logits: 1 row after prefill, one per slot after a
  * batch step (GpuStep::logits, mod.rs:116-118). */
@@ -131,6 +134,9 @@ typedef struct {
     double last_restore_seconds;
 } mslim_model_cold_info;
 int mslim_model_cold_report(void *model, int seq, mslim_model_cold_info *out);
+/* Directory of the slot's ColdStore ("" when none is attached), with NUL;
+ * fails if it does not fit in `capacity` bytes. */
+int mslim_model_cold_directory(void *model, int seq, char *out, size_t capacity);
 
 #ifdef __cplusplus
 }

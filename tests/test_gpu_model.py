@@ -503,3 +503,43 @@ def test_runner_coldstore_commit_digest_and_restore(ctx, tmp_path):
         assert third.position(0) == 0
     finally:
         third.close()
+
+
+def test_runner_reset_with_coldstore_opens_fresh_namespace(ctx, tmp_path):
+    # reset_session (gpu_llm/mod.rs:1530-1577): deferred tokens are committed
+    # first, then the slot continues in a fresh store at
+    # <parent>/session-<pid>-<nonce>; the finished session stays on disk and
+    # a new prompt may be prefilled into the slot.
+    from mslim_attn.model import Model, ModelSpec
+
+    w = random_weights(SPEC, np.random.default_rng(20261203))
+    dev = {k: to_torch(v) for k, v in w.items()}
+    spec = ModelSpec(SPEC.layers, SPEC.hidden, SPEC.q_heads, SPEC.kv_heads, SPEC.head_dim,
+                     SPEC.intermediate, SPEC.vocab, SPEC.rms_eps, SPEC.rope_theta)
+    directory = str(tmp_path / "first")
+    os.makedirs(directory)
+    prompt = list(np.random.default_rng(43).integers(0, SPEC.vocab, 21))
+    model = Model(ctx, spec, dev, max_batch=1, chunk_tokens=16, max_context=64)
+    try:
+        model.attach_cold_store(0, directory)
+        tok = model.prefill_only(0, prompt)
+        for _ in range(3):
+            tok = model.forward_batch([tok])[0]
+        digest = model.logical_kv_sha256(0)
+        model.reset(0)
+        fresh = model.cold_directory(0)
+        assert os.path.dirname(fresh) == str(tmp_path)
+        assert os.path.basename(fresh).startswith(f"session-{os.getpid()}-")
+        report = model.cold_report(0)
+        assert report["attached"] and report["committed_tokens"] == 0 and model.position(0) == 0
+        model.prefill_only(0, prompt[:5])
+        assert model.cold_report(0)["committed_tokens"] == 5
+    finally:
+        model.close()
+    again = Model(ctx, spec, dev, max_batch=1, chunk_tokens=16, max_context=64)
+    try:
+        again.attach_cold_store(0, directory)
+        assert again.cold_report(0)["committed_tokens"] == len(prompt) + 3
+        assert again.cold_logical_kv_sha256(0) == digest
+    finally:
+        again.close()

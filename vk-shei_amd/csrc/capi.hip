@@ -286,6 +286,9 @@ int mslim_attn_get_device_info(void *ctx, mslim_attn_device_info *out) {
     out->global_memory_bytes = (uint64_t)prop.totalGlobalMem;
     out->max_allocation_bytes = (uint64_t)free_bytes;
     out->lds_bytes_per_workgroup = (uint32_t)prop.sharedMemPerBlock;
+    out->max_clock_mhz = (uint32_t)(prop.clockRate / 1000);
+    out->memory_clock_mhz = (uint32_t)(prop.memoryClockRate / 1000);
+    out->memory_bus_bits = (uint32_t)prop.memoryBusWidth;
     return 0;
 }
 

@@ -4,9 +4,13 @@
 #include <chrono>
 #include <climits>
 #include <cmath>
+#include <cerrno>
 #include <cstring>
 
 #include "../../include/mslim_model.h"
+
+#include <sys/stat.h>
+#include <unistd.h>
 
 namespace mslim {
 namespace model {
@@ -298,7 +302,34 @@ void DecoderRunner::set_calibration_prefill_settings(const PrefillSettings &sett
 
 void DecoderRunner::reset(int seq) {
     ensure(seq >= 0 && seq < max_batch_, "sequence slot out of range");
+    if (cold_[seq]) {
+        // reset_session (gpu_llm/mod.rs:1530-1577): commit what is deferred,
+        // then continue in a fresh ColdStore namespace
+        // <parent>/session-<pid>-<nonce> beside the current directory, so
+        // the finished session stays on disk for a later restore.
+        if (cold_report_[seq].committed_tokens < positions_[seq]) flush_cold(seq);
+        std::string current = *cold_[seq]->config().cold_directory;
+        while (current.size() > 1 && current.back() == '/') current.pop_back();
+        const size_t cut = current.find_last_of('/');
+        const std::string root = cut == std::string::npos ? std::string(".") : cut == 0 ? std::string("/")
+                                                                                         : current.substr(0, cut);
+        const long long nonce = (long long)std::chrono::duration_cast<std::chrono::nanoseconds>(
+                                    std::chrono::system_clock::now().time_since_epoch()).count();
+        const std::string next = root + (root == "/" ? "" : "/") + "session-" + std::to_string((long long)getpid()) +
+                                 "-" + std::to_string(nonce);
+        ensure(mkdir(next.c_str(), 0777) == 0 || errno == EEXIST,
+               "create canonical ColdStore namespace " + next + ": " + std::strerror(errno));
+        cold_[seq].reset();
+        positions_[seq] = 0;
+        attach_cold_store(seq, next);
+        return;
+    }
     positions_[seq] = 0;
+}
+
+std::string DecoderRunner::cold_directory(int seq) const {
+    ensure(seq >= 0 && seq < max_batch_, "sequence slot out of range");
+    return cold_[seq] ? *cold_[seq]->config().cold_directory : std::string();
 }
 
 region::DevicePagePool DecoderRunner::all_layer_pool() const {
@@ -650,6 +681,19 @@ int mslim_model_cold_logical_kv_sha256(void *model, int seq, char *hex_out) {
         mslim::ensure(hex_out != nullptr, "null digest buffer");
         const std::string hex = runner_of(model).cold_logical_kv_sha256(seq);
         std::memcpy(hex_out, hex.c_str(), hex.size() + 1);
+        return 0;
+    } catch (const std::exception &e) {
+        return model_fail(e);
+    }
+}
+
+int mslim_model_cold_directory(void *model, int seq, char *out, size_t capacity) {
+    g_model_error.clear();
+    try {
+        mslim::ensure(out != nullptr, "null output");
+        const std::string dir = runner_of(model).cold_directory(seq);
+        mslim::ensure(dir.size() < capacity, "ColdStore directory does not fit in the output buffer");
+        std::memcpy(out, dir.c_str(), dir.size() + 1);
         return 0;
     } catch (const std::exception &e) {
         return model_fail(e);

@@ -92,6 +92,10 @@ public:
     // (generate_cancellable, mod.rs:2587-2700).  Returns the generated tokens.
     std::vector<int32_t> generate(int seq, const std::vector<int32_t> &prompt, int max_new,
                                   const std::vector<int32_t> &eos_ids);
+    // Empty slot `seq`.  With a ColdStore attached, deferred tokens are
+    // committed first and the slot continues in a fresh store at
+    // <parent>/session-<pid>-<nonce> beside the old directory
+    // (reset_session, gpu_llm/mod.rs:1530-1577).
     void reset(int seq);
     // BF16 logits of the last prefill (1 row) or forward_batch (one row per
     // slot), as raw bits.
@@ -128,6 +132,8 @@ public:
     void restore_session(int seq, int64_t tokens);
     std::string cold_logical_kv_sha256(int seq);
     ColdReport cold_report(int seq) const;
+    // Directory of the slot's ColdStore; empty when none is attached.
+    std::string cold_directory(int seq) const;
 
 private:
     void *alloc(size_t bytes);

@@ -34,7 +34,8 @@ class DeviceInfo(C.Structure):
     _fields_ = [("name", C.c_char * 256), ("arch", C.c_char * 64), ("vendor", C.c_char * 64),
                 ("driver_version", C.c_int), ("compute_units", C.c_uint32),
                 ("global_memory_bytes", C.c_uint64), ("max_allocation_bytes", C.c_uint64),
-                ("lds_bytes_per_workgroup", C.c_uint32)]
+                ("lds_bytes_per_workgroup", C.c_uint32), ("max_clock_mhz", C.c_uint32),
+                ("memory_clock_mhz", C.c_uint32), ("memory_bus_bits", C.c_uint32)]
 
 
 class Timings(C.Structure):

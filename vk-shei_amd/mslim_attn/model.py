@@ -34,6 +34,7 @@ MODEL_EXPORTS = (
     "mslim_model_restore_session",
     "mslim_model_cold_logical_kv_sha256",
     "mslim_model_cold_report",
+    "mslim_model_cold_directory",
 )
 
 
@@ -117,6 +118,7 @@ def host_library() -> C.CDLL:
         "mslim_model_restore_session": (I, [P, I, I64]),
         "mslim_model_cold_logical_kv_sha256": (I, [P, I, C.c_char_p]),
         "mslim_model_cold_report": (I, [P, I, C.POINTER(ColdReport)]),
+        "mslim_model_cold_directory": (I, [P, I, C.c_char_p, C.c_size_t]),
     }
     for name in MODEL_EXPORTS:
         res, args = sigs[name]
@@ -263,6 +265,12 @@ class Model:
         r = ColdReport()
         self._check("cold_report", self._lib.mslim_model_cold_report(self._h, seq, C.byref(r)))
         return r.as_dict()
+
+    def cold_directory(self, seq: int) -> str:
+        """Directory of the slot's ColdStore, "" when none is attached."""
+        out = C.create_string_buffer(4096)
+        self._check("cold_directory", self._lib.mslim_model_cold_directory(self._h, seq, out, 4096))
+        return os.fsdecode(out.value)
 
 
 def synthetic_weights(spec: ModelSpec, seed: int, scale: float = 0.02, embed_scale: float = 0.02,
