@@ -391,6 +391,8 @@ def cold_store_run(torch, ctx, spec, weights, model, prompts, steps: int, plain_
             t0 = time.perf_counter()
             for b in range(DEC_BATCH):
                 fresh.attach_cold_store(b, dirs[b])
+            attach_s = time.perf_counter() - t0
+            for b in range(DEC_BATCH):
                 fresh.restore_session(b, DEC_PROMPT + steps)
             torch.cuda.synchronize()
             restore_s = time.perf_counter() - t0
@@ -409,13 +411,16 @@ def cold_store_run(torch, ctx, spec, weights, model, prompts, steps: int, plain_
         "decode_with_flush_tokens_per_s": round(DEC_BATCH * steps / (decode_s + flush_s), 1),
         "flush_s": round(flush_s, 3),
         "restore_s": round(restore_s, 3),
+        "restore_open_s": round(attach_s, 3),
         "committed_tokens_per_slot": committed[0] if len(set(committed)) == 1 else committed,
         "coldstore_file_bytes": file_bytes,
         "tokens_equal_run_without_store": generated == plain_tokens,
         "cold_digest_equals_runner_digest": digests_equal,
         "restored_next_step_identical": restored_equal,
         "timing": ("host wall clock; prefill_s includes the end-of-prefill commit, flush_s the end-of-turn "
-                   "commit of the decode tokens of all slots, restore_s the device-verified load of all slots"),
+                   "commit of the decode tokens of all slots, restore_s the load of all slots: restore_open_s opening each store (every record verified on the "
+                   "host, twice, as the reference's open and catalogue rebuild do), then the device-verified "
+                   "copy into the page pool"),
     }
 
 

@@ -16,6 +16,7 @@
 #include <vector>
 
 #include "../../oracle/oracle.h"
+#include "../../vk-shei_amd/csrc/sha256.hpp"
 #include "../../vk-shei_amd/host/cold_store.hpp"
 #include "../../vk-shei_amd/host/json.hpp"
 #include "../../vk-shei_amd/host/native.hpp"
@@ -117,6 +118,59 @@ std::vector<uint8_t> oracle_record(uint64_t page_id, const PageGeometry &g, cons
 }  // namespace
 
 // ---- ColdStore: the reference's tests ------------------------------------------
+
+std::string sha_hex(const uint8_t d[32]) {
+    static const char digits[] = "0123456789abcdef";
+    std::string s;
+    for (int i = 0; i < 32; ++i) {
+        s.push_back(digits[d[i] >> 4]);
+        s.push_back(digits[d[i] & 15]);
+    }
+    return s;
+}
+
+// The host digest (SHA extensions when the CPU has them) against the FIPS
+// 180-4 example vectors, and against the portable compression and the
+// oracle's restatement on every length 0..300 and a multi-block message fed
+// in odd pieces (each padding boundary: 55, 56, 63, 64 bytes).
+TEST(sha256_host_paths_equal_fips_vectors_and_oracle) {
+    auto digest = [](const std::string &m) {
+        Sha256 sha;
+        sha.update(m.data(), m.size());
+        uint8_t d[32];
+        sha.finish(d);
+        return sha_hex(d);
+    };
+    CHECK(digest("") == "e3b0c44298fc1c149afbf4c8996fb92427ae41e4649b934ca495991b7852b855");
+    CHECK(digest("abc") == "ba7816bf8f01cfea414140de5dae2223b00361a396177a9cb410ff61f20015ad");
+    CHECK(digest("abcdbcdecdefdefgefghfghighijhijkijkljklmklmnlmnomnopnopq") ==
+          "248d6a61d20638b8e5c026930c3e6039a33ce45964ff2167f6ecedd419db06c1");
+    CHECK(digest(std::string(1000000, 'a')) == "cdc76e5c9914fb9281a1c7e284d73e67f1809a48a497200e046d39ccc7112cd0");
+    std::mt19937 rng(20261202);
+    std::vector<uint8_t> msg(4099);
+    for (auto &b : msg) b = (uint8_t)rng();
+    for (size_t n = 0; n <= 300; ++n) {
+        Sha256 sha;
+        sha.update(msg.data(), n);
+        uint8_t got[32], want[32];
+        sha.finish(got);
+        orc_sha256(msg.data(), n, want);
+        CHECK(std::memcmp(got, want, 32) == 0);
+    }
+    Sha256 pieces;
+    for (size_t at = 0, step = 1; at < msg.size(); at += step, step = step * 3 % 97 + 1)
+        pieces.update(msg.data() + at, std::min(step, msg.size() - at));
+    uint8_t got[32], want[32];
+    pieces.finish(got);
+    orc_sha256(msg.data(), msg.size(), want);
+    CHECK(std::memcmp(got, want, 32) == 0);
+    // The two compression paths on the same blocks.
+    uint32_t a[8] = {1, 2, 3, 4, 5, 6, 7, 8}, b[8] = {1, 2, 3, 4, 5, 6, 7, 8};
+    sha256_compress(a, msg.data(), msg.size() / 64);
+    sha256_compress_portable(b, msg.data(), msg.size() / 64);
+    CHECK(std::memcmp(a, b, sizeof a) == 0);
+    std::printf("sha256 host path: %s\n", sha256_uses_cpu_extensions() ? "x86 SHA extensions" : "portable");
+}
 
 TEST(cold_read_only_reopen_rejects_append_and_preserves_bytes) {
     TempPath t("readonly");

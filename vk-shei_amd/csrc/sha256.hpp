@@ -1,5 +1,8 @@
-// FIPS 180-4 SHA-256 for the logical K/V digest (the role the sha2 crate
-// plays at gpu_region_store.rs:350-370 and gpu_llm/mod.rs:1986-2027).
+// FIPS 180-4 SHA-256 for the ColdStore record digests and the logical K/V
+// digest (the role the sha2 crate plays at cold_store.rs:275-349 and
+// gpu_region_store.rs:350-370).  The block compression lives in
+// sha256_host.cpp (host code only): the x86 SHA extensions when the CPU has
+// them, a portable FIPS 180-4 loop otherwise.
 #pragma once
 
 #include <stddef.h>
@@ -7,6 +10,13 @@
 #include <string.h>
 
 namespace mslim {
+
+// Compress `blocks` 64-byte blocks into `state` (FIPS 180-4 section 6.2.2).
+void sha256_compress(uint32_t state[8], const uint8_t *data, size_t blocks);
+// The portable loop alone, for tests that compare the two paths.
+void sha256_compress_portable(uint32_t state[8], const uint8_t *data, size_t blocks);
+// True when sha256_compress uses the x86 SHA extensions.
+bool sha256_uses_cpu_extensions();
 
 class Sha256 {
 public:
@@ -24,65 +34,29 @@ public:
             memcpy(block_ + fill_, p, take);
             fill_ += take; p += take; n -= take;
             if (fill_ < 64) return;
-            compress(block_);
+            sha256_compress(state_, block_, 1);
             fill_ = 0;
         }
-        for (; n >= 64; n -= 64, p += 64) compress(p);
+        if (n >= 64) {
+            sha256_compress(state_, p, n / 64);
+            p += n & ~(size_t)63;
+            n &= 63;
+        }
         memcpy(block_, p, n);
         fill_ = n;
     }
 
     void finish(uint8_t out[32]) {
         const uint64_t bits = total_ * 8;
-        const uint8_t one = 0x80, zero = 0;
-        update(&one, 1);
-        while (fill_ != 56) update(&zero, 1);
-        uint8_t len[8];
-        for (int i = 0; i < 8; ++i) len[i] = (uint8_t)(bits >> (56 - 8 * i));
-        update(len, 8);
+        uint8_t pad[72] = {0x80};
+        const size_t zeros = (fill_ < 56 ? 56 - fill_ : 120 - fill_);
+        for (int i = 0; i < 8; ++i) pad[zeros + i] = (uint8_t)(bits >> (56 - 8 * i));
+        update(pad, zeros + 8);
         for (int i = 0; i < 8; ++i)
             for (int j = 0; j < 4; ++j) out[4 * i + j] = (uint8_t)(state_[i] >> (24 - 8 * j));
     }
 
 private:
-    static uint32_t rotr(uint32_t x, int n) { return (x >> n) | (x << (32 - n)); }
-
-    void compress(const uint8_t *p) {
-        static const uint32_t k[64] = {
-            0x428a2f98u, 0x71374491u, 0xb5c0fbcfu, 0xe9b5dba5u, 0x3956c25bu, 0x59f111f1u,
-            0x923f82a4u, 0xab1c5ed5u, 0xd807aa98u, 0x12835b01u, 0x243185beu, 0x550c7dc3u,
-            0x72be5d74u, 0x80deb1feu, 0x9bdc06a7u, 0xc19bf174u, 0xe49b69c1u, 0xefbe4786u,
-            0x0fc19dc6u, 0x240ca1ccu, 0x2de92c6fu, 0x4a7484aau, 0x5cb0a9dcu, 0x76f988dau,
-            0x983e5152u, 0xa831c66du, 0xb00327c8u, 0xbf597fc7u, 0xc6e00bf3u, 0xd5a79147u,
-            0x06ca6351u, 0x14292967u, 0x27b70a85u, 0x2e1b2138u, 0x4d2c6dfcu, 0x53380d13u,
-            0x650a7354u, 0x766a0abbu, 0x81c2c92eu, 0x92722c85u, 0xa2bfe8a1u, 0xa81a664bu,
-            0xc24b8b70u, 0xc76c51a3u, 0xd192e819u, 0xd6990624u, 0xf40e3585u, 0x106aa070u,
-            0x19a4c116u, 0x1e376c08u, 0x2748774cu, 0x34b0bcb5u, 0x391c0cb3u, 0x4ed8aa4au,
-            0x5b9cca4fu, 0x682e6ff3u, 0x748f82eeu, 0x78a5636fu, 0x84c87814u, 0x8cc70208u,
-            0x90befffau, 0xa4506cebu, 0xbef9a3f7u, 0xc67178f2u};
-        uint32_t w[64];
-        for (int i = 0; i < 16; ++i)
-            w[i] = (uint32_t)p[4 * i] << 24 | (uint32_t)p[4 * i + 1] << 16 |
-                   (uint32_t)p[4 * i + 2] << 8 | (uint32_t)p[4 * i + 3];
-        for (int i = 16; i < 64; ++i) {
-            const uint32_t s0 = rotr(w[i - 15], 7) ^ rotr(w[i - 15], 18) ^ (w[i - 15] >> 3);
-            const uint32_t s1 = rotr(w[i - 2], 17) ^ rotr(w[i - 2], 19) ^ (w[i - 2] >> 10);
-            w[i] = w[i - 16] + s0 + w[i - 7] + s1;
-        }
-        uint32_t v[8];
-        memcpy(v, state_, sizeof v);
-        for (int i = 0; i < 64; ++i) {
-            const uint32_t ch = (v[4] & v[5]) ^ (~v[4] & v[6]);
-            const uint32_t t1 = v[7] + (rotr(v[4], 6) ^ rotr(v[4], 11) ^ rotr(v[4], 25)) + ch + k[i] + w[i];
-            const uint32_t maj = (v[0] & v[1]) ^ (v[0] & v[2]) ^ (v[1] & v[2]);
-            const uint32_t t2 = (rotr(v[0], 2) ^ rotr(v[0], 13) ^ rotr(v[0], 22)) + maj;
-            memmove(v + 1, v, 7 * sizeof(uint32_t));
-            v[4] += t1;
-            v[0] = t1 + t2;
-        }
-        for (int i = 0; i < 8; ++i) state_[i] += v[i];
-    }
-
     uint32_t state_[8];
     uint8_t block_[64];
     size_t fill_ = 0;

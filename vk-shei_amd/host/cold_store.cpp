@@ -63,6 +63,54 @@ struct Span {
     size_t n;
 };
 
+// FNV-1a 64 of the same bytes continued in two states: a record checksum and
+// a payload checksum read every payload byte in the same order, and the two
+// multiply chains overlap in the pipeline instead of running back to back.
+void fnv1a64_two(const uint8_t *b, size_t n, uint64_t &first, uint64_t &second) {
+    uint64_t x = first, y = second;
+    for (size_t i = 0; i < n; ++i) {
+        x = (x ^ b[i]) * kFnvPrime;
+        y = (y ^ b[i]) * kFnvPrime;
+    }
+    first = x;
+    second = y;
+}
+
+// Run fn(i) for i in [0, n) on up to `threads` threads; the exception of the
+// smallest failing index is rethrown, so a parallel check reports the same
+// first failure as a sequential one.
+template <class F>
+void parallel_indices(size_t n, size_t threads, F fn) {
+    std::atomic<size_t> next{0};
+    std::mutex m;
+    size_t failed = SIZE_MAX;
+    std::exception_ptr error;
+    auto worker = [&] {
+        for (size_t i = next++; i < n; i = next++) {
+            try {
+                fn(i);
+            } catch (...) {
+                std::lock_guard<std::mutex> g(m);
+                if (i < failed) {
+                    failed = i;
+                    error = std::current_exception();
+                }
+            }
+        }
+    };
+    threads = std::max<size_t>(1, std::min(threads, n));
+    std::vector<std::thread> pool;
+    for (size_t t = 1; t < threads; ++t) pool.emplace_back(worker);
+    worker();
+    for (auto &t : pool) t.join();
+    if (error) std::rethrow_exception(error);
+}
+
+size_t verify_threads() {
+    const unsigned hw = std::thread::hardware_concurrency();
+    return std::min<size_t>(16, hw ? hw : 1);
+}
+
 uint64_t checksum_many(std::initializer_list<Span> parts) {
     uint64_t s = kFnvOffset;
     for (const Span &part : parts) s = fnv1a64(part.p, part.n, s);
@@ -158,8 +206,15 @@ ColdPagePayload read_and_verify(int fd, const PageMeta &m) {
     read_exact_at(fd, m.payload_offset, out.key.data(), out.key.size());
     read_exact_at(fd, m.payload_offset + m.key_len, out.value.data(), out.value.size());
     const std::string page = std::to_string(m.page_id);
-    if (fnv1a64(out.key.data(), out.key.size()) != m.key_checksum ||
-        fnv1a64(out.value.data(), out.value.size()) != m.value_checksum ||
+    // The record checksum runs over header, hash tables, K and V; the K and V
+    // checksums ride along on the same pass.
+    uint64_t record = checksum_many({{header.data(), header.size()},
+                                     {key_hashes.data(), key_hashes.size()},
+                                     {value_hashes.data(), value_hashes.size()}});
+    uint64_t key_sum = kFnvOffset, value_sum = kFnvOffset;
+    fnv1a64_two(out.key.data(), out.key.size(), record, key_sum);
+    fnv1a64_two(out.value.data(), out.value.size(), record, value_sum);
+    if (key_sum != m.key_checksum || value_sum != m.value_checksum ||
         fnv1a64(key_hashes.data(), key_hashes.size()) != m.key_hashes_checksum ||
         fnv1a64(value_hashes.data(), value_hashes.size()) != m.value_hashes_checksum)
         invalid("invalid K/V checksum in page " + page);
@@ -171,7 +226,7 @@ ColdPagePayload read_and_verify(int fd, const PageMeta &m) {
                                                {value_hashes.data(), value_hashes.size()},
                                                {out.key.data(), out.key.size()},
                                                {out.value.data(), out.value.size()}};
-    if (checksum_many(parts) != m.record_checksum) invalid("invalid record checksum in page " + page);
+    if (record != m.record_checksum) invalid("invalid record checksum in page " + page);
     uint8_t digest[32];
     digest_many(parts, digest);
     if (std::memcmp(digest, m.record_digest, 32) != 0) invalid("invalid cryptographic digest in page " + page);
@@ -195,9 +250,13 @@ void verify_mapped_record(const uint8_t *map, uint64_t map_len, const PageMeta &
     if (std::memcmp(footer.p, kFooterMagic, 8) != 0 || get_u64(footer.p, 8) != m.record_checksum ||
         get_u64(footer.p, 16) != m.record_len || std::memcmp(footer.p + 24, m.record_digest, 32) != 0)
         invalid("invalid mapped commit in page " + page);
-    if (fnv1a64(key.p, key.n) != m.key_checksum || fnv1a64(value.p, value.n) != m.value_checksum ||
+    uint64_t record = checksum_many({header, kh, vh});
+    uint64_t key_sum = kFnvOffset, value_sum = kFnvOffset;
+    fnv1a64_two(key.p, key.n, record, key_sum);
+    fnv1a64_two(value.p, value.n, record, value_sum);
+    if (key_sum != m.key_checksum || value_sum != m.value_checksum ||
         fnv1a64(kh.p, kh.n) != m.key_hashes_checksum || fnv1a64(vh.p, vh.n) != m.value_hashes_checksum ||
-        checksum_many({header, kh, vh, key, value}) != m.record_checksum)
+        record != m.record_checksum)
         invalid("invalid mapped checksum in page " + page);
     uint8_t digest[32];
     digest_many({header, kh, vh, key, value}, digest);
@@ -218,7 +277,26 @@ uint64_t fnv1a64(const uint8_t *bytes, size_t n, uint64_t state) {
 std::vector<uint64_t> token_hashes(const uint8_t *payload, size_t len, const PageGeometry &g) {
     const size_t per = bytes_per_head_token(len, g);
     std::vector<uint64_t> out(g.tokens);
-    for (uint32_t t = 0; t < g.tokens; ++t) {
+    uint32_t t0 = 0;
+    // Four tokens at a time: their rows sit side by side in each head's
+    // block, and the four chains are independent.
+    for (; t0 + 4 <= g.tokens; t0 += 4) {
+        uint64_t s0 = kFnvOffset, s1 = kFnvOffset, s2 = kFnvOffset, s3 = kFnvOffset;
+        for (uint32_t h = 0; h < g.heads; ++h) {
+            const uint8_t *p = payload + ((size_t)h * g.tokens + t0) * per;
+            for (size_t i = 0; i < per; ++i) {
+                s0 = (s0 ^ p[i]) * kFnvPrime;
+                s1 = (s1 ^ p[per + i]) * kFnvPrime;
+                s2 = (s2 ^ p[2 * per + i]) * kFnvPrime;
+                s3 = (s3 ^ p[3 * per + i]) * kFnvPrime;
+            }
+        }
+        out[t0] = s0;
+        out[t0 + 1] = s1;
+        out[t0 + 2] = s2;
+        out[t0 + 3] = s3;
+    }
+    for (uint32_t t = t0; t < g.tokens; ++t) {
         uint64_t s = kFnvOffset;
         for (uint32_t h = 0; h < g.heads; ++h) s = fnv1a64(payload + ((size_t)h * g.tokens + t) * per, per, s);
         out[t] = s;
@@ -330,33 +408,19 @@ void ColdStore::audit_mapped() {
     void *map = mmap(nullptr, (size_t)len, PROT_READ, MAP_SHARED, fd_, 0);
     if (map == MAP_FAILED) io_error("mmap " + path_, errno);
     const uint8_t *bytes = static_cast<const uint8_t *>(map);
-    std::atomic<size_t> next{0};
-    std::exception_ptr error;
-    std::mutex error_mutex;
-    auto worker = [&] {
-        for (size_t i = next++; i < pages_.size(); i = next++) {
-            try {
-                verify_mapped_record(bytes, len, pages_[i]);
-            } catch (...) {
-                std::lock_guard<std::mutex> g(error_mutex);
-                if (!error) error = std::current_exception();
-                next = pages_.size();
-            }
-        }
-    };
-    const size_t nthreads =
-        std::max<size_t>(1, std::min<size_t>(pages_.size(), std::max(1u, std::thread::hardware_concurrency())));
-    std::vector<std::thread> pool;
-    for (size_t t = 1; t < nthreads; ++t) pool.emplace_back(worker);
-    worker();
-    for (auto &t : pool) t.join();
+    try {
+        parallel_indices(pages_.size(), verify_threads(),
+                         [&](size_t i) { verify_mapped_record(bytes, len, pages_[i]); });
+    } catch (...) {
+        munmap(map, (size_t)len);
+        throw;
+    }
     munmap(map, (size_t)len);
-    if (error) std::rethrow_exception(error);
     cryptographic_digests_verified_ += pages_.size();
 }
 
 void ColdStore::audit() const {
-    for (const PageMeta &m : pages_) read_and_verify(fd_, m);
+    parallel_indices(pages_.size(), verify_threads(), [&](size_t i) { read_and_verify(fd_, pages_[i]); });
 }
 
 // ---- append ------------------------------------------------------------------
@@ -523,31 +587,42 @@ PageMeta ColdStore::append_framed(const uint8_t *frame, size_t frame_len, const 
 // ---- catalogue ---------------------------------------------------------------
 
 void ColdStore::rebuild_catalogue() {
-    // cold_store.rs:641-687
+    // cold_store.rs:641-687: walk the headers and footers in file order, then
+    // verify every record (on several threads; the first failure in file
+    // order is the one reported, before any structural error found later in
+    // the file, as the sequential walk reports).
     const uint64_t len = file_len(fd_);
     uint64_t offset = 0;
-    while (offset < len) {
-        const uint64_t remaining = len - offset;
-        if (remaining < kHeaderLen) break;  // torn uncommitted tail
-        uint8_t header[kHeaderLen];
-        read_exact_at(fd_, offset, header, kHeaderLen);
-        PageMeta m = parse_header(header, offset);
-        const uint64_t record_len =
-            kHeaderLen + (uint64_t)m.geometry.tokens * 16 + m.key_len + m.value_len + kFooterLen;
-        if (record_len > remaining) break;  // footer cannot exist: never committed
-        uint8_t footer[kFooterLen];
-        read_exact_at(fd_, offset + record_len - kFooterLen, footer, kFooterLen);
-        if (std::memcmp(footer, kFooterMagic, 8) != 0) invalid("invalid KV commit footer");
-        if (get_u64(footer, 16) != record_len) invalid("inconsistent KV record length");
-        if (m.page_id != pages_.size()) invalid("KV page_id sequence is not monotonic");
-        m.record_checksum = get_u64(footer, 8);
-        std::memcpy(m.record_digest, footer + 24, 32);
-        m.record_len = record_len;
-        read_and_verify(fd_, m);
-        pages_.push_back(m);
-        committed_bytes_ += record_len;
-        offset += record_len;
+    std::vector<PageMeta> found;
+    std::exception_ptr structural;
+    try {
+        while (offset < len) {
+            const uint64_t remaining = len - offset;
+            if (remaining < kHeaderLen) break;  // torn uncommitted tail
+            uint8_t header[kHeaderLen];
+            read_exact_at(fd_, offset, header, kHeaderLen);
+            PageMeta m = parse_header(header, offset);
+            const uint64_t record_len =
+                kHeaderLen + (uint64_t)m.geometry.tokens * 16 + m.key_len + m.value_len + kFooterLen;
+            if (record_len > remaining) break;  // footer cannot exist: never committed
+            uint8_t footer[kFooterLen];
+            read_exact_at(fd_, offset + record_len - kFooterLen, footer, kFooterLen);
+            if (std::memcmp(footer, kFooterMagic, 8) != 0) invalid("invalid KV commit footer");
+            if (get_u64(footer, 16) != record_len) invalid("inconsistent KV record length");
+            if (m.page_id != found.size()) invalid("KV page_id sequence is not monotonic");
+            m.record_checksum = get_u64(footer, 8);
+            std::memcpy(m.record_digest, footer + 24, 32);
+            m.record_len = record_len;
+            found.push_back(m);
+            offset += record_len;
+        }
+    } catch (const ColdStoreError &) {
+        structural = std::current_exception();
     }
+    parallel_indices(found.size(), verify_threads(), [&](size_t i) { read_and_verify(fd_, found[i]); });
+    if (structural) std::rethrow_exception(structural);
+    for (const PageMeta &m : found) committed_bytes_ += m.record_len;
+    pages_ = std::move(found);
     // Only bytes after the last commit footer are discarded; a read-only
     // store never modifies the file.
     if (offset < len && !read_only_) {
@@ -594,6 +669,20 @@ std::shared_ptr<const ColdPagePayload> ColdStore::read_page(uint64_t page_id) {
         touch(page_id);
     }
     return payload;
+}
+
+void ColdStore::for_each_verified(const std::vector<uint64_t> &ids,
+                                  const std::function<void(size_t, const ColdPagePayload &)> &fn) {
+    std::vector<const PageMeta *> metas;
+    metas.reserve(ids.size());
+    for (uint64_t id : ids) metas.push_back(&page_meta(id));
+    parallel_indices(ids.size(), verify_threads(), [&](size_t i) { fn(i, read_and_verify(fd_, *metas[i])); });
+    for (const PageMeta *m : metas) {
+        ++misses_;
+        ++reads_;
+        ++cryptographic_digests_verified_;
+        bytes_read_ += m->record_len - kFooterLen;
+    }
 }
 
 std::vector<uint8_t> ColdStore::read_key(uint64_t page_id) {
@@ -698,17 +787,26 @@ std::vector<uint8_t> ColdStore::read_token_subset(uint64_t page_id, const std::v
 
 void ColdStore::read_record_raw(uint64_t page_id, uint32_t slot_tokens, std::vector<uint8_t> &frame,
                                 std::vector<uint8_t> &key, std::vector<uint8_t> &value) {
+    const PageMeta &m = page_meta(page_id);
+    frame.resize(kHeaderLen + 16ull * slot_tokens + kFooterLen);
+    key.resize(m.key_len);
+    value.resize(m.value_len);
+    read_record_into(page_id, slot_tokens, frame.data(), key.data(), value.data());
+}
+
+void ColdStore::read_record_into(uint64_t page_id, uint32_t slot_tokens, uint8_t *frame, uint8_t *key,
+                                 uint8_t *value) {
     const PageMeta m = page_meta(page_id);
     if (m.geometry.tokens > slot_tokens) invalid("KV record has more tokens than the frame slot");
     const size_t prefix = kHeaderLen + 16ull * m.geometry.tokens;
-    frame.assign(kHeaderLen + 16ull * slot_tokens + kFooterLen, 0);
-    read_exact_at(fd_, m.record_offset, frame.data(), prefix);
-    read_exact_at(fd_, m.record_offset + m.record_len - kFooterLen, frame.data() + frame.size() - kFooterLen,
-                  kFooterLen);
-    key.resize(m.key_len);
-    value.resize(m.value_len);
-    read_exact_at(fd_, m.payload_offset, key.data(), key.size());
-    read_exact_at(fd_, m.payload_offset + m.key_len, value.data(), value.size());
+    const size_t frame_len = kHeaderLen + 16ull * slot_tokens + kFooterLen;
+    // Header and hash tables, then (after the payloads) the footer: the
+    // record's first `prefix` bytes and its last kFooterLen bytes.
+    read_exact_at(fd_, m.record_offset, frame, prefix);
+    std::memset(frame + prefix, 0, frame_len - kFooterLen - prefix);
+    read_exact_at(fd_, m.record_offset + m.record_len - kFooterLen, frame + frame_len - kFooterLen, kFooterLen);
+    read_exact_at(fd_, m.payload_offset, key, m.key_len);
+    read_exact_at(fd_, m.payload_offset + m.key_len, value, m.value_len);
     ++reads_;
     ++misses_;
     bytes_read_ += m.record_len;

@@ -21,6 +21,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <deque>
+#include <functional>
 #include <memory>
 #include <optional>
 #include <stdexcept>
@@ -160,6 +161,13 @@ public:
 
     // cold_store.rs:412-447
     std::shared_ptr<const ColdPagePayload> read_page(uint64_t page_id);
+    // read_page for many records at once, on several threads: each record is
+    // read and verified afresh (the LRU cache is neither consulted nor
+    // filled) and handed to fn(i, payload) for ids[i], possibly concurrently;
+    // reads are counted as read_page misses.  The failure of the smallest
+    // index is rethrown, the one a sequential loop would report first.
+    void for_each_verified(const std::vector<uint64_t> &ids,
+                           const std::function<void(size_t, const ColdPagePayload &)> &fn);
     // cold_store.rs:449-477
     std::vector<uint8_t> read_key(uint64_t page_id);
     std::vector<uint8_t> read_value(uint64_t page_id);
@@ -172,6 +180,10 @@ public:
     // device by recomputing the frame.
     void read_record_raw(uint64_t page_id, uint32_t slot_tokens, std::vector<uint8_t> &frame,
                          std::vector<uint8_t> &key, std::vector<uint8_t> &value);
+    // The same into caller buffers: `frame` of kHeaderLen + 16 * slot_tokens
+    // + kFooterLen bytes (the rows of absent tokens zeroed), `key` and
+    // `value` of the record's payload lengths.
+    void read_record_into(uint64_t page_id, uint32_t slot_tokens, uint8_t *frame, uint8_t *key, uint8_t *value);
     // cold_store.rs:627-633
     void audit() const;
 

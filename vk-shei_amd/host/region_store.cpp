@@ -8,6 +8,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <exception>
 
 #include "../csrc/sha256.hpp"
 
@@ -70,7 +71,21 @@ std::string hex(const uint8_t *d, size_t n) {
     return s;
 }
 
-bool bf16_nonfinite(uint16_t bits) { return (bits & 0x7f80u) == 0x7f80u; }
+// Scan `count` little-endian BF16 values: returns the largest magnitude's
+// bits (sign cleared; among finite BF16 the integer order of these bits is
+// the order of |x|) and sets *nonfinite when any exponent field is all ones.
+// Integer-only so the loop vectorises.
+__attribute__((optimize("O3"))) uint16_t bf16_scan(const uint8_t *p, size_t count, bool *nonfinite) {
+    uint16_t top = 0;
+    for (size_t i = 0; i < count; ++i) {
+        uint16_t bits;
+        std::memcpy(&bits, p + 2 * i, 2);
+        const uint16_t mag = (uint16_t)(bits & 0x7fffu);
+        top = mag > top ? mag : top;
+    }
+    *nonfinite = top >= 0x7f80u;
+    return top;
+}
 
 }  // namespace
 
@@ -106,30 +121,51 @@ RegionStore::~RegionStore() {
 void RegionStore::restore_catalogue() {
     const std::vector<cold::PageMeta> metadata = cold_.metadata();
     if (metadata.empty()) return;
-    const size_t row_bytes = geometry_.head_dim * 2;
     const size_t token_bytes = geometry_.kv_elements_per_token() * 2;
-    for (const cold::PageMeta &meta : metadata) {
-        const size_t layer = meta.geometry.layer;
-        ensure(layer < pages_.size(), "persisted KV layer out of range");
-        ensure(meta.geometry.heads == geometry_.kv_heads && meta.geometry.head_dim == geometry_.head_dim,
-               "persisted KV geometry does not match model");
-        const size_t start = meta.geometry.token_start;
-        const size_t count = meta.geometry.tokens;
-        ensure(pages_[layer].size() == start, "persisted KV pages are not a contiguous causal prefix");
-        auto payload = cold_.read_page(meta.page_id);
-        ensure(payload->key.size() == count * token_bytes && payload->value.size() == count * token_bytes,
-               "persisted KV payload shape mismatch");
-        // Head-major V; every value must be finite (:246-261).
-        for (size_t head = 0; head < geometry_.kv_heads; ++head) {
-            for (size_t token = 0; token < count; ++token) {
-                const uint8_t *row = payload->value.data() + (head * count + token) * row_bytes;
-                for (size_t d = 0; d < geometry_.head_dim; ++d) {
-                    const float x = bf16_to_f32(load_u16(row + 2 * d));
-                    ensure(std::isfinite(x), "persisted KV contains nonfinite V");
-                    value_abs_max_[layer][head] = std::max(value_abs_max_[layer][head], (double)std::fabs(x));
-                }
-            }
+    const size_t kvh = geometry_.kv_heads;
+    // The shape of the catalogue first, in record order, up to the first
+    // record that does not fit it.
+    std::vector<size_t> held(pages_.size(), 0);
+    std::vector<uint64_t> ids;
+    ids.reserve(metadata.size());
+    std::exception_ptr shape_error;
+    try {
+        for (const cold::PageMeta &meta : metadata) {
+            const size_t layer = meta.geometry.layer;
+            ensure(layer < pages_.size(), "persisted KV layer out of range");
+            ensure(meta.geometry.heads == geometry_.kv_heads && meta.geometry.head_dim == geometry_.head_dim,
+                   "persisted KV geometry does not match model");
+            ensure(held[layer] == meta.geometry.token_start,
+                   "persisted KV pages are not a contiguous causal prefix");
+            held[layer] += meta.geometry.tokens;
+            ids.push_back(meta.page_id);
         }
+    } catch (const Error &) {
+        shape_error = std::current_exception();
+    }
+    // Every record before it read back and verified, then its V checked
+    // finite (gpu_region_store.rs:246-261) with per-head magnitude maxima;
+    // records on several threads.  The failure reported is the one a
+    // record-by-record walk meets first.
+    std::vector<uint16_t> top(ids.size() * kvh, 0);
+    cold_.for_each_verified(ids, [&](size_t i, const cold::ColdPagePayload &payload) {
+        const size_t count = metadata[i].geometry.tokens;
+        ensure(payload.key.size() == count * token_bytes && payload.value.size() == count * token_bytes,
+               "persisted KV payload shape mismatch");
+        const size_t head_bytes = count * geometry_.head_dim * 2;
+        for (size_t head = 0; head < kvh; ++head) {
+            bool bad = false;
+            top[i * kvh + head] = bf16_scan(payload.value.data() + head * head_bytes, head_bytes / 2, &bad);
+            ensure(!bad, "persisted KV contains nonfinite V");
+        }
+    });
+    if (shape_error) std::rethrow_exception(shape_error);
+    for (size_t i = 0; i < metadata.size(); ++i) {
+        const cold::PageMeta &meta = metadata[i];
+        const size_t layer = meta.geometry.layer, count = meta.geometry.tokens;
+        for (size_t head = 0; head < kvh; ++head)
+            value_abs_max_[layer][head] =
+                std::max(value_abs_max_[layer][head], (double)bf16_to_f32(top[i * kvh + head]));
         if (layer == 0) axis_tokens_ += count;
         for (size_t offset = 0; offset < count; ++offset) pages_[layer].push_back({meta.page_id, offset});
     }
@@ -447,15 +483,16 @@ void RegionStore::seal_device_layers(DeviceStaging &st, size_t position, size_t 
                 const size_t n = descs[i].tokens;
                 const uint8_t *kp = st.h_k + i * page_bytes;
                 const uint8_t *vp = st.h_v + i * page_bytes;
-                if (layer == 0)
-                    for (size_t j = 0; j < n * kvh * row_bytes; j += 2)
-                        ensure(!bf16_nonfinite(load_u16(kp + j)), "GPU ColdStore K nonfinite");
-                for (size_t hd = 0; hd < kvh; ++hd)
-                    for (size_t j = 0; j < n * row_bytes; j += 2) {
-                        const float x = bf16_to_f32(load_u16(vp + hd * n * row_bytes + j));
-                        ensure(std::isfinite(x), "GPU ColdStore V nonfinite");
-                        maxima[li - g0][hd] = std::max(maxima[li - g0][hd], (double)std::fabs(x));
-                    }
+                bool bad = false;
+                if (layer == 0) {
+                    bf16_scan(kp, n * kvh * row_bytes / 2, &bad);
+                    ensure(!bad, "GPU ColdStore K nonfinite");
+                }
+                for (size_t hd = 0; hd < kvh; ++hd) {
+                    const uint16_t top = bf16_scan(vp + hd * n * row_bytes, n * row_bytes / 2, &bad);
+                    ensure(!bad, "GPU ColdStore V nonfinite");
+                    maxima[li - g0][hd] = std::max(maxima[li - g0][hd], (double)bf16_to_f32(top));
+                }
             }
         }
         for (size_t li = g0; li < g1; ++li) {
@@ -513,14 +550,12 @@ size_t RegionStore::restore_device_layers(DeviceStaging &st, const DevicePagePoo
     if (records == 0) return 0;
     st.reserve(records, (size_t)slot, page_bytes);
     auto *descs = reinterpret_cast<mslim_attn_page_record *>(st.h_desc);
-    std::vector<uint8_t> frame, key, value;
     std::vector<uint8_t> stored(records * slot);
     for (size_t i = 0; i < records; ++i) {
         const cold::PageMeta &m = cold_.metadata().at(items[i].page_id);
-        cold_.read_record_raw(items[i].page_id, (uint32_t)P, frame, key, value);
-        std::memcpy(stored.data() + i * slot, frame.data(), slot);
-        std::memcpy(st.h_k + i * page_bytes, key.data(), key.size());
-        std::memcpy(st.h_v + i * page_bytes, value.data(), value.size());
+        ensure(m.key_len <= page_bytes && m.value_len <= page_bytes, "a persisted record exceeds a pool page");
+        cold_.read_record_into(items[i].page_id, (uint32_t)P, stored.data() + i * slot, st.h_k + i * page_bytes,
+                               st.h_v + i * page_bytes);
         descs[i].page_id = m.page_id;
         descs[i].token_start = m.geometry.token_start;
         descs[i].layer = m.geometry.layer;
