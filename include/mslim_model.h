@@ -112,6 +112,12 @@ int mslim_model_logical_kv_sha256(void *model, int seq, char *hex_out);
 int mslim_model_attach_cold_store(void *model, int seq, const char *directory);
 int mslim_model_detach_cold_store(void *model, int seq);
 int mslim_model_flush_cold(void *model, int seq);
+/* Deferred (1, the default) or immediate (0) commit of decode steps, the
+ * reference's mslim_deferred_cold_commit switch: in immediate mode every
+ * mslim_model_forward_batch commits each attached slot's new token before it
+ * returns (gpu_llm/mod.rs:2162-2164); switching to it first commits what is
+ * deferred. */
+int mslim_model_set_deferred_cold_commit(void *model, int deferred);
 /* Load the store's committed prefix of `tokens` tokens (every layer must hold
  * exactly that many) into empty slot `seq`, verifying every record on the
  * device (header, token hashes, checksums, SHA-256) before any byte reaches

@@ -199,9 +199,8 @@ class CpuDecoderOracle:
         s, w = self.s, self.w
         if seq not in self.sessions:
             self.reset(seq)
-        sess = self.sessions[seq]
         qd, kvd = s.q_heads * s.head_dim, s.kv_heads * s.head_dim
-        position = sess.tokens + self.rope_shift
+        position = self._tokens(seq) + self.rope_shift
         state = read_bf16(np.asarray(w["embed"]).reshape(-1, s.hidden)[int(token)]).astype(np.float32)
         for l in range(s.layers):
             g = lambda name: w[f"layers.{l}.{name}"]  # noqa: E731
@@ -211,9 +210,9 @@ class CpuDecoderOracle:
             v = matvec_cpu(g("v"), n, kvd, s.hidden)
             q = rope_cpu(q, s.q_heads, s.head_dim, position, s.rope_theta)
             k = rope_cpu(k, s.kv_heads, s.head_dim, position, s.rope_theta)
-            sess.keys[l] = np.concatenate([sess.keys[l], write_bf16(k).reshape(1, kvd)])
-            sess.values[l] = np.concatenate([sess.values[l], write_bf16(v).reshape(1, kvd)])
-            a = dense_attention_bf16(q, sess.keys[l], sess.values[l], s.q_heads, s.kv_heads, s.head_dim)
+            self._append_kv(seq, l, write_bf16(k).reshape(1, kvd), write_bf16(v).reshape(1, kvd))
+            keys, values = self._layer_kv(seq, l)
+            a = dense_attention_bf16(q, keys, values, s.q_heads, s.kv_heads, s.head_dim)
             state = round_bf16(state + matvec_cpu(g("o"), a, s.hidden, qd))
             n = rms_norm_cpu(state, self._vector(f"layers.{l}.post_norm"), s.rms_eps)
             gate = matvec_cpu(g("gate"), n, s.intermediate, s.hidden)
@@ -226,6 +225,22 @@ class CpuDecoderOracle:
         final = rms_norm_cpu(state, self._vector("final_norm"), s.rms_eps)
         logits = matvec_cpu(w["lm_head"], final, s.vocab, s.hidden)
         return logits, argmax_total_last(logits)
+
+    # Where a layer's K/V live: the hot dense route keeps token-major BF16
+    # rows in the session (native_cpu_adapter.rs:458-484 with a hot budget);
+    # a subclass may keep them elsewhere, e.g. in a ColdStore, and read them
+    # back for attention (:385-455).
+    def _append_kv(self, seq: int, layer: int, k_bits: np.ndarray, v_bits: np.ndarray) -> None:
+        sess = self.sessions[seq]
+        sess.keys[layer] = np.concatenate([sess.keys[layer], k_bits])
+        sess.values[layer] = np.concatenate([sess.values[layer], v_bits])
+
+    def _layer_kv(self, seq: int, layer: int) -> tuple:
+        sess = self.sessions[seq]
+        return sess.keys[layer], sess.values[layer]
+
+    def _tokens(self, seq: int) -> int:
+        return self.sessions[seq].tokens
 
     def prefill(self, seq: int, prompt) -> tuple:
         """(logits, greedy token) after the prompt, token by token; the slot restarts."""

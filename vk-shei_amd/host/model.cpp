@@ -233,44 +233,60 @@ std::vector<Step> DecoderRunner::forward_batch(const std::vector<int32_t> &token
         pos[i] = (int32_t)positions_[i];
         lens[i] = pos[i] + 1;
     }
-    std::lock_guard<std::mutex> lock(ctx_->mutex());
-    void *h = ctx_->handle();
-    const ModelSpec &s = spec_;
-    const int qd = s.q_heads * s.head_dim, kvd = s.kv_heads * s.head_dim;
-    ctx_->check("upload token ids", mslim_attn_buf_write(h, ids_, 0, reinterpret_cast<const uint8_t *>(tokens.data()),
-                                                         (size_t)b * 4));
-    ctx_->check("upload positions", mslim_attn_buf_write(h, pos_, 0, reinterpret_cast<const uint8_t *>(pos.data()),
-                                                         (size_t)b * 4));
-    ctx_->check("embed", mslim_attn_embed(h, w_.embed, s.vocab, s.hidden, ids_, b, x_, nullptr));
-    for (int l = 0; l < s.layers; ++l) {
-        const LayerWeights &w = w_.layers[l];
-        ctx_->check("input norm", mslim_attn_rmsnorm(h, x_, w.input_norm, norm_, b, s.hidden, s.rms_eps));
-        ctx_->check("QKV projection", mslim_attn_gemm_qkv(h, w.q, w.k, w.v, norm_, q_, k_, v_, s.hidden, qd, kvd, b));
-        ctx_->check("RoPE + K/V append",
-                    mslim_attn_rope_append(h, q_, k_, v_, qr_, k_pools_[l], v_pools_[l], table_, pages_per_seq_,
-                                           page_tokens_, b, pos_, s.q_heads, s.kv_heads, s.head_dim, s.rope_theta,
-                                           s.llama3, s.rope_factor, s.rope_low, s.rope_high, s.rope_original_max));
-        if (layout_ == KvLayout::Dense)
-            ctx_->check("dense attention",
-                        mslim_attn_decode_dense(h, qr_, k_pools_[l], v_pools_[l], attn_, b, lens.data(), max_context_,
-                                                s.q_heads, s.kv_heads, s.head_dim, scale_, 0));
-        else
-            ctx_->check("paged attention",
-                        mslim_attn_decode_paged(h, qr_, k_pools_[l], v_pools_[l], attn_, b, lens.data(), table_,
-                                                pages_per_seq_, kPageTokens, s.q_heads, s.kv_heads, s.head_dim,
-                                                scale_, 0));
-        mlp(w, b);
-    }
-    head(x_, b);
+    // The context lock covers the step's device work only: an immediate
+    // commit below takes it again.
     std::vector<int32_t> next(b);
-    ctx_->check("read greedy tokens", mslim_attn_buf_read(h, next_, 0, reinterpret_cast<uint8_t *>(next.data()),
-                                                          (size_t)b * 4));
+    {
+        std::lock_guard<std::mutex> lock(ctx_->mutex());
+        void *h = ctx_->handle();
+        const ModelSpec &s = spec_;
+        const int qd = s.q_heads * s.head_dim, kvd = s.kv_heads * s.head_dim;
+        ctx_->check("upload token ids",
+                    mslim_attn_buf_write(h, ids_, 0, reinterpret_cast<const uint8_t *>(tokens.data()), (size_t)b * 4));
+        ctx_->check("upload positions", mslim_attn_buf_write(h, pos_, 0, reinterpret_cast<const uint8_t *>(pos.data()),
+                                                             (size_t)b * 4));
+        ctx_->check("embed", mslim_attn_embed(h, w_.embed, s.vocab, s.hidden, ids_, b, x_, nullptr));
+        for (int l = 0; l < s.layers; ++l) {
+            const LayerWeights &w = w_.layers[l];
+            ctx_->check("input norm", mslim_attn_rmsnorm(h, x_, w.input_norm, norm_, b, s.hidden, s.rms_eps));
+            ctx_->check("QKV projection", mslim_attn_gemm_qkv(h, w.q, w.k, w.v, norm_, q_, k_, v_, s.hidden, qd, kvd, b));
+            ctx_->check("RoPE + K/V append",
+                        mslim_attn_rope_append(h, q_, k_, v_, qr_, k_pools_[l], v_pools_[l], table_, pages_per_seq_,
+                                               page_tokens_, b, pos_, s.q_heads, s.kv_heads, s.head_dim, s.rope_theta,
+                                               s.llama3, s.rope_factor, s.rope_low, s.rope_high, s.rope_original_max));
+            if (layout_ == KvLayout::Dense)
+                ctx_->check("dense attention",
+                            mslim_attn_decode_dense(h, qr_, k_pools_[l], v_pools_[l], attn_, b, lens.data(), max_context_,
+                                                    s.q_heads, s.kv_heads, s.head_dim, scale_, 0));
+            else
+                ctx_->check("paged attention",
+                            mslim_attn_decode_paged(h, qr_, k_pools_[l], v_pools_[l], attn_, b, lens.data(), table_,
+                                                    pages_per_seq_, kPageTokens, s.q_heads, s.kv_heads, s.head_dim,
+                                                    scale_, 0));
+            mlp(w, b);
+        }
+        head(x_, b);
+        ctx_->check("read greedy tokens", mslim_attn_buf_read(h, next_, 0, reinterpret_cast<uint8_t *>(next.data()),
+                                                              (size_t)b * 4));
+    }
     std::vector<Step> steps(b);
     for (int i = 0; i < b; ++i) {
         positions_[i] += 1;
         steps[i] = Step{next[i], positions_[i]};
     }
+    // Immediate mode (gpu_llm/mod.rs:2162-2164): each step's K/V is committed
+    // before the step returns.
+    if (!deferred_cold_)
+        for (int i = 0; i < b; ++i)
+            if (cold_[i]) flush_cold(i);
     return steps;
+}
+
+void DecoderRunner::set_deferred_cold_commit(bool deferred) {
+    if (!deferred)
+        for (int i = 0; i < max_batch_; ++i)
+            if (cold_[i] && cold_report_[i].committed_tokens < positions_[i]) flush_cold(i);
+    deferred_cold_ = deferred;
 }
 
 std::vector<int32_t> DecoderRunner::generate(int seq, const std::vector<int32_t> &prompt, int max_new,
@@ -681,6 +697,16 @@ int mslim_model_cold_logical_kv_sha256(void *model, int seq, char *hex_out) {
         mslim::ensure(hex_out != nullptr, "null digest buffer");
         const std::string hex = runner_of(model).cold_logical_kv_sha256(seq);
         std::memcpy(hex_out, hex.c_str(), hex.size() + 1);
+        return 0;
+    } catch (const std::exception &e) {
+        return model_fail(e);
+    }
+}
+
+int mslim_model_set_deferred_cold_commit(void *model, int deferred) {
+    g_model_error.clear();
+    try {
+        runner_of(model).set_deferred_cold_commit(deferred != 0);
         return 0;
     } catch (const std::exception &e) {
         return model_fail(e);

@@ -134,6 +134,11 @@ public:
     ColdReport cold_report(int seq) const;
     // Directory of the slot's ColdStore; empty when none is attached.
     std::string cold_directory(int seq) const;
+    // Deferred (default) or immediate commit of decode steps: the reference's
+    // mslim_deferred_cold_commit switch.  Immediate mode commits each step's
+    // K/V before forward_batch returns (gpu_llm/mod.rs:2162-2164); switching
+    // to it first commits what is deferred.
+    void set_deferred_cold_commit(bool deferred);
 
 private:
     void *alloc(size_t bytes);
@@ -167,6 +172,7 @@ private:
     std::vector<std::unique_ptr<region::RegionStore>> cold_;
     std::vector<ColdReport> cold_report_;
     std::unique_ptr<region::DeviceStaging> staging_;
+    bool deferred_cold_ = true;
     int32_t *table_ = nullptr, *ids_ = nullptr, *pos_ = nullptr, *next_ = nullptr;
     uint16_t *x_ = nullptr, *norm_ = nullptr, *q_ = nullptr, *k_ = nullptr, *v_ = nullptr, *qr_ = nullptr,
              *kr_ = nullptr, *attn_ = nullptr, *act_ = nullptr,

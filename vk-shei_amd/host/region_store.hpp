@@ -128,6 +128,7 @@ public:
     // axis, which observes layer-0 keys).
     size_t axis_token_len() const { return axis_tokens_; }
     size_t layer_tokens(size_t layer) const;
+    size_t layer_count() const { return pages_.size(); }
     const std::vector<double> &value_abs_max(size_t layer) const { return value_abs_max_.at(layer); }
 
     // gpu_region_store.rs:341-371 (hex digest)

@@ -35,6 +35,7 @@ MODEL_EXPORTS = (
     "mslim_model_cold_logical_kv_sha256",
     "mslim_model_cold_report",
     "mslim_model_cold_directory",
+    "mslim_model_set_deferred_cold_commit",
 )
 
 
@@ -119,6 +120,7 @@ def host_library() -> C.CDLL:
         "mslim_model_cold_logical_kv_sha256": (I, [P, I, C.c_char_p]),
         "mslim_model_cold_report": (I, [P, I, C.POINTER(ColdReport)]),
         "mslim_model_cold_directory": (I, [P, I, C.c_char_p, C.c_size_t]),
+        "mslim_model_set_deferred_cold_commit": (I, [P, I]),
     }
     for name in MODEL_EXPORTS:
         res, args = sigs[name]
@@ -265,6 +267,11 @@ class Model:
         r = ColdReport()
         self._check("cold_report", self._lib.mslim_model_cold_report(self._h, seq, C.byref(r)))
         return r.as_dict()
+
+    def set_deferred_cold_commit(self, deferred: bool) -> None:
+        """Deferred (default) or immediate commit of each decode step's K/V."""
+        self._check("set_deferred_cold_commit",
+                    self._lib.mslim_model_set_deferred_cold_commit(self._h, 1 if deferred else 0))
 
     def cold_directory(self, seq: int) -> str:
         """Directory of the slot's ColdStore, "" when none is attached."""
