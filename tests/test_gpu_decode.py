@@ -270,9 +270,10 @@ def _merge_modes(ctx, fn):
 
 
 def test_decode_merge_modes_bitwise_ragged(ctx):
-    # The fused merge (last workgroup of each (sequence, kv head), partials
-    # published with release / acquire on the split counter) and the
-    # two-launch merge read the same partials in the same fixed order.
+    # The fused merge (the last workgroup of each (sequence, kv head) to
+    # count its split merges, partials published by agent-scope stores that
+    # complete before the counter atomic) and the two-launch merge read the
+    # same partials in the same fixed order.
     rng = np.random.default_rng(31)
     qh, kvh, d, stride = 32, 8, 128, 6000
     lens = [1, 300, 6000, 257, 4096, 1023, 2, 5555]
