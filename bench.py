@@ -889,7 +889,7 @@ def main() -> int:
             "frac": round(dec_gbps / PEAK_HBM_GBPS, 4),
             "traffic": traffic,
             "timing": "median of per-launch HIP event intervals over the timed launches",
-            "kernel": "decode_kernel<128,8,paged,2,fused,non-temporal> (one launch; the last workgroup of "
+            "kernel": "decode_kernel<128,8,paged,fused,non-temporal> (one launch; the last workgroup of "
                       f"each (sequence, kv head) merges the splits), algorithmic bytes {decode_bytes()} per launch",
         },
         "prefill": {
