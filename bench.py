@@ -109,6 +109,12 @@ def build_page_pool(ctx, torch, k_dense, v_dense, seed: int):
     return k_pool, v_pool, table_t, pages_per_seq
 
 
+def group_sizes(steps: int) -> list:
+    """Sizes of the (at most four) groups of back-to-back timed launches."""
+    n = min(4, steps)
+    return [steps // n + (1 if i < steps % n else 0) for i in range(n)]
+
+
 def device_peak_figures(ctx) -> dict:
     """The dense BF16 peak computed from what the device reports, beside the
     published figure the roofline fraction uses: CUs x peak engine clock x
@@ -762,31 +768,35 @@ def main() -> int:
     # prefill phase is preceded on the same stream, with no host wait, by
     # PREFILL_WARM untimed prefills; the events bracket exactly the K timed
     # launches of each phase.
-    # An event is recorded before every launch and after the last, so each
-    # launch's duration is measured and the roofline uses the median launch
-    # (the phase averages give ms_per_step).
+    # Events bracket groups of back-to-back launches (four groups of
+    # steps / 4): an event between every launch would add ~3 us of gap to
+    # each.  The phase average is the sum of the groups over `steps`
+    # launches; the roofline uses the median of the group averages.
     mk = lambda: torch.cuda.Event(enable_timing=True)
-    ev_dec = [mk() for _ in range(args.steps + 1)]
-    ev_pre = [mk() for _ in range(args.steps + 1)]
+    groups = group_sizes(args.steps)
+    ev_dec = [mk() for _ in range(len(groups) + 1)]
+    ev_pre = [mk() for _ in range(len(groups) + 1)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     torch.cuda._sleep(QUEUE_FILL_CYCLES)
-    for i in range(args.steps):
-        ev_dec[i].record()
-        decode()
-    ev_dec[args.steps].record()
+    for g, n in enumerate(groups):
+        ev_dec[g].record()
+        for _ in range(n):
+            decode()
+    ev_dec[len(groups)].record()
     for _ in range(PREFILL_WARM):
         prefill()
-    for i in range(args.steps):
-        ev_pre[i].record()
-        prefill()
-    ev_pre[args.steps].record()
+    for g, n in enumerate(groups):
+        ev_pre[g].record()
+        for _ in range(n):
+            prefill()
+    ev_pre[len(groups)].record()
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0 - ev_dec[args.steps].elapsed_time(ev_pre[0]) * 1e-3  # less the warm prefills
-    dec_avg = ev_dec[0].elapsed_time(ev_dec[args.steps]) / args.steps
-    pre_avg = ev_pre[0].elapsed_time(ev_pre[args.steps]) / args.steps
-    dec_med = float(np.median([ev_dec[i].elapsed_time(ev_dec[i + 1]) for i in range(args.steps)]))
-    pre_med = float(np.median([ev_pre[i].elapsed_time(ev_pre[i + 1]) for i in range(args.steps)]))
+    wall = time.perf_counter() - t0 - ev_dec[len(groups)].elapsed_time(ev_pre[0]) * 1e-3  # less the warm prefills
+    dec_avg = ev_dec[0].elapsed_time(ev_dec[len(groups)]) / args.steps
+    pre_avg = ev_pre[0].elapsed_time(ev_pre[len(groups)]) / args.steps
+    dec_med = float(np.median([ev_dec[g].elapsed_time(ev_dec[g + 1]) / n for g, n in enumerate(groups)]))
+    pre_med = float(np.median([ev_pre[g].elapsed_time(ev_pre[g + 1]) / n for g, n in enumerate(groups)]))
     step_ms = dec_avg + pre_avg
     log(f"bench: {args.steps} steps, {step_ms:.3f} ms/step (wall {wall * 1e3 / args.steps:.3f}), "
         f"decode {dec_avg * 1e3:.1f} us (median {dec_med * 1e3:.1f}), prefill {pre_avg * 1e3:.1f} us "
@@ -888,7 +898,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(dec_gbps / PEAK_HBM_GBPS, 4),
             "traffic": traffic,
-            "timing": "median of per-launch HIP event intervals over the timed launches",
+            "timing": "median over four groups of back-to-back timed launches of the group's HIP-event average",
             "kernel": "decode_kernel<128,8,paged,fused,non-temporal> (one launch; the last workgroup of "
                       f"each (sequence, kv head) merges the splits), algorithmic bytes {decode_bytes()} per launch",
         },
@@ -903,7 +913,7 @@ def main() -> int:
                 "unit": "TFLOP/s",
                 "frac": round(pre_tflops / PEAK_BF16_TFLOPS, 4),
                 "traffic": pre_traffic,
-                "timing": "median of per-launch HIP event intervals over the timed launches",
+                "timing": "median over four groups of back-to-back timed launches of the group's HIP-event average",
                 "peak_from_device": device_peaks["bf16_tflops"],
                 "kernel": f"prefill_mfma_kernel<128,8>, algorithmic FLOP {prefill_flops()} per launch",
             },
