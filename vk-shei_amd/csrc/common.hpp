@@ -74,21 +74,23 @@ __device__ __forceinline__ uint32_t lds_offset(const void *lds) {
         (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)lds);
 }
 
-// The same copy as dma16, issued through inline assembly so that the
+// The same copy as dma16 from a wavefront-uniform base (an SGPR pair) plus
+// a per-lane 32-bit byte offset, issued through inline assembly so that the
 // compiler does not order later LDS reads behind it (it cannot tell which
 // LDS stage an in-flight copy targets and would wait for all of them).  The
 // caller waits for it explicitly: s_waitcnt vmcnt, then a barrier, before any
-// wavefront reads the destination.
+// wavefront reads the destination.  A loop over tiles advances only the
+// scalar base, so a copy costs no per-lane address arithmetic.
 // M0 is reserved by the compiler, so the asm saves and restores it.
-__device__ __forceinline__ void dma16_async(const void *global, uint32_t lds_base) {
+__device__ __forceinline__ void dma16_async(const void *base, uint32_t offset, uint32_t lds_base) {
     uint32_t saved;
     asm volatile(
         "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %2\n\t"
-        "global_load_lds_dwordx4 %1, off\n\t"
+        "s_mov_b32 m0, %3\n\t"
+        "global_load_lds_dwordx4 %1, %2\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(saved)
-        : "v"(global), "s"(lds_base)
+        : "v"(offset), "s"(base), "s"(lds_base)
         : "memory");
 }
 
@@ -111,12 +113,12 @@ __device__ __forceinline__ float add_bf16_pair(bf16x2_t pair, float acc) {
     return __builtin_amdgcn_fdot2_f32_bf16(pair, ones, acc, false);
 }
 
-// Maximum of a lane's value and its partner's in the other 32-lane half
-// (v_permlane32_swap: lanes 0-31 receive the upper half's values in the first
-// result, lanes 32-63 the lower half's in the second).
+// Maximum of a lane's value and its partner's in the other 32-lane half.
+// v_permlane32_swap on two copies of x leaves, in every lane, x itself in one
+// result and the partner's x in the other, so their maximum is the answer.
 __device__ __forceinline__ float half_pair_max(float x) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return __builtin_fmaxf(x, __builtin_fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1])));
+    return __builtin_fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
 // Keeps a value's computation at this point of the program: an empty asm

@@ -189,17 +189,48 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
     // Copy of one K/V tile: wavefront w moves chunks w, w+8, ...; lane l of
     // chunk ch lands at row RPC*ch + l/NSLOT, physical slot l % NSLOT and
     // fetches the logical slot that the swizzle maps there.  Keys past the
-    // history are clamped to the last key (they are masked).
-    auto dma_tile = [&](uint16_t *kd, uint16_t *vd, int kt) __attribute__((always_inline)) {
+    // history are clamped to the last key (they are masked); only the tile
+    // that holds the last key has such rows, and its copies use a second set
+    // of lane offsets.  Offsets are bytes from the tile's first row, so a copy
+    // needs only the scalar tile base (no per-lane 64-bit address arithmetic
+    // per tile).
+    const uint32_t row_bytes = (uint32_t)a.kv_heads * D * 2;
+    const int tile_last = last_key / kBN;
+    const int last_row = last_key - tile_last * kBN;
+    uint32_t koff[CPW], voff[CPW], kclamp[CPW], vclamp[CPW];
 #pragma unroll
-        for (int i = 0; i < CPW; ++i) {
-            const int ch = wave + WAVES * i;
-            const int r = S::RPC * ch + lane / S::NSLOT;
-            const int p = lane % S::NSLOT;
-            const int key = min(kt * kBN + r, last_key);
-            const int64_t base = ((int64_t)key * a.kv_heads + kvh) * D;
-            dma16_async(a.k + base + S::k(r, p) * 8, lds_offset(kd + ch * 512));
-            dma16_async(a.v + base + S::v(r, p) * 8, lds_offset(vd + ch * 512));
+    for (int i = 0; i < CPW; ++i) {
+        const int ch = wave + WAVES * i;
+        const int r = S::RPC * ch + lane / S::NSLOT;
+        const int p = lane % S::NSLOT;
+        const uint32_t head_bytes = (uint32_t)kvh * D * 2;
+        const uint32_t rc = (uint32_t)min(r, last_row);
+        koff[i] = (uint32_t)r * row_bytes + head_bytes + S::k(r, p) * 16;
+        voff[i] = (uint32_t)r * row_bytes + head_bytes + S::v(r, p) * 16;
+        kclamp[i] = rc * row_bytes + head_bytes + S::k(r, p) * 16;
+        vclamp[i] = rc * row_bytes + head_bytes + S::v(r, p) * 16;
+    }
+    // LDS byte address of this wavefront's first chunk in every stage.
+    const uint32_t kst_lds[ST] = {lds_offset(k0 + wave * 512), lds_offset(k1 + wave * 512),
+                                  lds_offset(k2 + wave * 512), lds_offset(k3 + wave * 512)};
+    const uint32_t vst_lds[ST] = {lds_offset(v0 + wave * 512), lds_offset(v1 + wave * 512),
+                                  lds_offset(v2 + wave * 512), lds_offset(v3 + wave * 512)};
+    auto dma_tile = [&](int st, int kt) __attribute__((always_inline)) {
+        const int64_t base = (int64_t)kt * kBN * row_bytes;
+        const char *kb = reinterpret_cast<const char *>(a.k) + base;
+        const char *vb = reinterpret_cast<const char *>(a.v) + base;
+        if (kt != tile_last) {
+#pragma unroll
+            for (int i = 0; i < CPW; ++i) {
+                dma16_async(kb, koff[i], kst_lds[st] + i * WAVES * 1024);
+                dma16_async(vb, voff[i], vst_lds[st] + i * WAVES * 1024);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < CPW; ++i) {
+                dma16_async(kb, kclamp[i], kst_lds[st] + i * WAVES * 1024);
+                dma16_async(vb, vclamp[i], vst_lds[st] + i * WAVES * 1024);
+            }
         }
     };
 
@@ -208,7 +239,7 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[mt][r] = 0.0f;
-    float m_used = -INFINITY, l_run = 0.0f;
+    float m_used = -INFINITY, mc = -INFINITY, l_run = 0.0f;  // mc = m_used * c
     float alpha_pending = 1.0f;
     bool rescale_pending = false;
     floatx16_t s[2];
@@ -270,7 +301,7 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
             vq[0] = vfrag(0);
             vq[1] = vfrag(1);
         }
-        float mx = 0.0f, mc = 0.0f, psum = 0.0f;
+        float mx = 0.0f, psum = 0.0f;
         uint32_t pw[2][8];
 #pragma unroll
         for (int n = 0; n < NS; ++n) {
@@ -283,22 +314,27 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
                 o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vq[n % 3], pprev[kb][t], o[mt], 0, 0, 0);
             }
             if constexpr (do_sm) {
-                if (n == 0) {  // row maximum, first key block
-                    mx = __builtin_fmaxf(s[0][0], s[0][1]);
+                if (n == 0) {  // row maximum, first key block (three-way maxima)
+                    mx = s[0][0];
 #pragma unroll
-                    for (int r = 2; r < 16; r += 2) mx = __builtin_fmaxf(__builtin_fmaxf(mx, s[0][r]), s[0][r + 1]);
+                    for (int r = 1; r < 15; r += 2) mx = __builtin_fmaxf(__builtin_fmaxf(mx, s[0][r]), s[0][r + 1]);
                 } else if (n == 1) {  // second key block, both halves, lazy decision
+                    mx = __builtin_fmaxf(__builtin_fmaxf(mx, s[0][15]), s[1][0]);
 #pragma unroll
-                    for (int r = 0; r < 16; r += 2) mx = __builtin_fmaxf(__builtin_fmaxf(mx, s[1][r]), s[1][r + 1]);
-                    mx = half_pair_max(mx);
-                    const bool grow = wave_any(mx * c > m_used * c + kLazyLog2);
-                    const float m_new = grow ? fmaxf(m_used, mx) : m_used;
-                    const float alpha = __builtin_amdgcn_exp2f((m_used - m_new) * c);
-                    l_run *= alpha;
-                    alpha_pending = alpha;
-                    rescale_pending = grow;
-                    m_used = m_new;
-                    mc = m_used * c;
+                    for (int r = 1; r < 15; r += 2) mx = __builtin_fmaxf(__builtin_fmaxf(mx, s[1][r]), s[1][r + 1]);
+                    mx = half_pair_max(__builtin_fmaxf(mx, s[1][15]));
+                    // The reference moves only when some row maximum exceeds
+                    // it by more than 2^8 (rare after the first tile), so the
+                    // common path is one FMA and one compare.
+                    if (wave_any(fmaf(mx, c, -mc) > kLazyLog2)) {
+                        const float m_new = fmaxf(m_used, mx);
+                        const float alpha = __builtin_amdgcn_exp2f((m_used - m_new) * c);
+                        l_run *= alpha;
+                        alpha_pending = alpha;
+                        rescale_pending = true;
+                        m_used = m_new;
+                        mc = m_used * c;
+                    }
                 } else {
                     // pairs of scores, spread over slots 2 .. NS-1
 #pragma unroll
@@ -340,20 +376,19 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
             rescale_pending = false;
         }
     };
-    // One iteration j (1 <= j < nkt): kc = K(j), vp = V(j-1); the stage of
-    // tile j-2 (kd, vd) receives tile j+2.  Tiles entirely above a
+    // One iteration j (1 <= j < nkt): kc = K(j), vp = V(j-1); stage sd
+    // (that of tile j-2) receives tile j+2.  Tiles entirely above a
     // wavefront's rows are computed too: their scores are all masked, so
     // they add exactly zero.  Every iteration issues one copy batch (the
     // last tile is repeated past the end) so the wait below is exact.
     // j counts this workgroup's tiles from 0; its key tile is tb + j.
-    auto iteration = [&](int j, const uint16_t *kc, const uint16_t *vp, uint16_t *kd, uint16_t *vd)
-        __attribute__((always_inline)) {
+    auto iteration = [&](int j, const uint16_t *kc, const uint16_t *vp, int sd) __attribute__((always_inline)) {
         // This wavefront's copy of tile j has landed (that of tile j+1 may
         // still be in flight); the barrier publishes tile j and tells that
         // every wavefront is past iteration j-1, which freed stage j-2.
         __builtin_amdgcn_s_waitcnt(vmcnt_lds_imm(2 * CPW));
         raw_barrier();
-        dma_tile(kd, vd, tb + min(j + 2, ntl - 1));
+        dma_tile(sd, tb + min(j + 2, ntl - 1));
         apply_rescale();
         qk(kc);
         if ((tb + j) * kBN + kBN - 1 > a.prior + rw0) mask_tile(tb + j);
@@ -364,22 +399,25 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
     // end), tile 0 scored and turned into P.  Stage i holds tile j with
     // j % 4 == i; the loop is unrolled by four so every stage is a distinct
     // LDS object.
-    dma_tile(k0, v0, tb);
-    dma_tile(k1, v1, tb + min(1, ntl - 1));
-    dma_tile(k2, v2, tb + min(2, ntl - 1));
+    dma_tile(0, tb);
+    dma_tile(1, tb + min(1, ntl - 1));
+    dma_tile(2, tb + min(2, ntl - 1));
     __builtin_amdgcn_s_waitcnt(vmcnt_lds_imm(2 * 2 * CPW));
     raw_barrier();
     qk(k0);
     if (tb * kBN + kBN - 1 > a.prior + rw0) mask_tile(tb);
     pv_softmax(v0, No{}, Yes{});
+    // The first maximum always moves the reference from -inf; O is still
+    // zero then, so there is nothing to rescale.
+    rescale_pending = false;
     for (int j = 1; j < ntl; j += ST) {
-        iteration(j, k1, v0, k3, v3);
+        iteration(j, k1, v0, 3);
         if (j + 1 >= ntl) break;
-        iteration(j + 1, k2, v1, k0, v0);
+        iteration(j + 1, k2, v1, 0);
         if (j + 2 >= ntl) break;
-        iteration(j + 2, k3, v2, k1, v1);
+        iteration(j + 2, k3, v2, 1);
         if (j + 3 >= ntl) break;
-        iteration(j + 3, k0, v3, k2, v2);
+        iteration(j + 3, k0, v3, 2);
     }
     // P.V of the last tile, from the stage that holds it.
     __builtin_amdgcn_s_waitcnt(vmcnt_lds_imm(0));
@@ -392,17 +430,21 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // no DMA may still target LDS at exit
 
     const float l = l_run + __shfl_xor(l_run, 32, 64);
+    // O / l as O * (1 / l): one correctly rounded reciprocal per row instead
+    // of D divisions (within one f32 ulp of the quotient before the BF16
+    // rounding).
     auto write_out = [&](const floatx16_t *acc, float lsum) __attribute__((always_inline)) {
         if (row >= a.queries) return;
         uint16_t *op = a.out + ((int64_t)row * a.q_heads + head) * D;
+        const float inv = 1.0f / lsum;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
             for (int r4 = 0; r4 < 4; ++r4) {
                 const int d = mt * 32 + r4 * 8 + half * 4;
                 uint2 w;
-                w.x = pack_bf16x2(acc[mt][r4 * 4 + 0] / lsum, acc[mt][r4 * 4 + 1] / lsum);
-                w.y = pack_bf16x2(acc[mt][r4 * 4 + 2] / lsum, acc[mt][r4 * 4 + 3] / lsum);
+                w.x = pack_bf16x2(acc[mt][r4 * 4 + 0] * inv, acc[mt][r4 * 4 + 1] * inv);
+                w.y = pack_bf16x2(acc[mt][r4 * 4 + 2] * inv, acc[mt][r4 * 4 + 3] * inv);
                 *reinterpret_cast<uint2 *>(op + d) = w;
             }
     };
