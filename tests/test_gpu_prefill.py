@@ -55,6 +55,30 @@ def test_prefill_reference_inputs_multi_query(ctx):
             assert max_abs_bf16(got, ref) <= TOL, (n, queries)
 
 
+@pytest.mark.parametrize("qh,kvh,d", [(16, 2, 128), (8, 2, 64)])
+def test_prefill_moving_reference_recomputes_tiles(ctx, qh, kvh, d):
+    """Scores that climb by about 6.5 log2 units per 64-key tile, so every
+    tile's row sums under the previous reference exceed 2^8 and the kernel
+    must move the reference and recompute that tile's P; and one late key
+    whose score is ~280 log2 units above the reference, so p overflows to
+    inf before the recompute.  Q = 1, K[t] = 0.4 t / 64 (D = 128 scaling)
+    except K[450] = 20; V random.  Checked against the oracle."""
+    rng = np.random.default_rng(20261202 + d)
+    queries, prior = 512, 0
+    scale = (128.0 / d) ** 0.5  # the same log2 growth per tile at D = 64
+    q = np.ones((queries, qh, d), np.float32)
+    kvals = 0.4 * scale * np.arange(queries, dtype=np.float32) / 64.0
+    kvals[450] = 20.0 * scale
+    k = np.repeat(kvals[:, None, None], kvh, axis=1).repeat(d, axis=2)
+    qb = oracle.write_bf16(q).reshape(q.shape)
+    kb = oracle.write_bf16(k).reshape(k.shape)
+    vb = normal_bf16(rng, (queries, kvh, d))
+    got = _prefill(ctx, qb, kb, vb, queries, prior, qh, kvh, d)
+    ref = oracle.prefill_causal_cpu(oracle.read_bf16(qb), kb, vb, qh, kvh, d, queries, prior)
+    assert np.isfinite(oracle.read_bf16(got)).all()
+    assert max_abs_bf16(got, ref) <= TOL
+
+
 def _rows_reference(q_bits, k_bits, v_bits, rows, prior, qh, kvh, d):
     out = {}
     for r in rows:

@@ -69,7 +69,9 @@ struct PrefillArgs {
 constexpr int kBN = 64;          // keys per LDS tile
 constexpr int kCus = 256;        // MI355X compute units
 constexpr int kXcds = 8;         // MI355X accelerator complex dies
-constexpr float kLazyLog2 = 8.0f;  // rescale O only past 2^8 growth
+// Lazy rescale: the reference maximum moves only when a tile's row sum under
+// it exceeds 2^8 (so every p stays within 2^8 of the reference).
+constexpr float kLazyBound = 256.0f;
 
 template <int D>
 struct Swz {
@@ -280,11 +282,26 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
             }
     };
 
+    // Pair pidx of the current scores (key block pidx / 8, rows 2 (pidx % 8)
+    // and the next) under the reference mc: exp2, BF16 pack, and the row sum
+    // of the packed P that feeds the MFMA.
+    auto score_pair = [&](int pidx, uint32_t (&pw)[2][8], float &psum) __attribute__((always_inline)) {
+        const int kb = pidx / 8, r = (pidx % 8) * 2;
+        bf16x2_t pp;
+        pp[0] = (__bf16)__builtin_amdgcn_exp2f(fmaf(s[kb][r], c, -mc));
+        pp[1] = (__bf16)__builtin_amdgcn_exp2f(fmaf(s[kb][r + 1], c, -mc));
+        pw[kb][r >> 1] = __builtin_bit_cast(uint32_t, pp);
+        psum = add_bf16_pair(pp, psum);
+        pin_value(pw[kb][r >> 1]);
+    };
+
     // P.V of the previous tile (V stage vp, when do_pv) with the softmax of
     // the current scores (when do_sm) spread over the MFMA slots.
-    auto pv_softmax = [&](const uint16_t *vp, auto pv_tag, auto sm_tag) __attribute__((always_inline)) {
+    auto pv_softmax = [&](const uint16_t *vp, auto pv_tag, auto sm_tag, auto first_tag)
+        __attribute__((always_inline)) {
         constexpr bool do_pv = decltype(pv_tag)::value;
         constexpr bool do_sm = decltype(sm_tag)::value;
+        constexpr bool first = decltype(first_tag)::value;
         auto vfrag = [&](int n) __attribute__((always_inline)) {
             const int mt = n % MT, t = (n / MT) % 2, kb = n / (2 * MT);
             const int t0 = kb * 32 + 16 * t + 4 * (q4 >> 1) + rr;
@@ -313,42 +330,56 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
                 const int mt = n % MT, t = (n / MT) % 2, kb = n / (2 * MT);
                 o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vq[n % 3], pprev[kb][t], o[mt], 0, 0, 0);
             }
-            if constexpr (do_sm) {
-                if (n == 0) {  // row maximum, first key block (three-way maxima)
+            if constexpr (do_sm && first) {
+                // The workgroup's first tile: the reference is still -inf, so
+                // take the row maximum first (slots 0 and 1), then the pairs.
+                if (n == 0) {
                     mx = s[0][0];
 #pragma unroll
                     for (int r = 1; r < 15; r += 2) mx = __builtin_fmaxf(__builtin_fmaxf(mx, s[0][r]), s[0][r + 1]);
-                } else if (n == 1) {  // second key block, both halves, lazy decision
+                } else if (n == 1) {
+                    mx = __builtin_fmaxf(__builtin_fmaxf(mx, s[0][15]), s[1][0]);
+#pragma unroll
+                    for (int r = 1; r < 15; r += 2) mx = __builtin_fmaxf(__builtin_fmaxf(mx, s[1][r]), s[1][r + 1]);
+                    m_used = half_pair_max(__builtin_fmaxf(mx, s[1][15]));
+                    mc = m_used * c;
+                } else {
+#pragma unroll
+                    for (int pidx = 0; pidx < 16; ++pidx)
+                        if (2 + (pidx * (NS - 2)) / 16 == n) score_pair(pidx, pw, psum);
+                    pin_value(psum);
+                }
+            } else if constexpr (do_sm) {
+                // Every later tile: the pairs under the current reference in
+                // slots 0 .. NS-2, then the lazy-rescale test in the last slot.
+#pragma unroll
+                for (int pidx = 0; pidx < 16; ++pidx)
+                    if ((pidx * (NS - 1)) / 16 == n) score_pair(pidx, pw, psum);
+                pin_value(psum);
+                // Every p of the tile is at most its row sum, so the reference
+                // need not move while each row sum stays within 2^8 (exact: the
+                // final O / l uses the same reference).  Otherwise (rare after
+                // the first tile; also when a p overflowed) take the tile's row
+                // maximum, move the reference for the rows that exceed it, and
+                // recompute the tile's P under the new one.
+                if (n == NS - 1 && wave_any(psum > kLazyBound)) {
+                    mx = s[0][0];
+#pragma unroll
+                    for (int r = 1; r < 15; r += 2) mx = __builtin_fmaxf(__builtin_fmaxf(mx, s[0][r]), s[0][r + 1]);
                     mx = __builtin_fmaxf(__builtin_fmaxf(mx, s[0][15]), s[1][0]);
 #pragma unroll
                     for (int r = 1; r < 15; r += 2) mx = __builtin_fmaxf(__builtin_fmaxf(mx, s[1][r]), s[1][r + 1]);
                     mx = half_pair_max(__builtin_fmaxf(mx, s[1][15]));
-                    // The reference moves only when some row maximum exceeds
-                    // it by more than 2^8 (rare after the first tile), so the
-                    // common path is one FMA and one compare.
-                    if (wave_any(fmaf(mx, c, -mc) > kLazyLog2)) {
-                        const float m_new = fmaxf(m_used, mx);
-                        const float alpha = __builtin_amdgcn_exp2f((m_used - m_new) * c);
-                        l_run *= alpha;
-                        alpha_pending = alpha;
-                        rescale_pending = true;
-                        m_used = m_new;
-                        mc = m_used * c;
-                    }
-                } else {
-                    // pairs of scores, spread over slots 2 .. NS-1
+                    const float m_new = fmaxf(m_used, mx);
+                    const float alpha = __builtin_amdgcn_exp2f((m_used - m_new) * c);
+                    l_run *= alpha;
+                    alpha_pending = alpha;
+                    rescale_pending = true;
+                    m_used = m_new;
+                    mc = m_used * c;
+                    psum = 0.0f;
 #pragma unroll
-                    for (int pidx = 0; pidx < 16; ++pidx) {
-                        if (2 + (pidx * (NS - 2)) / 16 != n) continue;
-                        const int kb = pidx / 8, r = (pidx % 8) * 2;
-                        bf16x2_t pp;
-                        pp[0] = (__bf16)__builtin_amdgcn_exp2f(fmaf(s[kb][r], c, -mc));
-                        pp[1] = (__bf16)__builtin_amdgcn_exp2f(fmaf(s[kb][r + 1], c, -mc));
-                        pw[kb][r >> 1] = __builtin_bit_cast(uint32_t, pp);
-                        psum = add_bf16_pair(pp, psum);
-                        pin_value(pw[kb][r >> 1]);
-                    }
-                    pin_value(psum);
+                    for (int pidx = 0; pidx < 16; ++pidx) score_pair(pidx, pw, psum);
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -392,7 +423,7 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
         apply_rescale();
         qk(kc);
         if ((tb + j) * kBN + kBN - 1 > a.prior + rw0) mask_tile(tb + j);
-        pv_softmax(vp, Yes{}, Yes{});
+        pv_softmax(vp, Yes{}, Yes{}, No{});
     };
 
     // Prologue: tiles 0, 1, 2 in flight (repeats of the last tile past the
@@ -406,7 +437,7 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
     raw_barrier();
     qk(k0);
     if (tb * kBN + kBN - 1 > a.prior + rw0) mask_tile(tb);
-    pv_softmax(v0, No{}, Yes{});
+    pv_softmax(v0, No{}, Yes{}, Yes{});
     // The first maximum always moves the reference from -inf; O is still
     // zero then, so there is nothing to rescale.
     rescale_pending = false;
@@ -423,10 +454,10 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
     __builtin_amdgcn_s_waitcnt(vmcnt_lds_imm(0));
     apply_rescale();
     const int last_stage = (ntl - 1) % ST;
-    if (last_stage == 0) pv_softmax(v0, Yes{}, No{});
-    else if (last_stage == 1) pv_softmax(v1, Yes{}, No{});
-    else if (last_stage == 2) pv_softmax(v2, Yes{}, No{});
-    else pv_softmax(v3, Yes{}, No{});
+    if (last_stage == 0) pv_softmax(v0, Yes{}, No{}, No{});
+    else if (last_stage == 1) pv_softmax(v1, Yes{}, No{}, No{});
+    else if (last_stage == 2) pv_softmax(v2, Yes{}, No{}, No{});
+    else pv_softmax(v3, Yes{}, No{}, No{});
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // no DMA may still target LDS at exit
 
     const float l = l_run + __shfl_xor(l_run, 32, 64);
