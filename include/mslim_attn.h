@@ -113,6 +113,14 @@ int mslim_attn_ctx_set_stream(void *ctx, void *hip_stream);
  *     (same tolerance, deterministic; the output differs from the unsplit
  *     launch in rounding only); 0 never splits. */
 #define MSLIM_ATTN_OPT_PREFILL_SPLIT 2
+/*   MSLIM_ATTN_OPT_PREFILL_POOL: 1 (default) lets an unsplit
+ *     mslim_attn_prefill_causal launch with at least two row blocks per CU
+ *     hand its shortest row blocks out at run time (one atomic counter in
+ *     the context's device memory), so XCDs running at different clocks
+ *     finish together; 0 maps every row block statically.  Each row block
+ *     is computed the same way whichever workgroup takes it: the output is
+ *     bit-identical either way. */
+#define MSLIM_ATTN_OPT_PREFILL_POOL 3
 int mslim_attn_ctx_set_option(void *ctx, int option, int64_t value);
 
 /* queue.finish() equivalent (gpu_llm/mod.rs:1998-2001). */
@@ -220,6 +228,13 @@ int mslim_attn_prefill_causal(void *ctx, const void *q, const void *k, const voi
  * SPLIT off).  A function of the shape only.  Host only (no context, no
  * device work); -1 on invalid arguments.  No reference counterpart. */
 int mslim_attn_prefill_split_tiles(int queries, int prior, int q_heads, int kv_heads, int head_dim);
+
+/* Row blocks per XCD that mslim_attn_prefill_causal hands out at run time
+ * for this shape (MSLIM_ATTN_OPT_PREFILL_POOL on), or 0 when the launch maps
+ * every row block statically (split launches, fewer than two row blocks per
+ * CU, the any-geometry fallback).  A function of the shape only.  Host only;
+ * -1 on invalid arguments.  No reference counterpart. */
+int mslim_attn_prefill_pool_items(int queries, int prior, int q_heads, int kv_heads, int head_dim);
 
 /* ---- Portable backend (exact K/V frames) ------------------------------------ */
 

@@ -218,3 +218,51 @@ def test_prefill_split_plan_is_shape_only(ctx):
     assert mslim_attn.prefill_split_tiles(2048, 0, 32, 8, 128) == 17
     with pytest.raises(mslim_attn.MslimAttnError):
         mslim_attn.prefill_split_tiles(0, 0, 32, 8, 128)
+
+
+# Launches with at least two row blocks per CU hand their shortest row blocks
+# out at run time (an atomic counter in the context): cfg4-like 8 heads per
+# workgroup, 4 heads (64-row blocks), D = 64, and kv_heads = 4 with a work
+# list that does not fill the last XCD's slice (pool entries past the end).
+POOL_SHAPES = [(4096, 0, 64, 8, 128), (8192, 0, 32, 8, 128), (8192, 0, 16, 2, 64),
+               (4250, 100, 32, 4, 128), (3000, 500, 64, 8, 128)]
+
+
+def test_prefill_pool_matches_static_mapping(ctx):
+    import mslim_attn
+    sentinel = -0x40  # 0xFFC0: a BF16 NaN, so a row block left unwritten shows
+    for queries, prior, qh, kvh, d in POOL_SHAPES:
+        assert mslim_attn.prefill_pool_items(queries, prior, qh, kvh, d) > 0
+        hist = prior + queries
+        gen = torch.Generator(device="cuda").manual_seed(queries * 3 + qh)
+        q = torch.randn((queries, qh, d), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+        k = torch.randn((hist, kvh, d), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+        v = torch.randn((hist, kvh, d), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+        pooled = [torch.full_like(q, sentinel) for _ in range(2)]
+        static = torch.full_like(q, sentinel)
+        # two pooled launches back to back: the first must leave its counter at zero
+        for out in pooled:
+            ctx.prefill_causal(q, k, v, out, queries, prior, qh, kvh, d)
+        try:
+            ctx.set_prefill_pool(False)
+            ctx.prefill_causal(q, k, v, static, queries, prior, qh, kvh, d)
+        finally:
+            ctx.set_prefill_pool(True)
+        torch.cuda.synchronize()
+        shape = (queries, prior, qh, kvh, d)
+        assert not bool((static == sentinel).any()), shape
+        # each row block is computed the same way whichever workgroup takes it
+        assert torch.equal(pooled[0], static), shape
+        assert torch.equal(pooled[1], static), shape
+        got = from_torch(pooled[0])
+        qb, kb, vb = from_torch(q), from_torch(k), from_torch(v)
+        rows = [0, 31, 32, queries // 2, queries - 33, queries - 1]
+        ref = _rows_reference(qb, kb, vb, rows, prior, qh, kvh, d)
+        for r in rows:
+            assert max_abs_bf16(got[r], ref[r]) <= TOL, (shape, r)
+
+
+def test_prefill_pool_option_rejects_bad_values(ctx):
+    import mslim_attn
+    with pytest.raises(mslim_attn.MslimAttnError):
+        ctx.set_option(mslim_attn.OPT_PREFILL_POOL, 2)

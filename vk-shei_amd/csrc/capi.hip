@@ -46,10 +46,11 @@ struct Context {
     bool separate_merge = false;    // MSLIM_ATTN_OPT_DECODE_MERGE
     void *prefill_partial = nullptr;  // split prefill partials
     size_t prefill_partial_bytes = 0;
-    void *prefill_counters = nullptr;  // split prefill chunk counters, zero between launches
+    void *prefill_counters = nullptr;  // split chunk counters / pool counter, zero between launches
     size_t prefill_counter_bytes = 0;
     bool prefill_counters_dirty = false;
     bool prefill_split = true;        // MSLIM_ATTN_OPT_PREFILL_SPLIT
+    bool prefill_pool = true;         // MSLIM_ATTN_OPT_PREFILL_POOL
     void *staging = nullptr;       // device, digest serialisation
     size_t staging_bytes = 0;
     void *host_staging = nullptr;  // pinned host, digest readback
@@ -320,6 +321,10 @@ int mslim_attn_ctx_set_option(void *ctx, int option, int64_t value) {
         if (value != 0 && value != 1) return fail("prefill split must be 0 (never) or 1 (automatic)");
         c.prefill_split = value == 1;
         return 0;
+    case MSLIM_ATTN_OPT_PREFILL_POOL:
+        if (value != 0 && value != 1) return fail("prefill pool must be 0 (static mapping) or 1 (automatic)");
+        c.prefill_pool = value == 1;
+        return 0;
     default:
         return fail("unknown context option");
     }
@@ -518,6 +523,18 @@ int mslim_attn_prefill_split_tiles(int queries, int prior, int q_heads, int kv_h
     return mslim::prefill_split_plan(l).chunk_tiles;
 }
 
+int mslim_attn_prefill_pool_items(int queries, int prior, int q_heads, int kv_heads, int head_dim) {
+    g_error.clear();
+    if (!valid_geometry(q_heads, kv_heads, head_dim) || queries < 1 || prior < 0 ||
+        (int64_t)queries + prior > INT32_MAX - 64)
+        return fail("prefill pool query needs a valid geometry, queries >= 1 and prior >= 0");
+    mslim::PrefillLaunch l{};
+    l.queries = queries; l.prior = prior; l.q_heads = q_heads; l.kv_heads = kv_heads; l.head_dim = head_dim;
+    l.split_allowed = true;
+    l.pool_allowed = true;
+    return mslim::prefill_pool_items(l);
+}
+
 int mslim_attn_prefill_causal(void *ctx, const void *q, const void *k, const void *v, void *out,
                               int queries, int prior, int q_heads, int kv_heads, int head_dim,
                               float scale) {
@@ -539,12 +556,18 @@ int mslim_attn_prefill_causal(void *ctx, const void *q, const void *k, const voi
     l.queries = queries; l.prior = prior; l.q_heads = q_heads; l.kv_heads = kv_heads;
     l.head_dim = head_dim; l.scale = scale;
     l.split_allowed = c.prefill_split;
+    l.pool_allowed = c.prefill_pool;
     const mslim::PrefillSplit plan = mslim::prefill_split_plan(l);
-    if (plan.chunk_tiles) {
-        if (int rc = grow_device(c, &c.prefill_partial, &c.prefill_partial_bytes, plan.partial_bytes,
-                                 "hipMalloc prefill split partials"))
-            return rc;
-        const size_t ctr_bytes = (size_t)plan.counters * sizeof(int);
+    const int pool = plan.chunk_tiles ? 0 : mslim::prefill_pool_items(l);
+    if (plan.chunk_tiles || pool) {
+        if (plan.chunk_tiles) {
+            if (int rc = grow_device(c, &c.prefill_partial, &c.prefill_partial_bytes, plan.partial_bytes,
+                                     "hipMalloc prefill split partials"))
+                return rc;
+        }
+        // A split launch counts chunks per row block; a pooled one draws
+        // from counter 0.  Both leave their counters at zero.
+        const size_t ctr_bytes = plan.chunk_tiles ? (size_t)plan.counters * sizeof(int) : sizeof(int);
         if (c.prefill_counter_bytes < ctr_bytes) {
             if (int rc = grow_device(c, &c.prefill_counters, &c.prefill_counter_bytes, ctr_bytes,
                                      "hipMalloc prefill split counters"))
@@ -560,9 +583,10 @@ int mslim_attn_prefill_causal(void *ctx, const void *q, const void *k, const voi
         }
         l.partial = static_cast<float *>(c.prefill_partial);
         l.counters = static_cast<int *>(c.prefill_counters);
+        l.pool_counter = static_cast<int *>(c.prefill_counters);
     }
     const int rc = check_hip(mslim::launch_prefill(l, c.stream), "prefill attention launch");
-    if (rc && plan.chunk_tiles) c.prefill_counters_dirty = true;
+    if (rc && (plan.chunk_tiles || pool)) c.prefill_counters_dirty = true;
     return rc;
 }
 

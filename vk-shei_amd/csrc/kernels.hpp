@@ -67,8 +67,12 @@ struct PrefillLaunch {
     bool split_allowed;  // chunk long row blocks when the launch is small
     float *partial;      // split workspace of prefill_split_plan().partial_bytes
     int *counters;       // prefill_split_plan().counters ints, zero between launches
+    bool pool_allowed;   // hand the shortest row blocks out at run time (unsplit launches)
+    int *pool_counter;   // one int, zero between launches, when prefill_pool_items() > 0
 };
 bool prefill_fast_path(int head_dim, int group);
+// Row blocks per XCD that an unsplit launch hands out at run time (0: none).
+int prefill_pool_items(const PrefillLaunch &l);
 // How a launch splits its row blocks: chunk_tiles == 0 means no split.
 struct PrefillSplit {
     int chunk_tiles = 0, max_chunks = 1, items = 0, counters = 0;

@@ -21,11 +21,13 @@
 //     wavefront interleaves the two, so each wavefront software-pipelines its
 //     own tiles: the softmax of tile j runs in the MFMA slots of P.V of tile
 //     j-1;
-//   * O is rescaled only when a row maximum grows by more than 8 in log2
-//     units (exact: the final O / l uses the same stale maximum), row sums
-//     use v_dot2 on the BF16 P that feeds the MFMA;
+//   * O is rescaled only when a tile's row sum under the current maximum
+//     exceeds 2^8 (exact: the final O / l uses the same stale maximum), row
+//     sums use v_dot2 on the BF16 P that feeds the MFMA;
 //   * workgroups are mapped so that each XCD works through whole kv heads,
 //     longest row blocks first, keeping those heads' K/V resident in its L2;
+//     the shortest row blocks of every XCD form a pool taken at run time, so
+//     XCDs of different clocks finish together;
 //   * a launch too small to keep every CU busy for the length of its longest
 //     row block (cfg2's 2,048 tokens: 256 workgroups of 1 to 32 key tiles;
 //     the decoder's 512-token prompt chunks: 64 workgroups) splits long row
@@ -63,12 +65,21 @@ struct PrefillArgs {
     int chunk_tiles, max_chunks, items;
     float *partial;
     int *counters;
+    // Unsplit launches: the last pool_items entries of every XCD's slice of
+    // the work list go to a shared pool; each XCD runs pool_items +
+    // kPoolSpare workgroups that take pool entries through pool_counter.
+    int pool_items;
+    int *pool_counter;
     uint32_t item[kMaxSplitItems];
 };
 
 constexpr int kBN = 64;          // keys per LDS tile
 constexpr int kCus = 256;        // MI355X compute units
 constexpr int kXcds = 8;         // MI355X accelerator complex dies
+// Run-time pool of an unsplit launch: at most kPoolMax row blocks per XCD,
+// kPoolSpare extra workgroups per XCD to take them.
+constexpr int kPoolMax = 96;
+constexpr int kPoolSpare = 8;
 // Lazy rescale: the reference maximum moves only when a tile's row sum under
 // it exceeds 2^8 (so every p stays within 2^8 of the reference).
 constexpr float kLazyBound = 256.0f;
@@ -135,6 +146,14 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
     // every XCD a contiguous slice of the work list ordered (kv head, row
     // block longest first, head subgroup), so an XCD streams the K/V of as
     // few kv heads as possible and they stay in its L2.
+    //
+    // XCDs run at different clocks (measured up to 5% apart on one device),
+    // so equal slices finish at different times.  With a pool, the shortest
+    // pool_items entries of every slice are instead taken at run time, one
+    // atomic increment per workgroup, in the order (entry, XCD): a faster
+    // XCD reaches its pool workgroups sooner and takes more of them.  The
+    // pool has pool_items + kPoolSpare workgroups per XCD; those that find
+    // it empty exit, and the last of them to draw resets the counter.
     const int group = a.q_heads / a.kv_heads;
     const int subgroups = group / HW;
     const int nrb = (a.queries + RW - 1) / RW;
@@ -150,8 +169,27 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
     } else {
         const int total = nrb * a.kv_heads * subgroups;
         const int per_xcd = (total + kXcds - 1) / kXcds;
-        const int item = (int)(blockIdx.x % kXcds) * per_xcd + (int)(blockIdx.x / kXcds);
+        const int xcd = (int)(blockIdx.x % kXcds), slot = (int)(blockIdx.x / kXcds);
+        int item;
+        if (slot < per_xcd - a.pool_items) {
+            item = xcd * per_xcd + slot;
+        } else {
+            __shared__ int drawn;
+            if (tid == 0) {
+                const int g = __hip_atomic_fetch_add(a.pool_counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (g == kXcds * (a.pool_items + kPoolSpare) - 1)
+                    __hip_atomic_store(a.pool_counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                drawn = g;
+            }
+            __syncthreads();
+            const int g = __builtin_amdgcn_readfirstlane(drawn);
+            if (g >= kXcds * a.pool_items) return;
+            item = (g % kXcds) * per_xcd + per_xcd - a.pool_items + g / kXcds;
+        }
         if (item >= total) return;
+        // Uniform by construction; the compiler cannot prove it across the
+        // pool branch, and the K/V copies need the tile bases in SGPRs.
+        item = __builtin_amdgcn_readfirstlane(item);
         const int per_head = nrb * subgroups;
         kvh = item / per_head;
         rb = nrb - 1 - (item % per_head) / subgroups;
@@ -632,7 +670,8 @@ hipError_t launch_mfma(const PrefillArgs &a, hipStream_t stream) {
     const int group = a.q_heads / a.kv_heads;
     const int total = ((a.queries + RW - 1) / RW) * a.kv_heads * (group / HW);
     const int per_xcd = (total + kXcds - 1) / kXcds;
-    const unsigned grid = a.chunk_tiles ? (unsigned)a.items : (unsigned)(per_xcd * kXcds);
+    const int spare = a.pool_items ? kPoolSpare : 0;
+    const unsigned grid = a.chunk_tiles ? (unsigned)a.items : (unsigned)((per_xcd + spare) * kXcds);
     hipLaunchKernelGGL((prefill_mfma_kernel<D, HW>), dim3(grid), dim3(512), 0, stream, a);
     return hipGetLastError();
 }
@@ -694,6 +733,21 @@ PrefillSplit prefill_split_plan(const PrefillLaunch &l) {
     const int pairs = (l.head_dim / 32) * 8 + 1;
     p.partial_bytes = (size_t)groups * nrb * p.max_chunks * 8 * pairs * 64 * 2 * sizeof(float);
     return p;
+}
+
+int prefill_pool_items(const PrefillLaunch &l) {
+    const int group = l.q_heads / l.kv_heads;
+    if (!l.pool_allowed || !prefill_fast_path(l.head_dim, group) || prefill_split_plan(l).chunk_tiles) return 0;
+    const int hw = heads_per_workgroup(group);
+    const int rows = 32 * (8 / hw);
+    const int64_t total = (int64_t)((l.queries + rows - 1) / rows) * l.kv_heads * (group / hw);
+    const int64_t per_xcd = (total + kXcds - 1) / kXcds;
+    // Only launches with at least two row blocks per CU queue any; then the
+    // shortest three eighths of every slice, at most kPoolMax (at cfg4's
+    // 256 row blocks per XCD, 96 measured best: a larger pool moves longer
+    // row blocks away from the L2 that holds their kv head).
+    if (per_xcd < 2 * (kCus / kXcds)) return 0;
+    return (int)std::min<int64_t>(kPoolMax, per_xcd * 3 / 8);
 }
 
 hipError_t launch_prefill(const PrefillLaunch &l, hipStream_t stream) {
@@ -761,6 +815,10 @@ hipError_t launch_prefill(const PrefillLaunch &l, hipStream_t stream) {
         a.items = (int)slots;
         a.partial = l.partial;
         a.counters = l.counters;
+    } else if (const int pool = prefill_pool_items(l)) {
+        if (!l.pool_counter) return hipErrorInvalidValue;
+        a.pool_items = pool;
+        a.pool_counter = l.pool_counter;
     }
     if (l.head_dim == 128) {
         if (hw == 8) return launch_mfma<128, 8>(a, stream);

@@ -24,6 +24,7 @@ MAX_BATCH = 64
 OPT_DECODE_MERGE = 1                        # mslim_attn_ctx_set_option options
 DECODE_MERGE_FUSED, DECODE_MERGE_SEPARATE = 0, 1
 OPT_PREFILL_SPLIT = 2
+OPT_PREFILL_POOL = 3
 DECODE_STATIC_SCRATCH_BYTES = 16 << 20      # mslim_attn_decode_paged_noalloc partials bound
 FORMAT_BF16, FORMAT_F16, FORMAT_F32 = 1, 2, 3  # gpu_backend.rs:258-262
 ERR_NONFINITE = -2
@@ -68,6 +69,7 @@ EXPORTS = (
     "mslim_attn_decode_paged_noalloc",
     "mslim_attn_prefill_causal",
     "mslim_attn_prefill_split_tiles",
+    "mslim_attn_prefill_pool_items",
     "mslim_attn_frames_decode",
     "mslim_attn_backend_decode",
     "mslim_attn_rmsnorm",
@@ -150,6 +152,7 @@ def library() -> C.CDLL:
         "mslim_attn_decode_paged_noalloc": (I, [P, P, P, P, P, I, PI32, P, I, I, I, I, I, F, I]),
         "mslim_attn_prefill_causal": (I, [P, P, P, P, P, I, I, I, I, I, F]),
         "mslim_attn_prefill_split_tiles": (I, [I, I, I, I, I]),
+        "mslim_attn_prefill_pool_items": (I, [I, I, I, I, I]),
         "mslim_attn_frames_decode": (I, [P, P, P, I, P, I, P, I64, I, I, I]),
         "mslim_attn_backend_decode": (I, [P, P, P, I, P, I, I64, I, I, I, P, C.POINTER(Timings)]),
         "mslim_attn_rmsnorm": (I, [P, P, P, P, I, I, F]),
@@ -258,6 +261,12 @@ class Context:
         """Let prefill split long row blocks on small launches (True, the
         default) or never (False)."""
         self.set_option(OPT_PREFILL_SPLIT, 1 if allowed else 0)
+
+    def set_prefill_pool(self, allowed: bool) -> None:
+        """Let unsplit prefill launches hand their shortest row blocks out at
+        run time (True, the default) or map them statically (False); the
+        output is the same bits either way."""
+        self.set_option(OPT_PREFILL_POOL, 1 if allowed else 0)
 
     def use_torch_stream(self) -> None:
         import torch
@@ -515,4 +524,13 @@ def prefill_split_tiles(queries: int, prior: int, q_heads: int, kv_heads: int, h
     out = lib.mslim_attn_prefill_split_tiles(queries, prior, q_heads, kv_heads, head_dim)
     if out < 0:
         raise MslimAttnError("prefill_split_tiles", out, lib.mslim_attn_last_error().decode())
+    return out
+
+
+def prefill_pool_items(queries: int, prior: int, q_heads: int, kv_heads: int, head_dim: int) -> int:
+    """Row blocks per XCD that a prefill launch of this shape hands out at run time (0: none)."""
+    lib = library()
+    out = lib.mslim_attn_prefill_pool_items(queries, prior, q_heads, kv_heads, head_dim)
+    if out < 0:
+        raise MslimAttnError("prefill_pool_items", out, lib.mslim_attn_last_error().decode())
     return out
