@@ -565,9 +565,13 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
     // Merge in chunk order: M = the largest chunk maximum, then
     // O = sum_c O_c 2^((m_c - M) c) and l likewise, chunk 0 first; this
     // workgroup's own chunk enters from registers at its place in the order.
-    // M first (one batch of (m, l) loads), then the sums in chunk order; each
-    // other chunk's partial is loaded in two batches (round trips of uncached
-    // loads) and folded in.
+    // The O of the first other chunk and the (m, l) pairs of all chunks go
+    // out as one batch of uncached loads (one round trip); every further
+    // chunk's O is one more batch.
+    const int first_other = chunk == 0 ? 1 : 0;
+    float2 x[MT * 8];
+#pragma unroll
+    for (int e = 0; e < MT * 8; ++e) x[e] = get2(chunk_base(first_other) + e * 128);
     float2 ml[kMaxChunks];
 #pragma unroll
     for (int ch = 0; ch < kMaxChunks; ++ch)
@@ -584,8 +588,9 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[mt][r] = 0.0f;
-#pragma unroll 1
-    for (int ch = 0; ch < nchunks; ++ch) {
+#pragma unroll
+    for (int ch = 0; ch < kMaxChunks; ++ch) {
+        if (ch >= nchunks) break;
         if (ch == chunk) {
             const float w = __builtin_amdgcn_exp2f((m_used - mmax) * c);
 #pragma unroll
@@ -594,22 +599,18 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
                 for (int r = 0; r < 16; ++r) acc[mt][r] = fmaf(o[mt][r], w, acc[mt][r]);
             continue;
         }
-        const float *theirs = chunk_base(ch);
-        const float w = __builtin_amdgcn_exp2f((get2(theirs + (MT * 8) * 128).x - mmax) * c);
-        constexpr int HM = MT > 1 ? MT / 2 : 1;
+        if (ch != first_other) {
 #pragma unroll
-        for (int m0 = 0; m0 < MT; m0 += HM) {
-            float2 x[HM * 8];
-#pragma unroll
-            for (int e = 0; e < HM * 8; ++e) x[e] = get2(theirs + (m0 * 8 + e) * 128);
-#pragma unroll
-            for (int mh = 0; mh < HM; ++mh)
-#pragma unroll
-                for (int r = 0; r < 8; ++r) {
-                    acc[m0 + mh][2 * r] = fmaf(x[mh * 8 + r].x, w, acc[m0 + mh][2 * r]);
-                    acc[m0 + mh][2 * r + 1] = fmaf(x[mh * 8 + r].y, w, acc[m0 + mh][2 * r + 1]);
-                }
+            for (int e = 0; e < MT * 8; ++e) x[e] = get2(chunk_base(ch) + e * 128);
         }
+        const float w = __builtin_amdgcn_exp2f((ml[ch].x - mmax) * c);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                acc[mt][2 * r] = fmaf(x[mt * 8 + r].x, w, acc[mt][2 * r]);
+                acc[mt][2 * r + 1] = fmaf(x[mt * 8 + r].y, w, acc[mt][2 * r + 1]);
+            }
     }
     write_out(acc, lsum);
 }
