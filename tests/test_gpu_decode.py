@@ -306,6 +306,57 @@ def test_decode_merge_modes_bitwise_ragged(ctx):
             assert max_abs_bf16(got[b], _oracle_decode(qb[b], kb[b, :t], vb[b, :t], qh, kvh, d)) <= TOL, (split, b)
 
 
+# Launches with more partitions than two per CU (512) and at most 896 run the
+# partitions as 512 host-packed lists (fused merge only); the separate merge
+# launch keeps one partition per workgroup.  Same partitions, same fixed merge
+# order: the bits must agree.  cfg3's batch (640 partitions at the automatic
+# split), a D = 64 / group-8 geometry and a batch whose 896 partitions fill
+# the lists.
+LIST_CASES = [(32, 512, 8193, 20261203, 32, 8, 128, 0), (24, 300, 6001, 5, 16, 2, 64, 0),
+              (40, 2000, 6001, 6, 32, 8, 128, 1856)]
+
+
+@pytest.mark.parametrize("batch,lo,hi,seed,qh,kvh,d,split", LIST_CASES)
+def test_decode_list_mode_matches_one_partition_per_workgroup(ctx, batch, lo, hi, seed, qh, kvh, d, split):
+    import mslim_attn
+    lens = np.random.default_rng(seed).integers(lo, hi, size=batch).tolist()
+    s = split or mslim_attn.auto_split(lens, kvh)
+    parts = sum(-(-t // s) for t in lens) * kvh
+    assert 512 < parts <= 896, parts
+    stride = max(lens)
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    q = torch.randn((batch, qh, d), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    k = torch.randn((batch, stride, kvh, d), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    v = torch.randn((batch, stride, kvh, d), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    k_pool, v_pool, table_t, pps, _ = _paged_pool(ctx, k, v, lens, stride, 16, seed=seed)
+
+    def dense():
+        out = torch.empty_like(q)
+        ctx.decode_dense(q, k, v, out, lens, qh, kvh, d, seq_stride_tokens=stride, split_tokens=split)
+        torch.cuda.synchronize()
+        return from_torch(out)
+
+    def paged():
+        out = torch.empty_like(q)
+        ctx.decode_paged(q, k_pool, v_pool, out, lens, table_t, pps, 16, qh, kvh, d, split_tokens=split)
+        torch.cuda.synchronize()
+        return from_torch(out)
+
+    listed_d, static_d = _merge_modes(ctx, dense)
+    listed_p, static_p = _merge_modes(ctx, paged)
+    again = paged()
+    assert np.array_equal(listed_d, static_d)
+    assert np.array_equal(listed_p, static_p)
+    assert np.array_equal(listed_d, listed_p)
+    assert np.array_equal(listed_p, again)
+    got = listed_p.reshape(batch, -1)
+    qb = from_torch(q)
+    for b in (0, int(np.argmax(lens)), int(np.argmin(lens)), batch - 1):
+        t = lens[b]
+        kb, vb = from_torch(k[b, :t].contiguous()), from_torch(v[b, :t].contiguous())
+        assert max_abs_bf16(got[b], _oracle_decode(qb[b], kb, vb, qh, kvh, d)) <= TOL, b
+
+
 def _cfg4_hot_cold_pool(k, v, lens, hot_window, page_tokens, seed, ctx):
     """cfg4's layout: per sequence the cold pages are a seeded random
     permutation of pool slots and the most recent `hot_window` tokens one

@@ -25,7 +25,11 @@
 //   * the four wavefronts merge in LDS; the partitions of one (sequence, kv
 //     head) are merged in fixed partition order by the workgroup that
 //     finishes last (or, when the context asks for it, by a second launch;
-//     both orders give the same bits).
+//     both orders give the same bits);
+//   * launches of more partitions than two per CU run them as 512 host-
+//     packed lists, one workgroup per list (the LIST kernel), so that every
+//     CU gets the same work; which workgroup computes a partition does not
+//     change its bits.
 // Partitions are fixed by logical token index, and the paged and dense
 // variants differ only in how a 16-token block's base address is formed, so
 // both produce bit-identical outputs (the reference's dense == ColdStore
@@ -50,6 +54,10 @@ namespace {
 constexpr int kWaves = 4;
 constexpr int kDepth = 2;
 constexpr int kTile = 32;
+// List mode: two lists per CU (two workgroups fit), at most kMaxListItems
+// partitions in all (the tables ride in the kernel arguments).
+constexpr int kListBins = 512;
+constexpr int kMaxListItems = 896;
 
 struct DeviceArgs {
     const uint16_t *q, *k, *v;
@@ -70,6 +78,13 @@ struct DeviceArgs {
     // partitions, longest first (last_order: sequence indices).
     int full_begin[kMaxBatch + 1];
     int16_t last_order[kMaxBatch];
+    // List mode (list_bins > 0, the LIST kernel): workgroup w runs the
+    // partitions list[i], bin_start[w] <= i < bin_start[w + 1], one after
+    // another, each given by its launch index (what blockIdx.x is in the
+    // one-partition-per-workgroup kernel).
+    int list_bins;
+    uint16_t bin_start[kListBins + 1];
+    uint16_t list[kMaxListItems];
 };
 
 // Base of the 16-token block starting at logical token t0 (a multiple of 16).
@@ -158,7 +173,7 @@ template <int D, int G>
 __device__ __forceinline__ void merge_splits(const DeviceArgs &a, int b, int kvh, int tid, int nthreads,
                                              bool coherent);
 
-template <int D, int G, bool PAGED, bool FUSED, bool NT>
+template <int D, int G, bool PAGED, bool FUSED, bool NT, bool LIST>
 __global__ __launch_bounds__(64 * kWaves, 2) void decode_kernel(DeviceArgs a) {
     constexpr int DEPTH = kDepth;
     constexpr int KS = D / 32;        // Q.K MFMA k-steps per 16-token block
@@ -178,8 +193,10 @@ __global__ __launch_bounds__(64 * kWaves, 2) void decode_kernel(DeviceArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int row16 = lane & 15;
     const int grp = lane >> 4;
-    const int kvh = blockIdx.x % a.kv_heads;
-    const int sg = blockIdx.x / a.kv_heads;
+    // One partition, given by its launch index (kv head fastest).
+    auto partition = [&](const int launch_index) __attribute__((always_inline)) {
+    const int kvh = launch_index % a.kv_heads;
+    const int sg = launch_index / a.kv_heads;
     // Full partitions launch first and the shorter last partitions after
     // them, longest first: when a launch has more workgroups than fit at
     // once, the dispatcher hands the short ones to the CUs that free up.
@@ -447,6 +464,16 @@ __global__ __launch_bounds__(64 * kWaves, 2) void decode_kernel(DeviceArgs a) {
         if (!last) return;
         merge_splits<D, G>(a, b, kvh, tid, 64 * kWaves, true);
     }
+    };
+    if constexpr (LIST) {
+        const int i0 = a.bin_start[blockIdx.x], i1 = a.bin_start[blockIdx.x + 1];
+        for (int i = i0; i < i1; ++i) {
+            if (i > i0) __syncthreads();  // the previous partition's LDS is free
+            partition(a.list[i]);
+        }
+    } else {
+        partition((int)blockIdx.x);
+    }
 }
 
 // Fixed-order log-sum-exp merge of the split partials of one (sequence, kv
@@ -589,17 +616,17 @@ __global__ __launch_bounds__(64) void decode_generic_kernel(DeviceArgs a, int D)
     }
 }
 
-template <int D, int G, bool FUSED>
+template <int D, int G, bool FUSED, bool LIST>
 void launch_variant(const DeviceArgs &a, bool paged, bool nt, dim3 grid, hipStream_t stream) {
     const dim3 block(64 * kWaves);
     if (paged && nt)
-        hipLaunchKernelGGL((decode_kernel<D, G, true, FUSED, true>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((decode_kernel<D, G, true, FUSED, true, LIST>), grid, block, 0, stream, a);
     else if (paged)
-        hipLaunchKernelGGL((decode_kernel<D, G, true, FUSED, false>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((decode_kernel<D, G, true, FUSED, false, LIST>), grid, block, 0, stream, a);
     else if (nt)
-        hipLaunchKernelGGL((decode_kernel<D, G, false, FUSED, true>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((decode_kernel<D, G, false, FUSED, true, LIST>), grid, block, 0, stream, a);
     else
-        hipLaunchKernelGGL((decode_kernel<D, G, false, FUSED, false>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((decode_kernel<D, G, false, FUSED, false, LIST>), grid, block, 0, stream, a);
 }
 
 // fused: the last split workgroup of each (sequence, kv head) merges; else a
@@ -607,11 +634,13 @@ void launch_variant(const DeviceArgs &a, bool paged, bool nt, dim3 grid, hipStre
 template <int D, int G>
 hipError_t launch_fast(const DeviceArgs &a, bool paged, bool nt, int total_splits, bool merge, bool fused,
                        hipStream_t stream) {
-    const dim3 grid((unsigned)(total_splits * a.kv_heads));
-    if (fused)
-        launch_variant<D, G, true>(a, paged, nt, grid, stream);
+    // Lists are built for the fused merge only (launch_decode).
+    if (fused && a.list_bins)
+        launch_variant<D, G, true, true>(a, paged, nt, dim3((unsigned)a.list_bins), stream);
+    else if (fused)
+        launch_variant<D, G, true, false>(a, paged, nt, dim3((unsigned)(total_splits * a.kv_heads)), stream);
     else
-        launch_variant<D, G, false>(a, paged, nt, grid, stream);
+        launch_variant<D, G, false, false>(a, paged, nt, dim3((unsigned)(total_splits * a.kv_heads)), stream);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess || !merge || fused) return err;
     hipLaunchKernelGGL((decode_merge_kernel<D, G>), dim3((unsigned)(a.batch * a.kv_heads)), dim3(256), 0,
@@ -745,6 +774,59 @@ int decode_auto_split_tokens(const int32_t *seq_lens, int batch, int kv_heads) {
     return best_split;
 }
 
+// List mode, for fused-merge launches of more partitions than fit at once
+// (two workgroups per CU: 512) and at most kMaxListItems: the partitions,
+// longest first (ties in launch order), each go to the list with the least
+// work so far (tokens plus kListItemCost per partition for its first loads,
+// combine and publication; ties to the lower list), and the launch runs 512
+// workgroups, one per list.  With one partition per workgroup, a CU gets the
+// next workgroup whenever one of its two slots frees, and which partitions
+// share a CU follows from that order: the measured per-CU work of cfg3
+// (640 partitions) spread from 121 to 175 32-token tiles around a mean of
+// 144, and the call ended with the busiest CUs.  Packed lists give every
+// pair of lists on a CU nearly the same work.  Fixed-size arrays: the
+// allocation-free entry point plans too.
+constexpr int64_t kListItemCost = 256;
+
+void plan_lists(DeviceArgs &a, int total, const int32_t *seq_len) {
+    const int kvh = a.kv_heads;
+    const int items = total * kvh;
+    const int full = a.full_begin[a.batch];
+    std::pair<int, int> order[kMaxListItems];  // (tokens, launch index)
+    for (int i = 0; i < items; ++i) {
+        const int sg = i / kvh;
+        int tokens = a.split_tokens;
+        if (sg >= full) {
+            const int b = a.last_order[sg - full];
+            tokens = seq_len[b] - (a.split_begin[b + 1] - a.split_begin[b] - 1) * a.split_tokens;
+        }
+        order[i] = {tokens, i};
+    }
+    std::stable_sort(order, order + items,
+                     [](const std::pair<int, int> &x, const std::pair<int, int> &y) { return x.first > y.first; });
+    std::pair<int64_t, int> heap[kListBins];  // (work, list): least work on top
+    for (int w = 0; w < kListBins; ++w) heap[w] = {0, w};
+    const auto later = std::greater<std::pair<int64_t, int>>();
+    int16_t bin_of[kMaxListItems];
+    int count[kListBins] = {};
+    for (int i = 0; i < items; ++i) {
+        std::pop_heap(heap, heap + kListBins, later);
+        auto &top = heap[kListBins - 1];
+        bin_of[i] = (int16_t)top.second;
+        ++count[top.second];
+        top.first += order[i].first + kListItemCost;
+        std::push_heap(heap, heap + kListBins, later);
+    }
+    int cursor[kListBins];
+    a.bin_start[0] = 0;
+    for (int w = 0; w < kListBins; ++w) {
+        cursor[w] = a.bin_start[w];
+        a.bin_start[w + 1] = (uint16_t)(a.bin_start[w] + count[w]);
+    }
+    for (int i = 0; i < items; ++i) a.list[cursor[bin_of[i]]++] = (uint16_t)order[i].second;
+    a.list_bins = kListBins;
+}
+
 bool decode_fast_path(int head_dim, int group) {
     return (head_dim == 64 || head_dim == 128) &&
            (group == 1 || group == 2 || group == 4 || group == 8 || group == 16);
@@ -791,6 +873,9 @@ hipError_t launch_decode(const DecodeLaunch &l, hipStream_t stream) {
                      [&](int16_t x, int16_t y) { return last_len(x) > last_len(y); });
     const int group = l.q_heads / l.kv_heads;
     const bool nt = kv_tokens * l.kv_heads * l.head_dim * 2 * 2 >= kNonTemporalBytes;
+    const int64_t items = (int64_t)total * l.kv_heads;
+    if (decode_fast_path(l.head_dim, group) && !l.separate_merge && items > kListBins && items <= kMaxListItems)
+        plan_lists(a, total, l.seq_len);
     if (!decode_fast_path(l.head_dim, group)) {
         const dim3 grid((unsigned)(l.batch * l.q_heads));
         if (l.paged)
