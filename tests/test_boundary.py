@@ -152,13 +152,14 @@ def test_prefill_split_choices():
 
 def test_prefill_pool_choices():
     # host-only plan of mslim_attn_prefill_causal: row blocks per XCD handed
-    # out at run time; 3/8 of each XCD's slice up to 96, only for unsplit
-    # launches with at least two row blocks per CU (64 per XCD)
+    # out at run time; a quarter of each XCD's slice up to 64, only for
+    # unsplit launches with at least two row blocks per CU (64 per XCD)
     from mslim_attn import MslimAttnError, prefill_pool_items
-    assert prefill_pool_items(8192, 0, 64, 8, 128) == 96     # cfg4: 256 row blocks per XCD
-    assert prefill_pool_items(4096, 0, 64, 8, 128) == 48     # 128 per XCD
-    assert prefill_pool_items(8192, 0, 32, 8, 128) == 48     # 64-row blocks of 4 heads
-    assert prefill_pool_items(2048, 0, 64, 8, 128) == 24     # 64 per XCD
+    assert prefill_pool_items(8192, 0, 64, 8, 128) == 64     # cfg4: 256 row blocks per XCD
+    assert prefill_pool_items(16384, 0, 64, 8, 128) == 64    # 512 per XCD: capped
+    assert prefill_pool_items(4096, 0, 64, 8, 128) == 32     # 128 per XCD
+    assert prefill_pool_items(8192, 0, 32, 8, 128) == 32     # 64-row blocks of 4 heads
+    assert prefill_pool_items(2048, 0, 64, 8, 128) == 16     # 64 per XCD
     assert prefill_pool_items(1024, 0, 64, 8, 128) == 0      # 32 per XCD: one per CU
     assert prefill_pool_items(2048, 0, 32, 8, 128) == 0      # cfg2 is split
     assert prefill_pool_items(4096, 0, 4, 2, 80) == 0        # generic kernel: static

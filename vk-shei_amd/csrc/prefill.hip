@@ -78,7 +78,7 @@ constexpr int kCus = 256;        // MI355X compute units
 constexpr int kXcds = 8;         // MI355X accelerator complex dies
 // Run-time pool of an unsplit launch: at most kPoolMax row blocks per XCD,
 // kPoolSpare extra workgroups per XCD to take them.
-constexpr int kPoolMax = 96;
+constexpr int kPoolMax = 64;
 constexpr int kPoolSpare = 8;
 // Lazy rescale: the reference maximum moves only when a tile's row sum under
 // it exceeds 2^8 (so every p stays within 2^8 of the reference).
@@ -744,11 +744,13 @@ int prefill_pool_items(const PrefillLaunch &l) {
     const int64_t total = (int64_t)((l.queries + rows - 1) / rows) * l.kv_heads * (group / hw);
     const int64_t per_xcd = (total + kXcds - 1) / kXcds;
     // Only launches with at least two row blocks per CU queue any; then the
-    // shortest three eighths of every slice, at most kPoolMax (at cfg4's
-    // 256 row blocks per XCD, 96 measured best: a larger pool moves longer
-    // row blocks away from the L2 that holds their kv head).
+    // shortest quarter of every slice, at most kPoolMax.  At cfg4's 256 row
+    // blocks per XCD, 64 and 96 measured equally fast and 32 slower; every
+    // pooled row block that another XCD takes reads its kv head's K/V from
+    // beyond that XCD's L2 (fetched per call: 281 MB without a pool, 344 MB
+    // with 64, 448 MB with 96, 526 MB with 128).
     if (per_xcd < 2 * (kCus / kXcds)) return 0;
-    return (int)std::min<int64_t>(kPoolMax, per_xcd * 3 / 8);
+    return (int)std::min<int64_t>(kPoolMax, per_xcd / 4);
 }
 
 hipError_t launch_prefill(const PrefillLaunch &l, hipStream_t stream) {
