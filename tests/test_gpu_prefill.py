@@ -215,7 +215,7 @@ def test_prefill_split_plan_is_shape_only(ctx):
     assert mslim_attn.prefill_split_tiles(8192, 0, 64, 8, 128) == 0
     # tiny launches have nothing to split
     assert mslim_attn.prefill_split_tiles(100, 0, 32, 8, 128) == 0
-    assert mslim_attn.prefill_split_tiles(2048, 0, 32, 8, 128) == 17
+    assert mslim_attn.prefill_split_tiles(2048, 0, 32, 8, 128) == 19
     with pytest.raises(mslim_attn.MslimAttnError):
         mslim_attn.prefill_split_tiles(0, 0, 32, 8, 128)
 

@@ -37,6 +37,10 @@
 //     split row block to finish merges the chunks' (m, l, O) partials in
 //     fixed chunk order, so the result does not depend on timing.
 #include <algorithm>
+#include <mutex>
+#include <map>
+#include <array>
+#include <queue>
 #include <type_traits>
 #include <vector>
 
@@ -692,10 +696,90 @@ bool prefill_fast_path(int head_dim, int group) {
     return (head_dim == 64 || head_dim == 128) && (group == 1 || group == 2 || group % 4 == 0);
 }
 
+namespace {
+
+// Predicted span, in 64-key tiles, of a launch whose row blocks split into
+// chunks of tc tiles (tc >= the longest row block: no split).  The items go,
+// longest first, to the CU of their XCD that frees first (each XCD takes its
+// own kv heads when they divide evenly over the XCDs, as launch_prefill deals
+// them; otherwise all CUs share one list); an item costs its tiles plus
+// kItemFixedTiles (Q, the first copies, the partial or output write), and a
+// split row block ends kMergeTiles after its last chunk.  Fitted to cfg2 and
+// to the decoder's 512-token chunks after 3,584 tokens, whose measured best
+// chunk lengths (19-20 and 16 tiles) it reproduces.
+constexpr double kItemFixedTiles = 6.0;
+constexpr double kMergeTiles = 2.0;
+
+double split_span(const PrefillLaunch &l, int rows, int nrb, int groups, int subgroups, int tc) {
+    const bool by_head = l.kv_heads % kXcds == 0;
+    const int lists = by_head ? kXcds : 1;
+    const int cus = by_head ? kCus / kXcds : kCus;
+    double span = 0.0;
+    std::vector<std::pair<int, int>> items;  // (tiles, row block key)
+    std::vector<double> row_end((size_t)groups * nrb);
+    for (int x = 0; x < lists; ++x) {
+        items.clear();
+        for (int hg = 0; hg < groups; ++hg) {
+            if (by_head && ((hg / subgroups) / (l.kv_heads / kXcds)) % kXcds != x) continue;
+            for (int rb = 0; rb < nrb; ++rb) {
+                const int nkt = row_block_tiles(l, rows, rb);
+                const int nc = (nkt + tc - 1) / tc;
+                for (int c = 0; c < nc; ++c) items.push_back({c ? tc : nkt - (nc - 1) * tc, hg * nrb + rb});
+            }
+        }
+        std::stable_sort(items.begin(), items.end(),
+                         [](const std::pair<int, int> &a, const std::pair<int, int> &b) { return a.first > b.first; });
+        std::vector<double> free_at(cus, 0.0);
+        std::priority_queue<std::pair<double, int>, std::vector<std::pair<double, int>>,
+                            std::greater<std::pair<double, int>>> cu;
+        for (int c = 0; c < cus; ++c) cu.push({0.0, c});
+        for (const auto &it : items) {
+            auto top = cu.top();
+            cu.pop();
+            const double end = top.first + kItemFixedTiles + it.first;
+            cu.push({end, top.second});
+            row_end[(size_t)it.second] = std::max(row_end[(size_t)it.second], end);
+            span = std::max(span, end);
+        }
+    }
+    if (tc < (int)1e9) {
+        for (int hg = 0; hg < groups; ++hg)
+            for (int rb = 0; rb < nrb; ++rb)
+                if (row_block_tiles(l, rows, rb) > tc) span = std::max(span, row_end[(size_t)hg * nrb + rb] + kMergeTiles);
+    }
+    return span;
+}
+
+PrefillSplit plan_split(const PrefillLaunch &l);
+
+}  // namespace
+
+// The plan depends on the shape only and costs up to a few hundred us of
+// host time, so plans are kept per shape (a decoder repeats a few prompt-chunk
+// shapes over every layer and sequence).
 PrefillSplit prefill_split_plan(const PrefillLaunch &l) {
+    const int group = l.q_heads / l.kv_heads;
+    if (!l.split_allowed || !prefill_fast_path(l.head_dim, group)) return PrefillSplit{};
+    const std::array<int, 5> key = {l.queries, l.prior, l.q_heads, l.kv_heads, l.head_dim};
+    static std::mutex lock;
+    static std::map<std::array<int, 5>, PrefillSplit> plans;
+    {
+        std::lock_guard<std::mutex> guard(lock);
+        const auto it = plans.find(key);
+        if (it != plans.end()) return it->second;
+    }
+    const PrefillSplit p = plan_split(l);
+    std::lock_guard<std::mutex> guard(lock);
+    if (plans.size() >= 4096) plans.clear();
+    plans.emplace(key, p);
+    return p;
+}
+
+namespace {
+
+PrefillSplit plan_split(const PrefillLaunch &l) {
     PrefillSplit p;
     const int group = l.q_heads / l.kv_heads;
-    if (!l.split_allowed || !prefill_fast_path(l.head_dim, group)) return p;
     const int hw = heads_per_workgroup(group);
     const int rows = 32 * (8 / hw);
     const int nrb = (l.queries + rows - 1) / rows;
@@ -717,24 +801,38 @@ PrefillSplit prefill_split_plan(const PrefillLaunch &l) {
     // of three tile copies, so chunks are at least 4 tiles.
     const int min_chunk = std::max(4, rows / kBN + 2);
     if (longest <= target + target / 4 || longest <= min_chunk) return p;
-    int tc = (int)std::max<int64_t>(target, min_chunk);
-    for (;; ++tc) {
+    // Chunk lengths from a quarter below the mean work per CU to twice it
+    // (those the item table and the merge hold), and no split at all, scored
+    // by split_span; the shortest span wins, ties to the shorter chunk.
+    const int subgroups = group / hw;
+    const int lo = (int)std::max<int64_t>(min_chunk, target - target / 4);
+    const int hi = (int)std::min<int64_t>(longest - 1, 2 * target);
+    int best = 0;
+    int64_t best_items = 0;
+    double best_span = split_span(l, rows, nrb, groups, subgroups, (int)1e9);
+    for (int tc = lo; tc <= hi; ++tc) {
         int64_t items = 0;
         for (int rb = 0; rb < nrb; ++rb) items += (row_block_tiles(l, rows, rb) + tc - 1) / tc;
         items *= groups;
-        if (items <= kMaxSplitItems && (longest + tc - 1) / tc <= kMaxChunks) {
-            p.items = (int)items;
-            break;
+        if (items > kMaxSplitItems || (longest + tc - 1) / tc > kMaxChunks) continue;
+        const double span = split_span(l, rows, nrb, groups, subgroups, tc);
+        if (span < best_span) {
+            best_span = span;
+            best = tc;
+            best_items = items;
         }
     }
-    if (tc >= longest) return PrefillSplit{};
-    p.chunk_tiles = tc;
-    p.max_chunks = (longest + tc - 1) / tc;
+    if (!best) return p;
+    p.chunk_tiles = best;
+    p.items = (int)best_items;
+    p.max_chunks = (longest + best - 1) / best;
     p.counters = groups * nrb;
     const int pairs = (l.head_dim / 32) * 8 + 1;
     p.partial_bytes = (size_t)groups * nrb * p.max_chunks * 8 * pairs * 64 * 2 * sizeof(float);
     return p;
 }
+
+}  // namespace
 
 int prefill_pool_items(const PrefillLaunch &l) {
     const int group = l.q_heads / l.kv_heads;
