@@ -363,8 +363,9 @@ int mslim_attn_pages_append(void *ctx, void *k_pool, void *v_pool, const int32_t
  * with the V rows ([batch][kv_heads][head_dim]) to logical position
  * positions[b] of sequence b through page-table row b.  Equal, bit for bit, to
  * mslim_attn_rope_rows on Q and on K followed by mslim_attn_pages_append of
- * the rotated K and V.  The reference runs the two llm_rope launches and the
- * K/V copies of run_layer separately (gpu_llm/mod.rs:2094-2136). */
+ * the rotated K and V (head_dim a multiple of 8, at most 512).  The reference
+ * runs the two llm_rope launches and the K/V copies of run_layer separately
+ * (gpu_llm/mod.rs:2094-2136). */
 int mslim_attn_rope_append(void *ctx, const void *q, const void *k, const void *v, void *q_out,
                            void *k_pool, void *v_pool, const int32_t *page_table, int pages_per_seq,
                            int page_tokens, int batch, const int32_t *positions, int q_heads,

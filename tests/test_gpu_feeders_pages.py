@@ -39,10 +39,11 @@ def test_rope_bit_exact(ctx, llama3, start):
 
 
 def test_rope_other_head_dims(ctx):
-    # 64, 80, 256: 16-byte chunks; 72 (half not a multiple of 8): one element
-    # per lane; 1024: the per-element kernel (head_dim > 512)
+    # 64, 80, 256, 512: 16-byte chunks (512: the whole 256-pair frequency
+    # table); 72 (half not a multiple of 8): one element per lane; 1024: the
+    # per-element kernel (head_dim > 512)
     rng = np.random.default_rng(1)
-    for d in (64, 72, 80, 256, 1024):
+    for d in (64, 72, 80, 256, 512, 1024):
         xb = normal_bf16(rng, (5, 4, d))
         out = torch.empty((5, 4, d), dtype=torch.int16, device="cuda")
         ctx.rope(to_torch(xb), out, 5, 4, d, 123, 10000.0)

@@ -172,6 +172,18 @@ def test_rope_append_equals_rope_then_append(ctx, page_tokens, llama3):
     assert torch.equal(q_a, q_b) and torch.equal(k_a, k_b) and torch.equal(v_a, v_b)
 
 
+def test_rope_append_rejects_head_dim_above_512(ctx):
+    # the fused step takes its inverse frequencies from a 256-pair table
+    from mslim_attn import MslimAttnError
+    d = 520
+    q, k, v = (torch.zeros((1, 1, d), dtype=torch.int16, device="cuda") for _ in range(3))
+    q_out = torch.empty_like(q)
+    pool = torch.zeros((1, 1, 16, d), dtype=torch.int16, device="cuda")
+    with pytest.raises(MslimAttnError, match="invalid RoPE append arguments"):
+        ctx.rope_append(q, k, v, q_out, pool, pool.clone(), _dev_i32([[0]]), 1, 16, 1, _dev_i32([0]), 1, 1, d,
+                        500000.0)
+
+
 # ---- decoder runner ------------------------------------------------------------
 
 SPEC = Spec(layers=2, hidden=256, q_heads=8, kv_heads=2, head_dim=64, intermediate=512, vocab=1000)

@@ -819,7 +819,7 @@ int mslim_attn_rope_append(void *ctx, const void *q, const void *k, const void *
                            float original_max_position) {
     g_error.clear();
     if (!ctx || !q || !k || !v || !q_out || !k_pool || !v_pool || !page_table || !positions || batch < 1 ||
-        pages_per_seq < 1 || q_heads < 1 || kv_heads < 1 || head_dim < 8 || head_dim % 8 ||
+        pages_per_seq < 1 || q_heads < 1 || kv_heads < 1 || head_dim < 8 || head_dim % 8 || head_dim > 512 ||
         !is_pow2(page_tokens) || page_tokens > (1 << 20) || !(theta > 0.0f) || !std::isfinite(theta))
         return fail("invalid RoPE append arguments");
     if (q_out == q) return fail("RoPE output must not alias its input");

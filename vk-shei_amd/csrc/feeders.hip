@@ -9,6 +9,8 @@
 //   * exp, log, sin and cos are evaluated in double precision and rounded
 //     once to float.
 // No multiply-add is contracted: every stage rounds as written.
+#include <cmath>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -153,18 +155,25 @@ __device__ float rope_inverse_frequency(int fd, int head_dim, float theta, int l
     return inv;
 }
 
+// Inverse frequencies of the rotary pairs f = 0 .. head_dim/2 - 1 of one
+// launch, computed on the host (rope_table) with the same f32 operations as
+// rope_inverse_frequency and the same once-rounded f64 log and exp, so the
+// kernels need no f64 log or exp per lane.  Covers head_dim <= 2 * kRopeTable.
+constexpr int kRopeTable = 256;
+struct RopeTable {
+    float inv[kRopeTable];
+};
+
 // One rotated element of llm_rope / llm_prefill_rope (gpu_llm.cl:102-146,
 // :412-456): element d of head `head` of a token row [heads][head_dim] at
-// `position`, rotate-half partner, c and s rounded to BF16.
+// `position`, rotate-half partner, c and s rounded to BF16; `inv` is the
+// inverse frequency of pair d % (head_dim / 2).
 __device__ __forceinline__ uint16_t rope_element(const uint16_t *token_row, int head, int d, int head_dim,
-                                                 int64_t position, float theta, int llama3, float factor,
-                                                 float low, float high, float original_max) {
+                                                 int64_t position, float inv) {
     const int half = head_dim / 2;
     const uint16_t *h = token_row + (int64_t)head * head_dim;
     const float partner = read_bf16(h[d < half ? d + half : d - half]);
     const float rotated = d < half ? -partner : partner;
-    const int fd = (d % half) * 2;
-    const float inv = rope_inverse_frequency(fd, head_dim, theta, llama3, factor, low, high, original_max);
     const float phase = __fmul_rn((float)position, inv);
     const float cs = round_bf16((float)cos((double)phase));
     const float sn = round_bf16((float)sin((double)phase));
@@ -187,19 +196,20 @@ __global__ __launch_bounds__(256) void rope_kernel(const uint16_t *in, uint16_t 
     const int64_t token = i / elements;
     const int in_token = (int)(i % elements);
     const int64_t position = positions ? (int64_t)positions[token] : start + token;
-    out[i] = rope_element(in + token * elements, in_token / head_dim, in_token % head_dim, head_dim, position,
-                          theta, llama3, factor, low, high, original_max);
+    const int d = in_token % head_dim;
+    const float inv = rope_inverse_frequency((d % (head_dim / 2)) * 2, head_dim, theta, llama3, factor, low, high,
+                                             original_max);
+    out[i] = rope_element(in + token * elements, in_token / head_dim, d, head_dim, position, inv);
 }
 
 // The same rotation with one workgroup per token row: the row's c and s
 // (one pair per rotary dimension pair, head_dim / 2 <= 256) are computed once
-// into LDS and shared by all heads, instead of once per element.  Each value
-// is computed exactly as rope_element computes it, so the output is
-// bit-identical.
+// into LDS and shared by all heads, instead of once per element, from the
+// launch's inverse-frequency table.  Each value is computed exactly as
+// rope_element computes it, so the output is bit-identical.
 __global__ __launch_bounds__(256) void rope_token_kernel(const uint16_t *in, uint16_t *out, int heads,
                                                          int head_dim, int start, const int32_t *positions,
-                                                         float theta, int llama3, float factor, float low,
-                                                         float high, float original_max) {
+                                                         RopeTable table) {
     __shared__ float cs[256], sn[256];
     const int64_t token = blockIdx.x;
     const int half = head_dim / 2;
@@ -208,8 +218,7 @@ __global__ __launch_bounds__(256) void rope_token_kernel(const uint16_t *in, uin
     // table costs one trigonometric evaluation per lane, not two.
     for (int t = threadIdx.x; t < 2 * half; t += blockDim.x) {
         const int f = t % half;
-        const float inv = rope_inverse_frequency(2 * f, head_dim, theta, llama3, factor, low, high, original_max);
-        const float phase = __fmul_rn((float)position, inv);
+        const float phase = __fmul_rn((float)position, table.inv[f]);
         if (t < half) cs[f] = round_bf16((float)cos((double)phase));
         else sn[f] = round_bf16((float)sin((double)phase));
     }
@@ -266,7 +275,7 @@ __global__ __launch_bounds__(256) void rope_token_kernel(const uint16_t *in, uin
 // into the page pool through page-table row b.  Lanes [0, nq) rotate Q
 // elements, [nq, nq + nk) rotate K elements, the rest copy V 16 bytes at a
 // time.  Equal to rope_kernel on Q and on K followed by pages_append.
-__global__ __launch_bounds__(256) void rope_append_kernel(RopeAppendArgs a) {
+__global__ __launch_bounds__(256) void rope_append_kernel(RopeAppendArgs a, RopeTable table) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t nq = (int64_t)a.batch * a.q_heads * a.head_dim;
     const int64_t nk = (int64_t)a.batch * a.kv_heads * a.head_dim;
@@ -274,9 +283,9 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeAppendArgs a) {
     if (i >= nq + nk + nv) return;
     if (i < nq) {
         const int64_t elements = (int64_t)a.q_heads * a.head_dim;
-        const int b = (int)(i / elements), e = (int)(i % elements);
-        a.q_out[i] = rope_element(a.q + b * elements, e / a.head_dim, e % a.head_dim, a.head_dim, a.positions[b],
-                                  a.theta, a.llama3, a.factor, a.low, a.high, a.original_max);
+        const int b = (int)(i / elements), e = (int)(i % elements), d = e % a.head_dim;
+        a.q_out[i] = rope_element(a.q + b * elements, e / a.head_dim, d, a.head_dim, a.positions[b],
+                                  table.inv[d % (a.head_dim / 2)]);
         return;
     }
     const int64_t kvd = (int64_t)a.kv_heads * a.head_dim;
@@ -284,15 +293,14 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeAppendArgs a) {
     const int b = (int)((j < nk ? j : (j - nk) * 8) / kvd);
     const int64_t position = a.positions[b];
     if (position < 0 || position >= ((int64_t)a.pages_per_seq << a.shift)) return;
-    const int32_t *table = a.page_table + (int64_t)b * a.pages_per_seq;
+    const int32_t *rows = a.page_table + (int64_t)b * a.pages_per_seq;
     if (j < nk) {
         const int e = (int)(j % kvd), head = e / a.head_dim, d = e % a.head_dim;
-        a.k_pool[page_row(table, a.shift, a.kv_heads, head, position) * a.head_dim + d] =
-            rope_element(a.k + b * kvd, head, d, a.head_dim, position, a.theta, a.llama3, a.factor, a.low, a.high,
-                         a.original_max);
+        a.k_pool[page_row(rows, a.shift, a.kv_heads, head, position) * a.head_dim + d] =
+            rope_element(a.k + b * kvd, head, d, a.head_dim, position, table.inv[d % (a.head_dim / 2)]);
     } else {
         const int e = (int)(((j - nk) * 8) % kvd), head = e / a.head_dim, d = e % a.head_dim;
-        *reinterpret_cast<uint4 *>(a.v_pool + page_row(table, a.shift, a.kv_heads, head, position) * a.head_dim +
+        *reinterpret_cast<uint4 *>(a.v_pool + page_row(rows, a.shift, a.kv_heads, head, position) * a.head_dim +
                                    d) = *reinterpret_cast<const uint4 *>(a.v + b * kvd + e);
     }
 }
@@ -411,12 +419,61 @@ hipError_t launch_rmsnorm(const uint16_t *in, const uint16_t *w, uint16_t *out, 
     return hipGetLastError();
 }
 
+namespace {
+
+// rope_inverse_frequency on the host for pairs 0 .. head_dim/2 - 1: the same
+// f32 operations in the same order (no contraction in this file), log and exp
+// in f64 rounded once.  The last table is kept per thread, since a decoder
+// launches the same one for every layer.
+const RopeTable &rope_table(int head_dim, float theta, int llama3, float factor, float low, float high,
+                            float original_max) {
+    struct Cached {
+        bool valid = false;
+        int head_dim = 0, llama3 = 0;
+        float theta = 0, factor = 0, low = 0, high = 0, original_max = 0;
+        RopeTable table;
+    };
+    thread_local Cached c;
+    if (c.valid && c.head_dim == head_dim && c.theta == theta && c.llama3 == llama3 && c.factor == factor &&
+        c.low == low && c.high == high && c.original_max == original_max)
+        return c.table;
+    const float log_theta = (float)std::log((double)theta);
+    for (int f = 0; f < head_dim / 2; ++f) {
+        const float exponent = (-(float)(2 * f) * log_theta) / (float)head_dim;
+        float inv = (float)std::exp((double)exponent);
+        if (llama3) {
+            const float wavelength = 6.28318530717958647692f / inv;
+            const float low_wavelength = original_max / low;
+            const float high_wavelength = original_max / high;
+            if (wavelength > low_wavelength) {
+                inv = inv / factor;
+            } else if (wavelength >= high_wavelength) {
+                const float smooth = (original_max / wavelength - low) / (high - low);
+                inv = (1.0f - smooth) * (inv / factor) + smooth * inv;
+            }
+        }
+        c.table.inv[f] = inv;
+    }
+    c.valid = true;
+    c.head_dim = head_dim;
+    c.theta = theta;
+    c.llama3 = llama3;
+    c.factor = factor;
+    c.low = low;
+    c.high = high;
+    c.original_max = original_max;
+    return c.table;
+}
+
+}  // namespace
+
 hipError_t launch_rope(const uint16_t *in, uint16_t *out, int tokens, int heads, int head_dim,
                        int start, const int32_t *positions, float theta, int llama3, float factor,
                        float low, float high, float original_max, hipStream_t stream) {
-    if (head_dim <= 512) {
+    if (head_dim <= 2 * kRopeTable) {
+        const RopeTable &table = rope_table(head_dim, theta, llama3, factor, low, high, original_max);
         hipLaunchKernelGGL(rope_token_kernel, dim3((unsigned)tokens), dim3(256), 0, stream, in, out, heads,
-                           head_dim, start, positions, theta, llama3, factor, low, high, original_max);
+                           head_dim, start, positions, table);
         return hipGetLastError();
     }
     const int64_t total = (int64_t)tokens * heads * head_dim;
@@ -427,9 +484,11 @@ hipError_t launch_rope(const uint16_t *in, uint16_t *out, int tokens, int heads,
 }
 
 hipError_t launch_rope_append(const RopeAppendArgs &a, hipStream_t stream) {
+    if (a.head_dim > 2 * kRopeTable) return hipErrorInvalidValue;
+    const RopeTable &table = rope_table(a.head_dim, a.theta, a.llama3, a.factor, a.low, a.high, a.original_max);
     const int64_t nk = (int64_t)a.batch * a.kv_heads * a.head_dim;
     const int64_t total = (int64_t)a.batch * a.q_heads * a.head_dim + nk + nk / 8;
-    hipLaunchKernelGGL(rope_append_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(rope_append_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, a, table);
     return hipGetLastError();
 }
 
