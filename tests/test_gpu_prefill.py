@@ -209,6 +209,45 @@ def test_prefill_split_launches(ctx, queries, prior, qh, kvh, d):
     assert float(diff.max()) <= TOL
 
 
+def test_prefill_split_random_shapes_match_unsplit(ctx):
+    # The chunk length comes from a model of the dispatch and varies with the
+    # shape; every chunking must equal the unsplit launch up to rounding and
+    # repeat bit for bit.  Seeded shapes of every head layout the fast kernel
+    # takes, with and without a prior (195 such shapes passed the same check
+    # when the model was introduced; these are a fixed sample).
+    import mslim_attn
+    rng = np.random.default_rng(20261202)
+    layouts = [(32, 8), (64, 8), (16, 2), (8, 8), (32, 4), (28, 4), (16, 16), (24, 8)]
+    checked = 0
+    while checked < 24:
+        qh, kvh = layouts[int(rng.integers(len(layouts)))]
+        d = int(rng.choice([64, 128]))
+        queries = int(rng.integers(1, 4097))
+        prior = int(rng.choice([0, 0, int(rng.integers(0, 8193))]))
+        chunk = mslim_attn.prefill_split_tiles(queries, prior, qh, kvh, d)
+        if chunk <= 0:
+            continue
+        checked += 1
+        print(f"split shape {queries} after {prior}, {qh}/{kvh} heads, d {d}: chunks of {chunk} tiles", flush=True)
+        gen = torch.Generator(device="cuda").manual_seed(checked)
+        q = torch.randn((queries, qh, d), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+        k = torch.randn((prior + queries, kvh, d), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+        v = torch.randn((prior + queries, kvh, d), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+        out, again, whole = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
+        ctx.prefill_causal(q, k, v, out, queries, prior, qh, kvh, d)
+        ctx.prefill_causal(q, k, v, again, queries, prior, qh, kvh, d)
+        try:
+            ctx.set_prefill_split(False)
+            ctx.prefill_causal(q, k, v, whole, queries, prior, qh, kvh, d)
+        finally:
+            ctx.set_prefill_split(True)
+        torch.cuda.synchronize()
+        assert torch.equal(out, again)
+        got = out.view(torch.bfloat16).float()
+        assert bool(torch.isfinite(got).all())
+        assert (got - whole.view(torch.bfloat16).float()).abs().max().item() <= TOL
+
+
 def test_prefill_split_plan_is_shape_only(ctx):
     import mslim_attn
     # cfg4's 8,192-token prefill has 2,048 workgroups: never split
