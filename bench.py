@@ -685,7 +685,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
-              f"(no multi-GPU path is built; see DESIGN.md for how decode and prefill would shard)",
+              f"(no multi-GPU path is built: decode and prefill shard by kv head with no exchange, "
+              f"and the decode merge takes split partials from other GPUs unchanged)",
               file=sys.stderr)
         return 2
     if args.steps < 1 or args.warmup < 0:
