@@ -101,6 +101,14 @@ __device__ __forceinline__ short4_t lds_read_tr16(const uint16_t *lds) {
         (__attribute__((address_space(3))) short4_t *)(lds));
 }
 
+// The same two reads from a 32-bit LDS byte address.
+__device__ __forceinline__ short4_t lds_read_tr16_at(uint32_t addr) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4_t *)(uintptr_t)addr);
+}
+__device__ __forceinline__ bf16x8_t lds_read_b128(uint32_t addr) {
+    return *(const __attribute__((address_space(3))) bf16x8_t *)(uintptr_t)addr;
+}
+
 __device__ __forceinline__ bool wave_any(bool pred) {
     return __builtin_amdgcn_ballot_w64(pred) != 0;
 }

@@ -20,7 +20,15 @@
 //   * on gfx950 ordinary VALU work hides under MFMAs only when the same
 //     wavefront interleaves the two, so each wavefront software-pipelines its
 //     own tiles: the softmax of tile j runs in the MFMA slots of P.V of tile
-//     j-1;
+//     j-1.  The first two P.V MFMAs of tile j-1 run ahead of the QK MFMAs of
+//     tile j (their V fragments read before the barrier), and the copy of a
+//     later tile is issued behind the first QK MFMAs, so the SIMD has MFMA
+//     work while the tile's first K fragments are in flight;
+//   * Q enters the QK MFMAs pre-multiplied by scale * log2(e) (rounded to
+//     BF16) and the S accumulator starts from -m (the row's reference
+//     maximum), so each score leaves the MFMA as the exp2 argument: the
+//     softmax costs exp2, a BF16 pack and a row-sum step per score, no
+//     multiply;
 //   * O is rescaled only when a tile's row sum under the current maximum
 //     exceeds 2^8 (exact: the final O / l uses the same stale maximum), row
 //     sums use v_dot2 on the BF16 P that feeds the MFMA;
@@ -87,6 +95,10 @@ constexpr int kPoolSpare = 8;
 // Lazy rescale: the reference maximum moves only when a tile's row sum under
 // it exceeds 2^8 (so every p stays within 2^8 of the reference).
 constexpr float kLazyBound = 256.0f;
+// QK MFMA of a tile after which the copy of a later tile is issued.
+constexpr int kCopySlot = 3;
+// P.V slots of a tile issued ahead of the next tile's QK MFMAs.
+constexpr int kHead = 2;
 
 template <int D>
 struct Swz {
@@ -110,6 +122,10 @@ struct Swz {
 constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
 // The same with every LDS read of this wavefront complete (lgkmcnt 0).
 constexpr int vmcnt_lds_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4); }
+// The same with at most l LDS reads outstanding (lgkmcnt l).  LDS reads
+// complete in issue order when no scalar memory load is in flight, so the
+// last l reads may still be pending and every earlier one has completed.
+constexpr int vmcnt_lds_last_imm(int n, int l) { return vmcnt_lds_imm(n) | (l << 8); }
 
 // Workgroup barrier without the memory fence of __syncthreads(): with LDS
 // DMA in flight that fence would wait for every outstanding DMA (vmcnt 0).
@@ -134,10 +150,13 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
     constexpr int RW = 32 * (WAVES / HW);
     constexpr int NS = 4 * MT;  // P.V MFMA slots per tile
     static_assert(NS >= 8, "slot plan needs at least eight P.V slots");
+    static_assert(2 * kHead <= 15 && kHead + 2 <= NS, "head reads must fit the lgkmcnt field");
     using S = Swz<D>;
     constexpr int TILE = kBN * D;
-    __shared__ __align__(16) uint16_t k0[TILE], v0[TILE], k1[TILE], v1[TILE];
-    __shared__ __align__(16) uint16_t k2[TILE], v2[TILE], k3[TILE], v3[TILE];
+    // The four K stages, then the four V stages: each set spans 64 KiB, so
+    // one per-lane fragment address serves every stage through the LDS
+    // instructions' 16-bit immediate offset.
+    __shared__ __align__(16) uint16_t kv_lds[2 * ST][TILE];
     constexpr int CPW = S::CHUNKS / WAVES;  // 1 KB chunks of K (and of V) per wavefront
 
     const int tid = threadIdx.x;
@@ -206,12 +225,19 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
     const int row_abs = a.prior + row;
     const float c = a.scale_log2e;
 
+    // Q enters the MFMAs pre-multiplied by scale * log2(e) and rounded to
+    // BF16 (RNE), so every score comes out of the QK MFMAs in log2 units and
+    // the softmax needs no multiply per score.
     bf16x8_t qf[KS];
     {
         const int qrow = min(row, a.queries - 1);
         const uint16_t *qp = a.q + ((int64_t)qrow * a.q_heads + head) * D + half * 8;
 #pragma unroll
         for (int j = 0; j < KS; ++j) qf[j] = *reinterpret_cast<const bf16x8_t *>(qp + j * 16);
+#pragma unroll
+        for (int j = 0; j < KS; ++j)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qf[j][e] = (__bf16)((float)qf[j][e] * c);
     }
     // Q has landed before any K/V copy is issued (no wait inside the loop
     // may hold back copies in flight).
@@ -234,31 +260,28 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
     // chunk ch lands at row RPC*ch + l/NSLOT, physical slot l % NSLOT and
     // fetches the logical slot that the swizzle maps there.  Keys past the
     // history are clamped to the last key (they are masked); only the tile
-    // that holds the last key has such rows, and its copies use a second set
-    // of lane offsets.  Offsets are bytes from the tile's first row, so a copy
+    // that holds the last key has such rows, and its copies move those lanes'
+    // offsets back to the last key's row.  Offsets are bytes from the tile's first row, so a copy
     // needs only the scalar tile base (no per-lane 64-bit address arithmetic
     // per tile).
     const uint32_t row_bytes = (uint32_t)a.kv_heads * D * 2;
     const int tile_last = last_key / kBN;
     const int last_row = last_key - tile_last * kBN;
-    uint32_t koff[CPW], voff[CPW], kclamp[CPW], vclamp[CPW];
+    uint32_t koff[CPW], voff[CPW];
 #pragma unroll
     for (int i = 0; i < CPW; ++i) {
         const int ch = wave + WAVES * i;
         const int r = S::RPC * ch + lane / S::NSLOT;
         const int p = lane % S::NSLOT;
         const uint32_t head_bytes = (uint32_t)kvh * D * 2;
-        const uint32_t rc = (uint32_t)min(r, last_row);
         koff[i] = (uint32_t)r * row_bytes + head_bytes + S::k(r, p) * 16;
         voff[i] = (uint32_t)r * row_bytes + head_bytes + S::v(r, p) * 16;
-        kclamp[i] = rc * row_bytes + head_bytes + S::k(r, p) * 16;
-        vclamp[i] = rc * row_bytes + head_bytes + S::v(r, p) * 16;
     }
     // LDS byte address of this wavefront's first chunk in every stage.
-    const uint32_t kst_lds[ST] = {lds_offset(k0 + wave * 512), lds_offset(k1 + wave * 512),
-                                  lds_offset(k2 + wave * 512), lds_offset(k3 + wave * 512)};
-    const uint32_t vst_lds[ST] = {lds_offset(v0 + wave * 512), lds_offset(v1 + wave * 512),
-                                  lds_offset(v2 + wave * 512), lds_offset(v3 + wave * 512)};
+    const uint32_t kst_lds[ST] = {lds_offset(kv_lds[0] + wave * 512), lds_offset(kv_lds[1] + wave * 512),
+                                  lds_offset(kv_lds[2] + wave * 512), lds_offset(kv_lds[3] + wave * 512)};
+    const uint32_t vst_lds[ST] = {lds_offset(kv_lds[4] + wave * 512), lds_offset(kv_lds[5] + wave * 512),
+                                  lds_offset(kv_lds[6] + wave * 512), lds_offset(kv_lds[7] + wave * 512)};
     auto dma_tile = [&](int st, int kt) __attribute__((always_inline)) {
         const int64_t base = (int64_t)kt * kBN * row_bytes;
         const char *kb = reinterpret_cast<const char *>(a.k) + base;
@@ -270,10 +293,14 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
                 dma16_async(vb, voff[i], vst_lds[st] + i * WAVES * 1024);
             }
         } else {
+            // Rows past the last key fetch the last key's row (the same
+            // logical slot): the offset moves back by whole rows.
 #pragma unroll
             for (int i = 0; i < CPW; ++i) {
-                dma16_async(kb, kclamp[i], kst_lds[st] + i * WAVES * 1024);
-                dma16_async(vb, vclamp[i], vst_lds[st] + i * WAVES * 1024);
+                const int r = S::RPC * (wave + WAVES * i) + lane / S::NSLOT;
+                const uint32_t back = (uint32_t)max(r - last_row, 0) * row_bytes;
+                dma16_async(kb, koff[i] - back, kst_lds[st] + i * WAVES * 1024);
+                dma16_async(vb, voff[i] - back, vst_lds[st] + i * WAVES * 1024);
             }
         }
     };
@@ -283,7 +310,11 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[mt][r] = 0.0f;
-    float m_used = -INFINITY, mc = -INFINITY, l_run = 0.0f;  // mc = m_used * c
+    // m_used: the row's reference maximum in log2 units; seed holds -m_used
+    // in every element and is the QK accumulator's initial value, so the
+    // MFMAs return scores relative to the reference.
+    float m_used = -INFINITY, l_run = 0.0f;
+    floatx16_t seed;
     float alpha_pending = 1.0f;
     bool rescale_pending = false;
     floatx16_t s[2];
@@ -293,15 +324,34 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
     const int rr = (lane & 15) >> 2;
     const int jj = lane & 3;
 
-    auto qk = [&](const uint16_t *kl) __attribute__((always_inline)) {
+    // Per-lane LDS byte addresses of the fragment reads in stage 0.  The
+    // swizzles depend on a row only through row % 16 (K) and row % 4 (V),
+    // which the row steps below (kb * 32 rows, 16 and 8 rows of V) keep, so
+    // a stage (TILE * 2 bytes), a key block and a V row step are immediate
+    // offsets of the same address; the bases are opaque scalars, so the
+    // compiler folds every such step into the instruction.
+    constexpr uint32_t STAGE = TILE * 2;
+    uint32_t kaddr[KS], vaddr[MT];
+    {
+        const uint32_t kbase = lds_offset(kv_lds[0]), vbase = lds_offset(kv_lds[ST]);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+            kaddr[ks] = kbase + (uint32_t)(col * D * 2 + S::k(col, 2 * ks + half) * 16);
+        const int t0 = 4 * (q4 >> 1) + rr;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const int e = mt * 32 + 16 * (q4 & 1) + 4 * jj;
+            vaddr[mt] = vbase + (uint32_t)(t0 * D * 2 + S::v(t0, e >> 3) * 16 + (e & 7) * 2);
+        }
+    }
+
+    // S^T of one tile from K stage kst; seeded: relative to the reference
+    // (first tile of the workgroup: absolute, the reference is not known yet).
+    auto qk = [&](int kst, auto seeded_tag, auto &&mid) __attribute__((always_inline)) {
+        constexpr bool seeded = decltype(seeded_tag)::value;
         auto kfrag = [&](int ks, int kb) __attribute__((always_inline)) {
-            const int kr = kb * 32 + col;
-            return *reinterpret_cast<const bf16x8_t *>(kl + kr * D + S::k(kr, 2 * ks + half) * 8);
+            return lds_read_b128(kaddr[ks] + kst * STAGE + kb * 32 * D * 2);
         };
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) s[kb][r] = 0.0f;
         bf16x8_t kq[3];
         kq[0] = kfrag(0, 0);
         kq[1] = kfrag(0, 1);
@@ -309,94 +359,139 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
         for (int n = 0; n < 2 * KS; ++n) {
             if (n + 2 < 2 * KS) kq[(n + 2) % 3] = kfrag((n + 2) / 2, (n + 2) % 2);
             __builtin_amdgcn_sched_barrier(0);
-            s[n % 2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kq[n % 3], qf[n / 2], s[n % 2], 0, 0, 0);
+            if (n < 2) {
+                floatx16_t init;
+                if constexpr (seeded) {
+                    init = seed;
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) init[r] = 0.0f;
+                }
+                s[n] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kq[n], qf[0], init, 0, 0, 0);
+            } else {
+                s[n % 2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kq[n % 3], qf[n / 2], s[n % 2], 0, 0, 0);
+            }
+            if (n == kCopySlot) mid();
             __builtin_amdgcn_sched_barrier(0);
         }
     };
 
+    // Key kt * kBN + kb * 32 + (r >> 2) * 8 + half * 4 + (r & 3) of element
+    // (kb, r) is masked when it passes the row: one lane threshold, then a
+    // compare with a constant per element.
     auto mask_tile = [&](int kt) __attribute__((always_inline)) {
+        const int thr = row_abs - kt * kBN - half * 4;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int key = kt * kBN + kb * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
-                if (key > row_abs) s[kb][r] = -INFINITY;
-            }
+            for (int r = 0; r < 16; ++r)
+                if (kb * 32 + (r >> 2) * 8 + (r & 3) > thr) s[kb][r] = -INFINITY;
     };
 
+    using Yes = std::true_type;
+    using No = std::false_type;
     // Pair pidx of the current scores (key block pidx / 8, rows 2 (pidx % 8)
-    // and the next) under the reference mc: exp2, BF16 pack, and the row sum
-    // of the packed P that feeds the MFMA.
-    auto score_pair = [&](int pidx, uint32_t (&pw)[2][8], float &psum) __attribute__((always_inline)) {
+    // and the next): exp2 of the score less `sub` (none for scores already
+    // relative to the reference), BF16 pack, and the row sum of the packed P
+    // that feeds the MFMA.
+    auto score_pair = [&](int pidx, uint32_t (&pw)[2][8], float &psum, auto sub_tag, float sub)
+        __attribute__((always_inline)) {
+        constexpr bool do_sub = decltype(sub_tag)::value;
         const int kb = pidx / 8, r = (pidx % 8) * 2;
         bf16x2_t pp;
-        pp[0] = (__bf16)__builtin_amdgcn_exp2f(fmaf(s[kb][r], c, -mc));
-        pp[1] = (__bf16)__builtin_amdgcn_exp2f(fmaf(s[kb][r + 1], c, -mc));
+        if constexpr (do_sub) {
+            pp[0] = (__bf16)__builtin_amdgcn_exp2f(s[kb][r] - sub);
+            pp[1] = (__bf16)__builtin_amdgcn_exp2f(s[kb][r + 1] - sub);
+        } else {
+            pp[0] = (__bf16)__builtin_amdgcn_exp2f(s[kb][r]);
+            pp[1] = (__bf16)__builtin_amdgcn_exp2f(s[kb][r + 1]);
+        }
         pw[kb][r >> 1] = __builtin_bit_cast(uint32_t, pp);
         psum = add_bf16_pair(pp, psum);
         pin_value(pw[kb][r >> 1]);
     };
 
-    // P.V of the previous tile (V stage vp, when do_pv) with the softmax of
-    // the current scores (when do_sm) spread over the MFMA slots.
-    auto pv_softmax = [&](const uint16_t *vp, auto pv_tag, auto sm_tag, auto first_tag)
+    // V^T fragment of P.V slot n from V stage vst.
+    auto vfrag = [&](int vst, int n) __attribute__((always_inline)) {
+        const int mt = n % MT, t = (n / MT) % 2, kb = n / (2 * MT);
+        const uint32_t a0 = vaddr[mt] + vst * STAGE + (kb * 32 + 16 * t) * D * 2;
+        const short4_t lo = lds_read_tr16_at(a0);
+        const short4_t hi = lds_read_tr16_at(a0 + 8 * D * 2);
+        const short8_t both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        return __builtin_bit_cast(bf16x8_t, both);
+    };
+    // The first kHead P.V slots of a tile run ahead of the next tile's QK
+    // MFMAs, from fragments read before the barrier: the SIMD has MFMA work
+    // while the next tile's first K fragments are in flight.
+    bf16x8_t vhead[kHead];
+    auto read_head = [&](int vst) __attribute__((always_inline)) {
+#pragma unroll
+        for (int n = 0; n < kHead; ++n) vhead[n] = vfrag(vst, n);
+    };
+    auto pv_head = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int n = 0; n < kHead; ++n) {
+            const int mt = n % MT, t = (n / MT) % 2, kb = n / (2 * MT);
+            __builtin_amdgcn_sched_barrier(0);
+            o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vhead[n], pprev[kb][t], o[mt], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    // P.V slots kHead .. NS-1 of the previous tile (V stage vst, when do_pv)
+    // with the softmax of the current scores (when do_sm) spread over them
+    // (over all NS slots when there is no P.V).
+    auto pv_softmax = [&](int vst, auto pv_tag, auto sm_tag, auto first_tag)
         __attribute__((always_inline)) {
         constexpr bool do_pv = decltype(pv_tag)::value;
         constexpr bool do_sm = decltype(sm_tag)::value;
         constexpr bool first = decltype(first_tag)::value;
-        auto vfrag = [&](int n) __attribute__((always_inline)) {
-            const int mt = n % MT, t = (n / MT) % 2, kb = n / (2 * MT);
-            const int t0 = kb * 32 + 16 * t + 4 * (q4 >> 1) + rr;
-            const int t1 = t0 + 8;
-            const int e = mt * 32 + 16 * (q4 & 1) + 4 * jj;
-            const int slot = e >> 3, off = e & 7;
-            const short4_t lo = lds_read_tr16(vp + t0 * D + S::v(t0, slot) * 8 + off);
-            const short4_t hi = lds_read_tr16(vp + t1 * D + S::v(t1, slot) * 8 + off);
-            const short8_t both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-            return __builtin_bit_cast(bf16x8_t, both);
-        };
+        constexpr int N0 = do_pv ? kHead : 0;  // first slot
+        constexpr int NL = NS - N0;             // slots here
         bf16x8_t vq[3];
         if constexpr (do_pv) {
-            vq[0] = vfrag(0);
-            vq[1] = vfrag(1);
+            vq[0] = vfrag(vst, N0);
+            vq[1] = vfrag(vst, N0 + 1);
         }
         float mx = 0.0f, psum = 0.0f;
         uint32_t pw[2][8];
 #pragma unroll
-        for (int n = 0; n < NS; ++n) {
+        for (int i = 0; i < NL; ++i) {
+            const int n = N0 + i;
             if constexpr (do_pv) {
-                if (n + 2 < NS) vq[(n + 2) % 3] = vfrag(n + 2);
+                if (n + 2 < NS) vq[(i + 2) % 3] = vfrag(vst, n + 2);
             }
             __builtin_amdgcn_sched_barrier(0);
             if constexpr (do_pv) {
                 const int mt = n % MT, t = (n / MT) % 2, kb = n / (2 * MT);
-                o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vq[n % 3], pprev[kb][t], o[mt], 0, 0, 0);
+                o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vq[i % 3], pprev[kb][t], o[mt], 0, 0, 0);
             }
             if constexpr (do_sm && first) {
                 // The workgroup's first tile: the reference is still -inf, so
-                // take the row maximum first (slots 0 and 1), then the pairs.
-                if (n == 0) {
+                // take the row maximum first (slots 0 and 1), then the pairs
+                // less it.
+                if (i == 0) {
                     mx = s[0][0];
 #pragma unroll
                     for (int r = 1; r < 15; r += 2) mx = __builtin_fmaxf(__builtin_fmaxf(mx, s[0][r]), s[0][r + 1]);
-                } else if (n == 1) {
+                } else if (i == 1) {
                     mx = __builtin_fmaxf(__builtin_fmaxf(mx, s[0][15]), s[1][0]);
 #pragma unroll
                     for (int r = 1; r < 15; r += 2) mx = __builtin_fmaxf(__builtin_fmaxf(mx, s[1][r]), s[1][r + 1]);
                     m_used = half_pair_max(__builtin_fmaxf(mx, s[1][15]));
-                    mc = m_used * c;
                 } else {
 #pragma unroll
                     for (int pidx = 0; pidx < 16; ++pidx)
-                        if (2 + (pidx * (NS - 2)) / 16 == n) score_pair(pidx, pw, psum);
+                        if (2 + (pidx * (NL - 2)) / 16 == i) score_pair(pidx, pw, psum, Yes{}, m_used);
                     pin_value(psum);
                 }
             } else if constexpr (do_sm) {
-                // Every later tile: the pairs under the current reference in
-                // slots 0 .. NS-2, then the lazy-rescale test in the last slot.
+                // Every later tile: the pairs (scores already relative to the
+                // reference) in all slots but the last, then the lazy-rescale
+                // test in the last slot.
 #pragma unroll
                 for (int pidx = 0; pidx < 16; ++pidx)
-                    if ((pidx * (NS - 1)) / 16 == n) score_pair(pidx, pw, psum);
+                    if ((pidx * (NL - 1)) / 16 == i) score_pair(pidx, pw, psum, No{}, 0.0f);
                 pin_value(psum);
                 // Every p of the tile is at most its row sum, so the reference
                 // need not move while each row sum stays within 2^8 (exact: the
@@ -404,7 +499,7 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
                 // the first tile; also when a p overflowed) take the tile's row
                 // maximum, move the reference for the rows that exceed it, and
                 // recompute the tile's P under the new one.
-                if (n == NS - 1 && wave_any(psum > kLazyBound)) {
+                if (i == NL - 1 && wave_any(psum > kLazyBound)) {
                     mx = s[0][0];
 #pragma unroll
                     for (int r = 1; r < 15; r += 2) mx = __builtin_fmaxf(__builtin_fmaxf(mx, s[0][r]), s[0][r + 1]);
@@ -412,16 +507,18 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
 #pragma unroll
                     for (int r = 1; r < 15; r += 2) mx = __builtin_fmaxf(__builtin_fmaxf(mx, s[1][r]), s[1][r + 1]);
                     mx = half_pair_max(__builtin_fmaxf(mx, s[1][15]));
-                    const float m_new = fmaxf(m_used, mx);
-                    const float alpha = __builtin_amdgcn_exp2f((m_used - m_new) * c);
+                    // The row's maximum above the reference (0: it stays).
+                    const float shift = fmaxf(mx, 0.0f);
+                    const float alpha = __builtin_amdgcn_exp2f(-shift);
                     l_run *= alpha;
                     alpha_pending = alpha;
                     rescale_pending = true;
-                    m_used = m_new;
-                    mc = m_used * c;
+                    m_used += shift;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) seed[r] = -m_used;
                     psum = 0.0f;
 #pragma unroll
-                    for (int pidx = 0; pidx < 16; ++pidx) score_pair(pidx, pw, psum);
+                    for (int pidx = 0; pidx < 16; ++pidx) score_pair(pidx, pw, psum, Yes{}, shift);
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -438,8 +535,6 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
         }
     };
 
-    using Yes = std::true_type;
-    using No = std::false_type;
     auto apply_rescale = [&]() __attribute__((always_inline)) {
         if (rescale_pending) {
 #pragma unroll
@@ -449,23 +544,30 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
             rescale_pending = false;
         }
     };
-    // One iteration j (1 <= j < nkt): kc = K(j), vp = V(j-1); stage sd
+    // One iteration j (1 <= j < nkt): K stage kst holds tile j, V stage vst
+    // tile j-1; stage sd
     // (that of tile j-2) receives tile j+2.  Tiles entirely above a
     // wavefront's rows are computed too: their scores are all masked, so
     // they add exactly zero.  Every iteration issues one copy batch (the
     // last tile is repeated past the end) so the wait below is exact.
     // j counts this workgroup's tiles from 0; its key tile is tb + j.
-    auto iteration = [&](int j, const uint16_t *kc, const uint16_t *vp, int sd) __attribute__((always_inline)) {
+    auto iteration = [&](int j, int kst, int vst, int sd) __attribute__((always_inline)) {
         // This wavefront's copy of tile j has landed (that of tile j+1 may
         // still be in flight); the barrier publishes tile j and tells that
         // every wavefront is past iteration j-1, which freed stage j-2.
-        __builtin_amdgcn_s_waitcnt(vmcnt_lds_imm(2 * CPW));
+        // This wavefront's reads of stage j-2 are complete before the
+        // barrier frees it; the head reads (of stage j-1) may still be in
+        // flight.
+        read_head(vst);
+        __builtin_amdgcn_s_waitcnt(vmcnt_lds_last_imm(2 * CPW, 2 * kHead));
         raw_barrier();
-        dma_tile(sd, tb + min(j + 2, ntl - 1));
         apply_rescale();
-        qk(kc);
+        pv_head();
+        // The next copy goes out behind the first QK MFMAs, so the fragment
+        // reads and MFMAs of this tile start right after the barrier.
+        qk(kst, Yes{}, [&]() __attribute__((always_inline)) { dma_tile(sd, tb + min(j + 2, ntl - 1)); });
         if ((tb + j) * kBN + kBN - 1 > a.prior + rw0) mask_tile(tb + j);
-        pv_softmax(vp, Yes{}, Yes{}, No{});
+        pv_softmax(vst, Yes{}, Yes{}, No{});
     };
 
     // Prologue: tiles 0, 1, 2 in flight (repeats of the last tile past the
@@ -477,29 +579,33 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
     dma_tile(2, tb + min(2, ntl - 1));
     __builtin_amdgcn_s_waitcnt(vmcnt_lds_imm(2 * 2 * CPW));
     raw_barrier();
-    qk(k0);
+    qk(0, No{}, []() {});
     if (tb * kBN + kBN - 1 > a.prior + rw0) mask_tile(tb);
-    pv_softmax(v0, No{}, Yes{}, Yes{});
+    pv_softmax(0, No{}, Yes{}, Yes{});
     // The first maximum always moves the reference from -inf; O is still
     // zero then, so there is nothing to rescale.
     rescale_pending = false;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) seed[r] = -m_used;
     for (int j = 1; j < ntl; j += ST) {
-        iteration(j, k1, v0, 3);
+        iteration(j, 1, 0, 3);
         if (j + 1 >= ntl) break;
-        iteration(j + 1, k2, v1, 0);
+        iteration(j + 1, 2, 1, 0);
         if (j + 2 >= ntl) break;
-        iteration(j + 2, k3, v2, 1);
+        iteration(j + 2, 3, 2, 1);
         if (j + 3 >= ntl) break;
-        iteration(j + 3, k0, v3, 2);
+        iteration(j + 3, 0, 3, 2);
     }
     // P.V of the last tile, from the stage that holds it.
+    const int last_stage = (ntl - 1) % ST;
+    read_head(last_stage);
     __builtin_amdgcn_s_waitcnt(vmcnt_lds_imm(0));
     apply_rescale();
-    const int last_stage = (ntl - 1) % ST;
-    if (last_stage == 0) pv_softmax(v0, Yes{}, No{}, No{});
-    else if (last_stage == 1) pv_softmax(v1, Yes{}, No{}, No{});
-    else if (last_stage == 2) pv_softmax(v2, Yes{}, No{}, No{});
-    else pv_softmax(v3, Yes{}, No{}, No{});
+    pv_head();
+    if (last_stage == 0) pv_softmax(0, Yes{}, No{}, No{});
+    else if (last_stage == 1) pv_softmax(1, Yes{}, No{}, No{});
+    else if (last_stage == 2) pv_softmax(2, Yes{}, No{}, No{});
+    else pv_softmax(3, Yes{}, No{}, No{});
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // no DMA may still target LDS at exit
 
     const float l = l_run + __shfl_xor(l_run, 32, 64);
@@ -566,8 +672,8 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
     }
     __syncthreads();
     if (!last) return;
-    // Merge in chunk order: M = the largest chunk maximum, then
-    // O = sum_c O_c 2^((m_c - M) c) and l likewise, chunk 0 first; this
+    // Merge in chunk order: M = the largest chunk maximum (log2 units), then
+    // O = sum_c O_c 2^(m_c - M) and l likewise, chunk 0 first; this
     // workgroup's own chunk enters from registers at its place in the order.
     // The O of the first other chunk and the (m, l) pairs of all chunks go
     // out as one batch of uncached loads (one round trip); every further
@@ -586,7 +692,7 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
         if (ch < nchunks) mmax = fmaxf(mmax, ml[ch].x);
 #pragma unroll
     for (int ch = 0; ch < kMaxChunks; ++ch)
-        if (ch < nchunks) lsum = fmaf(ml[ch].y, __builtin_amdgcn_exp2f((ml[ch].x - mmax) * c), lsum);
+        if (ch < nchunks) lsum = fmaf(ml[ch].y, __builtin_amdgcn_exp2f(ml[ch].x - mmax), lsum);
     floatx16_t acc[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
@@ -596,7 +702,7 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
     for (int ch = 0; ch < kMaxChunks; ++ch) {
         if (ch >= nchunks) break;
         if (ch == chunk) {
-            const float w = __builtin_amdgcn_exp2f((m_used - mmax) * c);
+            const float w = __builtin_amdgcn_exp2f(m_used - mmax);
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -607,7 +713,7 @@ __global__ __launch_bounds__(512, 1) void prefill_mfma_kernel(PrefillArgs a) {
 #pragma unroll
             for (int e = 0; e < MT * 8; ++e) x[e] = get2(chunk_base(ch) + e * 128);
         }
-        const float w = __builtin_amdgcn_exp2f((ml[ch].x - mmax) * c);
+        const float w = __builtin_amdgcn_exp2f(ml[ch].x - mmax);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
