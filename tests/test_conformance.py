@@ -78,3 +78,34 @@ def test_bf16_neighbours():
     assert within_one_bf16_ulp([np.inf, 1.0], [np.inf, 1.0])
     assert not within_one_bf16_ulp([np.inf], [np.float32(3e38)])
     assert not within_one_bf16_ulp([1.0, 2.0], [1.0])
+
+
+def test_token_gate_catches_a_wrong_token_on_a_near_tie():
+    """The greedy-token gate of the model tests.  A near tie (top-1 / top-2
+    margin below twice the step's logit error) excuses equality with the
+    oracle's token but not a token other than the runner's own first maximum,
+    so a runner that picks a clearly wrong token fails on a near tie as on a
+    clear margin.  (With the runner's own maximum and the max logit error, the
+    near-tie bound and equality on clear margins both follow; the gate states
+    them too.)"""
+    import oracle
+    from _data import TokenGate
+
+    want = np.zeros(64, np.float32)
+    want[10], want[20], want[30] = 5.0, 4.96875, 1.0  # top-2 margin 0.03125
+    got = want.copy()
+    got[20] += 0.0625  # the runner's logits move by 0.0625: its maximum is now 20
+    wb, gb = oracle.write_bf16(want), oracle.write_bf16(got)
+    gate = TokenGate("planted")
+    gate.check(20, gb, wb, "near tie, runner picks the runner-up")  # excused: 4.97 >= 5 - 0.125
+    assert gate.excused == ["near tie, runner picks the runner-up"]
+    with pytest.raises(AssertionError, match="not its logits' argmax"):
+        gate.check(30, gb, wb, "near tie, runner picks a token 4 below the maximum")
+    clear = want.copy()
+    clear[20] = 3.0
+    with pytest.raises(AssertionError, match="not its logits' argmax"):
+        gate.check(20, oracle.write_bf16(clear), oracle.write_bf16(clear), "clear margin, wrong token")
+    gate.check(10, oracle.write_bf16(clear), oracle.write_bf16(clear), "clear margin")
+    assert gate.checked == 1
+    with pytest.raises(AssertionError):
+        gate.finish(max_excused=0)

@@ -3,7 +3,7 @@ hidden 4096, 32/8 heads of 128, SwiGLU FFN 14336, RMSNorm eps 1e-5, RoPE
 theta 500000, vocab 128256), random-init BF16 weights N(0, 0.02) from the
 bench's seed, through the C++ decoder runner.
 
-* Full size: batch 8, seeded 4,096-token prompts, 16 greedy steps.  The
+* Full size: batch 8, seeded 4,096-token prompts, all 128 greedy steps.  The
   ColdStore-exact paged K/V route and the dense route give the same tokens
   at every step and the same logical K/V SHA-256 for every slot (the
   reference's invariant, gpu_llm/mod.rs:2993-3048).
@@ -16,17 +16,18 @@ bench's seed, through the C++ decoder runner.
   from either.  So the checks are the reference's own conformance metrics
   (compare_logit_distributions, conformance.rs:75-155): logits within the
   cfg5 bounds below, greedy tokens equal at every step whose oracle top-1 /
-  top-2 margin exceeds twice that step's max logit difference, and top-1
-  agreement with the CPU decoder no worse than the GPU-runtime form's own
-  agreement with it, minus one step; excused steps and agreement are
-  counted and printed.
+  top-2 margin exceeds twice that step's max logit difference, and on every
+  other step (a near tie) a runner token that scores within twice that
+  difference of the oracle's maximum, and every token the first maximum of
+  the runner's own logits; top-1 agreement with the CPU decoder no worse than the
+  GPU-runtime form's own agreement with it, minus one step.
 """
 import numpy as np
 import pytest
 import torch
 
 import oracle
-from _data import from_torch, logit_error
+from _data import TokenGate, from_torch, logit_error
 
 pytestmark = pytest.mark.gpu
 
@@ -56,7 +57,7 @@ def cfg5_weights():
 
 def test_cfg5_full_size_paged_equals_dense(ctx, cfg5_weights):
     from mslim_attn.model import Model
-    batch, prompt_len, steps = 8, 4096, 16
+    batch, prompt_len, steps = 8, 4096, 128
     prompts = np.random.default_rng(20261202).integers(0, 128256, (batch, prompt_len))
     runs = {}
     for layout in ("paged", "dense"):
@@ -102,24 +103,19 @@ def test_cfg5_32_layers_against_cpu_decoders(ctx, cfg5_weights):
     model = Model(ctx, s, cfg5_weights, max_batch=2, chunk_tokens=16, max_context=32)
     cpu, gpu_form, planted = CpuDecoderOracle(spec, host), DecoderOracle(spec, host), CpuDecoderOracle(spec, host)
     worst = {"cpu": [0.0, 0.0], "gpu_form": [0.0, 0.0], "forms": [0.0, 0.0]}
-    excused, checked = [], 0
+    gates = {"cpu": TokenGate("cfg5 vs the CPU decoder"), "gpu_form": TokenGate("cfg5 vs the GPU-runtime form")}
     agree = {"runner": 0, "gpu_form": 0}
     points = 0
     try:
         def compare(label, got_bits, got_token, cpu_out, gpu_out):
-            nonlocal checked, points
+            nonlocal points
             cpu_bits = oracle.write_bf16(cpu_out[0])
             for name, (want, want_token) in (("cpu", (cpu_bits, cpu_out[1])), ("gpu_form", gpu_out)):
                 m, r = logit_error(got_bits, want)
                 print(f"cfg5 vs {name} {label}: max abs {m:.4f}, rel L2 {r:.2e}", flush=True)
                 worst[name] = [max(worst[name][0], m), max(worst[name][1], r)]
                 assert m <= CFG5_LOGIT_MAX_ABS and r <= CFG5_LOGIT_REL2, (name, label, m, r)
-                values = np.sort(oracle.read_bf16(want).astype(np.float64))
-                if values[-1] - values[-2] > 2 * m:
-                    assert got_token == want_token, (name, label, got_token, want_token)
-                    checked += 1
-                else:
-                    excused.append((name, label))
+                gates[name].check(got_token, got_bits, want, label, want_token=want_token)
             m, r = logit_error(gpu_out[0], cpu_bits)
             worst["forms"] = [max(worst["forms"][0], m), max(worst["forms"][1], r)]
             points += 1
@@ -151,9 +147,15 @@ def test_cfg5_32_layers_against_cpu_decoders(ctx, cfg5_weights):
             toks = nxt
     finally:
         model.close()
-    print(f"cfg5 vs oracles: worst (max abs, rel L2) {worst}; tokens checked {checked}, excused by margin "
-          f"{len(excused)}; top-1 agreement with the CPU decoder over {points} points: runner "
-          f"{agree['runner']}, GPU-runtime form {agree['gpu_form']}", flush=True)
+    print(f"cfg5 vs oracles: worst (max abs, rel L2) {worst}; top-1 agreement with the CPU decoder over "
+          f"{points} points: runner {agree['runner']}, GPU-runtime form {agree['gpu_form']}", flush=True)
+    # Through 32 random layers the measured logit error (max abs ~0.33)
+    # exceeds the top-1 / top-2 margin of every step, so every step is a near
+    # tie; each is held to the near-tie rule and to its own argmax, and the
+    # agreement gate below compares the runner with the reference's own
+    # GPU-runtime arithmetic.
+    for gate in gates.values():
+        gate.finish(max_excused=points)
     # the runner is as close to the reference CPU decoder as the reference's
     # own GPU-runtime arithmetic is
     assert worst["cpu"][1] <= 2 * worst["forms"][1] + 0.01, worst

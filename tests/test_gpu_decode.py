@@ -11,7 +11,7 @@ import pytest
 import torch
 
 import oracle
-from _data import from_torch, max_abs_bf16, normal_bf16, tiled_input, to_torch
+from _data import check_bf16, from_torch, normal_bf16, tiled_input, to_torch
 
 pytestmark = pytest.mark.gpu
 
@@ -43,9 +43,10 @@ def test_decode_cfg1_parity_repeatability_and_inputs_untouched(ctx):
     torch.cuda.synchronize()
     got = from_torch(out)
     ref = _oracle_decode(qb, kb, vb, qh, kvh, d)
-    assert max_abs_bf16(got, ref) <= TOL
+    check_bf16(got, ref, TOL, "test_decode_cfg1_parity_repeatability_and_inputs_untouched")
     rc, f64 = oracle.cpu_reference_decode(oracle.read_bf16(qb), kb, vb, 1, qh, kvh, d)
-    assert rc == 0 and max_abs_bf16(got, f64) <= TOL
+    assert rc == 0
+    check_bf16(got, f64, TOL, "decode cfg1 vs f64 CpuReferenceBackend")
     # repeat: bit-identical (tiled_attention.rs:380-387); K/V unmodified (:388-397)
     out2 = torch.empty_like(q)
     ctx.decode_dense(q, k, v, out2, [t], qh, kvh, d)
@@ -78,10 +79,8 @@ def test_decode_histories_and_geometries(ctx, qh, kvh, d):
         gpu_ref = oracle.gpu_reference_attention(qb, kb, vb, qh, kvh, d, 1, t - 1)
         for split in (0, 64):
             got = _decode(ctx, qb, kb, vb, [t], qh, kvh, d, split=split)
-            err = max_abs_bf16(got, ref)
-            assert err <= TOL, (qh, kvh, d, t, split, err)
-            err_gpu = max_abs_bf16(got, oracle.read_bf16(gpu_ref))
-            assert err_gpu <= ONLINE_TOL, (qh, kvh, d, t, split, err_gpu)
+            check_bf16(got, ref, TOL, "test_decode_histories_and_geometries")
+            check_bf16(got, oracle.read_bf16(gpu_ref), ONLINE_TOL, "decode vs reference GPU arithmetic")
 
 
 def test_decode_ragged_batch_dense(ctx):
@@ -94,7 +93,7 @@ def test_decode_ragged_batch_dense(ctx):
     got = _decode(ctx, qb, kb, vb, lens, qh, kvh, d, stride=stride).reshape(len(lens), -1)
     for b, t in enumerate(lens):
         ref = _oracle_decode(qb[b], kb[b, :t], vb[b, :t], qh, kvh, d)
-        assert max_abs_bf16(got[b], ref) <= TOL, b
+        check_bf16(got[b], ref, TOL, "test_decode_ragged_batch_dense")
 
 
 def test_decode_ragged_partition_order(ctx):
@@ -116,7 +115,7 @@ def test_decode_ragged_partition_order(ctx):
         got = _decode(ctx, qb, kb, vb, lens, qh, kvh, d, split=split, stride=stride).reshape(len(lens), -1)
         for b, t in enumerate(lens):
             ref = _oracle_decode(qb[b], kb[b, :t], vb[b, :t], qh, kvh, d)
-            assert max_abs_bf16(got[b], ref) <= TOL, (split, b)
+            check_bf16(got[b], ref, TOL, "test_decode_ragged_partition_order")
         paged = torch.empty_like(q)
         ctx.decode_paged(q, k_pool, v_pool, paged, lens, table_t, pps, 16, qh, kvh, d, split_tokens=split)
         torch.cuda.synchronize()
@@ -173,7 +172,7 @@ def test_paged_equals_dense_bitwise_cfg3(ctx):
         kb = from_torch(k[b, :t])
         vb = from_torch(v[b, :t])
         qb = from_torch(q[b])
-        assert max_abs_bf16(dn[b], _oracle_decode(qb, kb, vb, qh, kvh, d)) <= TOL, b
+        check_bf16(dn[b], _oracle_decode(qb, kb, vb, qh, kvh, d), TOL, "test_paged_equals_dense_bitwise_cfg3")
     # the pool holds the dense bytes exactly: gather each session back
     for b in (0, 5, 31):
         t = lens[b]
@@ -203,7 +202,7 @@ def test_paged_parity_small_pages_and_tails(ctx):
         got = from_torch(paged).reshape(len(lens), -1)
         for b, t in enumerate(lens):
             ref = _oracle_decode(qb[b], kb[b, :t], vb[b, :t], qh, kvh, d)
-            assert max_abs_bf16(got[b], ref) <= TOL, (pt, b)
+            check_bf16(got[b], ref, TOL, "test_paged_parity_small_pages_and_tails")
 
 
 def test_decode_cfg4_shape_parity(ctx):
@@ -220,7 +219,7 @@ def test_decode_cfg4_shape_parity(ctx):
     got = from_torch(out).reshape(batch, -1)
     for b in (0, 3):
         ref = _oracle_decode(from_torch(q[b]), from_torch(k[b]), from_torch(v[b]), qh, kvh, d)
-        assert max_abs_bf16(got[b], ref) <= TOL, b
+        check_bf16(got[b], ref, TOL, "test_decode_cfg4_shape_parity")
 
 
 def test_extreme_scores_are_stable(ctx):
@@ -303,7 +302,7 @@ def test_decode_merge_modes_bitwise_ragged(ctx):
         got = fused_d.reshape(len(lens), -1)
         for b in (0, 2, 7):
             t = lens[b]
-            assert max_abs_bf16(got[b], _oracle_decode(qb[b], kb[b, :t], vb[b, :t], qh, kvh, d)) <= TOL, (split, b)
+            check_bf16(got[b], _oracle_decode(qb[b], kb[b, :t], vb[b, :t], qh, kvh, d), TOL, "test_decode_merge_modes_bitwise_ragged")
 
 
 # Launches with more partitions than two per CU (512) and at most 896 run the
@@ -354,7 +353,7 @@ def test_decode_list_mode_matches_one_partition_per_workgroup(ctx, batch, lo, hi
     for b in (0, int(np.argmax(lens)), int(np.argmin(lens)), batch - 1):
         t = lens[b]
         kb, vb = from_torch(k[b, :t].contiguous()), from_torch(v[b, :t].contiguous())
-        assert max_abs_bf16(got[b], _oracle_decode(qb[b], kb, vb, qh, kvh, d)) <= TOL, b
+        check_bf16(got[b], _oracle_decode(qb[b], kb, vb, qh, kvh, d), TOL, "test_decode_list_mode_matches_one_partition_per_workgroup")
 
 
 def _cfg4_hot_cold_pool(k, v, lens, hot_window, page_tokens, seed, ctx):
@@ -409,7 +408,7 @@ def test_decode_cfg4_hot_window_cold_pages_against_oracle(ctx):
     got = fused.reshape(batch, -1)
     for b in (1, 2):
         ref = _oracle_decode(from_torch(q[b]), from_torch(k[b]), from_torch(v[b]), qh, kvh, d)
-        assert max_abs_bf16(got[b], ref) <= TOL, b
+        check_bf16(got[b], ref, TOL, "test_decode_cfg4_hot_window_cold_pages_against_oracle")
 
 
 def test_decode_stream_switch_between_ragged_split_decodes(ctx):

@@ -19,7 +19,7 @@ import torch
 
 import oracle
 from oracle.decoder import DecoderOracle, Spec, random_weights
-from _data import MODEL_LOGIT_MAX_ABS, MODEL_LOGIT_REL2, from_torch, logit_error, normal_bf16, to_torch
+from _data import MODEL_LOGIT_MAX_ABS, MODEL_LOGIT_REL2, TokenGate, from_torch, logit_error, normal_bf16, to_torch
 
 pytestmark = pytest.mark.gpu
 
@@ -207,17 +207,6 @@ def _check_logits(got_bits, want_bits, label):
     assert m <= MODEL_LOGIT_MAX_ABS and r <= MODEL_LOGIT_REL2, f"{label}: max abs {m:.4f}, rel L2 {r:.2e}"
 
 
-def _margin(bits):
-    v = np.sort(oracle.read_bf16(bits).astype(np.float64))
-    return v[-1] - v[-2]
-
-
-def _check_token(got, want_bits, label):
-    want = int(oracle.argmax_bf16(want_bits, 1, want_bits.size)[0])
-    if _margin(want_bits) > 2 * MODEL_LOGIT_MAX_ABS:
-        assert got == want, f"{label}: token {got} != oracle {want}"
-
-
 def test_runner_one_token_prompts(tiny_model):
     # A one-token history attends only to itself (attention output = V), so
     # the only difference left is hipBLASLt's accumulation order, which now and
@@ -228,6 +217,7 @@ def test_runner_one_token_prompts(tiny_model):
     ref = DecoderOracle(SPEC, w)
     exact = 0
     tokens = range(0, SPEC.vocab, 25)
+    gate = TokenGate("one-token prompts")
     for token in tokens:
         got = model.prefill_only(0, [token])
         want_logits, want = ref.prefill(0, [token])
@@ -235,7 +225,8 @@ def test_runner_one_token_prompts(tiny_model):
         exact += bool(np.array_equal(got_logits, want_logits))
         m, r = logit_error(got_logits, want_logits)
         assert m <= MODEL_LOGIT_MAX_ABS / 2 and r <= MODEL_LOGIT_REL2 / 2, (token, m, r)
-        _check_token(got, want_logits, f"one-token prompt {token}")
+        gate.check(got, got_logits, want_logits, f"prompt {token}")
+    gate.finish(max_excused=len(tokens) // 8)
     assert exact >= len(tokens) // 2, f"only {exact} of {len(tokens)} one-token prompts bit-exact"
 
 
@@ -246,11 +237,12 @@ def test_runner_prefill_and_batched_decode_match_oracle(tiny_model):
     # slot 0 spans three causal chunks (16 + 16 + 5), exercising the page gather
     prompts = [list(rng.integers(0, SPEC.vocab, n)) for n in (37, 16, 1)]
     tokens = []
+    gate = TokenGate("tiny prefill + batched decode")
     for seq, prompt in enumerate(prompts):
         tok = model.prefill_only(seq, prompt)
         want_logits, _ = ref.prefill(seq, prompt)
         _check_logits(model.logits()[0], want_logits, f"prefill slot {seq}")
-        _check_token(tok, want_logits, f"prefill slot {seq}")
+        gate.check(tok, model.logits()[0], want_logits, f"prefill slot {seq}")
         assert model.position(seq) == len(prompt)
         tokens.append(tok)
     for step in range(6):
@@ -259,9 +251,10 @@ def test_runner_prefill_and_batched_decode_match_oracle(tiny_model):
         for seq in range(3):
             want_logits, _ = ref.step(seq, tokens[seq])  # teacher-forced with the GPU token
             _check_logits(got_logits[seq], want_logits, f"step {step} slot {seq}")
-            _check_token(nxt[seq], want_logits, f"step {step} slot {seq}")
+            gate.check(nxt[seq], got_logits[seq], want_logits, f"step {step} slot {seq}")
             assert model.position(seq) == len(prompts[seq]) + step + 1
         tokens = nxt
+    gate.finish(max_excused=7)  # a third of the 21 steps
 
 
 def test_runner_is_deterministic_and_digest_tracks_pages(tiny_model):
@@ -380,11 +373,12 @@ def test_runner_llama3_8b_width_reduced_depth(ctx):
         ref = DecoderOracle(spec, host)
         prompts = [[11, 5000, 99999, 128255, 7], [3, 64000, 1]]
         toks = []
+        gate = TokenGate("full-width 2 layers")
         for seq, prompt in enumerate(prompts):
             got = model.prefill_only(seq, prompt)
             want_logits, _ = ref.prefill(seq, prompt)
             _check_logits(model.logits()[0], want_logits, f"prefill {seq}")
-            _check_token(got, want_logits, f"prefill {seq}")
+            gate.check(got, model.logits()[0], want_logits, f"prefill {seq}")
             toks.append(got)
         for step in range(2):
             nxt = model.forward_batch(toks)
@@ -392,8 +386,12 @@ def test_runner_llama3_8b_width_reduced_depth(ctx):
             for seq in range(2):
                 want_logits, _ = ref.step(seq, toks[seq])
                 _check_logits(logits[seq], want_logits, f"step {step} slot {seq}")
-                _check_token(nxt[seq], want_logits, f"step {step} slot {seq}")
+                gate.check(nxt[seq], logits[seq], want_logits, f"step {step} slot {seq}")
             toks = nxt
+        # a 128,256-entry vocabulary leaves top-1 / top-2 gaps below twice the
+        # logit error on most steps (measured 4 of 6); each is still held to
+        # the near-tie rule
+        gate.finish(max_excused=5)
     finally:
         model.close()
 
@@ -418,7 +416,9 @@ def test_runner_prefill_settings(tiny_model):
         got = model.prefill_only(0, prompt)  # five causal chunks of <= 8 tokens
         want_logits, _ = ref.prefill(0, prompt)
         _check_logits(model.logits()[0], want_logits, "prefill in chunks of 8")
-        _check_token(got, want_logits, "prefill in chunks of 8")
+        gate = TokenGate("prefill in chunks of 8")
+        gate.check(got, model.logits()[0], want_logits, "prefill")
+        gate.finish(max_excused=1)
         with pytest.raises(MslimAttnError, match="empty session"):
             model.set_prefill_settings({"batch_tokens": 4, "weight_reuse_tokens": 8})
         model.reset(0)

@@ -9,7 +9,7 @@ import pytest
 import torch
 
 import oracle
-from _data import from_torch, max_abs_bf16, normal_bf16, tiled_input, to_torch
+from _data import check_bf16, from_torch, max_abs_bf16, normal_bf16, tiled_input, to_torch
 
 pytestmark = pytest.mark.gpu
 
@@ -35,10 +35,9 @@ def test_prefill_small_shapes(ctx, qh, kvh, d):
         vb = normal_bf16(rng, (hist, kvh, d))
         got = _prefill(ctx, qb, kb, vb, queries, prior, qh, kvh, d)
         ref = oracle.prefill_causal_cpu(oracle.read_bf16(qb), kb, vb, qh, kvh, d, queries, prior)
-        err = max_abs_bf16(got, ref)
-        assert err <= TOL, (queries, prior, err)
+        check_bf16(got, ref, TOL, "test_prefill_small_shapes")
         gref = oracle.gpu_reference_attention(qb, kb, vb, qh, kvh, d, queries, prior)
-        assert max_abs_bf16(got, oracle.read_bf16(gref)) <= TOL
+        check_bf16(got, oracle.read_bf16(gref), TOL, "prefill vs reference GPU arithmetic")
 
 
 def test_prefill_reference_inputs_multi_query(ctx):
@@ -52,7 +51,7 @@ def test_prefill_reference_inputs_multi_query(ctx):
             vb = tiled_input(n * kvh * d, 11).reshape(n, kvh, d)
             got = _prefill(ctx, qb, kb, vb, queries, prior, qh, kvh, d)
             ref = oracle.prefill_causal_cpu(oracle.read_bf16(qb), kb, vb, qh, kvh, d, queries, prior)
-            assert max_abs_bf16(got, ref) <= TOL, (n, queries)
+            check_bf16(got, ref, TOL, "test_prefill_reference_inputs_multi_query")
 
 
 @pytest.mark.parametrize("qh,kvh,d", [(16, 2, 128), (8, 2, 64)])
@@ -76,7 +75,7 @@ def test_prefill_moving_reference_recomputes_tiles(ctx, qh, kvh, d):
     got = _prefill(ctx, qb, kb, vb, queries, prior, qh, kvh, d)
     ref = oracle.prefill_causal_cpu(oracle.read_bf16(qb), kb, vb, qh, kvh, d, queries, prior)
     assert np.isfinite(oracle.read_bf16(got)).all()
-    assert max_abs_bf16(got, ref) <= TOL
+    check_bf16(got, ref, TOL, "test_prefill_moving_reference_recomputes_tiles")
 
 
 def _rows_reference(q_bits, k_bits, v_bits, rows, prior, qh, kvh, d):
@@ -114,7 +113,7 @@ def test_prefill_cfg2_with_rope(ctx):
         [int(x) for x in rng.integers(0, s, size=12)]
     ref = _rows_reference(q_rot, k_rot, vb, rows, 0, qh, kvh, d)
     for r in rows:
-        assert max_abs_bf16(got[r], ref[r]) <= TOL, r
+        check_bf16(got[r], ref[r], TOL, "test_prefill_cfg2_with_rope")
     # repeat is bit-identical and inputs are unmodified
     out2 = torch.empty_like(q)
     ctx.prefill_causal(q, k, v, out2, s, 0, qh, kvh, d)
@@ -138,7 +137,7 @@ def test_prefill_cfg4_shape_rows(ctx):
     rows = [0, 8191, 4095, 4096, 127, 128, 5000, 7777]
     ref = _rows_reference(qb, kb, vb, rows, 0, qh, kvh, d)
     for r in rows:
-        assert max_abs_bf16(got[r], ref[r]) <= TOL, r
+        check_bf16(got[r], ref[r], TOL, "test_prefill_cfg4_shape_rows")
 
 
 def test_prefill_chunk_after_prior_matches_single_pass(ctx):
@@ -151,7 +150,7 @@ def test_prefill_chunk_after_prior_matches_single_pass(ctx):
     whole = _prefill(ctx, qb, kb, vb, s, 0, qh, kvh, d)
     second = _prefill(ctx, qb[200:], kb, vb, 100, 200, qh, kvh, d)
     ref = oracle.prefill_causal_cpu(oracle.read_bf16(qb[200:]), kb, vb, qh, kvh, d, 100, 200)
-    assert max_abs_bf16(second, ref) <= TOL
+    check_bf16(second, ref, TOL, "test_prefill_chunk_after_prior_matches_single_pass")
     assert max_abs_bf16(whole[200:], oracle.read_bf16(second)) <= TOL
 
 
@@ -202,8 +201,8 @@ def test_prefill_split_launches(ctx, queries, prior, qh, kvh, d):
                   {int(x) for x in rng.integers(0, queries, size=10)})
     ref = _rows_reference(qb, kb, vb, rows, prior, qh, kvh, d)
     for r in rows:
-        assert max_abs_bf16(got[r], ref[r]) <= TOL, r
-        assert max_abs_bf16(unsplit[r], ref[r]) <= TOL, r
+        check_bf16(got[r], ref[r], TOL, "test_prefill_split_launches")
+        check_bf16(unsplit[r], ref[r], TOL, "test_prefill_split_launches")
     # split and unsplit launches differ in rounding only
     diff = np.abs(oracle.read_bf16(got).astype(np.float64) - oracle.read_bf16(unsplit).astype(np.float64))
     assert float(diff.max()) <= TOL
@@ -298,7 +297,7 @@ def test_prefill_pool_matches_static_mapping(ctx):
         rows = [0, 31, 32, queries // 2, queries - 33, queries - 1]
         ref = _rows_reference(qb, kb, vb, rows, prior, qh, kvh, d)
         for r in rows:
-            assert max_abs_bf16(got[r], ref[r]) <= TOL, (shape, r)
+            check_bf16(got[r], ref[r], TOL, "test_prefill_pool_matches_static_mapping")
 
 
 def test_prefill_pool_option_rejects_bad_values(ctx):

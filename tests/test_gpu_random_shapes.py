@@ -14,7 +14,7 @@ import torch
 
 import mslim_attn
 import oracle
-from _data import from_torch, max_abs_bf16, normal_bf16, to_torch
+from _data import check_bf16, from_torch, normal_bf16, to_torch
 
 pytestmark = pytest.mark.gpu
 
@@ -81,8 +81,7 @@ def test_random_decode_dense_paged_and_merge_modes(ctx, seed):
     dense = dense.reshape(b, -1)
     for i, t in enumerate(lens):
         ref = oracle.dense_attention_bf16(oracle.read_bf16(qb[i]), kb[i, :t], vb[i, :t], qh, kvh, d)
-        err = max_abs_bf16(dense[i], ref)
-        assert err <= TOL, (case, i, err)
+        check_bf16(dense[i], ref, TOL, "test_random_decode_dense_paged_and_merge_modes")
 
     # scatter into a seeded random page pool with the product's page writer
     needed = [(t + page - 1) // page for t in lens]
@@ -133,8 +132,7 @@ def test_random_prefill_against_oracle(ctx, seed):
     torch.cuda.synchronize()
     assert torch.equal(out, again), case
     ref = oracle.prefill_causal_cpu(oracle.read_bf16(qb), kb, vb, qh, kvh, d, queries, prior)
-    err = max_abs_bf16(from_torch(out), ref)
-    assert err <= TOL, (case, err)
+    check_bf16(from_torch(out), ref, TOL, "test_random_prefill_against_oracle")
     if split_tiles:
         whole = torch.empty_like(q)
         try:
@@ -143,8 +141,7 @@ def test_random_prefill_against_oracle(ctx, seed):
         finally:
             ctx.set_prefill_split(True)
         torch.cuda.synchronize()
-        err = max_abs_bf16(from_torch(whole), ref)
-        assert err <= TOL, (case, "unsplit", err)
+        check_bf16(from_torch(whole), ref, TOL, "test_random_prefill_against_oracle (unsplit)")
 
 
 def test_random_sweep_reaches_both_prefill_launch_forms():
