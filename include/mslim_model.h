@@ -144,6 +144,38 @@ int mslim_model_cold_report(void *model, int seq, mslim_model_cold_info *out);
  * fails if it does not fit in `capacity` bytes. */
 int mslim_model_cold_directory(void *model, int seq, char *out, size_t capacity);
 
+/* ---- failure handling ----------------------------------------------------- */
+
+/* Cooperative cancellation (the AtomicBool `cancel` of GpuLlm::prefill_only
+ * and generate_cancellable, src/gpu_llm/mod.rs:2499-2700): `flag` points to a
+ * caller-owned int32 (nonzero = cancel) that the runner reads, relaxed, at
+ * every prompt chunk and layer boundary of a prefill (prefill_batched,
+ * src/gpu_llm/prefill.rs:653-680) and at every token boundary of
+ * mslim_model_forward_batch and mslim_model_generate.  A cancelled prefill
+ * fails with "GPU batch prefill cancelled[ at layer boundary]" and poisons
+ * its slot; a cancelled generation seals the turn's decoded prefix in an
+ * attached ColdStore (mod.rs:2704-2712) and fails with "GPU generation
+ * cancelled by client", leaving the slot usable.  NULL clears the flag. */
+int mslim_model_set_cancel_flag(void *model, const int32_t *flag);
+/* 1 when slot `seq` is poisoned, 0 when healthy, -1 on error.  A device step
+ * that fails after its arguments were accepted (a library error, a failed
+ * ColdStore commit, a prefill cancelled mid-prompt) poisons the slots it was
+ * writing (every slot of a forward_batch); every later call that would use a
+ * poisoned slot fails until mslim_model_reset(seq), which discards the
+ * slot's K/V without committing them.  (The reference's poisoned GpuLlm,
+ * src/gpu_llm/mod.rs:2462-2483, refuses even the reset; its worker is
+ * restarted instead.) */
+int mslim_model_poisoned(void *model, int seq);
+/* Failure injection for failure-handling tests (no counterpart in the
+ * reference): the next device step that reaches layer `layer` fails there,
+ * once, with an argument error from the attention library (kind
+ * MSLIM_MODEL_INJECT_ARGUMENT_ERROR) or as if the cancel flag had been raised
+ * at that layer boundary of a prefill (kind MSLIM_MODEL_INJECT_CANCEL).
+ * Kind 0 disarms. */
+#define MSLIM_MODEL_INJECT_ARGUMENT_ERROR 1
+#define MSLIM_MODEL_INJECT_CANCEL 2
+int mslim_model_inject_failure(void *model, int kind, int layer);
+
 #ifdef __cplusplus
 }
 #endif

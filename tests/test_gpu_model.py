@@ -396,6 +396,106 @@ def test_runner_llama3_8b_width_reduced_depth(ctx):
         model.close()
 
 
+def test_runner_failed_step_poisons_until_reset(tiny_model):
+    """GpuLlm's poisoned state (gpu_llm/mod.rs:2462-2483): a step that fails
+    after its arguments were accepted -- here an argument error from the
+    attention library injected at layer 1, not a GPU fault -- poisons the
+    slots it was writing, and every later call on them fails until the slot
+    is reset.  After the resets the runner reproduces a clean run bit for
+    bit."""
+    from mslim_attn import MslimAttnError
+
+    w, model = tiny_model
+    for seq in range(3):
+        model.reset(seq)
+    prompts = [[5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18, 19, 20, 21], [30, 31, 32]]
+    clean = [model.prefill_only(s, p) for s, p in enumerate(prompts)]
+    clean_step = model.forward_batch(clean)
+    clean_logits = model.logits().copy()
+    for seq in range(2):
+        model.reset(seq)
+
+    toks = [model.prefill_only(s, p) for s, p in enumerate(prompts)]
+    assert toks == clean
+    model.inject_failure(model.INJECT_ARGUMENT_ERROR, 1)
+    with pytest.raises(MslimAttnError, match="input norm failed.*invalid RMSNorm arguments"):
+        model.forward_batch(toks)
+    assert model.poisoned(0) and model.poisoned(1) and not model.poisoned(2)
+    with pytest.raises(MslimAttnError, match="poisoned"):
+        model.forward_batch(toks)
+    with pytest.raises(MslimAttnError, match="poisoned"):
+        model.forward_batch(toks[:1])
+    with pytest.raises(MslimAttnError, match="poisoned"):
+        model.prefill_only(1, prompts[1])
+    with pytest.raises(MslimAttnError, match="poisoned"):
+        model.logical_kv_sha256(0)
+    with pytest.raises(MslimAttnError, match="healthy, empty session"):
+        model.set_prefill_settings({"batch_tokens": 8, "weight_reuse_tokens": 8})
+    for seq in range(2):
+        model.reset(seq)
+        assert not model.poisoned(seq) and model.position(seq) == 0
+    toks = [model.prefill_only(s, p) for s, p in enumerate(prompts)]
+    assert toks == clean and model.forward_batch(toks) == clean_step
+    assert np.array_equal(model.logits(), clean_logits)
+
+    # a failure inside a prompt poisons that slot only
+    model.inject_failure(model.INJECT_ARGUMENT_ERROR, 0)
+    with pytest.raises(MslimAttnError, match="invalid RMSNorm arguments"):
+        model.prefill_only(2, prompts[0])
+    assert model.poisoned(2) and not model.poisoned(0)
+    model.reset(2)
+    assert model.prefill_only(2, prompts[0]) == clean[0]
+    for seq in range(3):
+        model.reset(seq)
+
+
+def test_runner_cancel_flag(tiny_model):
+    """Cooperative cancellation: the flag is read at prompt chunk and layer
+    boundaries of a prefill (prefill_batched, gpu_llm/prefill.rs:653-680),
+    which then fails and poisons its slot, and at token boundaries of a
+    decode step (generate_cancellable, gpu_llm/mod.rs:2652-2656), which then
+    fails before any work and leaves the slot usable."""
+    import ctypes
+    from mslim_attn import MslimAttnError
+
+    w, model = tiny_model
+    for seq in range(3):
+        model.reset(seq)
+    prompt = list(range(40, 77))  # three chunks of 16
+    flag = ctypes.c_int32(0)
+    model.set_cancel_flag(flag)
+    try:
+        want = model.prefill_only(0, prompt)
+        want_next = model.forward_batch([want])
+        model.reset(0)
+
+        model.inject_failure(model.INJECT_CANCEL, 1)  # raised during layer 0 of the first chunk
+        with pytest.raises(MslimAttnError, match="GPU batch prefill cancelled at layer boundary"):
+            model.prefill_only(0, prompt)
+        assert model.poisoned(0)
+        model.reset(0)
+
+        flag.value = 1
+        with pytest.raises(MslimAttnError, match="GPU batch prefill cancelled"):
+            model.prefill_only(0, prompt)
+        assert model.poisoned(0)
+        flag.value = 0
+        model.reset(0)
+
+        assert model.prefill_only(0, prompt) == want
+        flag.value = 1
+        with pytest.raises(MslimAttnError, match="GPU generation cancelled by client"):
+            model.forward_batch([want])
+        assert not model.poisoned(0) and model.position(0) == len(prompt)
+        flag.value = 0
+        assert model.forward_batch([want]) == want_next
+    finally:
+        model.set_cancel_flag(None)
+        model.inject_failure(0, 0)
+        for seq in range(3):
+            model.reset(seq)
+
+
 def test_runner_prefill_settings(tiny_model):
     # GpuLlm::prefill_settings / set_calibration_prefill_settings: the prompt
     # chunk follows batch_tokens; tuning needs empty slots; experimental

@@ -55,6 +55,7 @@ DecoderRunner::DecoderRunner(std::shared_ptr<NativeContext> ctx, ModelSpec spec,
     settings_.weight_reuse_tokens = chunk_tokens_ >= 8 ? 8 : 1;
     scale_ = (float)(1.0 / std::sqrt((double)spec_.head_dim));
     positions_.assign(max_batch_, 0);
+    poisoned_.assign(max_batch_, 0);
 
     const size_t kvd = (size_t)spec_.kv_heads * spec_.head_dim, qd = (size_t)spec_.q_heads * spec_.head_dim;
     const size_t pool_pages = (size_t)max_batch_ * pages_per_seq_;
@@ -146,6 +147,8 @@ void DecoderRunner::chunk(int seq, const int32_t *ids, int n, int64_t prior) {
     ctx_->check("embed", mslim_attn_embed(h, w_.embed, s.vocab, s.hidden, ids_, n, x_, nullptr));
     for (int l = 0; l < s.layers; ++l) {
         const LayerWeights &w = w_.layers[l];
+        check_cancel("GPU batch prefill cancelled at layer boundary", l);
+        injected_error(l);
         ctx_->check("input norm", mslim_attn_rmsnorm(h, x_, w.input_norm, norm_, n, s.hidden, s.rms_eps));
         ctx_->check("QKV projection", mslim_attn_gemm_qkv(h, w.q, w.k, w.v, norm_, q_, k_, v_, s.hidden, qd, kvd, n));
         ctx_->check("query RoPE", mslim_attn_rope(h, q_, qr_, n, s.q_heads, s.head_dim, (int)prior, s.rope_theta,
@@ -194,31 +197,41 @@ Step DecoderRunner::prefill_only(int seq, const std::vector<int32_t> &prompt) {
     ensure(!prompt.empty(), "GPU prompt IDs empty");
     ensure(prompt.size() < (size_t)max_context_, "GPU context capacity not large enough for prompt");
     for (int32_t id : prompt) ensure(id >= 0 && id < spec_.vocab, "token id outside the vocabulary");
+    check_healthy(seq);
     if (cold_[seq])
         ensure(cold_report_[seq].committed_tokens == 0,
                "GPU prefill into a slot whose ColdStore already holds a session; restore it or attach an empty "
                "directory");
     int32_t next = 0;
     const int n_total = (int)prompt.size();
-    {
-        std::lock_guard<std::mutex> lock(ctx_->mutex());
-        positions_[seq] = 0;
-        for (int start = 0; start < n_total; start += chunk_tokens_) {
-            const int n = std::min(chunk_tokens_, n_total - start);
-            chunk(seq, prompt.data() + start, n, start);
-            if (start + n == n_total) head(x_ + (size_t)(n - 1) * spec_.hidden, 1);
+    // From here on a failure (or a cancellation) leaves the slot's K/V
+    // written for some chunks or layers only: the slot is poisoned
+    // (prefill_batched's error path, gpu_llm/mod.rs:2545-2550).
+    try {
+        {
+            std::lock_guard<std::mutex> lock(ctx_->mutex());
+            positions_[seq] = 0;
+            for (int start = 0; start < n_total; start += chunk_tokens_) {
+                check_cancel("GPU batch prefill cancelled", -1);
+                const int n = std::min(chunk_tokens_, n_total - start);
+                chunk(seq, prompt.data() + start, n, start);
+                if (start + n == n_total) head(x_ + (size_t)(n - 1) * spec_.hidden, 1);
+            }
+            positions_[seq] = n_total;
+            ctx_->check("read greedy token", mslim_attn_buf_read(ctx_->handle(), next_, 0,
+                                                                 reinterpret_cast<uint8_t *>(&next), 4));
         }
-        positions_[seq] = n_total;
-        ctx_->check("read greedy token", mslim_attn_buf_read(ctx_->handle(), next_, 0,
-                                                             reinterpret_cast<uint8_t *>(&next), 4));
-    }
-    if (cold_[seq]) {
-        // The prompt's K/V are committed to the canonical ColdStore at the end
-        // of prefill (gpu_llm/prefill.rs:760-790).
-        const auto t0 = std::chrono::steady_clock::now();
-        seal_slot(seq, 0, n_total);
-        cold_report_[seq].prefill_seal_seconds =
-            std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+        if (cold_[seq]) {
+            // The prompt's K/V are committed to the canonical ColdStore at the
+            // end of prefill (gpu_llm/prefill.rs:760-790).
+            const auto t0 = std::chrono::steady_clock::now();
+            seal_slot(seq, 0, n_total);
+            cold_report_[seq].prefill_seal_seconds =
+                std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+        }
+    } catch (...) {
+        poisoned_[seq] = 1;
+        throw;
     }
     return Step{next, n_total};
 }
@@ -229,14 +242,19 @@ std::vector<Step> DecoderRunner::forward_batch(const std::vector<int32_t> &token
     for (int32_t id : tokens) ensure(id >= 0 && id < spec_.vocab, "token id outside the vocabulary");
     std::vector<int32_t> pos(b), lens(b);
     for (int i = 0; i < b; ++i) {
+        check_healthy(i);
         ensure(positions_[i] < max_context_, "GPU KV capacity exceeded: configure larger --max-context-tokens");
         pos[i] = (int32_t)positions_[i];
         lens[i] = pos[i] + 1;
     }
+    // A token boundary: nothing of this step has run, so a cancellation here
+    // leaves every slot consistent.
+    check_cancel("GPU generation cancelled by client", -1);
     // The context lock covers the step's device work only: an immediate
-    // commit below takes it again.
+    // commit below takes it again.  A failure inside poisons every slot of
+    // the batch (forward_token_internal, gpu_llm/mod.rs:2476-2482).
     std::vector<int32_t> next(b);
-    {
+    try {
         std::lock_guard<std::mutex> lock(ctx_->mutex());
         void *h = ctx_->handle();
         const ModelSpec &s = spec_;
@@ -248,6 +266,7 @@ std::vector<Step> DecoderRunner::forward_batch(const std::vector<int32_t> &token
         ctx_->check("embed", mslim_attn_embed(h, w_.embed, s.vocab, s.hidden, ids_, b, x_, nullptr));
         for (int l = 0; l < s.layers; ++l) {
             const LayerWeights &w = w_.layers[l];
+            injected_error(l);
             ctx_->check("input norm", mslim_attn_rmsnorm(h, x_, w.input_norm, norm_, b, s.hidden, s.rms_eps));
             ctx_->check("QKV projection", mslim_attn_gemm_qkv(h, w.q, w.k, w.v, norm_, q_, k_, v_, s.hidden, qd, kvd, b));
             ctx_->check("RoPE + K/V append",
@@ -268,6 +287,9 @@ std::vector<Step> DecoderRunner::forward_batch(const std::vector<int32_t> &token
         head(x_, b);
         ctx_->check("read greedy tokens", mslim_attn_buf_read(h, next_, 0, reinterpret_cast<uint8_t *>(next.data()),
                                                               (size_t)b * 4));
+    } catch (...) {
+        for (int i = 0; i < b; ++i) poisoned_[i] = 1;
+        throw;
     }
     std::vector<Step> steps(b);
     for (int i = 0; i < b; ++i) {
@@ -275,17 +297,24 @@ std::vector<Step> DecoderRunner::forward_batch(const std::vector<int32_t> &token
         steps[i] = Step{next[i], positions_[i]};
     }
     // Immediate mode (gpu_llm/mod.rs:2162-2164): each step's K/V is committed
-    // before the step returns.
+    // before the step returns; a failed commit poisons its slot.
     if (!deferred_cold_)
         for (int i = 0; i < b; ++i)
-            if (cold_[i]) flush_cold(i);
+            if (cold_[i]) {
+                try {
+                    flush_cold(i);
+                } catch (...) {
+                    poisoned_[i] = 1;
+                    throw;
+                }
+            }
     return steps;
 }
 
 void DecoderRunner::set_deferred_cold_commit(bool deferred) {
     if (!deferred)
         for (int i = 0; i < max_batch_; ++i)
-            if (cold_[i] && cold_report_[i].committed_tokens < positions_[i]) flush_cold(i);
+            if (cold_[i] && !poisoned_[i] && cold_report_[i].committed_tokens < positions_[i]) flush_cold(i);
     deferred_cold_ = deferred;
 }
 
@@ -298,6 +327,20 @@ std::vector<int32_t> DecoderRunner::generate(int seq, const std::vector<int32_t>
     Step current = prefill_only(seq, prompt);
     std::vector<int32_t> generated;
     for (int step = 0; step < max_new; ++step) {
+        if (cancel_ && __atomic_load_n(cancel_, __ATOMIC_RELAXED)) {
+            // A cancelled turn's decoded prefix is sealed before the error
+            // (generate_cancellable, gpu_llm/mod.rs:2704-2712); a failed seal
+            // poisons the slot.
+            if (cold_[seq] && deferred_cold_ && cold_report_[seq].committed_tokens < positions_[seq]) {
+                try {
+                    flush_cold(seq);
+                } catch (...) {
+                    poisoned_[seq] = 1;
+                    throw;
+                }
+            }
+            throw Error("GPU generation cancelled by client");
+        }
         const int32_t token = current.argmax_token;
         bool eos = false;
         for (int32_t e : eos_ids) eos = eos || e == token;
@@ -310,7 +353,8 @@ std::vector<int32_t> DecoderRunner::generate(int seq, const std::vector<int32_t>
 
 void DecoderRunner::set_calibration_prefill_settings(const PrefillSettings &settings) {
     settings.validate();
-    for (int64_t p : positions_) ensure(p == 0, "prefill tuning requires a healthy, empty session");
+    for (int i = 0; i < max_batch_; ++i)
+        ensure(positions_[i] == 0 && !poisoned_[i], "prefill tuning requires a healthy, empty session");
     ensure(settings.chunk_tokens() <= rows_cap_, "prefill batch exceeds the chunk this runner was built for");
     chunk_tokens_ = settings.chunk_tokens();
     settings_ = settings;
@@ -318,12 +362,16 @@ void DecoderRunner::set_calibration_prefill_settings(const PrefillSettings &sett
 
 void DecoderRunner::reset(int seq) {
     ensure(seq >= 0 && seq < max_batch_, "sequence slot out of range");
+    // A poisoned slot's deferred K/V are not committed: its device state is
+    // not trusted.  The reset discards it and clears the poison.
+    const bool was_poisoned = poisoned_[seq] != 0;
+    poisoned_[seq] = 0;
     if (cold_[seq]) {
         // reset_session (gpu_llm/mod.rs:1530-1577): commit what is deferred,
         // then continue in a fresh ColdStore namespace
         // <parent>/session-<pid>-<nonce> beside the current directory, so
         // the finished session stays on disk for a later restore.
-        if (cold_report_[seq].committed_tokens < positions_[seq]) flush_cold(seq);
+        if (!was_poisoned && cold_report_[seq].committed_tokens < positions_[seq]) flush_cold(seq);
         std::string current = *cold_[seq]->config().cold_directory;
         while (current.size() > 1 && current.back() == '/') current.pop_back();
         const size_t cut = current.find_last_of('/');
@@ -380,6 +428,7 @@ void DecoderRunner::seal_slot(int seq, int64_t from, int64_t to) {
 void DecoderRunner::attach_cold_store(int seq, const std::string &directory) {
     ensure(seq >= 0 && seq < max_batch_, "sequence slot out of range");
     ensure(layout_ == KvLayout::Paged, "the ColdStore-exact route needs the paged K/V layout");
+    check_healthy(seq);
     ensure(positions_[seq] == 0, "attach a ColdStore to an empty slot");
     region::RegionConfig config;
     config.cold_directory = directory;
@@ -404,6 +453,7 @@ void DecoderRunner::detach_cold_store(int seq) {
 void DecoderRunner::flush_cold(int seq) {
     ensure(seq >= 0 && seq < max_batch_, "sequence slot out of range");
     ensure(cold_[seq] != nullptr, "deferred commit requires canonical ColdStore");
+    check_healthy(seq);
     const auto t0 = std::chrono::steady_clock::now();
     const int64_t from = cold_report_[seq].committed_tokens, to = positions_[seq];
     ensure(from <= to, "GPU ColdStore prefill prefix missing/longer than in-flight KV");
@@ -415,6 +465,7 @@ void DecoderRunner::flush_cold(int seq) {
 void DecoderRunner::restore_session(int seq, int64_t tokens) {
     ensure(seq >= 0 && seq < max_batch_, "sequence slot out of range");
     ensure(cold_[seq] != nullptr, "canonical GPU restore requires persistent LOD/ColdStore");
+    check_healthy(seq);
     ensure(positions_[seq] == 0, "canonical GPU restore requires a fresh session");
     ensure(tokens > 0, "canonical GPU restore prefix is empty");
     ensure(tokens < max_context_, "canonical GPU restore must leave capacity for continuation");
@@ -451,8 +502,43 @@ std::vector<uint16_t> DecoderRunner::last_logits() const {
     return out;
 }
 
+bool DecoderRunner::poisoned(int seq) const {
+    ensure(seq >= 0 && seq < max_batch_, "sequence slot out of range");
+    return poisoned_[seq] != 0;
+}
+
+void DecoderRunner::check_healthy(int seq) const {
+    ensure(!poisoned_[seq], "GPU slot " + std::to_string(seq) +
+                                " was poisoned by an earlier failed forward pass; reset the slot");
+}
+
+void DecoderRunner::inject_failure(int kind, int layer) {
+    ensure(kind == 0 || kind == kInjectArgumentError || kind == kInjectCancel, "unknown failure injection");
+    ensure(layer >= 0 && layer < spec_.layers, "injected failure layer out of range");
+    inject_kind_ = kind;
+    inject_layer_ = layer;
+}
+
+void DecoderRunner::check_cancel(const char *where, int layer) {
+    bool raised = cancel_ && __atomic_load_n(cancel_, __ATOMIC_RELAXED) != 0;
+    if (inject_kind_ == kInjectCancel && layer == inject_layer_) {
+        inject_kind_ = 0;
+        raised = true;
+    }
+    ensure(!raised, where);
+}
+
+void DecoderRunner::injected_error(int layer) {
+    if (inject_kind_ != kInjectArgumentError || layer != inject_layer_) return;
+    inject_kind_ = 0;
+    // A launch with an invalid shape: the library rejects it before any work.
+    ctx_->check("input norm", mslim_attn_rmsnorm(ctx_->handle(), x_, w_.layers[layer].input_norm, norm_, -1,
+                                                 spec_.hidden, spec_.rms_eps));
+}
+
 std::string DecoderRunner::logical_kv_sha256(int seq) const {
     ensure(seq >= 0 && seq < max_batch_, "sequence slot out of range");
+    check_healthy(seq);
     std::vector<const int32_t *> tables(spec_.layers, table_row(seq));
     std::vector<const void *> keys(k_pools_.begin(), k_pools_.end()), values(v_pools_.begin(), v_pools_.end());
     const bool dense = layout_ == KvLayout::Dense;
@@ -749,6 +835,37 @@ int mslim_model_logical_kv_sha256(void *model, int seq, char *hex_out) {
         mslim::ensure(hex_out != nullptr, "null digest buffer");
         const std::string hex = runner_of(model).logical_kv_sha256(seq);
         std::memcpy(hex_out, hex.c_str(), hex.size() + 1);
+        return 0;
+    } catch (const std::exception &e) {
+        return model_fail(e);
+    }
+}
+
+/* ---- failure handling ---------------------------------------------------- */
+
+int mslim_model_set_cancel_flag(void *model, const int32_t *flag) {
+    g_model_error.clear();
+    try {
+        runner_of(model).set_cancel_flag(flag);
+        return 0;
+    } catch (const std::exception &e) {
+        return model_fail(e);
+    }
+}
+
+int mslim_model_poisoned(void *model, int seq) {
+    g_model_error.clear();
+    try {
+        return runner_of(model).poisoned(seq) ? 1 : 0;
+    } catch (const std::exception &e) {
+        return model_fail(e);
+    }
+}
+
+int mslim_model_inject_failure(void *model, int kind, int layer) {
+    g_model_error.clear();
+    try {
+        runner_of(model).inject_failure(kind, layer);
         return 0;
     } catch (const std::exception &e) {
         return model_fail(e);

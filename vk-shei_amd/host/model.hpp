@@ -140,7 +140,33 @@ public:
     // to it first commits what is deferred.
     void set_deferred_cold_commit(bool deferred);
 
+    // Cooperative cancellation: a caller-owned flag (nonzero = cancel), read
+    // at every prompt chunk and layer boundary of a prefill
+    // (prefill_batched, gpu_llm/prefill.rs:653-680) and at every token
+    // boundary of forward_batch and generate (generate_cancellable,
+    // gpu_llm/mod.rs:2587-2700).  nullptr clears it.
+    void set_cancel_flag(const int32_t *flag) { cancel_ = flag; }
+    // A slot whose device step failed after its arguments were accepted
+    // (a library error, a failed commit, or a prefill cancelled mid-prompt)
+    // holds K/V written for some layers only.  It is poisoned and every call
+    // that would use it fails until reset(seq), which discards its K/V
+    // (the reference's poisoned runtime, gpu_llm/mod.rs:2462-2483, refuses
+    // even the reset and is restarted instead).  A cancellation at a token
+    // boundary leaves the slot consistent and does not poison it.
+    bool poisoned(int seq) const;
+    // Failure injection for the failure-handling tests: the next device step
+    // that reaches layer `layer` fails there, once, with an argument error
+    // from the attention library (kInjectArgumentError) or as if the cancel
+    // flag had been raised (kInjectCancel).
+    static constexpr int kInjectArgumentError = 1, kInjectCancel = 2;
+    void inject_failure(int kind, int layer);
+
 private:
+    // Throws the prefill cancellation error when the flag is raised (or an
+    // injected cancel is due at `layer`).
+    void check_cancel(const char *where, int layer);
+    void injected_error(int layer);
+    void check_healthy(int seq) const;
     void *alloc(size_t bytes);
     void chunk(int seq, const int32_t *ids, int n, int64_t prior);
     // The page pool of every layer (one allocation each for K and V) and the
@@ -173,6 +199,9 @@ private:
     std::vector<ColdReport> cold_report_;
     std::unique_ptr<region::DeviceStaging> staging_;
     bool deferred_cold_ = true;
+    const int32_t *cancel_ = nullptr;
+    std::vector<char> poisoned_;
+    int inject_kind_ = 0, inject_layer_ = -1;
     int32_t *table_ = nullptr, *ids_ = nullptr, *pos_ = nullptr, *next_ = nullptr;
     uint16_t *x_ = nullptr, *norm_ = nullptr, *q_ = nullptr, *k_ = nullptr, *v_ = nullptr, *qr_ = nullptr,
              *kr_ = nullptr, *attn_ = nullptr, *act_ = nullptr,

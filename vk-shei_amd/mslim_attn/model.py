@@ -36,6 +36,9 @@ MODEL_EXPORTS = (
     "mslim_model_cold_report",
     "mslim_model_cold_directory",
     "mslim_model_set_deferred_cold_commit",
+    "mslim_model_set_cancel_flag",
+    "mslim_model_poisoned",
+    "mslim_model_inject_failure",
 )
 
 
@@ -121,6 +124,9 @@ def host_library() -> C.CDLL:
         "mslim_model_cold_report": (I, [P, I, C.POINTER(ColdReport)]),
         "mslim_model_cold_directory": (I, [P, I, C.c_char_p, C.c_size_t]),
         "mslim_model_set_deferred_cold_commit": (I, [P, I]),
+        "mslim_model_set_cancel_flag": (I, [P, PI32]),
+        "mslim_model_poisoned": (I, [P, I]),
+        "mslim_model_inject_failure": (I, [P, I, I]),
     }
     for name in MODEL_EXPORTS:
         res, args = sigs[name]
@@ -278,6 +284,31 @@ class Model:
         out = C.create_string_buffer(4096)
         self._check("cold_directory", self._lib.mslim_model_cold_directory(self._h, seq, out, 4096))
         return os.fsdecode(out.value)
+
+    # ---- failure handling ----------------------------------------------
+
+    def set_cancel_flag(self, flag) -> None:
+        """Install a cancel flag: a ctypes c_int32 the caller keeps alive and
+        sets nonzero to cancel (None clears).  Read at prompt chunk and layer
+        boundaries of a prefill and at token boundaries of forward_batch and
+        generate."""
+        self._cancel = flag
+        ptr = C.cast(C.byref(flag), C.POINTER(C.c_int32)) if flag is not None else None
+        self._check("set_cancel_flag", self._lib.mslim_model_set_cancel_flag(self._h, ptr))
+
+    def poisoned(self, seq: int) -> bool:
+        rc = self._lib.mslim_model_poisoned(self._h, seq)
+        if rc < 0:
+            raise MslimAttnError("poisoned", rc, self._error())
+        return rc == 1
+
+    INJECT_ARGUMENT_ERROR = 1
+    INJECT_CANCEL = 2
+
+    def inject_failure(self, kind: int, layer: int) -> None:
+        """Failure injection for tests: the next device step that reaches
+        `layer` fails there once (INJECT_ARGUMENT_ERROR, INJECT_CANCEL)."""
+        self._check("inject_failure", self._lib.mslim_model_inject_failure(self._h, kind, layer))
 
 
 def synthetic_weights(spec: ModelSpec, seed: int, scale: float = 0.02, embed_scale: float = 0.02,
