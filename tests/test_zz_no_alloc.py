@@ -62,6 +62,30 @@ def test_noalloc_decode_equals_decode_paged_two_calls(ctx):
     assert np.array_equal(got3, want3)
 
 
+def test_noalloc_decode_on_a_fresh_context_allocates_nothing(ctx):
+    """The first call on a new context leaves the device's free memory
+    unchanged (no hipMalloc, no context buffer grown), then matches the
+    allocating entry point, which grows the context's workspace."""
+    qh, kvh, d, pt = 32, 8, 128, 16
+    lens = [int(x) for x in np.random.default_rng(5).integers(512, 8193, size=32)]
+    q, kp, vp, table, pps = _pool(lens, qh, kvh, d, pt, seed=21)
+    got, want = torch.empty_like(q), torch.empty_like(q)
+    torch.cuda.synchronize()
+    fresh = mslim_attn.Context()
+    fresh.use_torch_stream()
+    try:
+        before, _ = torch.cuda.mem_get_info()
+        fresh.decode_paged_noalloc(q, kp, vp, got, lens, table, pps, pt, qh, kvh, d)
+        torch.cuda.synchronize()
+        after, _ = torch.cuda.mem_get_info()
+        assert after == before, (before, after)
+        fresh.decode_paged(q, kp, vp, want, lens, table, pps, pt, qh, kvh, d)
+        torch.cuda.synchronize()
+        assert np.array_equal(from_torch(got), from_torch(want))
+    finally:
+        fresh.close()
+
+
 def test_noalloc_decode_rejects_partials_above_the_fixed_array(ctx):
     # 64 sequences x 32,768 tokens at 64-token splits: 32,768 partitions x
     # 8 kv heads x 8 heads x 130 floats = 1.09 GB of partials > 16 MiB.  The

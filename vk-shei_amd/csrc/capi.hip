@@ -119,9 +119,21 @@ bool valid_geometry(int q_heads, int kv_heads, int head_dim) {
 
 bool is_pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
 
+// Serialises calls on a context and makes its device current for the call;
+// the calling thread's device is restored on the way out.
 struct Lock {
-    explicit Lock(Context &c) : guard(c.mutex) { (void)hipSetDevice(c.device); }
+    explicit Lock(Context &c) : guard(c.mutex), device(c.device) {
+        if (hipGetDevice(&saved) != hipSuccess) saved = -1;
+        if (saved != device) (void)hipSetDevice(device);
+    }
+    ~Lock() {
+        if (saved >= 0 && saved != device) (void)hipSetDevice(saved);
+    }
+    Lock(const Lock &) = delete;
+    Lock &operator=(const Lock &) = delete;
     std::lock_guard<std::mutex> guard;
+    int device;
+    int saved = -1;
 };
 
 // Argument checks and the split choice shared by every decode entry point.
@@ -262,6 +274,14 @@ void *mslim_attn_ctx_new(void) {
         return nullptr;
     }
     c->stream = c->own_stream;
+    // The allocation-free decode's fixed partials array: its address on this
+    // device is taken here, once, so that entry point's first call loads
+    // nothing.
+    float *scratch = nullptr;
+    if (check_hip(mslim::decode_static_scratch(device, &scratch), "hipGetSymbolAddress decode scratch")) {
+        delete c;
+        return nullptr;
+    }
     return c;
 }
 

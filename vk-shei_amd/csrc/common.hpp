@@ -4,6 +4,15 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+// Device code is written for gfx950 (MI355X) only.  Besides the MFMA shapes,
+// LDS transpose reads and DMA forms it uses, the split merges of decode and
+// prefill publish partials across XCDs with relaxed agent-scope atomics whose
+// order is gfx950's implementation (write-through stores, L2-bypassing
+// loads), so any other target is refused at compile time.
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
+#error "mslim_attn device code targets gfx950 only"
+#endif
+
 namespace mslim {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));

@@ -802,8 +802,12 @@ void plan_lists(DeviceArgs &a, int total, const int32_t *seq_len) {
         }
         order[i] = {tokens, i};
     }
-    std::stable_sort(order, order + items,
-                     [](const std::pair<int, int> &x, const std::pair<int, int> &y) { return x.first > y.first; });
+    // Longest first, ties in launch order (the order a stable sort keeps);
+    // std::sort with the index as tie-break allocates nothing, as the
+    // allocation-free entry point needs.
+    std::sort(order, order + items, [](const std::pair<int, int> &x, const std::pair<int, int> &y) {
+        return x.first != y.first ? x.first > y.first : x.second < y.second;
+    });
     std::pair<int64_t, int> heap[kListBins];  // (work, list): least work on top
     for (int w = 0; w < kListBins; ++w) heap[w] = {0, w};
     const auto later = std::greater<std::pair<int64_t, int>>();
@@ -869,8 +873,12 @@ hipError_t launch_decode(const DecodeLaunch &l, hipStream_t stream) {
     auto last_len = [&](int i) {
         return l.seq_len[i] - (a.split_begin[i + 1] - a.split_begin[i] - 1) * l.split_tokens;
     };
-    std::stable_sort(a.last_order, a.last_order + l.batch,
-                     [&](int16_t x, int16_t y) { return last_len(x) > last_len(y); });
+    // Longest last partition first, ties in sequence order; no allocation
+    // (std::stable_sort may take a temporary buffer from the heap).
+    std::sort(a.last_order, a.last_order + l.batch, [&](int16_t x, int16_t y) {
+        const int lx = last_len(x), ly = last_len(y);
+        return lx != ly ? lx > ly : x < y;
+    });
     const int group = l.q_heads / l.kv_heads;
     const bool nt = kv_tokens * l.kv_heads * l.head_dim * 2 * 2 >= kNonTemporalBytes;
     const int64_t items = (int64_t)total * l.kv_heads;
