@@ -40,6 +40,8 @@ def upload(ctx, bits):
     (4096, 28672, 2),   # gate + up
     (128, 96, 3),
     (4096, 6144, 512),  # prefill chunk, first rows checked
+    (14336, 4096, 40),  # down projection of a prompt chunk: the k range split in two, merged
+    (8192, 200, 33),    # split with ragged row and token tiles
 ])
 def test_matrix_multiply_matches_oracle(ctx, inner, rows, tokens):
     rng = np.random.default_rng(inner + rows + tokens)
@@ -118,12 +120,15 @@ def test_unaligned_inner_uses_library_path(ctx):
     assert within_bound(host_bits(out), w, x, inner, rows, tokens)
 
 
-@pytest.mark.parametrize("tokens", [1, 8, 16, 17, 40])
-def test_fused_projections_equal_unfused(ctx, tokens):
+@pytest.mark.parametrize("tokens,inner", [(1, 512), (8, 512), (16, 512), (17, 512), (40, 512), (300, 512),
+                                          (40, 8192)])
+def test_fused_projections_equal_unfused(ctx, tokens, inner):
     # the fused entries are the unfused product followed by the elementwise
-    # kernel, bit for bit, on both sides of the decode-kernel token limit
-    rng = np.random.default_rng(tokens)
-    inner, qr, kvr, inter = 512, 256, 64, 704
+    # kernel, bit for bit, on both sides of the decode-kernel token limit, for
+    # both tile shapes of the prompt-chunk kernel (300 tokens) and with the
+    # split k range of long inner dimensions (8192)
+    rng = np.random.default_rng(tokens + inner)
+    qr, kvr, inter = 256, 64, 704
     x = dev_bits(bf16(rng, tokens * inner))
     wq, wk, wv = (dev_bits(bf16(rng, r * inner, 0.05)) for r in (qr, kvr, kvr))
     wg, wu = dev_bits(bf16(rng, inter * inner, 0.05)), dev_bits(bf16(rng, inter * inner, 0.05))
@@ -147,7 +152,17 @@ def test_fused_projections_equal_unfused(ctx, tokens):
     ctx.gemm_bf16_add(wo, q, in_place, in_place, qr, inner, tokens)
     ctx.gemm_bf16(wo, q, prod, qr, inner, tokens)
     ctx.add(resid, prod, added2, tokens * inner)
+    # a down-like product over the full inner dimension (split when long)
+    wd = dev_bits(bf16(rng, qr * inner, 0.05))
+    resid_d = dev_bits(bf16(rng, tokens * qr, 2.0))
+    down, down_prod, down2 = empty(qr), empty(qr), empty(qr)
+    ctx.gemm_bf16_add(wd, x, resid_d, down, inner, qr, tokens)
+    ctx.gemm_bf16(wd, x, down_prod, inner, qr, tokens)
+    ctx.add(resid_d, down_prod, down2, tokens * qr)
     torch.cuda.synchronize()
     assert torch.equal(q, q2) and torch.equal(k, k2) and torch.equal(v, v2)
     assert torch.equal(act, act2)
     assert torch.equal(added, added2) and torch.equal(in_place, added2)
+    assert torch.equal(down, down2)
+    wd_bits, x_bits = host_bits(wd), host_bits(x)
+    assert within_bound(host_bits(down_prod), wd_bits, x_bits, inner, qr, min(tokens, 8))

@@ -39,6 +39,9 @@ struct Context {
     hipStream_t stream = nullptr;
     std::mutex mutex;
     void *workspace = nullptr;      // decode split partials
+    uint16_t *swiglu_table = nullptr;  // SwiGLU activation of every BF16 gate value
+    void *proj_partial = nullptr;      // fp32 partials of split projections
+    size_t proj_partial_bytes = 0;
     size_t workspace_bytes = 0;
     int *counters = nullptr;        // decode split counters, zero between launches
     size_t counter_bytes = 0;
@@ -58,19 +61,16 @@ struct Context {
     void *backend = nullptr;       // device, backend_decode query/frames/output
     size_t backend_bytes = 0;
     hipEvent_t ev_start = nullptr, ev_end = nullptr;
-    mslim::GemmState *gemm = nullptr;  // hipBLASLt handle and plans, created on first use
     void *gemm_in = nullptr, *gemm_out = nullptr;  // device staging of matrix_multiply
     size_t gemm_in_bytes = 0, gemm_out_bytes = 0;
-    void *fuse_tmp = nullptr;  // products of the fused entries above the skinny token limit
-    size_t fuse_tmp_bytes = 0;
 
     ~Context() {
         if (stream) (void)hipStreamSynchronize(stream);
-        mslim::gemm_state_destroy(gemm);
         if (gemm_in) (void)hipFree(gemm_in);
         if (gemm_out) (void)hipFree(gemm_out);
-        if (fuse_tmp) (void)hipFree(fuse_tmp);
         if (workspace) (void)hipFree(workspace);
+        if (swiglu_table) (void)hipFree(swiglu_table);
+        if (proj_partial) (void)hipFree(proj_partial);
         if (prefill_partial) (void)hipFree(prefill_partial);
         if (prefill_counters) (void)hipFree(prefill_counters);
         if (counters) (void)hipFree(counters);
@@ -274,6 +274,14 @@ void *mslim_attn_ctx_new(void) {
         return nullptr;
     }
     c->stream = c->own_stream;
+    // The SwiGLU activation of every BF16 gate value, for the fused
+    // projection epilogue (128 KiB, built once, ready when this returns).
+    if (check_hip(hipMalloc(&c->swiglu_table, (size_t)mslim::kSwigluTableEntries * 2), "hipMalloc SwiGLU table") ||
+        check_hip(mslim::launch_swiglu_table(c->swiglu_table, c->own_stream), "SwiGLU table launch") ||
+        check_hip(hipStreamSynchronize(c->own_stream), "SwiGLU table")) {
+        delete c;
+        return nullptr;
+    }
     // The allocation-free decode's fixed partials array: its address on this
     // device is taken here, once, so that entry point's first call loads
     // nothing.
@@ -1066,22 +1074,34 @@ int mslim_attn_record_payloads(void *ctx, void *k_pool, void *v_pool, int64_t po
     return check_hip(mslim::launch_record_payloads(l, direction == 0, c.stream), "record payload launch");
 }
 
+// The fp32 partials of a split projection (none for other shapes), in a
+// context buffer that only grows (stage code 400 if it cannot).
+// `outputs`: products x the matrices' total rows (2 x rows for SwiGLU).
+static int proj_partials(Context &c, int inner, int64_t outputs, int tokens, float **partial) {
+    *partial = nullptr;
+    const int split = mslim::proj_ksplit(inner);
+    if (split < 2) return 0;
+    if (grow_device(c, &c.proj_partial, &c.proj_partial_bytes, (size_t)split * outputs * tokens * sizeof(float),
+                    "hipMalloc projection partials"))
+        return 400;
+    *partial = static_cast<float *>(c.proj_partial);
+    return 0;
+}
+
 // One product on the context's stream: the MFMA decode kernel for up to 16
-// aligned tokens, hipBLASLt otherwise.
+// aligned tokens, the tiled MFMA kernel (or its any-shape form) above.  A
+// failed launch is stage code 404, as the reference's matmul stage.
 static int project(Context &c, const void *weight, const void *input, void *output, int inner, int rows,
                    int tokens) {
-    if (mslim::skinny_supported(inner, tokens, input, weight)) {
-        const mslim::SkinnyMatrix m{static_cast<const uint16_t *>(weight), static_cast<uint16_t *>(output), rows};
-        return check_hip(mslim::launch_skinny_gemm(&m, 1, static_cast<const uint16_t *>(input), inner, tokens,
-                                                   c.stream),
-                         "decode projection launch")
+    const mslim::SkinnyMatrix m{static_cast<const uint16_t *>(weight), static_cast<uint16_t *>(output), rows};
+    const auto *x = static_cast<const uint16_t *>(input);
+    if (mslim::skinny_supported(inner, tokens, input, weight))
+        return check_hip(mslim::launch_skinny_gemm(&m, 1, x, inner, tokens, c.stream), "decode projection launch")
                    ? 404
                    : 0;
-    }
-    std::string err;
-    if (int code = mslim::gemm_bf16(c.gemm, weight, input, output, inner, rows, tokens, c.stream, err))
-        return fail(err, code);
-    return 0;
+    float *partial = nullptr;
+    if (int rc = proj_partials(c, inner, rows, tokens, &partial)) return rc;
+    return check_hip(mslim::launch_proj(&m, 1, x, inner, tokens, partial, c.stream), "projection launch") ? 404 : 0;
 }
 
 // tv_hip_matrix_multiply's argument limits (hipblaslt_bridge.cpp:207-210).
@@ -1140,13 +1160,14 @@ int mslim_attn_gemm_bf16_add(void *ctx, const void *weight, const void *input, c
                    ? 404
                    : 0;
     }
-    const size_t n = (size_t)rows * tokens;
-    if (grow_device(c, &c.fuse_tmp, &c.fuse_tmp_bytes, n * 2, "hipMalloc projection scratch")) return 400;
-    if (int rc = project(c, weight, input, c.fuse_tmp, inner, rows, tokens)) return rc;
-    return check_hip(mslim::launch_add(static_cast<const uint16_t *>(residual),
-                                       static_cast<const uint16_t *>(c.fuse_tmp), static_cast<uint16_t *>(output),
-                                       n, c.stream),
-                     "residual add launch");
+    const mslim::SkinnyMatrix m{w, static_cast<uint16_t *>(output), rows};
+    float *partial = nullptr;
+    if (int rc = proj_partials(c, inner, rows, tokens, &partial)) return rc;
+    return check_hip(mslim::launch_proj_add(m, static_cast<const uint16_t *>(residual), x, inner, tokens, partial,
+                                            c.stream),
+                     "projection launch")
+               ? 404
+               : 0;
 }
 
 int mslim_attn_gemm_swiglu(void *ctx, const void *gate_weight, const void *up_weight, const void *input,
@@ -1168,13 +1189,15 @@ int mslim_attn_gemm_swiglu(void *ctx, const void *gate_weight, const void *up_we
                    ? 404
                    : 0;
     }
-    const size_t n = (size_t)rows * tokens;
-    if (grow_device(c, &c.fuse_tmp, &c.fuse_tmp_bytes, n * 4, "hipMalloc projection scratch")) return 400;
-    uint16_t *gate = static_cast<uint16_t *>(c.fuse_tmp), *up = gate + n;
-    if (int rc = project(c, gate_weight, input, gate, inner, rows, tokens)) return rc;
-    if (int rc = project(c, up_weight, input, up, inner, rows, tokens)) return rc;
-    return check_hip(mslim::launch_swiglu(gate, up, static_cast<uint16_t *>(output), n, c.stream),
-                     "SwiGLU launch");
+    float *partial = nullptr;
+    if (int rc = proj_partials(c, inner, 2 * (int64_t)rows, tokens, &partial)) return rc;
+    return check_hip(mslim::launch_proj_swiglu(static_cast<const uint16_t *>(gate_weight),
+                                               static_cast<const uint16_t *>(up_weight),
+                                               static_cast<uint16_t *>(output), rows, x, inner, tokens,
+                                               c.swiglu_table, partial, c.stream),
+                     "projection launch")
+               ? 404
+               : 0;
 }
 
 int mslim_attn_gemm_qkv(void *ctx, const void *q_weight, const void *k_weight, const void *v_weight,
@@ -1199,9 +1222,16 @@ int mslim_attn_gemm_qkv(void *ctx, const void *q_weight, const void *k_weight, c
                    ? 404
                    : 0;
     }
-    if (int rc = project(c, q_weight, input, q_out, inner, q_rows, tokens)) return rc;
-    if (int rc = project(c, k_weight, input, k_out, inner, kv_rows, tokens)) return rc;
-    return project(c, v_weight, input, v_out, inner, kv_rows, tokens);
+    const mslim::SkinnyMatrix m[3] = {
+        {static_cast<const uint16_t *>(q_weight), static_cast<uint16_t *>(q_out), q_rows},
+        {static_cast<const uint16_t *>(k_weight), static_cast<uint16_t *>(k_out), kv_rows},
+        {static_cast<const uint16_t *>(v_weight), static_cast<uint16_t *>(v_out), kv_rows}};
+    float *partial = nullptr;
+    if (int rc = proj_partials(c, inner, (int64_t)q_rows + 2 * (int64_t)kv_rows, tokens, &partial)) return rc;
+    return check_hip(mslim::launch_proj(m, 3, static_cast<const uint16_t *>(input), inner, tokens, partial, c.stream),
+                     "projection launch")
+               ? 404
+               : 0;
 }
 
 }  // extern "C"

@@ -49,12 +49,19 @@ __device__ __forceinline__ int64_t page_row(const int32_t *table, int shift, int
 
 // llm_swiglu's arithmetic (gpu_llm.cl:225-237) on BF16 gate and up values:
 // BF16(BF16(g / (1 + e^-g)) * u), e^-g evaluated in double and rounded once,
-// every other step correctly rounded in f32.
-__device__ __forceinline__ uint16_t swiglu_bf16(uint16_t gate, uint16_t up) {
+// every other step correctly rounded in f32.  The first stage depends on the
+// 16 gate bits only, so kernels with many outputs read it from a 65,536-entry
+// table of swiglu_act_bf16 (built once per context) instead.
+__device__ __forceinline__ uint16_t swiglu_act_bf16(uint16_t gate) {
     const float g = read_bf16(gate);
     const float e = (float)exp(-(double)g);
-    const float activated = __fdiv_rn(g, __fadd_rn(1.0f, e));
-    return write_bf16(__fmul_rn(round_bf16(activated), read_bf16(up)));
+    return write_bf16(__fdiv_rn(g, __fadd_rn(1.0f, e)));
+}
+__device__ __forceinline__ uint16_t swiglu_mul_bf16(uint16_t activated, uint16_t up) {
+    return write_bf16(__fmul_rn(read_bf16(activated), read_bf16(up)));
+}
+__device__ __forceinline__ uint16_t swiglu_bf16(uint16_t gate, uint16_t up) {
+    return swiglu_mul_bf16(swiglu_act_bf16(gate), up);
 }
 
 // IEEE binary16 -> f32, exact for every encoding (subnormals, inf, NaN
@@ -75,6 +82,16 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 // bytes land at lds_base + 16*l; lds_base must be wavefront-uniform.
 __device__ __forceinline__ void dma16(const void *global, void *lds_base) {
     __builtin_amdgcn_global_load_lds(global, lds_base, 16, 0, 0);
+}
+
+// A pointer that is the same in every lane, kept in SGPRs (the compiler
+// cannot always prove uniformity; scalar-base copies need it).
+template <typename T>
+__device__ __forceinline__ T *uniform_ptr(T *p) {
+    const uint64_t v = reinterpret_cast<uintptr_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return reinterpret_cast<T *>((uintptr_t)(((uint64_t)hi << 32) | lo));
 }
 
 // LDS offset (wave-uniform, in an SGPR) of a __shared__ address.
@@ -117,6 +134,21 @@ __device__ __forceinline__ short4_t lds_read_tr16_at(uint32_t addr) {
 __device__ __forceinline__ bf16x8_t lds_read_b128(uint32_t addr) {
     return *(const __attribute__((address_space(3))) bf16x8_t *)(uintptr_t)addr;
 }
+
+// s_waitcnt immediate that waits until at most n vector-memory operations
+// are outstanding and leaves the LDS/scalar and export counters alone.
+constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+// The same with every LDS read of this wavefront complete (lgkmcnt 0).
+constexpr int vmcnt_lds_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4); }
+// The same with at most l LDS reads outstanding (lgkmcnt l).  LDS reads
+// complete in issue order when no scalar memory load is in flight, so the
+// last l reads may still be pending and every earlier one has completed.
+constexpr int vmcnt_lds_last_imm(int n, int l) { return vmcnt_lds_imm(n) | (l << 8); }
+
+// Workgroup barrier without the memory fence of __syncthreads(): with LDS
+// DMA in flight that fence would wait for every outstanding DMA (vmcnt 0).
+// Callers order LDS themselves with vmcnt_lds_imm waits before it.
+__device__ __forceinline__ void raw_barrier() { __builtin_amdgcn_s_barrier(); }
 
 __device__ __forceinline__ bool wave_any(bool pred) {
     return __builtin_amdgcn_ballot_w64(pred) != 0;

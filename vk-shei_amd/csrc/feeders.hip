@@ -492,6 +492,17 @@ hipError_t launch_rope_append(const RopeAppendArgs &a, hipStream_t stream) {
     return hipGetLastError();
 }
 
+// The first SwiGLU stage for every BF16 gate value (kSwigluTableEntries).
+__global__ __launch_bounds__(256) void swiglu_table_kernel(uint16_t *table) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    table[i] = swiglu_act_bf16((uint16_t)i);
+}
+
+hipError_t launch_swiglu_table(uint16_t *table, hipStream_t stream) {
+    hipLaunchKernelGGL(swiglu_table_kernel, dim3(kSwigluTableEntries / 256), dim3(256), 0, stream, table);
+    return hipGetLastError();
+}
+
 hipError_t launch_swiglu(const uint16_t *gate, const uint16_t *up, uint16_t *out, size_t n,
                          hipStream_t stream) {
     const unsigned blocks = (unsigned)((n + 255) / 256);

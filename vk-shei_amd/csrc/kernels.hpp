@@ -119,6 +119,9 @@ struct RopeAppendArgs {
     float factor, low, high, original_max;
 };
 hipError_t launch_rope_append(const RopeAppendArgs &a, hipStream_t stream);
+// Table of swiglu_act_bf16 for every BF16 gate value (128 KiB).
+constexpr int kSwigluTableEntries = 65536;
+hipError_t launch_swiglu_table(uint16_t *table, hipStream_t stream);
 hipError_t launch_swiglu(const uint16_t *gate, const uint16_t *up, uint16_t *out, size_t n,
                          hipStream_t stream);
 hipError_t launch_add(const uint16_t *a, const uint16_t *b, uint16_t *out, size_t n, hipStream_t stream);
@@ -163,15 +166,6 @@ struct PayloadMoveLaunch {
 };
 hipError_t launch_record_payloads(const PayloadMoveLaunch &a, bool to_staging, hipStream_t stream);
 
-// BF16 projection GEMM through hipBLASLt (csrc/gemm.hip).
-struct GemmState;
-void gemm_state_destroy(GemmState *state);
-// out[tokens][rows] = BF16(in[tokens][inner] . weight[rows][inner]^T) on
-// device buffers, stream-ordered.  Returns 0, 100+hipError_t, 200+hipBLASLt
-// status, 403 (no plan) or 404 (matmul failed) with `err` set.
-int gemm_bf16(GemmState *&state, const void *weight, const void *input, void *output, int inner, int rows,
-              int tokens, hipStream_t stream, std::string &err);
-
 // Decode-batch projections on MFMA (tokens <= kSkinnyMaxTokens, inner a
 // multiple of 32, x and weights 16-byte aligned): out[t][r] =
 // BF16(sum_k x[t][k] w[r][k]) for up to three matrices in one launch, or with
@@ -190,6 +184,22 @@ hipError_t launch_skinny_gemm_add(const SkinnyMatrix &m, const uint16_t *resid, 
                                   int tokens, hipStream_t stream);
 hipError_t launch_skinny_swiglu(const uint16_t *w_gate, const uint16_t *w_up, uint16_t *out, int rows,
                                 const uint16_t *x, int inner, int tokens, hipStream_t stream);
+
+// The same products for any number of token rows (csrc/proj.hip): the tiled
+// MFMA kernel when inner is a multiple of 64 and x and the weights are
+// 16-byte aligned, one wavefront per output otherwise.  Same epilogues.
+// Split launches (proj_ksplit(inner) > 1) keep fp32 partials in `partial`:
+// proj_ksplit * products * tokens * (sum of the matrices' rows) floats, with
+// products 2 for SwiGLU (gate and up) and 1 otherwise.
+int proj_ksplit(int inner);
+hipError_t launch_proj(const SkinnyMatrix *m, int count, const uint16_t *x, int inner, int tokens, float *partial,
+                       hipStream_t stream);
+hipError_t launch_proj_add(const SkinnyMatrix &m, const uint16_t *resid, const uint16_t *x, int inner, int tokens,
+                           float *partial, hipStream_t stream);
+// act_table: launch_swiglu_table's table (device, 128 KiB).
+hipError_t launch_proj_swiglu(const uint16_t *w_gate, const uint16_t *w_up, uint16_t *out, int rows,
+                              const uint16_t *x, int inner, int tokens, const uint16_t *act_table, float *partial,
+                              hipStream_t stream);
 
 hipError_t launch_pages_write(uint16_t *k_pool, uint16_t *v_pool, const int32_t *page_table,
                               int page_tokens, int kv_heads, int head_dim, int64_t first_token,

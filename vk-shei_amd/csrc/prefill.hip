@@ -117,21 +117,6 @@ struct Swz {
     }
 };
 
-// s_waitcnt immediate that waits until at most n vector-memory operations
-// are outstanding and leaves the LDS/scalar and export counters alone.
-constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
-// The same with every LDS read of this wavefront complete (lgkmcnt 0).
-constexpr int vmcnt_lds_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4); }
-// The same with at most l LDS reads outstanding (lgkmcnt l).  LDS reads
-// complete in issue order when no scalar memory load is in flight, so the
-// last l reads may still be pending and every earlier one has completed.
-constexpr int vmcnt_lds_last_imm(int n, int l) { return vmcnt_lds_imm(n) | (l << 8); }
-
-// Workgroup barrier without the memory fence of __syncthreads(): with LDS
-// DMA in flight that fence would wait for every outstanding DMA (vmcnt 0).
-// Callers order LDS themselves with vmcnt_lds_imm waits before it.
-__device__ __forceinline__ void raw_barrier() { __builtin_amdgcn_s_barrier(); }
-
 // Iteration j of a wavefront issues the QK MFMAs of tile j, then the P.V
 // MFMAs of tile j-1 with the softmax of tile j spread over their slots (row
 // maximum in the first two slots, exp2 / BF16 pack / row sums in the rest).
