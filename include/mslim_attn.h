@@ -85,6 +85,15 @@ typedef struct {
 } mslim_attn_device_info;
 int mslim_attn_get_device_info(void *ctx, mslim_attn_device_info *out);
 
+/* Device self-check of the BF16 encoder every kernel writes with: gfx950's
+ * f32 -> bf16 conversion instruction against the reference's integer rule
+ * (round to nearest even; NaN keeps sign and upper payload with the quiet
+ * bit forced; gpu_llm.cl:10-21), over all 2^32 f32 encodings.  Stores the
+ * number that differ (0 on a conforming device) in *mismatches; takes a few
+ * milliseconds and 4 MiB of temporary device memory.  No reference
+ * counterpart: it backs the library's use of the instruction. */
+int mslim_attn_check_bf16_encoding(void *ctx, uint64_t *mismatches);
+
 /* Route this context's work onto an existing HIP stream; NULL names the HIP
  * null (legacy default) stream.  Until this is called the context uses a
  * stream of its own.  No reference counterpart: the OpenCL engine owns its
@@ -471,13 +480,14 @@ int mslim_attn_record_payloads(void *ctx, void *k_pool, void *v_pool, int64_t po
 
 /* Replaces tv_hip_matrix_multiply (hipblaslt_bridge.cpp:203-233, bound at
  * native_hip.rs:19-20): output[tokens][rows] = BF16(input[tokens][inner] .
- * weight[rows][inner]^T), fp32 accumulation rounded once, through hipBLASLt.
- * weight is a device buffer (mslim_attn_buf_upload); input and output are
- * HOST buffers of BF16 bits and the call blocks, as in the reference.
- * Limits as the reference: 0 < tokens <= 512, 0 < inner <= 32768,
- * 0 < rows <= 500000.  Codes: -1 arguments, 100+hipError_t, 200+hipBLASLt
- * status, 400/401 staging allocation, 402 H2D, 403 no algorithm, 404
- * matmul, 405 D2H (hipblaslt_bridge.cpp:217-231). */
+ * weight[rows][inner]^T), fp32 accumulation rounded once, on the library's
+ * own MFMA kernels (no hipBLASLt).  weight is a device buffer
+ * (mslim_attn_buf_upload); input and output are HOST buffers of BF16 bits
+ * and the call blocks, as in the reference.  Limits as the reference:
+ * 0 < tokens <= 512, 0 < inner <= 32768, 0 < rows <= 500000.  Codes: -1
+ * arguments, 100+hipError_t, 400/401 staging allocation, 402 H2D, 404
+ * product launch, 405 D2H (the stage codes of hipblaslt_bridge.cpp:217-231;
+ * the 200+ library statuses and 403 no longer arise). */
 int mslim_attn_matrix_multiply(void *ctx, const void *weight, const uint8_t *input, uint8_t *output,
                                int inner, int rows, int tokens);
 
@@ -486,10 +496,14 @@ int mslim_attn_matrix_multiply(void *ctx, const void *weight, const uint8_t *inp
  * (norm -> QKV -> RoPE -> attention -> O -> SwiGLU -> down) chains without
  * host round trips.  output must not alias input or weight.  Decode batches
  * (tokens <= 16, inner a multiple of 32, input and weight 16-byte aligned)
- * run on the library's MFMA kernel that streams the weights once, the role
- * of the reference's decode GEMVs (llm_gemv_bf16 / reuse-8, gpu_llm.cl:38-68,
- * :553-596); larger products go to hipBLASLt.  Both accumulate in fp32 in
- * their own order: results agree within the rounding of the f64 product. */
+ * run on the MFMA kernel that streams the weights once, the role of the
+ * reference's decode GEMVs (llm_gemv_bf16 / reuse-8, gpu_llm.cl:38-68,
+ * :553-596); larger products run on the tiled MFMA kernel of the prompt
+ * chunks (llm_prefill_gemv_reuse8/16/32, gpu_llm.cl:553-683), or, for inner
+ * not a multiple of 64 or unaligned buffers, a kernel of one wavefront per
+ * output.  Each product of a given shape is summed in one fixed order, so
+ * every entry point below that fuses an epilogue gives the same bits as this
+ * one followed by the elementwise call. */
 int mslim_attn_gemm_bf16(void *ctx, const void *weight, const void *input, void *output, int inner,
                          int rows, int tokens);
 
@@ -513,6 +527,22 @@ int mslim_attn_gemm_swiglu(void *ctx, const void *gate_weight, const void *up_we
 int mslim_attn_gemm_qkv(void *ctx, const void *q_weight, const void *k_weight, const void *v_weight,
                         const void *input, void *q_out, void *k_out, void *v_out, int inner, int q_rows,
                         int kv_rows, int tokens);
+
+/* The RMSNorm that precedes a projection in run_layer (llm_rmsnorm,
+ * gpu_llm.cl:72-98, then the product; gpu_llm/mod.rs:2056-2350), in one
+ * call: bit-identical to mslim_attn_rmsnorm(input, norm_weight, epsilon)
+ * followed by mslim_attn_gemm_bf16 / _gemm_qkv / _gemm_swiglu on the
+ * normalised rows.  Decode batches of up to 8 rows of up to 4096 inputs
+ * normalise inside the projection kernel (no launch and no buffer for the
+ * normalised rows); other shapes normalise into a context buffer first. */
+int mslim_attn_rmsnorm_gemm_bf16(void *ctx, const void *norm_weight, float epsilon, const void *weight,
+                                 const void *input, void *output, int inner, int rows, int tokens);
+int mslim_attn_rmsnorm_gemm_qkv(void *ctx, const void *norm_weight, float epsilon, const void *q_weight,
+                                const void *k_weight, const void *v_weight, const void *input, void *q_out,
+                                void *k_out, void *v_out, int inner, int q_rows, int kv_rows, int tokens);
+int mslim_attn_rmsnorm_gemm_swiglu(void *ctx, const void *norm_weight, float epsilon, const void *gate_weight,
+                                   const void *up_weight, const void *input, void *output, int inner, int rows,
+                                   int tokens);
 
 #ifdef __cplusplus
 }

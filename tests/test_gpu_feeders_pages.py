@@ -24,6 +24,12 @@ def test_rmsnorm_bit_exact(ctx, tokens, hidden):
     assert np.array_equal(from_torch(out).reshape(-1), oracle.rmsnorm_gpu(xb, wb, tokens, hidden, 1e-5))
 
 
+def test_bf16_encoder_matches_the_rule_on_every_encoding(ctx):
+    # the conversion instruction every kernel writes with, against the
+    # reference's integer rule (gpu_llm.cl:10-21), over all 2^32 f32 inputs
+    assert ctx.check_bf16_encoding() == 0
+
+
 @pytest.mark.parametrize("llama3", [False, True])
 @pytest.mark.parametrize("start", [0, 1, 4090, 32760])
 def test_rope_bit_exact(ctx, llama3, start):

@@ -120,7 +120,7 @@ def test_unaligned_inner_uses_library_path(ctx):
     assert within_bound(host_bits(out), w, x, inner, rows, tokens)
 
 
-@pytest.mark.parametrize("tokens,inner", [(1, 512), (8, 512), (16, 512), (17, 512), (40, 512), (300, 512),
+@pytest.mark.parametrize("tokens,inner", [(1, 512), (8, 512), (16, 512), (17, 512), (40, 512), (300, 512), (8, 4096), (4, 14336),
                                           (40, 8192)])
 def test_fused_projections_equal_unfused(ctx, tokens, inner):
     # the fused entries are the unfused product followed by the elementwise
@@ -166,3 +166,52 @@ def test_fused_projections_equal_unfused(ctx, tokens, inner):
     assert torch.equal(down, down2)
     wd_bits, x_bits = host_bits(wd), host_bits(x)
     assert within_bound(host_bits(down_prod), wd_bits, x_bits, inner, qr, min(tokens, 8))
+
+
+@pytest.mark.parametrize("tokens,inner", [(1, 4096), (8, 4096), (3, 96), (9, 4096), (4, 4104), (40, 512),
+                                          (2, 8192)])
+def test_rmsnorm_fused_projections_equal_unfused(ctx, tokens, inner):
+    # RMSNorm + projection entries equal mslim_attn_rmsnorm followed by the
+    # plain, QKV and SwiGLU products, bit for bit: inside the decode kernel
+    # (<= 8 rows of <= 4096), and through the normalised-rows buffer for
+    # 9 rows, inner 4104 (no MFMA decode kernel), prompt chunks and inner 8192
+    rng = np.random.default_rng(7 * tokens + inner)
+    qr, kvr, inter = 320, 64, 208
+    x = dev_bits(bf16(rng, tokens * inner, 3.0))
+    nw = dev_bits(bf16(rng, inner, 0.5))
+    eps = 1e-5
+    wq, wk, wv = (dev_bits(bf16(rng, r * inner, 0.05)) for r in (qr, kvr, kvr))
+    wg, wu = dev_bits(bf16(rng, inter * inner, 0.05)), dev_bits(bf16(rng, inter * inner, 0.05))
+    empty = lambda n: torch.empty(tokens * n, dtype=torch.int16, device="cuda")  # noqa: E731
+    normed = empty(inner)
+    ctx.rmsnorm(x, nw, normed, tokens, inner, eps)
+    plain, plain2 = empty(qr), empty(qr)
+    ctx.gemm_bf16(wq, normed, plain, inner, qr, tokens)
+    ctx.rmsnorm_gemm_bf16(nw, eps, wq, x, plain2, inner, qr, tokens)
+    q, k, v, q2, k2, v2 = empty(qr), empty(kvr), empty(kvr), empty(qr), empty(kvr), empty(kvr)
+    ctx.gemm_qkv(wq, wk, wv, normed, q, k, v, inner, qr, kvr, tokens)
+    ctx.rmsnorm_gemm_qkv(nw, eps, wq, wk, wv, x, q2, k2, v2, inner, qr, kvr, tokens)
+    act, act2 = empty(inter), empty(inter)
+    ctx.gemm_swiglu(wg, wu, normed, act, inner, inter, tokens)
+    ctx.rmsnorm_gemm_swiglu(nw, eps, wg, wu, x, act2, inner, inter, tokens)
+    torch.cuda.synchronize()
+    assert torch.equal(plain, plain2)
+    assert torch.equal(q, q2) and torch.equal(k, k2) and torch.equal(v, v2)
+    assert torch.equal(q, plain)
+    assert torch.equal(act, act2)
+    # the normalised rows themselves are the oracle's
+    want = oracle.rmsnorm_gpu(host_bits(x), host_bits(nw), tokens, inner, eps)
+    assert np.array_equal(host_bits(normed), want)
+
+
+def test_rmsnorm_fused_rejects_bad_arguments(ctx):
+    x = torch.zeros(4 * 64, dtype=torch.int16, device="cuda")
+    w = torch.zeros(32 * 64, dtype=torch.int16, device="cuda")
+    out = torch.empty(4 * 32, dtype=torch.int16, device="cuda")
+    nw = torch.zeros(64, dtype=torch.int16, device="cuda")
+    with pytest.raises(mslim_attn.MslimAttnError, match="code=-1"):
+        ctx.rmsnorm_gemm_bf16(None, 1e-5, w, x, out, 64, 32, 4)
+    with pytest.raises(mslim_attn.MslimAttnError, match="code=-1"):
+        ctx.rmsnorm_gemm_bf16(nw, float("nan"), w, x, out, 64, 32, 4)
+    with pytest.raises(mslim_attn.MslimAttnError, match="code=-1"):
+        ctx.rmsnorm_gemm_swiglu(nw, -1.0, w, w, x, out, 64, 32, 4)

@@ -418,7 +418,7 @@ def test_runner_failed_step_poisons_until_reset(tiny_model):
     toks = [model.prefill_only(s, p) for s, p in enumerate(prompts)]
     assert toks == clean
     model.inject_failure(model.INJECT_ARGUMENT_ERROR, 1)
-    with pytest.raises(MslimAttnError, match="input norm failed.*invalid RMSNorm arguments"):
+    with pytest.raises(MslimAttnError, match="input norm \\+ QKV projection failed.*invalid RMSNorm"):
         model.forward_batch(toks)
     assert model.poisoned(0) and model.poisoned(1) and not model.poisoned(2)
     with pytest.raises(MslimAttnError, match="poisoned"):
@@ -440,7 +440,7 @@ def test_runner_failed_step_poisons_until_reset(tiny_model):
 
     # a failure inside a prompt poisons that slot only
     model.inject_failure(model.INJECT_ARGUMENT_ERROR, 0)
-    with pytest.raises(MslimAttnError, match="invalid RMSNorm arguments"):
+    with pytest.raises(MslimAttnError, match="invalid RMSNorm \\+ BF16 matrix arguments"):
         model.prefill_only(2, prompts[0])
     assert model.poisoned(2) and not model.poisoned(0)
     model.reset(2)

@@ -13,6 +13,7 @@
 #include <mutex>
 #include <new>
 #include <string>
+#include <vector>
 
 #include "kernels.hpp"
 #include "sha256.hpp"
@@ -42,6 +43,8 @@ struct Context {
     uint16_t *swiglu_table = nullptr;  // SwiGLU activation of every BF16 gate value
     void *proj_partial = nullptr;      // fp32 partials of split projections
     size_t proj_partial_bytes = 0;
+    void *norm_rows = nullptr;         // normalised rows of the RMSNorm + product entries
+    size_t norm_rows_bytes = 0;
     size_t workspace_bytes = 0;
     int *counters = nullptr;        // decode split counters, zero between launches
     size_t counter_bytes = 0;
@@ -71,6 +74,7 @@ struct Context {
         if (workspace) (void)hipFree(workspace);
         if (swiglu_table) (void)hipFree(swiglu_table);
         if (proj_partial) (void)hipFree(proj_partial);
+        if (norm_rows) (void)hipFree(norm_rows);
         if (prefill_partial) (void)hipFree(prefill_partial);
         if (prefill_counters) (void)hipFree(prefill_counters);
         if (counters) (void)hipFree(counters);
@@ -318,6 +322,28 @@ int mslim_attn_get_device_info(void *ctx, mslim_attn_device_info *out) {
     out->max_clock_mhz = (uint32_t)(prop.clockRate / 1000);
     out->memory_clock_mhz = (uint32_t)(prop.memoryClockRate / 1000);
     out->memory_bus_bits = (uint32_t)prop.memoryBusWidth;
+    return 0;
+}
+
+int mslim_attn_check_bf16_encoding(void *ctx, uint64_t *mismatches) {
+    g_error.clear();
+    if (!ctx || !mismatches) return fail("encoding check needs a context and an output");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    uint32_t *counts = nullptr;
+    const size_t bytes = (size_t)mslim::kEncodingCheckThreads * sizeof(uint32_t);
+    if (int rc = check_hip(hipMalloc(reinterpret_cast<void **>(&counts), bytes), "hipMalloc encoding check"))
+        return rc;
+    std::vector<uint32_t> host(mslim::kEncodingCheckThreads);
+    int rc = check_hip(mslim::launch_bf16_encoding_check(counts, c.stream), "encoding check launch");
+    if (!rc) rc = check_hip(hipMemcpyAsync(host.data(), counts, bytes, hipMemcpyDeviceToHost, c.stream), "D2H");
+    if (!rc) rc = check_hip(hipStreamSynchronize(c.stream), "hipStreamSynchronize");
+    const int free_rc = check_hip(hipFree(counts), "hipFree encoding check");
+    if (rc) return rc;
+    if (free_rc) return free_rc;
+    uint64_t total = 0;
+    for (uint32_t v : host) total += v;
+    *mismatches = total;
     return 0;
 }
 
@@ -1184,7 +1210,7 @@ int mslim_attn_gemm_swiglu(void *ctx, const void *gate_weight, const void *up_we
         return check_hip(mslim::launch_skinny_swiglu(static_cast<const uint16_t *>(gate_weight),
                                                      static_cast<const uint16_t *>(up_weight),
                                                      static_cast<uint16_t *>(output), rows, x, inner, tokens,
-                                                     c.stream),
+                                                     c.swiglu_table, c.stream),
                          "decode projection launch")
                    ? 404
                    : 0;
@@ -1229,6 +1255,127 @@ int mslim_attn_gemm_qkv(void *ctx, const void *q_weight, const void *k_weight, c
     float *partial = nullptr;
     if (int rc = proj_partials(c, inner, (int64_t)q_rows + 2 * (int64_t)kv_rows, tokens, &partial)) return rc;
     return check_hip(mslim::launch_proj(m, 3, static_cast<const uint16_t *>(input), inner, tokens, partial, c.stream),
+                     "projection launch")
+               ? 404
+               : 0;
+}
+
+// ---- RMSNorm + projections ----------------------------------------------
+
+// The rows normalised into a context buffer (shapes the projection kernels do
+// not normalise themselves): mslim_attn_rmsnorm's kernels.
+static int normalise_rows(Context &c, const void *input, const void *norm_weight, float epsilon, int inner,
+                          int tokens, const void **rows) {
+    if (grow_device(c, &c.norm_rows, &c.norm_rows_bytes, (size_t)inner * tokens * 2, "hipMalloc normalised rows"))
+        return 400;
+    if (int rc = check_hip(mslim::launch_rmsnorm(static_cast<const uint16_t *>(input),
+                                                 static_cast<const uint16_t *>(norm_weight),
+                                                 static_cast<uint16_t *>(c.norm_rows), tokens, inner, epsilon,
+                                                 c.stream),
+                           "RMSNorm launch"))
+        return rc;
+    *rows = c.norm_rows;
+    return 0;
+}
+
+static bool norm_args_ok(const void *norm_weight, float epsilon) {
+    return norm_weight && std::isfinite(epsilon) && epsilon >= 0.0f;
+}
+
+int mslim_attn_rmsnorm_gemm_bf16(void *ctx, const void *norm_weight, float epsilon, const void *weight,
+                                 const void *input, void *output, int inner, int rows, int tokens) {
+    g_error.clear();
+    if (!gemm_args_ok(ctx, weight, input, output, inner, rows, tokens) || !norm_args_ok(norm_weight, epsilon))
+        return fail("invalid RMSNorm + BF16 matrix arguments");
+    if (output == input || output == weight || output == norm_weight) return fail("GEMM output must not alias its inputs");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    if (mslim::skinny_supported(inner, tokens, input, weight) &&
+        mslim::skinny_norm_supported(inner, tokens, norm_weight)) {
+        const mslim::SkinnyMatrix m{static_cast<const uint16_t *>(weight), static_cast<uint16_t *>(output), rows};
+        return check_hip(mslim::launch_skinny_gemm(&m, 1, static_cast<const uint16_t *>(input), inner, tokens,
+                                                   c.stream, static_cast<const uint16_t *>(norm_weight), epsilon),
+                         "decode projection launch")
+                   ? 404
+                   : 0;
+    }
+    const void *x = nullptr;
+    if (int rc = normalise_rows(c, input, norm_weight, epsilon, inner, tokens, &x)) return rc;
+    return project(c, weight, x, output, inner, rows, tokens);
+}
+
+int mslim_attn_rmsnorm_gemm_qkv(void *ctx, const void *norm_weight, float epsilon, const void *q_weight,
+                                const void *k_weight, const void *v_weight, const void *input, void *q_out,
+                                void *k_out, void *v_out, int inner, int q_rows, int kv_rows, int tokens) {
+    g_error.clear();
+    if (!gemm_args_ok(ctx, q_weight, input, q_out, inner, q_rows, tokens) ||
+        !gemm_args_ok(ctx, k_weight, input, k_out, inner, kv_rows, tokens) ||
+        !gemm_args_ok(ctx, v_weight, input, v_out, inner, kv_rows, tokens) || !norm_args_ok(norm_weight, epsilon))
+        return fail("invalid RMSNorm + BF16 matrix arguments");
+    if (q_out == input || k_out == input || v_out == input) return fail("GEMM output must not alias its inputs");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    const mslim::SkinnyMatrix m[3] = {
+        {static_cast<const uint16_t *>(q_weight), static_cast<uint16_t *>(q_out), q_rows},
+        {static_cast<const uint16_t *>(k_weight), static_cast<uint16_t *>(k_out), kv_rows},
+        {static_cast<const uint16_t *>(v_weight), static_cast<uint16_t *>(v_out), kv_rows}};
+    if (mslim::skinny_supported(inner, tokens, input, q_weight, k_weight, v_weight) &&
+        mslim::skinny_norm_supported(inner, tokens, norm_weight))
+        return check_hip(mslim::launch_skinny_gemm(m, 3, static_cast<const uint16_t *>(input), inner, tokens,
+                                                   c.stream, static_cast<const uint16_t *>(norm_weight), epsilon),
+                         "decode projection launch")
+                   ? 404
+                   : 0;
+    const void *x = nullptr;
+    if (int rc = normalise_rows(c, input, norm_weight, epsilon, inner, tokens, &x)) return rc;
+    if (mslim::skinny_supported(inner, tokens, x, q_weight, k_weight, v_weight))
+        return check_hip(mslim::launch_skinny_gemm(m, 3, static_cast<const uint16_t *>(x), inner, tokens, c.stream),
+                         "decode projection launch")
+                   ? 404
+                   : 0;
+    float *partial = nullptr;
+    if (int rc = proj_partials(c, inner, (int64_t)q_rows + 2 * (int64_t)kv_rows, tokens, &partial)) return rc;
+    return check_hip(mslim::launch_proj(m, 3, static_cast<const uint16_t *>(x), inner, tokens, partial, c.stream),
+                     "projection launch")
+               ? 404
+               : 0;
+}
+
+int mslim_attn_rmsnorm_gemm_swiglu(void *ctx, const void *norm_weight, float epsilon, const void *gate_weight,
+                                   const void *up_weight, const void *input, void *output, int inner, int rows,
+                                   int tokens) {
+    g_error.clear();
+    if (!gemm_args_ok(ctx, gate_weight, input, output, inner, rows, tokens) || !up_weight ||
+        !norm_args_ok(norm_weight, epsilon))
+        return fail("invalid RMSNorm + BF16 matrix arguments");
+    if (output == input || output == gate_weight || output == up_weight)
+        return fail("GEMM output must not alias its inputs");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    const auto *gw = static_cast<const uint16_t *>(gate_weight), *uw = static_cast<const uint16_t *>(up_weight);
+    if (mslim::skinny_supported(inner, tokens, input, gate_weight, up_weight) &&
+        mslim::skinny_norm_supported(inner, tokens, norm_weight))
+        return check_hip(mslim::launch_skinny_swiglu(gw, uw, static_cast<uint16_t *>(output), rows,
+                                                     static_cast<const uint16_t *>(input), inner, tokens,
+                                                     c.swiglu_table, c.stream,
+                                                     static_cast<const uint16_t *>(norm_weight), epsilon),
+                         "decode projection launch")
+                   ? 404
+                   : 0;
+    const void *x = nullptr;
+    if (int rc = normalise_rows(c, input, norm_weight, epsilon, inner, tokens, &x)) return rc;
+    if (mslim::skinny_supported(inner, tokens, x, gate_weight, up_weight))
+        return check_hip(mslim::launch_skinny_swiglu(gw, uw, static_cast<uint16_t *>(output), rows,
+                                                     static_cast<const uint16_t *>(x), inner, tokens,
+                                                     c.swiglu_table, c.stream),
+                         "decode projection launch")
+                   ? 404
+                   : 0;
+    float *partial = nullptr;
+    if (int rc = proj_partials(c, inner, 2 * (int64_t)rows, tokens, &partial)) return rc;
+    return check_hip(mslim::launch_proj_swiglu(gw, uw, static_cast<uint16_t *>(output), rows,
+                                               static_cast<const uint16_t *>(x), inner, tokens, c.swiglu_table,
+                                               partial, c.stream),
                      "projection launch")
                ? 404
                : 0;

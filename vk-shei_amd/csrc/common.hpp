@@ -29,13 +29,22 @@ __device__ __forceinline__ float read_bf16(uint16_t bits) { return __uint_as_flo
 
 // BF16 encode with the reference's exact rule (gpu_llm.cl:10-21): NaN keeps
 // sign and upper payload with the quiet bit forced; everything else rounds to
-// nearest even.  Used for every value a kernel writes out.
-__device__ __forceinline__ uint16_t write_bf16(float value) {
+// nearest even.  write_bf16_rule states the rule in integer steps;
+// write_bf16, used for every value a kernel writes out, is gfx950's
+// conversion instruction (a scalar cast, v_cvt_pk_bf16_f32 with the value in
+// the low half), one instruction instead of seven.  The two agree on every
+// one of the 2^32 f32 encodings, NaNs and subnormals included:
+// mslim_attn_check_bf16_encoding compares them over all of them on the
+// device.  (The two-value form through __builtin_convertvector gave wrong
+// high halves in the same comparison and is not used.)
+__device__ __forceinline__ uint16_t write_bf16_rule(float value) {
     uint32_t bits = __float_as_uint(value);
     if ((bits & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((bits >> 16) | 0x0040u);
     bits += 0x7fffu + ((bits >> 16) & 1u);
     return (uint16_t)(bits >> 16);
 }
+
+__device__ __forceinline__ uint16_t write_bf16(float value) { return __builtin_bit_cast(uint16_t, (__bf16)value); }
 
 __device__ __forceinline__ float round_bf16(float value) { return read_bf16(write_bf16(value)); }
 

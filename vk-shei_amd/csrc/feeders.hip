@@ -503,6 +503,35 @@ hipError_t launch_swiglu_table(uint16_t *table, hipStream_t stream) {
     return hipGetLastError();
 }
 
+// write_bf16 against write_bf16_rule over every f32 encoding: thread t
+// checks encodings t, t + threads, ... and stores its mismatch count.  Each
+// step converts two values into one packed pair as kernels that write BF16
+// vectors do (the instruction's two-source form, which the compiler uses for
+// such pairs): encoding b in the low half and the bijection b * 0x9e3779b1
+// (odd, so every encoding appears once) in the high half.
+__global__ __launch_bounds__(256) void bf16_encoding_check_kernel(uint32_t *mismatches) {
+    const uint32_t tid = blockIdx.x * 256u + threadIdx.x;
+    const uint32_t threads = gridDim.x * 256u;
+    uint32_t bad = 0;
+    for (uint64_t b = tid; b < (1ull << 32); b += threads) {
+        const float lo = __uint_as_float((uint32_t)b);
+        const float hi = __uint_as_float((uint32_t)b * 0x9e3779b1u);
+        bf16x2_t pair;
+        pair[0] = __builtin_bit_cast(__bf16, write_bf16(lo));
+        pair[1] = __builtin_bit_cast(__bf16, write_bf16(hi));
+        const uint32_t got = __builtin_bit_cast(uint32_t, pair);
+        bad += (got & 0xffffu) != write_bf16_rule(lo);
+        bad += (got >> 16) != write_bf16_rule(hi);
+    }
+    mismatches[tid] = bad;
+}
+
+hipError_t launch_bf16_encoding_check(uint32_t *mismatches, hipStream_t stream) {
+    hipLaunchKernelGGL(bf16_encoding_check_kernel, dim3(kEncodingCheckThreads / 256), dim3(256), 0, stream,
+                       mismatches);
+    return hipGetLastError();
+}
+
 hipError_t launch_swiglu(const uint16_t *gate, const uint16_t *up, uint16_t *out, size_t n,
                          hipStream_t stream) {
     const unsigned blocks = (unsigned)((n + 255) / 256);

@@ -122,6 +122,10 @@ hipError_t launch_rope_append(const RopeAppendArgs &a, hipStream_t stream);
 // Table of swiglu_act_bf16 for every BF16 gate value (128 KiB).
 constexpr int kSwigluTableEntries = 65536;
 hipError_t launch_swiglu_table(uint16_t *table, hipStream_t stream);
+// Mismatch counts of write_bf16 against write_bf16_rule over all 2^32 f32
+// encodings, one uint32 per thread (kEncodingCheckThreads of them).
+constexpr int kEncodingCheckThreads = 1 << 20;
+hipError_t launch_bf16_encoding_check(uint32_t *mismatches, hipStream_t stream);
 hipError_t launch_swiglu(const uint16_t *gate, const uint16_t *up, uint16_t *out, size_t n,
                          hipStream_t stream);
 hipError_t launch_add(const uint16_t *a, const uint16_t *b, uint16_t *out, size_t n, hipStream_t stream);
@@ -178,12 +182,18 @@ struct SkinnyMatrix {
 };
 bool skinny_supported(int inner, int tokens, const void *x, const void *w0, const void *w1 = nullptr,
                       const void *w2 = nullptr);
+// The plain and SwiGLU forms can apply the RMSNorm (weights norm_w, eps) to x
+// first when skinny_norm_supported: bit-identical to launch_rmsnorm followed
+// by the product.
+bool skinny_norm_supported(int inner, int tokens, const void *norm_w);
 hipError_t launch_skinny_gemm(const SkinnyMatrix *m, int count, const uint16_t *x, int inner, int tokens,
-                              hipStream_t stream);
+                              hipStream_t stream, const uint16_t *norm_w = nullptr, float eps = 0.0f);
 hipError_t launch_skinny_gemm_add(const SkinnyMatrix &m, const uint16_t *resid, const uint16_t *x, int inner,
                                   int tokens, hipStream_t stream);
+// act_table: launch_swiglu_table's table (device, 128 KiB).
 hipError_t launch_skinny_swiglu(const uint16_t *w_gate, const uint16_t *w_up, uint16_t *out, int rows,
-                                const uint16_t *x, int inner, int tokens, hipStream_t stream);
+                                const uint16_t *x, int inner, int tokens, const uint16_t *act_table,
+                                hipStream_t stream, const uint16_t *norm_w = nullptr, float eps = 0.0f);
 
 // The same products for any number of token rows (csrc/proj.hip): the tiled
 // MFMA kernel when inner is a multiple of 64 and x and the weights are

@@ -6,17 +6,31 @@
 // 366-378) stream every weight once per step, so the work is HBM-bound on the
 // weights; the token vectors are a few hundred KiB and stay in L2.
 //
-// A workgroup owns 16 output rows and all tokens.  Each wavefront takes every
-// WAVES-th block of 32*kUnroll inputs and runs v_mfma_f32_16x16x32_bf16 with
-// the weights as A (16 rows x 32 inputs, one 16-byte load per lane) and the
-// tokens as B (32 inputs x 16 tokens, padded with zeros), kUnroll loads in
-// flight per operand.  When the token rows fit (<= 8 tokens of <= 4096
-// inputs) the workgroup stages them in LDS first: the per-k-step B loads cost
-// a quarter of the streaming rate when they go to L2.  The WAVES partial 16x16 tiles are summed in LDS in
-// fixed wave order, so results do not depend on timing.  Epilogues:
+// Workgroups of 8 wavefronts work through 16-row tiles of the output (a grid
+// of a few workgroups per CU, each taking every grid-th tile).  A tile's sum
+// over the inner dimension is cut into 16 partial sums: partial j folds the
+// 128-input blocks j, j + 16, ... in order, four v_mfma_f32_16x16x32_bf16
+// steps per block with the weights as A (16 rows x 32 inputs, one 16-byte
+// load per lane) and the tokens as B (32 inputs x 16 tokens, padded with
+// zeros); wavefront w keeps partials w and w + 8, and the 16 partial 16x16
+// tiles are added in LDS in order 0 .. 15.  That order depends on the inner
+// dimension only, so a product gives the same bits in every entry point,
+// fused form and launch shape.  Each wavefront keeps a ring of two (or
+// four) load batches in flight, and the next tile's first batches go out
+// before a tile's partials are summed.
+//
+// When the token rows fit (<= 8 tokens of <= 4096 inputs) the workgroup
+// stages them in LDS once for all its tiles, by DMA while its first weight
+// batches are in flight (the per-k-step B loads cost a quarter of the
+// streaming rate when they go to L2), and can apply the
+// RMSNorm that precedes the product there: the reference's llm_rmsnorm
+// (gpu_llm.cl:72-98) with its 128-lane strided sums, 64..1 tree and BF16
+// stages, bit-identical to mslim_attn_rmsnorm followed by the product.
+// Epilogues:
 //   plain   out = BF16(acc)
 //   add     out = BF16(resid + BF16(acc))           (llm_add after the product)
-//   swiglu  out = SwiGLU(BF16(acc_gate), BF16(acc_up))   (llm_swiglu after both)
+//   swiglu  out = SwiGLU(BF16(acc_gate), BF16(acc_up))   (llm_swiglu after both;
+//           its first stage read from the context's table of every gate value)
 // which equal the unfused product followed by the elementwise kernel bit for
 // bit.  Up to three matrices with separate outputs share one launch (Q, K, V).
 #include "common.hpp"
@@ -29,12 +43,16 @@ namespace mslim {
 namespace {
 
 constexpr int kTileRows = 16;
-// MFMA steps per load batch: kUnroll 16-byte weight loads in flight per lane
-// before the first MFMA of the batch.  Unroll 8, a two-deep register ring of
-// batches, a persistent grid and non-temporal weight loads each measured no
-// faster (non-temporal loads cost 10-30%).
-constexpr int kUnroll = 4;
+// The k range of a tile is cut into blocks of kBlock inputs; partial sum j
+// (of kSlots) folds blocks j, j + kSlots, ... in ascending order, four MFMA
+// steps per block, and the tile's result is the partials added in order
+// 0 .. kSlots-1.  That order depends on the inner dimension only, so every
+// launch shape and entry point gives the same bits for the same product.
+constexpr int kSlots = 16;
+constexpr int kUnroll = 4;   // MFMA steps (16-byte weight loads per lane) per block
+constexpr int kBlock = 32 * kUnroll;
 constexpr int kMaxSegments = 3;
+constexpr int kCus = 256;
 
 enum Epilogue { kPlain = 0, kAdd = 1, kSwiglu = 2 };
 
@@ -48,156 +66,355 @@ struct SkinnyArgs {
     const uint16_t *x;       // [tokens][inner]
     const uint16_t *w_up;    // swiglu: up weights beside w[0] (gate)
     const uint16_t *resid;   // add: [tokens][rows[0]], may equal out[0]
+    const uint16_t *norm_w;  // staged rows only: RMSNorm weights [inner], or null
+    const uint16_t *act_table;  // swiglu: swiglu_act_bf16 of every BF16 gate value
+    float eps;
     int inner, tokens;
 };
 
 __device__ __forceinline__ bf16x8_t load8(const uint16_t *p) { return *reinterpret_cast<const bf16x8_t *>(p); }
 
-
 // Token vectors staged in LDS (XLDS): up to kStageTokens rows of up to
-// kStageInner inputs, each row padded by 16 bytes so that the 16 token rows
-// of a B fragment read fall in different banks.
+// kStageInner inputs, 8 KiB per row, with 16-byte chunk c of row r stored at
+// chunk c ^ (r & 7), so that the eight rows of a B fragment read (same c)
+// fall in different banks.
 constexpr int kStageTokens = 8;
 constexpr int kStageInner = 4096;
-constexpr int kStageStride = kStageInner + 8;
+constexpr int kStageBytes = kStageTokens * kStageInner * 2;
+constexpr int kPartialBytes = kSlots * 64 * 16;  // one matrix's partial tiles
+// RMSNorm weights staged in the partial space, after the norm scratch.
+constexpr uint32_t kNormWeightOffset = 4096;
+static_assert(kNormWeightOffset + kStageInner * 2 <= kPartialBytes, "RMSNorm weights fit the partial space");
 
-template <int WAVES, int EPI, bool XLDS>
-__global__ __launch_bounds__(WAVES * 64) void skinny_kernel(SkinnyArgs a) {
-    // One LDS region holds the staged token rows during the k loop and the
-    // wavefronts' partial tiles after it, so two workgroups fit on a CU.
-    constexpr int kPartialBytes = (EPI == kSwiglu ? 2 : 1) * WAVES * 64 * 16;
-    constexpr int kStageBytes = XLDS ? kStageTokens * kStageStride * 2 : 0;
-    __shared__ __align__(16) unsigned char lds[kPartialBytes > kStageBytes ? kPartialBytes : kStageBytes];
-    auto partial = reinterpret_cast<floatx4_t(*)[WAVES][64]>(lds);
+__device__ __forceinline__ int stage_index(int row, int col) {
+    return row * kStageInner + ((((col >> 3) ^ row) & 7) | ((col >> 3) & ~7)) * 8 + (col & 7);
+}
+
+template <int EPI, bool XLDS, bool NORM, int WAVES, int DEPTH>
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(4))) void skinny_kernel(SkinnyArgs a) {
+    // Partial slots per wavefront, MFMA steps per load batch (half a block
+    // when two matrices stream, to fit two batches in flight in the register
+    // budget) and batches per block.
+    constexpr int NS = kSlots / WAVES;
+    constexpr int UB = EPI == kSwiglu ? kUnroll / 2 : kUnroll;
+    constexpr int PB = kUnroll / UB;
+    // Batches per loop iteration: a multiple of the ring depth and of the
+    // slot cycle (powers of two), so that every batch's ring entry and
+    // accumulator are known at compile time.
+    constexpr int PERIOD = PB * NS > DEPTH ? PB * NS : DEPTH;
+    constexpr int kThreads = WAVES * 64;
+    // LDS: the staged rows, then one matrix's partial tiles (SwiGLU sums
+    // gate and up one after the other in the same space); the RMSNorm
+    // scratch lives in the partial space before the first tile ends.
+    __shared__ __align__(16) unsigned char lds[(XLDS ? kStageBytes : 0) + kPartialBytes];
     uint16_t *xs = reinterpret_cast<uint16_t *>(lds);
+    auto partial = reinterpret_cast<floatx4_t(*)[64]>(lds + (XLDS ? kStageBytes : 0));
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int tile = blockIdx.x;  // one workgroup per 16-row tile
-    if (XLDS) {
-        // The B operand (token rows) is the same for every row tile: read it
-        // once per workgroup with 16-byte loads instead of once per k-step
-        // per wavefront.
-        // All of a thread's loads go out before its first LDS write (a
-        // load-wait-write loop costs one L2 round trip per 16 bytes); past
-        // the last chunk the index is clamped in bounds and not written.
-        constexpr int kPerThread = kStageTokens * kStageInner / 8 / (WAVES * 64);
-        const int chunks = a.inner / 8;
-        const int total = a.tokens * chunks;
-        bf16x8_t v[kPerThread];
-#pragma unroll
-        for (int k = 0; k < kPerThread; ++k) {
-            const int i = min((int)threadIdx.x + k * WAVES * 64, total - 1);
-            v[k] = load8(a.x + (int64_t)(i / chunks) * a.inner + (i % chunks) * 8);
-        }
-        __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the writes
-#pragma unroll
-        for (int k = 0; k < kPerThread; ++k) {
-            const int i = (int)threadIdx.x + k * WAVES * 64;
-            if (i < total) *reinterpret_cast<bf16x8_t *>(xs + (i / chunks) * kStageStride + (i % chunks) * 8) = v[k];
-        }
-        __syncthreads();
-    }
-    int seg = 0;
-    if (a.segments > 1 && tile >= a.first_tile[1]) seg = 1;
-    if (a.segments > 2 && tile >= a.first_tile[2]) seg = 2;
-    const int rows = a.rows[seg];
-    const int r0 = (tile - a.first_tile[seg]) * kTileRows;
-    // A operand: lane l holds row r0 + l%16, inputs 8*(l/16) .. +7 of each
-    // 32-input block; B operand: token l%16, the same inputs.  Rows past the
-    // end re-read the last row and are not written.
-    const int row = min(r0 + (lane & 15), rows - 1);
     const int kq = (lane >> 4) * 8;
     const int tok = lane & 15;
     const bool live = tok < a.tokens;
-    const uint16_t *wp = a.w[seg] + (int64_t)row * a.inner + kq;
-    const uint16_t *up = EPI == kSwiglu ? a.w_up + (int64_t)row * a.inner + kq : nullptr;
-    const uint16_t *xp = a.x + (int64_t)(live ? tok : 0) * a.inner + kq;
-    const uint16_t *xl = xs + (live ? tok : 0) * kStageStride + kq;
-    floatx4_t acc = {0.0f, 0.0f, 0.0f, 0.0f}, acc_up = {0.0f, 0.0f, 0.0f, 0.0f};
     const bf16x8_t zero = {};
-    // inner % 32 == 0: a block that starts inside the row ends inside it.
-    struct Batch {
-        bf16x8_t wa[kUnroll], wu[kUnroll], xb[kUnroll];
+
+    // The tile's weights: lane l holds row r0 + l % 16, inputs 8 (l / 16) ..
+    // +7 of each 32-input step; rows past the end re-read the last row and
+    // are not written.
+    struct Tile {
+        const uint16_t *wp, *up;
+        uint16_t *out;
+        int rows, r0;
     };
-    auto load_batch = [&](Batch &bt, int k0) {
+    auto tile_of = [&](int tile) __attribute__((always_inline)) {
+        int seg = 0;
+        if (a.segments > 1 && tile >= a.first_tile[1]) seg = 1;
+        if (a.segments > 2 && tile >= a.first_tile[2]) seg = 2;
+        Tile t;
+        t.rows = a.rows[seg];
+        t.r0 = (tile - a.first_tile[seg]) * kTileRows;
+        const int row = min(t.r0 + (lane & 15), t.rows - 1);
+        t.wp = a.w[seg] + (int64_t)row * a.inner + kq;
+        t.up = EPI == kSwiglu ? a.w_up + (int64_t)row * a.inner + kq : nullptr;
+        t.out = a.out[seg];
+        return t;
+    };
+    struct Batch {
+        bf16x8_t wa[UB], wu[UB], xb[UB];
+    };
+    const uint16_t *xp = a.x + (int64_t)(live ? tok : 0) * a.inner + kq;
+    // inner % 32 == 0: a step that starts inside the row ends inside it.
+    auto load_batch = [&](Batch &bt, const Tile &t, int k0) __attribute__((always_inline)) {
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
+        for (int u = 0; u < UB; ++u) {
             const int k = k0 + u * 32;
             const bool in = k < a.inner;
-            bt.wa[u] = in ? load8(wp + k) : zero;
-            if (EPI == kSwiglu) bt.wu[u] = in ? load8(up + k) : zero;
-            if (XLDS) bt.xb[u] = in && live ? *reinterpret_cast<const bf16x8_t *>(xl + k) : zero;
-            else bt.xb[u] = in && live ? load8(xp + k) : zero;
+            bt.wa[u] = in ? load8(t.wp + k) : zero;
+            if (EPI == kSwiglu) bt.wu[u] = in ? load8(t.up + k) : zero;
+            if (!XLDS) bt.xb[u] = in && live ? load8(xp + k) : zero;
         }
     };
-    auto use_batch = [&](const Batch &bt) {
+    // The same with every load issued (addresses clamped into the row,
+    // values past it replaced by zeros): a fixed count of vector memory
+    // instructions, kRingLoads for a whole ring.
+    auto load_batch_all = [&](Batch &bt, const Tile &t, int k0) __attribute__((always_inline)) {
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bt.wa[u], bt.xb[u], acc, 0, 0, 0);
-            if (EPI == kSwiglu) acc_up = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bt.wu[u], bt.xb[u], acc_up, 0, 0, 0);
+        for (int u = 0; u < UB; ++u) {
+            const int k = k0 + u * 32;
+            const int kc = min(k, a.inner - 32);
+            const bf16x8_t w = load8(t.wp + kc);
+            bt.wa[u] = k < a.inner ? w : zero;
+            if (EPI == kSwiglu) {
+                const bf16x8_t wu = load8(t.up + kc);
+                bt.wu[u] = k < a.inner ? wu : zero;
+            }
         }
     };
-    const int step = WAVES * 32 * kUnroll;
-    for (int k0 = wave * 32 * kUnroll; k0 < a.inner; k0 += step) {
-        Batch bt;
-        load_batch(bt, k0);
-        use_batch(bt);
-    }
-    if (XLDS) __syncthreads();  // every wavefront is done with the staged rows
-    partial[0][wave][lane] = acc;
-    if (EPI == kSwiglu) partial[EPI == kSwiglu ? 1 : 0][wave][lane] = acc_up;
-    __syncthreads();
-    if (wave != 0) return;
-    floatx4_t sum = partial[0][0][lane], sum_up = partial[EPI == kSwiglu ? 1 : 0][0][lane];
-    for (int w = 1; w < WAVES; ++w) {
-        sum += partial[0][w][lane];
-        if (EPI == kSwiglu) sum_up += partial[EPI == kSwiglu ? 1 : 0][w][lane];
-    }
-    // D layout: lane l holds rows 4*(l/16) + j, token l%16.
-    if (!live) return;
-    uint16_t *out = a.out[seg] + (int64_t)tok * rows;
+    constexpr int kRingLoads = DEPTH * UB * (EPI == kSwiglu ? 2 : 1);
+    floatx4_t acc[NS], acc_up[NS];
+    auto use_batch = [&](const Batch &bt, int k0, int m) __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int r = r0 + 4 * (lane >> 4) + j;
-        if (r >= rows) continue;
-        const uint16_t y = write_bf16(sum[j]);
-        if (EPI == kPlain) {
-            out[r] = y;
-        } else if (EPI == kAdd) {
-            out[r] = write_bf16(__fadd_rn(read_bf16(a.resid[(int64_t)tok * rows + r]), read_bf16(y)));
-        } else {
-            out[r] = swiglu_bf16(y, write_bf16(sum_up[j]));
+        for (int u = 0; u < UB; ++u) {
+            const int k = k0 + u * 32;
+            bf16x8_t xb;
+            if (XLDS) xb = k < a.inner && live ? *reinterpret_cast<const bf16x8_t *>(xs + stage_index(tok, k + kq)) : zero;
+            else xb = bt.xb[u];
+            acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bt.wa[u], xb, acc[m], 0, 0, 0);
+            if (EPI == kSwiglu) acc_up[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bt.wu[u], xb, acc_up[m], 0, 0, 0);
         }
+    };
+    // Batch i of a wavefront: block wave + (i / PB) * WAVES, part i % PB.
+    auto k_of = [&](int kb0, int u) __attribute__((always_inline)) {
+        return kb0 + (u / PB) * WAVES * kBlock + (u % PB) * 32 * UB;
+    };
+    const int kfirst = wave * kBlock;
+
+    int tile = blockIdx.x;
+    Batch ring[DEPTH];
+    Tile t = tile_of(tile);
+    if constexpr (!XLDS) {
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d)
+            if (k_of(kfirst, d) < a.inner) load_batch(ring[d], t, k_of(kfirst, d));
+    } else {
+        // The B operand (token rows) is the same for every row tile: it goes
+        // to LDS once per workgroup, by DMA (global_load_lds_dwordx4, no
+        // registers held), ahead of the first DEPTH weight batches, which
+        // then stay in flight through the staging and the RMSNorm: the wait
+        // below leaves exactly the kRingLoads weight loads outstanding.
+        // Wave instruction j fills LDS chunks 64 j .. 64 j + 63, i.e. row
+        // j / 8; lane l takes the row's logical chunk (64 (j % 8) + l) ^
+        // (row & 7).
+        const int chunks = a.inner / 8;
+        const uint32_t xs_lds = lds_offset(xs);
+        const int uwave = __builtin_amdgcn_readfirstlane(wave);
+        for (int j = uwave; j < a.tokens * (kStageInner / 8 / 64); j += WAVES) {
+            const int r = j >> 3;
+            const int c = ((j & 7) * 64 + lane) ^ (r & 7);
+            if (c < chunks) dma16_async(a.x, (uint32_t)(r * a.inner + c * 8) * 2u, xs_lds + (uint32_t)j * 1024u);
+        }
+        if constexpr (NORM) {
+            // the RMSNorm weights into the partial space, after its scratch
+            for (int j = uwave; j * 64 < chunks; j += WAVES)
+                if (j * 64 + lane < chunks)
+                    dma16_async(a.norm_w, (uint32_t)(j * 64 + lane) * 16u,
+                                lds_offset(partial) + kNormWeightOffset + (uint32_t)j * 1024u);
+        }
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) load_batch_all(ring[d], t, k_of(kfirst, d));
+        // The DMA is not tracked by the compiler: wait for it by count.
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(kRingLoads));
+        __syncthreads();
+        if constexpr (NORM) {
+            // RMSNorm of each staged row (gpu_llm.cl:72-98) as
+            // mslim_attn_rmsnorm computes it: 128 lanes per row, lane g sums
+            // elements g, g + 128, ... in order; the tree adds pairs
+            // (g, g + 64) through LDS, then 32 .. 1 by shuffles.  A group of
+            // 128 lanes takes rows grp, grp + kGroups, ...
+            constexpr int kGroups = kThreads / 128;
+            constexpr int kRowsPerGroup = kStageTokens / kGroups;
+            float *norm_part = reinterpret_cast<float *>(partial);    // [kStageTokens][64]
+            float *norm_factor = norm_part + kStageTokens * 64;      // [kStageTokens]
+            const uint16_t *norm_w = reinterpret_cast<const uint16_t *>(
+                reinterpret_cast<const unsigned char *>(partial) + kNormWeightOffset);
+            const int grp = threadIdx.x >> 7, g = threadIdx.x & 127;
+            float s[kRowsPerGroup];
+#pragma unroll
+            for (int rr = 0; rr < kRowsPerGroup; ++rr) {
+                const int r = grp + rr * kGroups;
+                s[rr] = 0.0f;
+                if (r < a.tokens) {
+                    // eight reads ahead of their FMAs, in element order;
+                    // reads past the row's end stay inside its LDS row and
+                    // add exact zeros (the sum is never -0)
+#pragma unroll
+                    for (int j0 = 0; j0 < kStageInner / 128; j0 += 8) {
+                        float e[8];
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) {
+                            const int i = g + 128 * (j0 + j);
+                            const float v = read_bf16(xs[stage_index(r, i)]);
+                            e[j] = i < a.inner ? v : 0.0f;
+                        }
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) s[rr] = __fmaf_rn(e[j], e[j], s[rr]);
+                    }
+                    if (g >= 64) norm_part[r * 64 + g - 64] = s[rr];
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int rr = 0; rr < kRowsPerGroup; ++rr) {
+                const int r = grp + rr * kGroups;
+                if (r < a.tokens && g < 64) {
+                    float sum = __fadd_rn(s[rr], norm_part[r * 64 + g]);
+#pragma unroll
+                    for (int stride = 32; stride > 0; stride >>= 1)
+                        sum = __fadd_rn(sum, __shfl_down(sum, stride, 64));
+                    if (g == 0) {
+                        const float mean = __fdiv_rn(sum, (float)a.inner);
+                        norm_factor[r] = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, a.eps)));
+                    }
+                }
+            }
+            __syncthreads();
+            // BF16(BF16(x * factor) * w), eight elements per chunk, in place:
+            // thread t takes chunk t % kRowChunks of rows t / kRowChunks,
+            // + kThreads / kRowChunks, ..., so its weights are read and
+            // widened once.
+            constexpr int kRowChunks = kStageInner / 8;
+            const int c = (int)threadIdx.x % kRowChunks;
+            if (c < chunks) {
+                const bf16x8_t wv = *reinterpret_cast<const bf16x8_t *>(norm_w + c * 8);
+                float wf[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) wf[e] = (float)wv[e];
+                for (int r = (int)threadIdx.x / kRowChunks; r < a.tokens; r += kThreads / kRowChunks) {
+                    bf16x8_t *p = reinterpret_cast<bf16x8_t *>(xs + stage_index(r, c * 8));
+                    const bf16x8_t xv = *p;
+                    const float f = norm_factor[r];
+                    bf16x8_t y;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const __bf16 n = (__bf16)__fmul_rn((float)xv[e], f);
+                        y[e] = (__bf16)__fmul_rn((float)n, wf[e]);
+                    }
+                    *p = y;
+                }
+            }
+            __syncthreads();
+        }
+    }
+
+    while (true) {
+#pragma unroll
+        for (int m = 0; m < NS; ++m) {
+            acc[m] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            acc_up[m] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        // A ring of DEPTH batches: batch i + DEPTH loads into batch i's
+        // registers once batch i is used.
+        for (int kb0 = kfirst; kb0 < a.inner; kb0 += (PERIOD / PB) * WAVES * kBlock) {
+#pragma unroll
+            for (int u = 0; u < PERIOD; ++u) {
+                Batch &b = ring[u % DEPTH];
+                const int k = k_of(kb0, u);
+                if (k < a.inner) {
+                    use_batch(b, k, (u / PB) % NS);
+                    const int kn = k_of(kb0, u + DEPTH);
+                    if (kn < a.inner) load_batch(b, t, kn);
+                }
+            }
+        }
+        // The next tile's first batches go out before this tile's partials
+        // are summed.
+        const Tile cur = t;
+        const int next = tile + (int)gridDim.x;
+        if (next < a.tiles) {
+            t = tile_of(next);
+#pragma unroll
+            for (int d = 0; d < DEPTH; ++d)
+                if (k_of(kfirst, d) < a.inner) load_batch(ring[d], t, k_of(kfirst, d));
+        }
+        floatx4_t sum, sum_up;
+#pragma unroll
+        for (int p = 0; p < (EPI == kSwiglu ? 2 : 1); ++p) {
+#pragma unroll
+            for (int m = 0; m < NS; ++m) partial[wave + m * WAVES][lane] = p ? acc_up[m] : acc[m];
+            __syncthreads();
+            if (wave == 0) {
+                floatx4_t s = partial[0][lane];
+                for (int j = 1; j < kSlots; ++j) s += partial[j][lane];
+                if (p) sum_up = s;
+                else sum = s;
+            }
+            __syncthreads();  // the partials are read before they are written again
+        }
+        if (wave == 0 && live) {
+            // D layout: lane l holds rows 4*(l/16) + j, token l%16.
+            uint16_t *out = cur.out + (int64_t)tok * cur.rows;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int r = cur.r0 + 4 * (lane >> 4) + j;
+                if (r >= cur.rows) continue;
+                const uint16_t y = write_bf16(sum[j]);
+                if (EPI == kPlain) {
+                    out[r] = y;
+                } else if (EPI == kAdd) {
+                    out[r] = write_bf16(__fadd_rn(read_bf16(a.resid[(int64_t)tok * cur.rows + r]), read_bf16(y)));
+                } else {
+                    out[r] = swiglu_mul_bf16(a.act_table[y], write_bf16(sum_up[j]));
+                }
+            }
+        }
+        if (next >= a.tiles) break;
+        tile = next;
     }
 }
 
 int tiles_of(int rows) { return (rows + kTileRows - 1) / kTileRows; }
 
-template <int EPI, bool XLDS>
+// Launch shape: wavefronts per workgroup, workgroups per CU (a grid of at
+// most per_cu * kCus workgroups, each working through every grid-th tile)
+// and load batches in flight per wavefront.
+struct Shape {
+    int waves, per_cu, depth;
+};
+
+// Measured at the cfg5 decode shapes (1 and 8 tokens, weights cycled
+// through more memory than the last-level cache): 8 wavefronts per
+// workgroup with two workgroups per CU ahead of 16 with one (QKV's 384
+// tiles then all run at once, and one workgroup's reduction overlaps the
+// other's loads); a four-deep ring and a grid of up to four workgroups per
+// CU for the SwiGLU pair; a two-deep ring elsewhere (four gained nothing for
+// one matrix and spills when the token rows are not staged).
+Shape skinny_shape(int epi, bool xlds, bool norm) {
+    if (epi == kSwiglu && xlds && !norm) return Shape{8, 4, 4};
+    return Shape{8, 2, 2};
+}
+
+template <int EPI, bool XLDS, bool NORM>
 hipError_t launch_with(SkinnyArgs &a, hipStream_t stream) {
     int tiles = 0;
     for (int s = 0; s < a.segments; ++s) {
         a.first_tile[s] = tiles;
         tiles += tiles_of(a.rows[s]);
     }
-    // Few row tiles get more wavefronts each, so that enough weight loads are
-    // in flight to cover HBM latency.
     a.tiles = tiles;
-    // Measured per shape at 8 tokens (weights cycled through more memory
-    // than the Infinity Cache holds): 8 wavefronts for the gate/up pair,
-    // for inputs too wide to stage and for many row tiles; 16 for the rest.
-    const int waves = (EPI == kSwiglu || a.inner > kStageInner || tiles >= 1024) ? 8 : 16;
-    const unsigned grid = (unsigned)tiles;
-    if (waves == 16)
-        hipLaunchKernelGGL((skinny_kernel<16, EPI, XLDS>), dim3(grid), dim3(16 * 64), 0, stream, a);
+    const Shape sh = skinny_shape(EPI, XLDS, NORM);
+    const unsigned grid = (unsigned)std::min(tiles, sh.per_cu * kCus);
+    if constexpr (EPI == kSwiglu && XLDS && !NORM)
+        hipLaunchKernelGGL((skinny_kernel<EPI, XLDS, NORM, 8, 4>), dim3(grid), dim3(8 * 64), 0, stream, a);
     else
-        hipLaunchKernelGGL((skinny_kernel<8, EPI, XLDS>), dim3(grid), dim3(8 * 64), 0, stream, a);
+        hipLaunchKernelGGL((skinny_kernel<EPI, XLDS, NORM, 8, 2>), dim3(grid), dim3(8 * 64), 0, stream, a);
     return hipGetLastError();
 }
 
 template <int EPI>
 hipError_t launch(SkinnyArgs &a, hipStream_t stream) {
-    if (a.tokens <= kStageTokens && a.inner <= kStageInner) return launch_with<EPI, true>(a, stream);
-    return launch_with<EPI, false>(a, stream);
+    if (a.tokens <= kStageTokens && a.inner <= kStageInner) {
+        if (a.norm_w) return launch_with<EPI, true, true>(a, stream);
+        return launch_with<EPI, true, false>(a, stream);
+    }
+    if (a.norm_w) return hipErrorInvalidValue;  // the caller normalises first
+    return launch_with<EPI, false, false>(a, stream);
 }
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -209,8 +426,12 @@ bool skinny_supported(int inner, int tokens, const void *x, const void *w0, cons
            aligned16(w0) && aligned16(w1) && aligned16(w2);
 }
 
+bool skinny_norm_supported(int inner, int tokens, const void *norm_w) {
+    return tokens <= kStageTokens && inner <= kStageInner && aligned16(norm_w);
+}
+
 hipError_t launch_skinny_gemm(const SkinnyMatrix *m, int count, const uint16_t *x, int inner, int tokens,
-                              hipStream_t stream) {
+                              hipStream_t stream, const uint16_t *norm_w, float eps) {
     SkinnyArgs a{};
     for (int s = 0; s < count; ++s) {
         a.w[s] = m[s].w;
@@ -221,6 +442,8 @@ hipError_t launch_skinny_gemm(const SkinnyMatrix *m, int count, const uint16_t *
     a.x = x;
     a.inner = inner;
     a.tokens = tokens;
+    a.norm_w = norm_w;
+    a.eps = eps;
     return launch<kPlain>(a, stream);
 }
 
@@ -239,7 +462,8 @@ hipError_t launch_skinny_gemm_add(const SkinnyMatrix &m, const uint16_t *resid, 
 }
 
 hipError_t launch_skinny_swiglu(const uint16_t *w_gate, const uint16_t *w_up, uint16_t *out, int rows,
-                                const uint16_t *x, int inner, int tokens, hipStream_t stream) {
+                                const uint16_t *x, int inner, int tokens, const uint16_t *act_table,
+                                hipStream_t stream, const uint16_t *norm_w, float eps) {
     SkinnyArgs a{};
     a.w[0] = w_gate;
     a.w_up = w_up;
@@ -249,6 +473,9 @@ hipError_t launch_skinny_swiglu(const uint16_t *w_gate, const uint16_t *w_up, ui
     a.x = x;
     a.inner = inner;
     a.tokens = tokens;
+    a.norm_w = norm_w;
+    a.eps = eps;
+    a.act_table = act_table;
     return launch<kSwiglu>(a, stream);
 }
 

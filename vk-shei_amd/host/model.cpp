@@ -88,7 +88,6 @@ DecoderRunner::DecoderRunner(std::shared_ptr<NativeContext> ctx, ModelSpec spec,
         pos_ = static_cast<int32_t *>(alloc(r * 4));
         next_ = static_cast<int32_t *>(alloc(r * 4));
         x_ = static_cast<uint16_t *>(alloc(r * spec_.hidden * 2));
-        norm_ = static_cast<uint16_t *>(alloc(r * spec_.hidden * 2));
         q_ = static_cast<uint16_t *>(alloc(r * qd * 2));
         qr_ = static_cast<uint16_t *>(alloc(r * qd * 2));
         attn_ = static_cast<uint16_t *>(alloc(r * qd * 2));
@@ -122,16 +121,12 @@ void *DecoderRunner::alloc(size_t bytes) {
     return p;
 }
 
-void DecoderRunner::gemm(const void *w, const void *in, void *out, int inner, int rows, int tokens) {
-    ctx_->check("projection", mslim_attn_gemm_bf16(ctx_->handle(), w, in, out, inner, rows, tokens));
-}
-
 // Final norm, LM head and greedy token of `rows` hidden rows.
 void DecoderRunner::head(const uint16_t *rows_in, int rows) {
     void *h = ctx_->handle();
-    ctx_->check("final norm", mslim_attn_rmsnorm(h, rows_in, w_.final_norm, norm_, rows, spec_.hidden,
-                                                 spec_.rms_eps));
-    gemm(w_.lm_head, norm_, logits_, spec_.hidden, spec_.vocab, rows);
+    ctx_->check("final norm + LM head", mslim_attn_rmsnorm_gemm_bf16(h, w_.final_norm, spec_.rms_eps, w_.lm_head,
+                                                                     rows_in, logits_, spec_.hidden, spec_.vocab,
+                                                                     rows));
     ctx_->check("argmax", mslim_attn_argmax(h, logits_, rows, spec_.vocab, next_));
     logits_rows_ = rows;
 }
@@ -149,8 +144,9 @@ void DecoderRunner::chunk(int seq, const int32_t *ids, int n, int64_t prior) {
         const LayerWeights &w = w_.layers[l];
         check_cancel("GPU batch prefill cancelled at layer boundary", l);
         injected_error(l);
-        ctx_->check("input norm", mslim_attn_rmsnorm(h, x_, w.input_norm, norm_, n, s.hidden, s.rms_eps));
-        ctx_->check("QKV projection", mslim_attn_gemm_qkv(h, w.q, w.k, w.v, norm_, q_, k_, v_, s.hidden, qd, kvd, n));
+        ctx_->check("input norm + QKV projection",
+                    mslim_attn_rmsnorm_gemm_qkv(h, w.input_norm, s.rms_eps, w.q, w.k, w.v, x_, q_, k_, v_, s.hidden,
+                                                qd, kvd, n));
         ctx_->check("query RoPE", mslim_attn_rope(h, q_, qr_, n, s.q_heads, s.head_dim, (int)prior, s.rope_theta,
                                                   s.llama3, s.rope_factor, s.rope_low, s.rope_high,
                                                   s.rope_original_max));
@@ -186,8 +182,9 @@ void DecoderRunner::mlp(const LayerWeights &w, int n) {
     const ModelSpec &s = spec_;
     const int qd = s.q_heads * s.head_dim;
     ctx_->check("O projection + residual", mslim_attn_gemm_bf16_add(h, w.o, attn_, x_, x_, qd, s.hidden, n));
-    ctx_->check("post norm", mslim_attn_rmsnorm(h, x_, w.post_norm, norm_, n, s.hidden, s.rms_eps));
-    ctx_->check("gate/up + SwiGLU", mslim_attn_gemm_swiglu(h, w.gate, w.up, norm_, act_, s.hidden, s.intermediate, n));
+    ctx_->check("post norm + gate/up + SwiGLU",
+                mslim_attn_rmsnorm_gemm_swiglu(h, w.post_norm, s.rms_eps, w.gate, w.up, x_, act_, s.hidden,
+                                               s.intermediate, n));
     ctx_->check("down projection + residual",
                 mslim_attn_gemm_bf16_add(h, w.down, act_, x_, x_, s.intermediate, s.hidden, n));
 }
@@ -267,8 +264,9 @@ std::vector<Step> DecoderRunner::forward_batch(const std::vector<int32_t> &token
         for (int l = 0; l < s.layers; ++l) {
             const LayerWeights &w = w_.layers[l];
             injected_error(l);
-            ctx_->check("input norm", mslim_attn_rmsnorm(h, x_, w.input_norm, norm_, b, s.hidden, s.rms_eps));
-            ctx_->check("QKV projection", mslim_attn_gemm_qkv(h, w.q, w.k, w.v, norm_, q_, k_, v_, s.hidden, qd, kvd, b));
+            ctx_->check("input norm + QKV projection",
+                        mslim_attn_rmsnorm_gemm_qkv(h, w.input_norm, s.rms_eps, w.q, w.k, w.v, x_, q_, k_, v_,
+                                                    s.hidden, qd, kvd, b));
             ctx_->check("RoPE + K/V append",
                         mslim_attn_rope_append(h, q_, k_, v_, qr_, k_pools_[l], v_pools_[l], table_, pages_per_seq_,
                                                page_tokens_, b, pos_, s.q_heads, s.kv_heads, s.head_dim, s.rope_theta,
@@ -532,8 +530,11 @@ void DecoderRunner::injected_error(int layer) {
     if (inject_kind_ != kInjectArgumentError || layer != inject_layer_) return;
     inject_kind_ = 0;
     // A launch with an invalid shape: the library rejects it before any work.
-    ctx_->check("input norm", mslim_attn_rmsnorm(ctx_->handle(), x_, w_.layers[layer].input_norm, norm_, -1,
-                                                 spec_.hidden, spec_.rms_eps));
+    const LayerWeights &w = w_.layers[layer];
+    ctx_->check("input norm + QKV projection",
+                mslim_attn_rmsnorm_gemm_qkv(ctx_->handle(), w.input_norm, spec_.rms_eps, w.q, w.k, w.v, x_, q_, k_,
+                                            v_, spec_.hidden, spec_.q_heads * spec_.head_dim,
+                                            spec_.kv_heads * spec_.head_dim, -1));
 }
 
 std::string DecoderRunner::logical_kv_sha256(int seq) const {

@@ -174,7 +174,6 @@ private:
     region::DevicePagePool all_layer_pool() const;
     std::vector<region::LayerBlocks> slot_blocks(int seq) const;
     void seal_slot(int seq, int64_t from, int64_t to);
-    void gemm(const void *w, const void *in, void *out, int inner, int rows, int tokens);
     void head(const uint16_t *rows_in, int rows);
     void mlp(const LayerWeights &w, int n);
     const int32_t *table_row(int seq) const { return table_ + (int64_t)seq * pages_per_seq_; }
@@ -203,7 +202,7 @@ private:
     std::vector<char> poisoned_;
     int inject_kind_ = 0, inject_layer_ = -1;
     int32_t *table_ = nullptr, *ids_ = nullptr, *pos_ = nullptr, *next_ = nullptr;
-    uint16_t *x_ = nullptr, *norm_ = nullptr, *q_ = nullptr, *k_ = nullptr, *v_ = nullptr, *qr_ = nullptr,
+    uint16_t *x_ = nullptr, *q_ = nullptr, *k_ = nullptr, *v_ = nullptr, *qr_ = nullptr,
              *kr_ = nullptr, *attn_ = nullptr, *act_ = nullptr,
              *kd_ = nullptr, *vd_ = nullptr, *logits_ = nullptr;
     int logits_rows_ = 0;

@@ -53,6 +53,7 @@ EXPORTS = (
     "mslim_attn_ctx_new",
     "mslim_attn_ctx_destroy",
     "mslim_attn_get_device_info",
+    "mslim_attn_check_bf16_encoding",
     "mslim_attn_ctx_set_stream",
     "mslim_attn_ctx_set_option",
     "mslim_attn_synchronize",
@@ -90,6 +91,9 @@ EXPORTS = (
     "mslim_attn_gemm_bf16_add",
     "mslim_attn_gemm_swiglu",
     "mslim_attn_gemm_qkv",
+    "mslim_attn_rmsnorm_gemm_bf16",
+    "mslim_attn_rmsnorm_gemm_qkv",
+    "mslim_attn_rmsnorm_gemm_swiglu",
     "mslim_attn_add",
     "mslim_attn_embed",
     "mslim_attn_argmax",
@@ -136,6 +140,7 @@ def library() -> C.CDLL:
         "mslim_attn_ctx_new": (P, []),
         "mslim_attn_ctx_destroy": (None, [P]),
         "mslim_attn_get_device_info": (I, [P, C.POINTER(DeviceInfo)]),
+        "mslim_attn_check_bf16_encoding": (I, [P, C.POINTER(C.c_uint64)]),
         "mslim_attn_ctx_set_stream": (I, [P, P]),
         "mslim_attn_ctx_set_option": (I, [P, I, I64]),
         "mslim_attn_synchronize": (I, [P]),
@@ -173,6 +178,9 @@ def library() -> C.CDLL:
         "mslim_attn_gemm_bf16_add": (I, [P, P, P, P, P, I, I, I]),
         "mslim_attn_gemm_swiglu": (I, [P, P, P, P, P, I, I, I]),
         "mslim_attn_gemm_qkv": (I, [P, P, P, P, P, P, P, P, I, I, I, I]),
+        "mslim_attn_rmsnorm_gemm_bf16": (I, [P, P, F, P, P, P, I, I, I]),
+        "mslim_attn_rmsnorm_gemm_qkv": (I, [P, P, F, P, P, P, P, P, P, P, I, I, I, I]),
+        "mslim_attn_rmsnorm_gemm_swiglu": (I, [P, P, F, P, P, P, P, I, I, I]),
         "mslim_attn_add": (I, [P, P, P, P, SZ]),
         "mslim_attn_embed": (I, [P, P, I, I, P, I, P, P]),
         "mslim_attn_argmax": (I, [P, P, I, I, P]),
@@ -277,6 +285,12 @@ class Context:
         self._check("device_info", self._lib.mslim_attn_get_device_info(self._h, C.byref(info)))
         return {name: (getattr(info, name).decode() if isinstance(getattr(info, name), bytes)
                        else getattr(info, name)) for name, _ in DeviceInfo._fields_}
+
+    def check_bf16_encoding(self) -> int:
+        """Encodings (of all 2^32 f32) where the device's BF16 encoder differs from the rule."""
+        n = C.c_uint64(0)
+        self._check("check_bf16_encoding", self._lib.mslim_attn_check_bf16_encoding(self._h, C.byref(n)))
+        return int(n.value)
 
     def synchronize(self) -> None:
         self._check("synchronize", self._lib.mslim_attn_synchronize(self._h))
@@ -481,6 +495,23 @@ class Context:
         self._check("gemm_qkv", self._lib.mslim_attn_gemm_qkv(
             self._h, _ptr(q_weight), _ptr(k_weight), _ptr(v_weight), _ptr(input_dev), _ptr(q_out),
             _ptr(k_out), _ptr(v_out), inner, q_rows, kv_rows, tokens))
+
+    def rmsnorm_gemm_bf16(self, norm_weight, eps: float, weight, input_dev, output, inner: int, rows: int,
+                          tokens: int) -> None:
+        self._check("rmsnorm_gemm_bf16", self._lib.mslim_attn_rmsnorm_gemm_bf16(
+            self._h, _ptr(norm_weight), eps, _ptr(weight), _ptr(input_dev), _ptr(output), inner, rows, tokens))
+
+    def rmsnorm_gemm_qkv(self, norm_weight, eps: float, q_weight, k_weight, v_weight, input_dev, q_out, k_out,
+                         v_out, inner: int, q_rows: int, kv_rows: int, tokens: int) -> None:
+        self._check("rmsnorm_gemm_qkv", self._lib.mslim_attn_rmsnorm_gemm_qkv(
+            self._h, _ptr(norm_weight), eps, _ptr(q_weight), _ptr(k_weight), _ptr(v_weight), _ptr(input_dev),
+            _ptr(q_out), _ptr(k_out), _ptr(v_out), inner, q_rows, kv_rows, tokens))
+
+    def rmsnorm_gemm_swiglu(self, norm_weight, eps: float, gate_weight, up_weight, input_dev, output, inner: int,
+                            rows: int, tokens: int) -> None:
+        self._check("rmsnorm_gemm_swiglu", self._lib.mslim_attn_rmsnorm_gemm_swiglu(
+            self._h, _ptr(norm_weight), eps, _ptr(gate_weight), _ptr(up_weight), _ptr(input_dev), _ptr(output),
+            inner, rows, tokens))
 
     def add(self, a, b, out, n: int) -> None:
         self._check("add", self._lib.mslim_attn_add(self._h, _ptr(a), _ptr(b), _ptr(out), n))
