@@ -578,8 +578,7 @@ def other_configs_leg(torch, ctx, np, steps: int) -> dict:
     q2r, k2r, o2 = torch.empty_like(q2), torch.empty_like(k2), torch.empty_like(q2)
 
     def rope2():
-        ctx.rope(q2, q2r, s2, qh, d, 0, 500000.0)
-        ctx.rope(k2, k2r, s2, kvh, d, 0, 500000.0)
+        ctx.rope_qk(q2, q2r, k2, k2r, s2, qh, kvh, d, 0, 500000.0)
 
     f2 = lambda: ctx.prefill_causal(q2r, k2r, v2, o2, s2, 0, qh, kvh, d)
     rope2()
@@ -592,6 +591,7 @@ def other_configs_leg(torch, ctx, np, steps: int) -> dict:
     flops2 = 2 * d * qh * s2 * (s2 + 1)
     out["cfg2_prefill"] = {"us": round(ms2 * 1e3, 2), "tflops": round(flops2 / (ms2 * 1e-3) / 1e12, 1),
                            "flop": flops2, "rope_qk_us": round(ms2r * 1e3, 2),
+                           "rope_qk_gbps": round(s2 * (qh + kvh) * d * 2 * 2 / (ms2r * 1e-3) / 1e9, 1),
                            "split_chunk_tiles": mslim_attn.prefill_split_tiles(s2, 0, qh, kvh, d),
                            "note": "256 (64-row block, 4-head group) tiles of 1 to 32 causal key "
                                    "tiles; the long rows split into chunks of split_chunk_tiles key "

@@ -310,6 +310,18 @@ int mslim_attn_rope(void *ctx, const void *input, void *output, int tokens, int 
                     float factor, float low_freq_factor, float high_freq_factor,
                     float original_max_position);
 
+/* The prefill RoPE of a prompt chunk's Q ([tokens][q_heads][head_dim]) and K
+ * ([tokens][kv_heads][head_dim]) in one call: the same bits as
+ * mslim_attn_rope on Q and on K at the same start_position (prefill.rs:322-361
+ * rotates the two with two llm_prefill_rope launches, gpu_llm.cl:412-456).
+ * One launch shares each row's cos/sin between the Q and K heads when
+ * head_dim is a multiple of 16 (at most 512), the rows are 16-byte aligned
+ * and (q_heads + kv_heads) * head_dim <= 32768; otherwise two. */
+int mslim_attn_rope_qk(void *ctx, const void *q, void *q_out, const void *k, void *k_out, int tokens,
+                       int q_heads, int kv_heads, int head_dim, int start_position, float theta,
+                       int llama3_scaling, float factor, float low_freq_factor, float high_freq_factor,
+                       float original_max_position);
+
 /* The same RoPE with row t at position positions[t] (device int32 [tokens],
  * each >= 0): one decode row per sequence of a batch, each sequence at its own
  * position.  The reference rotates one sequence per call (llm_rope's `pos`,

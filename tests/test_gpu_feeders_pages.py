@@ -44,6 +44,30 @@ def test_rope_bit_exact(ctx, llama3, start):
     assert np.array_equal(from_torch(out).reshape(-1), ref)
 
 
+@pytest.mark.parametrize("tokens,qh,kvh,d,start,llama3", [
+    (2048, 32, 8, 128, 0, False),     # cfg2's prompt: six rows per workgroup
+    (13, 32, 8, 128, 4090, True),     # a ragged last workgroup
+    (9, 64, 8, 128, 7, False),        # three rows per workgroup
+    (7, 4, 2, 64, 123, False),
+    (3, 2, 1, 512, 32760, True),      # the whole 256-pair table
+    (4, 8, 8, 256, 1, False),
+    (5, 4, 4, 72, 9, False),          # head_dim % 16 != 0: two separate launches
+])
+def test_rope_qk_bit_exact(ctx, tokens, qh, kvh, d, start, llama3):
+    # one launch for Q and K gives mslim_attn_rope's bits on each
+    rng = np.random.default_rng(tokens * 7 + d)
+    qb, kb = normal_bf16(rng, (tokens, qh, d)), normal_bf16(rng, (tokens, kvh, d), 2.0)
+    params = (8.0, 1.0, 4.0, 8192.0) if llama3 else (1.0, 1.0, 2.0, 1.0)
+    qo = torch.empty((tokens, qh, d), dtype=torch.int16, device="cuda")
+    ko = torch.empty((tokens, kvh, d), dtype=torch.int16, device="cuda")
+    ctx.rope_qk(to_torch(qb), qo, to_torch(kb), ko, tokens, qh, kvh, d, start, 500000.0, llama3, *params)
+    torch.cuda.synchronize()
+    assert np.array_equal(from_torch(qo).reshape(-1), oracle.rope_gpu(qb, tokens, qh, d, start, 500000.0,
+                                                                      int(llama3), *params))
+    assert np.array_equal(from_torch(ko).reshape(-1), oracle.rope_gpu(kb, tokens, kvh, d, start, 500000.0,
+                                                                      int(llama3), *params))
+
+
 def test_rope_other_head_dims(ctx):
     # 64, 80, 256, 512: 16-byte chunks (512: the whole 256-pair frequency
     # table); 72 (half not a multiple of 8): one element per lane; 1024: the

@@ -767,6 +767,38 @@ int mslim_attn_rope(void *ctx, const void *input, void *output, int tokens, int 
                      "RoPE launch");
 }
 
+int mslim_attn_rope_qk(void *ctx, const void *q, void *q_out, const void *k, void *k_out, int tokens, int q_heads,
+                       int kv_heads, int head_dim, int start_position, float theta, int llama3_scaling, float factor,
+                       float low_freq_factor, float high_freq_factor, float original_max_position) {
+    g_error.clear();
+    if (!ctx || !q || !q_out || !k || !k_out || tokens < 1 || q_heads < 1 || kv_heads < 1 || head_dim < 2 ||
+        head_dim % 2 || start_position < 0 || !(theta > 0.0f) || !std::isfinite(theta))
+        return fail("invalid RoPE arguments");
+    if (q_out == q || q_out == k || k_out == q || k_out == k || q_out == k_out)
+        return fail("RoPE outputs must not alias the inputs or each other");
+    if (llama3_scaling && (!(factor > 0.0f) || !(high_freq_factor > low_freq_factor) ||
+                           !(low_freq_factor > 0.0f) || !(original_max_position > 0.0f)))
+        return fail("invalid llama3 RoPE scaling parameters");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    const auto *qi = static_cast<const uint16_t *>(q), *ki = static_cast<const uint16_t *>(k);
+    auto *qo = static_cast<uint16_t *>(q_out), *ko = static_cast<uint16_t *>(k_out);
+    if (mslim::rope_qk_supported(head_dim, q, q_out, k, k_out) && (q_heads + kv_heads) * head_dim <= 32768)
+        return check_hip(mslim::launch_rope_qk(qi, qo, ki, ko, tokens, q_heads, kv_heads, head_dim, start_position,
+                                               theta, llama3_scaling, factor, low_freq_factor, high_freq_factor,
+                                               original_max_position, c.stream),
+                         "RoPE launch");
+    if (int rc = check_hip(mslim::launch_rope(qi, qo, tokens, q_heads, head_dim, start_position, nullptr, theta,
+                                              llama3_scaling, factor, low_freq_factor, high_freq_factor,
+                                              original_max_position, c.stream),
+                           "RoPE launch"))
+        return rc;
+    return check_hip(mslim::launch_rope(ki, ko, tokens, kv_heads, head_dim, start_position, nullptr, theta,
+                                        llama3_scaling, factor, low_freq_factor, high_freq_factor,
+                                        original_max_position, c.stream),
+                     "RoPE launch");
+}
+
 int mslim_attn_rope_rows(void *ctx, const void *input, void *output, int tokens, int heads, int head_dim,
                          const int32_t *positions, float theta, int llama3_scaling, float factor,
                          float low_freq_factor, float high_freq_factor, float original_max_position) {

@@ -14,6 +14,8 @@
 #include "common.hpp"
 #include "kernels.hpp"
 
+#include <algorithm>
+
 #pragma clang fp contract(off)
 
 namespace mslim {
@@ -270,6 +272,68 @@ __global__ __launch_bounds__(256) void rope_token_kernel(const uint16_t *in, uin
     }
 }
 
+// Q and K of a prompt chunk in one launch: a workgroup takes kRopeRows-or-
+// fewer consecutive token rows, and its lanes rotate (d, d + half) pairs of
+// 8-element chunks, the chunk and its rotate-half partner loaded once and
+// both outputs written, over the rows' Q heads then K heads.  Every load of
+// a lane goes out before the c and s table of the rows is computed (one
+// trigonometric evaluation per lane per row, shared by Q and K), so the
+// loads' latency hides under the table.  Each output is rope_element's value
+// for its position, bit-identical to rope_token_kernel on Q and on K.
+// head_dim % 16 == 0 and 16-byte aligned rows.
+constexpr int kRopeRows = 8;
+constexpr int kRopePairsPerLane = 8;
+__global__ __launch_bounds__(256) void rope_qk_kernel(const uint16_t *q, uint16_t *q_out, const uint16_t *k,
+                                                      uint16_t *k_out, int tokens, int rows_per_group,
+                                                      int q_heads, int kv_heads, int head_dim, int start,
+                                                      RopeTable table) {
+    __shared__ float cs[kRopeRows][kRopeTable], sn[kRopeRows][kRopeTable];
+    const int half = head_dim / 2;
+    const int hchunks = half / 8;                       // pair units per head
+    const int units = (q_heads + kv_heads) * hchunks;  // pair units per row
+    const int row0 = blockIdx.x * rows_per_group;
+    const int rows = min(rows_per_group, tokens - row0);
+    const int work = rows * units;
+    uint4 x[kRopePairsPerLane], p[kRopePairsPerLane];
+#pragma unroll
+    for (int j = 0; j < kRopePairsPerLane; ++j) {
+        const int i = min((int)threadIdx.x + j * 256, work - 1);
+        const int r = i / units, u = i % units, head = u / hchunks, c = (u % hchunks) * 8;
+        const uint16_t *src = head < q_heads ? q + ((int64_t)(row0 + r) * q_heads + head) * head_dim
+                                             : k + ((int64_t)(row0 + r) * kv_heads + head - q_heads) * head_dim;
+        x[j] = *reinterpret_cast<const uint4 *>(src + c);
+        p[j] = *reinterpret_cast<const uint4 *>(src + c + half);
+    }
+    for (int t = threadIdx.x; t < rows * 2 * half; t += 256) {
+        const int r = t / (2 * half), f = t % (2 * half) % half;
+        const float phase = __fmul_rn((float)(start + row0 + r), table.inv[f]);
+        if (t % (2 * half) < half) cs[r][f] = round_bf16((float)cos((double)phase));
+        else sn[r][f] = round_bf16((float)sin((double)phase));
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kRopePairsPerLane; ++j) {
+        const int i = (int)threadIdx.x + j * 256;
+        if (i >= work) break;
+        const int r = i / units, u = i % units, head = u / hchunks, c = (u % hchunks) * 8;
+        uint16_t *dst = head < q_heads ? q_out + ((int64_t)(row0 + r) * q_heads + head) * head_dim
+                                       : k_out + ((int64_t)(row0 + r) * kv_heads + head - q_heads) * head_dim;
+        const uint16_t *xs = reinterpret_cast<const uint16_t *>(&x[j]);
+        const uint16_t *ps = reinterpret_cast<const uint16_t *>(&p[j]);
+        uint16_t lo[8], hi[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int f = c + e;
+            const float a = read_bf16(xs[e]), b = read_bf16(ps[e]);
+            // first half: x * c + (-partner) * s; second half: x * c + partner * s
+            lo[e] = write_bf16(__fadd_rn(round_bf16(__fmul_rn(a, cs[r][f])), round_bf16(__fmul_rn(-b, sn[r][f]))));
+            hi[e] = write_bf16(__fadd_rn(round_bf16(__fmul_rn(b, cs[r][f])), round_bf16(__fmul_rn(a, sn[r][f]))));
+        }
+        *reinterpret_cast<uint4 *>(dst + c) = *reinterpret_cast<const uint4 *>(lo);
+        *reinterpret_cast<uint4 *>(dst + c + half) = *reinterpret_cast<const uint4 *>(hi);
+    }
+}
+
 // A decode step's RoPE and K/V append in one launch, each sequence b at
 // positions[b]: rotated Q rows to q_out; rotated K and the V rows straight
 // into the page pool through page-table row b.  Lanes [0, nq) rotate Q
@@ -480,6 +544,25 @@ hipError_t launch_rope(const uint16_t *in, uint16_t *out, int tokens, int heads,
     const unsigned blocks = (unsigned)((total + 255) / 256);
     hipLaunchKernelGGL(rope_kernel, dim3(blocks), dim3(256), 0, stream, in, out, total, heads, head_dim,
                        start, positions, theta, llama3, factor, low, high, original_max);
+    return hipGetLastError();
+}
+
+bool rope_qk_supported(int head_dim, const void *q, const void *q_out, const void *k, const void *k_out) {
+    return head_dim % 16 == 0 && head_dim <= 2 * kRopeTable &&
+           ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(q_out) | reinterpret_cast<uintptr_t>(k) |
+             reinterpret_cast<uintptr_t>(k_out)) & 15) == 0;
+}
+
+hipError_t launch_rope_qk(const uint16_t *q, uint16_t *q_out, const uint16_t *k, uint16_t *k_out, int tokens,
+                          int q_heads, int kv_heads, int head_dim, int start, float theta, int llama3, float factor,
+                          float low, float high, float original_max, hipStream_t stream) {
+    const RopeTable &table = rope_table(head_dim, theta, llama3, factor, low, high, original_max);
+    const int units = (q_heads + kv_heads) * (head_dim / 16);
+    // rows per workgroup: as many as kRopePairsPerLane pairs per lane cover
+    const int rows = std::max(1, std::min(kRopeRows, kRopePairsPerLane * 256 / units));
+    if (units > kRopePairsPerLane * 256) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rope_qk_kernel, dim3((unsigned)((tokens + rows - 1) / rows)), dim3(256), 0, stream, q, q_out,
+                       k, k_out, tokens, rows, q_heads, kv_heads, head_dim, start, table);
     return hipGetLastError();
 }
 

@@ -147,12 +147,9 @@ void DecoderRunner::chunk(int seq, const int32_t *ids, int n, int64_t prior) {
         ctx_->check("input norm + QKV projection",
                     mslim_attn_rmsnorm_gemm_qkv(h, w.input_norm, s.rms_eps, w.q, w.k, w.v, x_, q_, k_, v_, s.hidden,
                                                 qd, kvd, n));
-        ctx_->check("query RoPE", mslim_attn_rope(h, q_, qr_, n, s.q_heads, s.head_dim, (int)prior, s.rope_theta,
-                                                  s.llama3, s.rope_factor, s.rope_low, s.rope_high,
-                                                  s.rope_original_max));
-        ctx_->check("key RoPE", mslim_attn_rope(h, k_, kr_, n, s.kv_heads, s.head_dim, (int)prior, s.rope_theta,
-                                                s.llama3, s.rope_factor, s.rope_low, s.rope_high,
-                                                s.rope_original_max));
+        ctx_->check("RoPE", mslim_attn_rope_qk(h, q_, qr_, k_, kr_, n, s.q_heads, s.kv_heads, s.head_dim, (int)prior,
+                                               s.rope_theta, s.llama3, s.rope_factor, s.rope_low, s.rope_high,
+                                               s.rope_original_max));
         ctx_->check("page write", mslim_attn_pages_write(h, k_pools_[l], v_pools_[l], table_row(seq), page_tokens_,
                                                          s.kv_heads, s.head_dim, prior, n, kr_, v_));
         const void *keys = kr_, *values = v_;

@@ -76,6 +76,7 @@ EXPORTS = (
     "mslim_attn_rmsnorm",
     "mslim_attn_rope",
     "mslim_attn_rope_rows",
+    "mslim_attn_rope_qk",
     "mslim_attn_swiglu",
     "mslim_attn_pages_write",
     "mslim_attn_pages_append",
@@ -163,6 +164,7 @@ def library() -> C.CDLL:
         "mslim_attn_rmsnorm": (I, [P, P, P, P, I, I, F]),
         "mslim_attn_rope": (I, [P, P, P, I, I, I, I, F, I, F, F, F, F]),
         "mslim_attn_rope_rows": (I, [P, P, P, I, I, I, P, F, I, F, F, F, F]),
+        "mslim_attn_rope_qk": (I, [P, P, P, P, P, I, I, I, I, I, F, I, F, F, F, F]),
         "mslim_attn_swiglu": (I, [P, P, P, P, SZ]),
         "mslim_attn_pages_write": (I, [P, P, P, P, I, I, I, I64, I64, P, P]),
         "mslim_attn_pages_append": (I, [P, P, P, P, I, I, I, I, I, P, P, P]),
@@ -404,6 +406,15 @@ class Context:
         self._check("rope_rows", self._lib.mslim_attn_rope_rows(
             self._h, _ptr(x), _ptr(out), tokens, heads, head_dim, _ptr(positions), theta,
             int(bool(llama3_scaling)), factor, low_freq_factor, high_freq_factor,
+            original_max_position))
+
+    def rope_qk(self, q, q_out, k, k_out, tokens: int, q_heads: int, kv_heads: int, head_dim: int,
+                start_position: int, theta: float, llama3_scaling: bool = False, factor: float = 1.0,
+                low_freq_factor: float = 1.0, high_freq_factor: float = 2.0,
+                original_max_position: float = 1.0) -> None:
+        self._check("rope_qk", self._lib.mslim_attn_rope_qk(
+            self._h, _ptr(q), _ptr(q_out), _ptr(k), _ptr(k_out), tokens, q_heads, kv_heads, head_dim,
+            start_position, theta, int(bool(llama3_scaling)), factor, low_freq_factor, high_freq_factor,
             original_max_position))
 
     def swiglu(self, gate, up, out, n: int) -> None:
