@@ -740,25 +740,33 @@ TEST(gpu_region_device_seal_writes_the_host_append_file_and_restores) {
     pool.pool_pages = (int64_t)pool_pages;
     pool.page_tokens = (int)P;
 
-    TempPath da("unused-a"), db("unused-b");
-    region::RegionConfig ca, cb;
+    TempPath da("unused-a"), db("unused-b"), dc("unused-c");
+    region::RegionConfig ca, cb, cc;
     ca.cold_directory = da.dir;
     cb.cold_directory = db.dir;
+    cc.cold_directory = dc.dir;
     std::string digest;
     {
-        region::RegionStore host(g, 2, ca), dev(g, 2, cb);
+        // dev frames its 10-record seals on the device, dev_host on the host
+        region::RegionStore host(g, 2, ca), dev(g, 2, cb), dev_host(g, 2, cc);
+        dev.set_host_framing_below(0);
+        dev_host.set_host_framing_below(SIZE_MAX);
         host.append_batch(0, 0, k_rows, v_rows, P);
         host.append_batch(1, 0, v_rows, k_rows, P);
-        dev.seal_device_pages(*ctx, 0, 0, pool, blocks, tokens);
         region::DevicePagePool swapped = pool;
         std::swap(swapped.k_pool, swapped.v_pool);
-        dev.seal_device_pages(*ctx, 1, 0, swapped, blocks, tokens);
-        CHECK(dev.stats.device_sealed_pages == 20);
-        CHECK(dev.logical_kv_sha256() == host.logical_kv_sha256());
+        for (region::RegionStore *s : {&dev, &dev_host}) {
+            s->seal_device_pages(*ctx, 0, 0, pool, blocks, tokens);
+            s->seal_device_pages(*ctx, 1, 0, swapped, blocks, tokens);
+            CHECK(s->stats.device_sealed_pages == 20);
+            CHECK(s->logical_kv_sha256() == host.logical_kv_sha256());
+        }
         digest = host.logical_kv_sha256();
     }
-    // The device-framed store is byte-identical to the host-framed one.
+    // The device-sealed stores, framed on the device or on the host, are
+    // byte-identical to the host-appended one.
     CHECK(read_file(da.dir + "/pages-exact.kv") == read_file(db.dir + "/pages-exact.kv"));
+    CHECK(read_file(da.dir + "/pages-exact.kv") == read_file(dc.dir + "/pages-exact.kv"));
 
     // Restore layer 0 into a fresh pool through another page table; the
     // gathered rows equal the originals.
@@ -865,15 +873,25 @@ TEST(gpu_region_device_seal_mid_page_multi_layer_and_restore) {
     pool.v_pool = dv.ptr;
     pool.pool_pages = (int64_t)pool_pages;
     pool.page_tokens = (int)P;
-    TempPath da("unused-a"), db("unused-b");
-    region::RegionConfig ca, cb;
+    TempPath da("unused-a"), db("unused-b"), dc("unused-c");
+    region::RegionConfig ca, cb, cc;
     ca.cold_directory = da.dir;
     cb.cold_directory = db.dir;
+    cc.cold_directory = dc.dir;
     std::string digest;
+    {
+        // the same two commits framed on the device: the same file bytes
+        region::RegionStore framed_on_device(g, layers, cc);
+        framed_on_device.set_host_framing_below(0);
+        region::DeviceStaging staging(*ctx);
+        framed_on_device.seal_device_layers(staging, 0, 20, pool, lb);
+        framed_on_device.seal_device_layers(staging, 20, tokens - 20, pool, lb);
+    }
     {
         region::RegionStore host(g, layers, ca), dev(g, layers, cb);
         for (size_t l = 0; l < layers; ++l) host.append_batch(l, 0, k_rows[l], v_rows[l], P);
         region::DeviceStaging staging(*ctx);
+        CHECK(dev.host_framing_below() > 4);  // these commits frame on the host
         dev.seal_device_layers(staging, 0, 20, pool, lb);
         CHECK(dev.layer_tokens(0) == 20 && dev.layer_tokens(1) == 20);
         dev.seal_device_layers(staging, 20, tokens - 20, pool, lb);
@@ -886,6 +904,7 @@ TEST(gpu_region_device_seal_mid_page_multi_layer_and_restore) {
         digest = host.logical_kv_sha256();
         CHECK(dev.logical_kv_sha256() == digest);
     }
+    CHECK(read_file(db.dir + "/pages-exact.kv") == read_file(dc.dir + "/pages-exact.kv"));
     region::RegionStore reopened(g, layers, cb);
     CHECK(reopened.logical_kv_sha256() == digest);
     std::vector<uint8_t> zeros(pool_pages * page_bytes, 0);

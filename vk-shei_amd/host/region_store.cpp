@@ -5,14 +5,51 @@
 #include <unistd.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
 #include <exception>
+#include <mutex>
+#include <thread>
 
 #include "../csrc/sha256.hpp"
 
 namespace mslim {
+namespace {
+
+// fn(i) for i in [0, n) on up to 16 threads; the exception of the smallest
+// failing index is rethrown.
+template <class F>
+void parallel_for(size_t n, F fn) {
+    const unsigned hw = std::thread::hardware_concurrency();
+    const size_t threads = std::max<size_t>(1, std::min<size_t>({n, 16, hw ? hw : 1}));
+    std::atomic<size_t> next{0};
+    std::mutex m;
+    size_t failed = SIZE_MAX;
+    std::exception_ptr error;
+    auto worker = [&] {
+        for (size_t i = next++; i < n; i = next++) {
+            try {
+                fn(i);
+            } catch (...) {
+                std::lock_guard<std::mutex> g(m);
+                if (i < failed) {
+                    failed = i;
+                    error = std::current_exception();
+                }
+            }
+        }
+    };
+    std::vector<std::thread> pool;
+    for (size_t t = 1; t < threads; ++t) pool.emplace_back(worker);
+    worker();
+    for (auto &t : pool) t.join();
+    if (error) std::rethrow_exception(error);
+}
+
+}  // namespace
+
 namespace region {
 
 namespace {
@@ -453,22 +490,25 @@ void RegionStore::seal_device_layers(DeviceStaging &st, size_t position, size_t 
                 d.pool_page = block;
                 d.first_row = (uint32_t)(r == 0 ? first_row : 0);
             }
+        const bool host_frames = records < host_framing_below_;
         {
             std::lock_guard<std::mutex> guard(ctx.mutex());
             void *h = ctx.handle();
             ctx.check("upload record descriptors",
                       mslim_attn_buf_write(h, st.d_desc, 0, st.h_desc, records * sizeof(mslim_attn_page_record)));
-            ctx.check("record frames",
-                      mslim_attn_record_frames(h, pool.k_pool, pool.v_pool, pool.pool_pages, (int)P, (int)kvh,
-                                               (int)geometry_.head_dim, tile,
-                                               static_cast<const mslim_attn_page_record *>(st.d_desc), (int)records,
-                                               st.d_frames));
+            if (!host_frames)
+                ctx.check("record frames",
+                          mslim_attn_record_frames(h, pool.k_pool, pool.v_pool, pool.pool_pages, (int)P, (int)kvh,
+                                                   (int)geometry_.head_dim, tile,
+                                                   static_cast<const mslim_attn_page_record *>(st.d_desc),
+                                                   (int)records, st.d_frames));
             ctx.check("record payloads",
                       mslim_attn_record_payloads(h, pool.k_pool, pool.v_pool, pool.pool_pages, (int)P, (int)kvh,
                                                  (int)geometry_.head_dim,
                                                  static_cast<const mslim_attn_page_record *>(st.d_desc),
                                                  (int)records, st.d_k, st.d_v, 0));
-            ctx.check("read record frames", mslim_attn_buf_read(h, st.d_frames, 0, st.h_frames, records * slot));
+            if (!host_frames)
+                ctx.check("read record frames", mslim_attn_buf_read(h, st.d_frames, 0, st.h_frames, records * slot));
             ctx.check("read K payloads", mslim_attn_buf_read(h, st.d_k, 0, st.h_k, records * page_bytes));
             ctx.check("read V payloads", mslim_attn_buf_read(h, st.d_v, 0, st.h_v, records * page_bytes));
         }
@@ -495,14 +535,31 @@ void RegionStore::seal_device_layers(DeviceStaging &st, size_t position, size_t 
                 }
             }
         }
+        std::vector<cold::PreparedPage> prepared;
+        if (host_frames) {
+            prepared.resize(records);
+            parallel_for(records, [&](size_t i) {
+                cold::PageGeometry pg;
+                pg.layer = descs[i].layer;
+                pg.token_start = descs[i].token_start;
+                pg.tokens = descs[i].tokens;
+                pg.heads = (uint32_t)kvh;
+                pg.head_dim = (uint32_t)geometry_.head_dim;
+                pg.tile = tile;
+                const size_t len = (size_t)descs[i].tokens * kvh * row_bytes;
+                prepared[i] = cold::ColdStore::prepare_page(descs[i].page_id, pg, st.h_k + i * page_bytes, len,
+                                                            st.h_v + i * page_bytes, len);
+            });
+        }
         for (size_t li = g0; li < g1; ++li) {
             const size_t layer = layers[li].layer;
             for (size_t r = 0; r < per_layer; ++r) {
                 const size_t i = (li - g0) * per_layer + r;
                 const size_t n = descs[i].tokens;
                 const cold::PageMeta meta =
-                    cold_.append_framed(st.h_frames + i * slot, (size_t)slot, st.h_k + i * page_bytes,
-                                        st.h_v + i * page_bytes, n * kvh * row_bytes, false);
+                    host_frames ? cold_.append_prepared(std::move(prepared[i]), false)
+                                : cold_.append_framed(st.h_frames + i * slot, (size_t)slot, st.h_k + i * page_bytes,
+                                                      st.h_v + i * page_bytes, n * kvh * row_bytes, false);
                 for (size_t offset = 0; offset < n; ++offset) pages_[layer].push_back({meta.page_id, offset});
                 stats.prefill_batched_page_tokens = std::max(stats.prefill_batched_page_tokens, n);
             }

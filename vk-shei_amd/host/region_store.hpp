@@ -110,6 +110,13 @@ struct LayerBlocks {
     std::vector<int32_t> blocks;
 };
 
+// Device seals of fewer records than this frame them on the host (see
+// RegionStore::seal_device_layers).  Measured on MI355X with 16 host threads,
+// 64 KiB records (8 kv heads x 16 tokens x 128 dims), whole seal wall time,
+// device framing / host framing: 32 records 5.2 / 1.2 ms, 256: 7.6 / 6.4 ms,
+// 512: 11.1 / 12.7 ms, 4096: 59.7 / 105.2 ms.
+constexpr size_t kHostFramingRecords = 384;
+
 class RegionStore {
 public:
     // gpu_region_store.rs:137-207: opens (and restores) or creates
@@ -172,8 +179,16 @@ public:
     // groups of at most `max_group_bytes` of payload; each group is checked
     // (V finite on every layer, K finite on layer 0) before any of its
     // records is committed, as append_batch checks each layer.
+    // A group of fewer than host_framing_below() records is framed on the
+    // host (header, token hashes, checksums and SHA-256 of each record from
+    // the payloads read back anyway, records on parallel threads, SHA-NI
+    // where the CPU has it) instead of by mslim_attn_record_frames, whose
+    // serial SHA-256 chain per record gives each launch a floor of about
+    // 4 ms; both write the same bytes.
     void seal_device_layers(DeviceStaging &staging, size_t position, size_t count, const DevicePagePool &pool,
                             const std::vector<LayerBlocks> &layers, size_t max_group_bytes = (size_t)256 << 20);
+    size_t host_framing_below() const { return host_framing_below_; }
+    void set_host_framing_below(size_t records) { host_framing_below_ = records; }
     // Load every committed record of the listed layers into the pool and
     // verify each on the device (header, token hashes, checksums, SHA-256)
     // from its staged copy BEFORE any byte reaches the pool: a corrupt store
@@ -194,6 +209,7 @@ private:
 
     RegionConfig config_;
     portable::AttentionGeometry geometry_;
+    size_t host_framing_below_ = kHostFramingRecords;
     std::string temp_dir_;  // non-empty when the store owns a temporary directory
     cold::ColdStore cold_;
     std::vector<std::vector<PageAddress>> pages_;
