@@ -68,6 +68,29 @@ def test_rope_qk_bit_exact(ctx, tokens, qh, kvh, d, start, llama3):
                                                                       int(llama3), *params))
 
 
+def test_rope_cossin_table_limit_and_configurations(ctx):
+    # The context keeps a table of c and s by position (at most 32 MiB:
+    # 131,072 positions at head_dim 128).  Rows inside it read the table,
+    # rows past it (and workgroups that straddle it) compute c and s
+    # themselves, and a new configuration rebuilds it; every case gives the
+    # oracle's bits.
+    rng = np.random.default_rng(11)
+    qh, kvh, d = 4, 2, 128
+    for theta in (500000.0, 10000.0, 500000.0):
+        for start, tokens in ((131060, 20), (200000, 3), (5, 9)):
+            qb, kb = normal_bf16(rng, (tokens, qh, d)), normal_bf16(rng, (tokens, kvh, d))
+            qo = torch.empty((tokens, qh, d), dtype=torch.int16, device="cuda")
+            ko = torch.empty((tokens, kvh, d), dtype=torch.int16, device="cuda")
+            ro = torch.empty((tokens, qh, d), dtype=torch.int16, device="cuda")
+            ctx.rope_qk(to_torch(qb), qo, to_torch(kb), ko, tokens, qh, kvh, d, start, theta)
+            ctx.rope(to_torch(qb), ro, tokens, qh, d, start, theta)
+            torch.cuda.synchronize()
+            want_q = oracle.rope_gpu(qb, tokens, qh, d, start, theta)
+            assert np.array_equal(from_torch(qo).reshape(-1), want_q), (theta, start)
+            assert np.array_equal(from_torch(ro).reshape(-1), want_q), (theta, start)
+            assert np.array_equal(from_torch(ko).reshape(-1), oracle.rope_gpu(kb, tokens, kvh, d, start, theta))
+
+
 def test_rope_other_head_dims(ctx):
     # 64, 80, 256, 512: 16-byte chunks (512: the whole 256-pair frequency
     # table); 72 (half not a multiple of 8): one element per lane; 1024: the

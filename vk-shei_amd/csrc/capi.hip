@@ -45,6 +45,12 @@ struct Context {
     size_t proj_partial_bytes = 0;
     void *norm_rows = nullptr;         // normalised rows of the RMSNorm + product entries
     size_t norm_rows_bytes = 0;
+    // RoPE cos/sin by position for the last RoPE configuration used
+    uint16_t *rope_rows = nullptr;
+    int64_t rope_positions = 0;
+    size_t rope_bytes = 0;
+    float rope_key[6] = {};    // head_dim, theta, llama3, factor, low, high
+    float rope_key_max = 0.0f;  // original_max
     size_t workspace_bytes = 0;
     int *counters = nullptr;        // decode split counters, zero between launches
     size_t counter_bytes = 0;
@@ -75,6 +81,7 @@ struct Context {
         if (swiglu_table) (void)hipFree(swiglu_table);
         if (proj_partial) (void)hipFree(proj_partial);
         if (norm_rows) (void)hipFree(norm_rows);
+        if (rope_rows) (void)hipFree(rope_rows);
         if (prefill_partial) (void)hipFree(prefill_partial);
         if (prefill_counters) (void)hipFree(prefill_counters);
         if (counters) (void)hipFree(counters);
@@ -746,6 +753,62 @@ int mslim_attn_rmsnorm(void *ctx, const void *input, const void *weight, void *o
                      "RMSNorm launch");
 }
 
+// The context's RoPE cos/sin table for this configuration, covering at
+// least min(need, the size limit) positions: built (or rebuilt for another
+// configuration) on the context stream, behind any RoPE work already queued.
+// A table the size limit or the device memory does not allow is simply not
+// used: the kernels compute those positions themselves, with the same bits.
+constexpr size_t kRopeTableMaxBytes = (size_t)32 << 20;
+constexpr int64_t kRopeTableMinPositions = 8192;
+
+static mslim::RopeCosSin rope_cossin(Context &c, int head_dim, float theta, int llama3, float factor, float low,
+                                     float high, float original_max, int64_t need) {
+    if (head_dim > 512 || head_dim % 2) return {};
+    const float key[6] = {(float)head_dim, theta, (float)llama3, llama3 ? factor : 0.0f, llama3 ? low : 0.0f,
+                          llama3 ? high : 0.0f};
+    const float key_max = llama3 ? original_max : 0.0f;
+    const bool same = std::memcmp(key, c.rope_key, sizeof key) == 0 &&
+                      std::memcmp(&key_max, &c.rope_key_max, sizeof key_max) == 0 && c.rope_rows;
+    const size_t row_bytes = (size_t)head_dim * 2;  // c and s of head_dim / 2 pairs
+    const int64_t limit = (int64_t)(kRopeTableMaxBytes / row_bytes);
+    int64_t want = std::min(limit, std::max(need, kRopeTableMinPositions));
+    want = std::min(limit, (want + 4095) / 4096 * 4096);
+    if (same && c.rope_positions >= std::min(want, std::max(need, (int64_t)1))) return {c.rope_rows, c.rope_positions};
+    if (same) want = std::max(want, c.rope_positions);
+    const size_t bytes = (size_t)want * row_bytes;
+    if (bytes > c.rope_bytes) {
+        // work queued on the stream may still read the old table
+        if (c.rope_rows) {
+            if (hipStreamSynchronize(c.stream) != hipSuccess || hipFree(c.rope_rows) != hipSuccess) {
+                (void)hipGetLastError();
+                c.rope_rows = nullptr;
+                c.rope_bytes = 0;
+                c.rope_positions = 0;
+                return {};
+            }
+        }
+        c.rope_rows = nullptr;
+        c.rope_bytes = 0;
+        c.rope_positions = 0;
+        if (hipMalloc(reinterpret_cast<void **>(&c.rope_rows), bytes) != hipSuccess) {
+            (void)hipGetLastError();
+            c.rope_rows = nullptr;
+            return {};
+        }
+        c.rope_bytes = bytes;
+    }
+    if (mslim::launch_rope_cossin(c.rope_rows, want, head_dim, theta, llama3, factor, low, high, original_max,
+                                  c.stream) != hipSuccess) {
+        (void)hipGetLastError();
+        c.rope_positions = 0;
+        return {};
+    }
+    std::memcpy(c.rope_key, key, sizeof key);
+    c.rope_key_max = key_max;
+    c.rope_positions = want;
+    return {c.rope_rows, c.rope_positions};
+}
+
 int mslim_attn_rope(void *ctx, const void *input, void *output, int tokens, int heads, int head_dim,
                     int start_position, float theta, int llama3_scaling, float factor,
                     float low_freq_factor, float high_freq_factor, float original_max_position) {
@@ -759,10 +822,13 @@ int mslim_attn_rope(void *ctx, const void *input, void *output, int tokens, int 
         return fail("invalid llama3 RoPE scaling parameters");
     Context &c = *ctx_of(ctx);
     Lock lock(c);
+    const mslim::RopeCosSin table = rope_cossin(c, head_dim, theta, llama3_scaling, factor, low_freq_factor,
+                                                high_freq_factor, original_max_position,
+                                                (int64_t)start_position + tokens);
     return check_hip(mslim::launch_rope(static_cast<const uint16_t *>(input),
                                         static_cast<uint16_t *>(output), tokens, heads, head_dim,
                                         start_position, nullptr, theta, llama3_scaling, factor,
-                                        low_freq_factor, high_freq_factor, original_max_position,
+                                        low_freq_factor, high_freq_factor, original_max_position, table,
                                         c.stream),
                      "RoPE launch");
 }
@@ -783,19 +849,22 @@ int mslim_attn_rope_qk(void *ctx, const void *q, void *q_out, const void *k, voi
     Lock lock(c);
     const auto *qi = static_cast<const uint16_t *>(q), *ki = static_cast<const uint16_t *>(k);
     auto *qo = static_cast<uint16_t *>(q_out), *ko = static_cast<uint16_t *>(k_out);
+    const mslim::RopeCosSin table = rope_cossin(c, head_dim, theta, llama3_scaling, factor, low_freq_factor,
+                                                high_freq_factor, original_max_position,
+                                                (int64_t)start_position + tokens);
     if (mslim::rope_qk_supported(head_dim, q, q_out, k, k_out) && (q_heads + kv_heads) * head_dim <= 32768)
         return check_hip(mslim::launch_rope_qk(qi, qo, ki, ko, tokens, q_heads, kv_heads, head_dim, start_position,
                                                theta, llama3_scaling, factor, low_freq_factor, high_freq_factor,
-                                               original_max_position, c.stream),
+                                               original_max_position, table, c.stream),
                          "RoPE launch");
     if (int rc = check_hip(mslim::launch_rope(qi, qo, tokens, q_heads, head_dim, start_position, nullptr, theta,
                                               llama3_scaling, factor, low_freq_factor, high_freq_factor,
-                                              original_max_position, c.stream),
+                                              original_max_position, table, c.stream),
                            "RoPE launch"))
         return rc;
     return check_hip(mslim::launch_rope(ki, ko, tokens, kv_heads, head_dim, start_position, nullptr, theta,
                                         llama3_scaling, factor, low_freq_factor, high_freq_factor,
-                                        original_max_position, c.stream),
+                                        original_max_position, table, c.stream),
                      "RoPE launch");
 }
 
@@ -812,10 +881,13 @@ int mslim_attn_rope_rows(void *ctx, const void *input, void *output, int tokens,
         return fail("invalid llama3 RoPE scaling parameters");
     Context &c = *ctx_of(ctx);
     Lock lock(c);
+    // positions live on the device: the table covers what it covers
+    const mslim::RopeCosSin table = rope_cossin(c, head_dim, theta, llama3_scaling, factor, low_freq_factor,
+                                                high_freq_factor, original_max_position, 0);
     return check_hip(mslim::launch_rope(static_cast<const uint16_t *>(input),
                                         static_cast<uint16_t *>(output), tokens, heads, head_dim, 0,
                                         positions, theta, llama3_scaling, factor, low_freq_factor,
-                                        high_freq_factor, original_max_position, c.stream),
+                                        high_freq_factor, original_max_position, table, c.stream),
                      "RoPE launch");
 }
 
@@ -936,6 +1008,9 @@ int mslim_attn_rope_append(void *ctx, const void *q, const void *k, const void *
     a.low = low_freq_factor;
     a.high = high_freq_factor;
     a.original_max = original_max_position;
+    // every position the page table can hold
+    a.cossin = rope_cossin(c, head_dim, theta, llama3_scaling, factor, low_freq_factor, high_freq_factor,
+                           original_max_position, (int64_t)pages_per_seq << a.shift);
     return check_hip(mslim::launch_rope_append(a, c.stream), "RoPE append launch");
 }
 

@@ -170,18 +170,42 @@ struct RopeTable {
 // :412-456): element d of head `head` of a token row [heads][head_dim] at
 // `position`, rotate-half partner, c and s rounded to BF16; `inv` is the
 // inverse frequency of pair d % (head_dim / 2).
-__device__ __forceinline__ uint16_t rope_element(const uint16_t *token_row, int head, int d, int head_dim,
-                                                 int64_t position, float inv) {
+__device__ __forceinline__ uint16_t rope_element_cs(const uint16_t *token_row, int head, int d, int head_dim,
+                                                    float cs, float sn) {
     const int half = head_dim / 2;
     const uint16_t *h = token_row + (int64_t)head * head_dim;
     const float partner = read_bf16(h[d < half ? d + half : d - half]);
     const float rotated = d < half ? -partner : partner;
-    const float phase = __fmul_rn((float)position, inv);
-    const float cs = round_bf16((float)cos((double)phase));
-    const float sn = round_bf16((float)sin((double)phase));
     const float left = round_bf16(__fmul_rn(read_bf16(h[d]), cs));
     const float right = round_bf16(__fmul_rn(rotated, sn));
     return write_bf16(__fadd_rn(left, right));
+}
+
+// c and s of pair f at `position`: BF16(cos(position * inv)), BF16(sin(...))
+// with the phase in f32 and the functions in f64.
+__device__ __forceinline__ void rope_trig(int64_t position, float inv, float &cs, float &sn) {
+    const float phase = __fmul_rn((float)position, inv);
+    cs = round_bf16((float)cos((double)phase));
+    sn = round_bf16((float)sin((double)phase));
+}
+
+// The same from the context's table where it covers the position.
+__device__ __forceinline__ void rope_cs(const RopeCosSin &t, int64_t position, int f, int half, float inv,
+                                        float &cs, float &sn) {
+    if (position >= 0 && position < t.positions) {
+        const uint16_t *row = t.rows + position * 2 * half;
+        cs = read_bf16(row[f]);
+        sn = read_bf16(row[half + f]);
+    } else {
+        rope_trig(position, inv, cs, sn);
+    }
+}
+
+__device__ __forceinline__ uint16_t rope_element(const uint16_t *token_row, int head, int d, int head_dim,
+                                                 int64_t position, float inv) {
+    float cs, sn;
+    rope_trig(position, inv, cs, sn);
+    return rope_element_cs(token_row, head, d, head_dim, cs, sn);
 }
 
 // One lane per element.  Row t sits at position start + t, or at
@@ -211,18 +235,22 @@ __global__ __launch_bounds__(256) void rope_kernel(const uint16_t *in, uint16_t 
 // rope_element computes it, so the output is bit-identical.
 __global__ __launch_bounds__(256) void rope_token_kernel(const uint16_t *in, uint16_t *out, int heads,
                                                          int head_dim, int start, const int32_t *positions,
-                                                         RopeTable table) {
+                                                         RopeTable table, RopeCosSin cossin) {
     __shared__ float cs[256], sn[256];
     const int64_t token = blockIdx.x;
     const int half = head_dim / 2;
     const int64_t position = positions ? (int64_t)positions[token] : start + token;
     // Lanes [0, half) compute c and lanes [half, 2 * half) compute s, so the
     // table costs one trigonometric evaluation per lane, not two.
-    for (int t = threadIdx.x; t < 2 * half; t += blockDim.x) {
-        const int f = t % half;
-        const float phase = __fmul_rn((float)position, table.inv[f]);
-        if (t < half) cs[f] = round_bf16((float)cos((double)phase));
-        else sn[f] = round_bf16((float)sin((double)phase));
+    if (position < cossin.positions) {
+        for (int f = threadIdx.x; f < half; f += blockDim.x) rope_cs(cossin, position, f, half, 0.0f, cs[f], sn[f]);
+    } else {
+        for (int t = threadIdx.x; t < 2 * half; t += blockDim.x) {
+            const int f = t % half;
+            const float phase = __fmul_rn((float)position, table.inv[f]);
+            if (t < half) cs[f] = round_bf16((float)cos((double)phase));
+            else sn[f] = round_bf16((float)sin((double)phase));
+        }
     }
     __syncthreads();
     const int elements = heads * head_dim;
@@ -276,17 +304,20 @@ __global__ __launch_bounds__(256) void rope_token_kernel(const uint16_t *in, uin
 // fewer consecutive token rows, and its lanes rotate (d, d + half) pairs of
 // 8-element chunks, the chunk and its rotate-half partner loaded once and
 // both outputs written, over the rows' Q heads then K heads.  Every load of
-// a lane goes out before the c and s table of the rows is computed (one
-// trigonometric evaluation per lane per row, shared by Q and K), so the
-// loads' latency hides under the table.  Each output is rope_element's value
-// for its position, bit-identical to rope_token_kernel on Q and on K.
+// a lane goes out before the rows' c and s are gathered into LDS (from the
+// context's table, or one trigonometric evaluation per lane per row where
+// the table does not reach), shared by Q and K.  Each output is
+// rope_element's value for its position, bit-identical to rope_token_kernel
+// on Q and on K.
 // head_dim % 16 == 0 and 16-byte aligned rows.
+// Four pairs per lane (three cfg2 rows per workgroup, 683 workgroups)
+// measured 9.05 us at cfg2 against 11.2 us for eight (342 workgroups).
 constexpr int kRopeRows = 8;
-constexpr int kRopePairsPerLane = 8;
+constexpr int kRopePairsPerLane = 4;
 __global__ __launch_bounds__(256) void rope_qk_kernel(const uint16_t *q, uint16_t *q_out, const uint16_t *k,
                                                       uint16_t *k_out, int tokens, int rows_per_group,
                                                       int q_heads, int kv_heads, int head_dim, int start,
-                                                      RopeTable table) {
+                                                      RopeTable table, RopeCosSin cossin) {
     __shared__ float cs[kRopeRows][kRopeTable], sn[kRopeRows][kRopeTable];
     const int half = head_dim / 2;
     const int hchunks = half / 8;                       // pair units per head
@@ -304,11 +335,18 @@ __global__ __launch_bounds__(256) void rope_qk_kernel(const uint16_t *q, uint16_
         x[j] = *reinterpret_cast<const uint4 *>(src + c);
         p[j] = *reinterpret_cast<const uint4 *>(src + c + half);
     }
-    for (int t = threadIdx.x; t < rows * 2 * half; t += 256) {
-        const int r = t / (2 * half), f = t % (2 * half) % half;
-        const float phase = __fmul_rn((float)(start + row0 + r), table.inv[f]);
-        if (t % (2 * half) < half) cs[r][f] = round_bf16((float)cos((double)phase));
-        else sn[r][f] = round_bf16((float)sin((double)phase));
+    if (start + row0 + rows <= cossin.positions) {
+        // the rows' c and s from the context's table
+        for (int t = threadIdx.x; t < rows * half; t += 256)
+            rope_cs(cossin, start + row0 + t / half, t % half, half, 0.0f, cs[t / half][t % half],
+                    sn[t / half][t % half]);
+    } else {
+        for (int t = threadIdx.x; t < rows * 2 * half; t += 256) {
+            const int r = t / (2 * half), f = t % (2 * half) % half;
+            const float phase = __fmul_rn((float)(start + row0 + r), table.inv[f]);
+            if (t % (2 * half) < half) cs[r][f] = round_bf16((float)cos((double)phase));
+            else sn[r][f] = round_bf16((float)sin((double)phase));
+        }
     }
     __syncthreads();
 #pragma unroll
@@ -348,8 +386,10 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeAppendArgs a, Rope
     if (i < nq) {
         const int64_t elements = (int64_t)a.q_heads * a.head_dim;
         const int b = (int)(i / elements), e = (int)(i % elements), d = e % a.head_dim;
-        a.q_out[i] = rope_element(a.q + b * elements, e / a.head_dim, d, a.head_dim, a.positions[b],
-                                  table.inv[d % (a.head_dim / 2)]);
+        const int half = a.head_dim / 2;
+        float cs, sn;
+        rope_cs(a.cossin, a.positions[b], d % half, half, table.inv[d % half], cs, sn);
+        a.q_out[i] = rope_element_cs(a.q + b * elements, e / a.head_dim, d, a.head_dim, cs, sn);
         return;
     }
     const int64_t kvd = (int64_t)a.kv_heads * a.head_dim;
@@ -360,8 +400,11 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeAppendArgs a, Rope
     const int32_t *rows = a.page_table + (int64_t)b * a.pages_per_seq;
     if (j < nk) {
         const int e = (int)(j % kvd), head = e / a.head_dim, d = e % a.head_dim;
+        const int half = a.head_dim / 2;
+        float cs, sn;
+        rope_cs(a.cossin, position, d % half, half, table.inv[d % half], cs, sn);
         a.k_pool[page_row(rows, a.shift, a.kv_heads, head, position) * a.head_dim + d] =
-            rope_element(a.k + b * kvd, head, d, a.head_dim, position, table.inv[d % (a.head_dim / 2)]);
+            rope_element_cs(a.k + b * kvd, head, d, a.head_dim, cs, sn);
     } else {
         const int e = (int)(((j - nk) * 8) % kvd), head = e / a.head_dim, d = e % a.head_dim;
         *reinterpret_cast<uint4 *>(a.v_pool + page_row(rows, a.shift, a.kv_heads, head, position) * a.head_dim +
@@ -531,13 +574,36 @@ const RopeTable &rope_table(int head_dim, float theta, int llama3, float factor,
 
 }  // namespace
 
+// Table rows of positions 0 .. positions - 1, one lane per (position, pair).
+__global__ __launch_bounds__(256) void rope_cossin_kernel(uint16_t *rows, int64_t positions, int half,
+                                                          RopeTable table) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= positions * half) return;
+    const int64_t p = i / half;
+    const int f = (int)(i % half);
+    float cs, sn;
+    rope_trig(p, table.inv[f], cs, sn);
+    rows[p * 2 * half + f] = write_bf16(cs);
+    rows[p * 2 * half + half + f] = write_bf16(sn);
+}
+
+hipError_t launch_rope_cossin(uint16_t *rows, int64_t positions, int head_dim, float theta, int llama3, float factor,
+                              float low, float high, float original_max, hipStream_t stream) {
+    if (head_dim > 2 * kRopeTable || head_dim % 2) return hipErrorInvalidValue;
+    const RopeTable &table = rope_table(head_dim, theta, llama3, factor, low, high, original_max);
+    const int half = head_dim / 2;
+    hipLaunchKernelGGL(rope_cossin_kernel, dim3((unsigned)((positions * half + 255) / 256)), dim3(256), 0, stream,
+                       rows, positions, half, table);
+    return hipGetLastError();
+}
+
 hipError_t launch_rope(const uint16_t *in, uint16_t *out, int tokens, int heads, int head_dim,
                        int start, const int32_t *positions, float theta, int llama3, float factor,
-                       float low, float high, float original_max, hipStream_t stream) {
+                       float low, float high, float original_max, RopeCosSin cossin, hipStream_t stream) {
     if (head_dim <= 2 * kRopeTable) {
         const RopeTable &table = rope_table(head_dim, theta, llama3, factor, low, high, original_max);
         hipLaunchKernelGGL(rope_token_kernel, dim3((unsigned)tokens), dim3(256), 0, stream, in, out, heads,
-                           head_dim, start, positions, table);
+                           head_dim, start, positions, table, cossin);
         return hipGetLastError();
     }
     const int64_t total = (int64_t)tokens * heads * head_dim;
@@ -555,14 +621,14 @@ bool rope_qk_supported(int head_dim, const void *q, const void *q_out, const voi
 
 hipError_t launch_rope_qk(const uint16_t *q, uint16_t *q_out, const uint16_t *k, uint16_t *k_out, int tokens,
                           int q_heads, int kv_heads, int head_dim, int start, float theta, int llama3, float factor,
-                          float low, float high, float original_max, hipStream_t stream) {
+                          float low, float high, float original_max, RopeCosSin cossin, hipStream_t stream) {
     const RopeTable &table = rope_table(head_dim, theta, llama3, factor, low, high, original_max);
     const int units = (q_heads + kv_heads) * (head_dim / 16);
     // rows per workgroup: as many as kRopePairsPerLane pairs per lane cover
     const int rows = std::max(1, std::min(kRopeRows, kRopePairsPerLane * 256 / units));
     if (units > kRopePairsPerLane * 256) return hipErrorInvalidValue;
     hipLaunchKernelGGL(rope_qk_kernel, dim3((unsigned)((tokens + rows - 1) / rows)), dim3(256), 0, stream, q, q_out,
-                       k, k_out, tokens, rows, q_heads, kv_heads, head_dim, start, table);
+                       k, k_out, tokens, rows, q_heads, kv_heads, head_dim, start, table, cossin);
     return hipGetLastError();
 }
 

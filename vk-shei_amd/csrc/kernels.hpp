@@ -101,10 +101,21 @@ hipError_t launch_frames_decode(const FramesLaunch &l, hipStream_t stream);
 
 hipError_t launch_rmsnorm(const uint16_t *in, const uint16_t *w, uint16_t *out, int tokens,
                           int hidden, float eps, hipStream_t stream);
+// Cos and sin of every rotary pair by position, as BF16: row p (p <
+// positions) holds c[0 .. half) then s[0 .. half), the values the RoPE
+// kernels would compute for position p.  Built once per context and RoPE
+// configuration by launch_rope_cossin; the launchers below take it
+// optionally (rows null: none) and compute positions past it themselves.
+struct RopeCosSin {
+    const uint16_t *rows = nullptr;
+    int64_t positions = 0;
+};
+hipError_t launch_rope_cossin(uint16_t *rows, int64_t positions, int head_dim, float theta, int llama3, float factor,
+                              float low, float high, float original_max, hipStream_t stream);
 // Row t at position start + t, or positions[t] (device int32) when not null.
 hipError_t launch_rope(const uint16_t *in, uint16_t *out, int tokens, int heads, int head_dim,
                        int start, const int32_t *positions, float theta, int llama3, float factor,
-                       float low, float high, float original_max, hipStream_t stream);
+                       float low, float high, float original_max, RopeCosSin cossin, hipStream_t stream);
 // RoPE of a prompt chunk's Q ([tokens][q_heads][head_dim]) and K
 // ([tokens][kv_heads][head_dim]) rows at positions start + t in one launch,
 // bit-identical to launch_rope on each; when rope_qk_supported (head_dim a
@@ -113,7 +124,7 @@ hipError_t launch_rope(const uint16_t *in, uint16_t *out, int tokens, int heads,
 bool rope_qk_supported(int head_dim, const void *q, const void *q_out, const void *k, const void *k_out);
 hipError_t launch_rope_qk(const uint16_t *q, uint16_t *q_out, const uint16_t *k, uint16_t *k_out, int tokens,
                           int q_heads, int kv_heads, int head_dim, int start, float theta, int llama3, float factor,
-                          float low, float high, float original_max, hipStream_t stream);
+                          float low, float high, float original_max, RopeCosSin cossin, hipStream_t stream);
 // A decode step's RoPE of Q and K and the append of rotated K and V to the
 // page pool, one token per sequence at positions[b] (device int32).
 struct RopeAppendArgs {
@@ -126,6 +137,7 @@ struct RopeAppendArgs {
     float theta;
     int llama3;
     float factor, low, high, original_max;
+    RopeCosSin cossin;
 };
 hipError_t launch_rope_append(const RopeAppendArgs &a, hipStream_t stream);
 // Table of swiglu_act_bf16 for every BF16 gate value (128 KiB).
