@@ -556,6 +556,23 @@ int mslim_attn_rmsnorm_gemm_swiglu(void *ctx, const void *norm_weight, float eps
                                    const void *up_weight, const void *input, void *output, int inner, int rows,
                                    int tokens);
 
+/* The head of a decode step's layer in one call (run_layer,
+ * gpu_llm/mod.rs:2056-2136: input norm, fused QKV, the two RoPEs and the K/V
+ * copy into the cache): bit-identical to mslim_attn_rmsnorm_gemm_qkv into
+ * [batch][q_heads * head_dim] / [batch][kv_heads * head_dim] rows followed by
+ * mslim_attn_rope_append with the same arguments.  q_out receives the rotated
+ * Q rows; the rotated K and the V row of sequence b go into the pools at
+ * positions[b] through page_table row b (no append for a position outside
+ * the table).  Batches of up to 8 rows of up to 4096 inputs with head_dim a
+ * multiple of 16 run as one kernel (RoPE and append in the projection's
+ * epilogue); other shapes run the two calls through a context buffer. */
+int mslim_attn_rmsnorm_qkv_rope_append(void *ctx, const void *norm_weight, float epsilon, const void *q_weight,
+                                       const void *k_weight, const void *v_weight, const void *input, void *q_out,
+                                       void *k_pool, void *v_pool, const int32_t *page_table, int pages_per_seq,
+                                       int page_tokens, int batch, const int32_t *positions, int inner, int q_heads,
+                                       int kv_heads, int head_dim, float theta, int llama3_scaling, float factor,
+                                       float low_freq_factor, float high_freq_factor, float original_max_position);
+
 #ifdef __cplusplus
 }
 #endif

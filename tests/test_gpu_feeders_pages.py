@@ -68,6 +68,28 @@ def test_rope_qk_bit_exact(ctx, tokens, qh, kvh, d, start, llama3):
                                                                       int(llama3), *params))
 
 
+@pytest.mark.parametrize("llama3", [False, True])
+def test_rope_table_equals_the_oracle_at_every_position(ctx, llama3):
+    # Rows of ones in the first half of a head and zeros in the second make
+    # RoPE output c (first half) and s (second half) of every pair, so one
+    # call over positions 0 .. 36,863 reads back the whole c/s table the
+    # context builds for them, through the per-token and the fused Q + K
+    # kernels; each must equal the oracle's c and s at every position.
+    d, tokens = 128, 36864
+    row = np.concatenate([np.full(d // 2, 0x3F80, np.uint16), np.zeros(d // 2, np.uint16)])
+    xb = np.tile(row, (tokens, 1))
+    params = (8.0, 1.0, 4.0, 8192.0) if llama3 else (1.0, 1.0, 2.0, 1.0)
+    want = oracle.rope_gpu(xb, tokens, 1, d, 0, 500000.0, int(llama3), *params)
+    out = torch.empty((tokens, 1, d), dtype=torch.int16, device="cuda")
+    ctx.rope(to_torch(xb), out, tokens, 1, d, 0, 500000.0, llama3, *params)
+    qo, ko = torch.empty_like(out), torch.empty_like(out)
+    ctx.rope_qk(to_torch(xb), qo, to_torch(xb), ko, tokens, 1, 1, d, 0, 500000.0, llama3, *params)
+    torch.cuda.synchronize()
+    for got in (out, qo, ko):
+        bad = np.nonzero(from_torch(got).reshape(-1) != want)[0]
+        assert bad.size == 0, f"{bad.size} values differ, first at position {bad[0] // d}, pair {bad[0] % d}"
+
+
 def test_rope_cossin_table_limit_and_configurations(ctx):
     # The context keeps a table of c and s by position (at most 32 MiB:
     # 131,072 positions at head_dim 128).  Rows inside it read the table,

@@ -172,6 +172,48 @@ def test_rope_append_equals_rope_then_append(ctx, page_tokens, llama3):
     assert torch.equal(q_a, q_b) and torch.equal(k_a, k_b) and torch.equal(v_a, v_b)
 
 
+@pytest.mark.parametrize("batch,inner,d,qh,kvh,page_tokens,llama3", [
+    (8, 4096, 128, 32, 8, 16, False),   # a cfg5 layer's head of the decode step: one kernel
+    (1, 4096, 128, 32, 8, 16, True),
+    (5, 512, 64, 8, 2, 32, False),
+    (3, 256, 80, 4, 2, 16, False),      # head_dim % 16 != 0: the two calls
+    (9, 512, 128, 8, 2, 16, False),     # nine rows: the two calls
+])
+def test_rmsnorm_qkv_rope_append_equals_the_two_calls(ctx, batch, inner, d, qh, kvh, page_tokens, llama3):
+    # one call == mslim_attn_rmsnorm_gemm_qkv then mslim_attn_rope_append, bit
+    # for bit: the rotated Q rows and both pools, including a position past
+    # the page table (Q rotates, nothing is appended) and pool bytes no token
+    # touches
+    rng = np.random.default_rng(batch * 131 + inner + d)
+    pps = 96 // page_tokens
+    pool_pages = batch * pps
+    table = _dev_i32(rng.permutation(pool_pages).astype(np.int32).reshape(batch, pps))
+    pos = [int(p) for p in rng.integers(0, 96, size=batch)]
+    if batch >= 3:
+        pos[2] = 96
+    positions = _dev_i32(pos)
+    params = (8.0, 1.0, 4.0, 8192.0) if llama3 else (1.0, 1.0, 2.0, 1.0)
+    x = to_torch(normal_bf16(rng, (batch, inner), 3.0))
+    nw = to_torch(normal_bf16(rng, (inner,), 0.5))
+    wq, wk, wv = (to_torch(normal_bf16(rng, (h * d, inner), 0.05)) for h in (qh, kvh, kvh))
+    shape = (pool_pages, kvh, page_tokens, d)
+    k_a, v_a = (to_torch(normal_bf16(rng, shape)) for _ in range(2))
+    k_b, v_b = k_a.clone(), v_a.clone()
+    q_a = torch.empty((batch, qh * d), dtype=torch.int16, device="cuda")
+    q_b = torch.empty_like(q_a)
+    q = torch.empty_like(q_a)
+    k = torch.empty((batch, kvh * d), dtype=torch.int16, device="cuda")
+    v = torch.empty_like(k)
+    ctx.rmsnorm_qkv_rope_append(nw, 1e-5, wq, wk, wv, x, q_a, k_a, v_a, table, pps, page_tokens, batch, positions,
+                                inner, qh, kvh, d, 500000.0, llama3, *params)
+    ctx.rmsnorm_gemm_qkv(nw, 1e-5, wq, wk, wv, x, q, k, v, inner, qh * d, kvh * d, batch)
+    ctx.rope_append(q, k, v, q_b, k_b, v_b, table, pps, page_tokens, batch, positions, qh, kvh, d, 500000.0,
+                    llama3, *params)
+    torch.cuda.synchronize()
+    assert torch.equal(q_a, q_b)
+    assert torch.equal(k_a, k_b) and torch.equal(v_a, v_b)
+
+
 def test_rope_append_rejects_head_dim_above_512(ctx):
     # the fused step takes its inverse frequencies from a 256-pair table
     from mslim_attn import MslimAttnError

@@ -45,6 +45,8 @@ struct Context {
     size_t proj_partial_bytes = 0;
     void *norm_rows = nullptr;         // normalised rows of the RMSNorm + product entries
     size_t norm_rows_bytes = 0;
+    void *qkv_rows = nullptr;          // Q, K, V rows of the unfused RMSNorm + QKV + RoPE + append
+    size_t qkv_rows_bytes = 0;
     // RoPE cos/sin by position for the last RoPE configuration used
     uint16_t *rope_rows = nullptr;
     int64_t rope_positions = 0;
@@ -81,6 +83,7 @@ struct Context {
         if (swiglu_table) (void)hipFree(swiglu_table);
         if (proj_partial) (void)hipFree(proj_partial);
         if (norm_rows) (void)hipFree(norm_rows);
+        if (qkv_rows) (void)hipFree(qkv_rows);
         if (rope_rows) (void)hipFree(rope_rows);
         if (prefill_partial) (void)hipFree(prefill_partial);
         if (prefill_counters) (void)hipFree(prefill_counters);
@@ -1486,6 +1489,74 @@ int mslim_attn_rmsnorm_gemm_swiglu(void *ctx, const void *norm_weight, float eps
                      "projection launch")
                ? 404
                : 0;
+}
+
+int mslim_attn_rmsnorm_qkv_rope_append(void *ctx, const void *norm_weight, float epsilon, const void *q_weight,
+                                       const void *k_weight, const void *v_weight, const void *input, void *q_out,
+                                       void *k_pool, void *v_pool, const int32_t *page_table, int pages_per_seq,
+                                       int page_tokens, int batch, const int32_t *positions, int inner, int q_heads,
+                                       int kv_heads, int head_dim, float theta, int llama3_scaling, float factor,
+                                       float low_freq_factor, float high_freq_factor, float original_max_position) {
+    g_error.clear();
+    const int q_rows = q_heads * head_dim, kv_rows = kv_heads * head_dim;
+    if (!ctx || !norm_args_ok(norm_weight, epsilon) || !q_weight || !k_weight || !v_weight || !input || !q_out ||
+        !k_pool || !v_pool || !page_table || !positions || batch < 1 || batch > 512 || inner < 1 ||
+        inner > 32768 || pages_per_seq < 1 || q_heads < 1 || kv_heads < 1 || head_dim < 8 || head_dim % 8 ||
+        head_dim > 512 || !is_pow2(page_tokens) || page_tokens > (1 << 20) || !(theta > 0.0f) ||
+        !std::isfinite(theta))
+        return fail("invalid RMSNorm + QKV + RoPE append arguments");
+    if (llama3_scaling && (!(factor > 0.0f) || !(high_freq_factor > low_freq_factor) ||
+                           !(low_freq_factor > 0.0f) || !(original_max_position > 0.0f)))
+        return fail("invalid llama3 RoPE scaling parameters");
+    if (q_out == input || q_out == k_pool || q_out == v_pool) return fail("Q output must not alias the inputs or pools");
+    Context &c = *ctx_of(ctx);
+    int shift = 0;
+    while ((1 << shift) < page_tokens) ++shift;
+    if (mslim::skinny_rope_supported(inner, batch, head_dim, input, q_weight, k_weight, v_weight, norm_weight)) {
+        Lock lock(c);
+        mslim::SkinnyRope r{};
+        r.positions = positions;
+        r.page_table = page_table;
+        r.k_pool = static_cast<uint16_t *>(k_pool);
+        r.v_pool = static_cast<uint16_t *>(v_pool);
+        r.pages_per_seq = pages_per_seq;
+        r.shift = shift;
+        r.kv_heads = kv_heads;
+        r.head_dim = head_dim;
+        r.theta = theta;
+        r.llama3 = llama3_scaling;
+        r.factor = factor;
+        r.low = low_freq_factor;
+        r.high = high_freq_factor;
+        r.original_max = original_max_position;
+        r.cossin = rope_cossin(c, head_dim, theta, llama3_scaling, factor, low_freq_factor, high_freq_factor,
+                               original_max_position, (int64_t)pages_per_seq << shift);
+        const mslim::SkinnyMatrix m[3] = {
+            {static_cast<const uint16_t *>(q_weight), static_cast<uint16_t *>(q_out), q_rows},
+            {static_cast<const uint16_t *>(k_weight), nullptr, kv_rows},
+            {static_cast<const uint16_t *>(v_weight), nullptr, kv_rows}};
+        return check_hip(mslim::launch_skinny_qkv_rope(m, static_cast<const uint16_t *>(input), inner, batch,
+                                                       static_cast<const uint16_t *>(norm_weight), epsilon, r,
+                                                       c.stream),
+                         "decode projection launch")
+                   ? 404
+                   : 0;
+    }
+    // Other shapes: the two calls, Q, K and V through a context buffer.
+    uint16_t *rows = nullptr;
+    {
+        Lock lock(c);
+        const size_t bytes = (size_t)batch * (q_rows + 2 * (size_t)kv_rows) * 2;
+        if (grow_device(c, &c.qkv_rows, &c.qkv_rows_bytes, bytes, "hipMalloc QKV rows")) return 400;
+        rows = static_cast<uint16_t *>(c.qkv_rows);
+    }
+    uint16_t *q = rows, *k = rows + (size_t)batch * q_rows, *v = k + (size_t)batch * kv_rows;
+    if (int rc = mslim_attn_rmsnorm_gemm_qkv(ctx, norm_weight, epsilon, q_weight, k_weight, v_weight, input, q, k, v,
+                                             inner, q_rows, kv_rows, batch))
+        return rc;
+    return mslim_attn_rope_append(ctx, q, k, v, q_out, k_pool, v_pool, page_table, pages_per_seq, page_tokens, batch,
+                                  positions, q_heads, kv_heads, head_dim, theta, llama3_scaling, factor,
+                                  low_freq_factor, high_freq_factor, original_max_position);
 }
 
 }  // extern "C"

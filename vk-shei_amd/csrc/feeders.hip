@@ -157,15 +157,6 @@ __device__ float rope_inverse_frequency(int fd, int head_dim, float theta, int l
     return inv;
 }
 
-// Inverse frequencies of the rotary pairs f = 0 .. head_dim/2 - 1 of one
-// launch, computed on the host (rope_table) with the same f32 operations as
-// rope_inverse_frequency and the same once-rounded f64 log and exp, so the
-// kernels need no f64 log or exp per lane.  Covers head_dim <= 2 * kRopeTable.
-constexpr int kRopeTable = 256;
-struct RopeTable {
-    float inv[kRopeTable];
-};
-
 // One rotated element of llm_rope / llm_prefill_rope (gpu_llm.cl:102-146,
 // :412-456): element d of head `head` of a token row [heads][head_dim] at
 // `position`, rotate-half partner, c and s rounded to BF16; `inv` is the
@@ -179,26 +170,6 @@ __device__ __forceinline__ uint16_t rope_element_cs(const uint16_t *token_row, i
     const float left = round_bf16(__fmul_rn(read_bf16(h[d]), cs));
     const float right = round_bf16(__fmul_rn(rotated, sn));
     return write_bf16(__fadd_rn(left, right));
-}
-
-// c and s of pair f at `position`: BF16(cos(position * inv)), BF16(sin(...))
-// with the phase in f32 and the functions in f64.
-__device__ __forceinline__ void rope_trig(int64_t position, float inv, float &cs, float &sn) {
-    const float phase = __fmul_rn((float)position, inv);
-    cs = round_bf16((float)cos((double)phase));
-    sn = round_bf16((float)sin((double)phase));
-}
-
-// The same from the context's table where it covers the position.
-__device__ __forceinline__ void rope_cs(const RopeCosSin &t, int64_t position, int f, int half, float inv,
-                                        float &cs, float &sn) {
-    if (position >= 0 && position < t.positions) {
-        const uint16_t *row = t.rows + position * 2 * half;
-        cs = read_bf16(row[f]);
-        sn = read_bf16(row[half + f]);
-    } else {
-        rope_trig(position, inv, cs, sn);
-    }
 }
 
 __device__ __forceinline__ uint16_t rope_element(const uint16_t *token_row, int head, int d, int head_dim,
@@ -595,6 +566,11 @@ hipError_t launch_rope_cossin(uint16_t *rows, int64_t positions, int head_dim, f
     hipLaunchKernelGGL(rope_cossin_kernel, dim3((unsigned)((positions * half + 255) / 256)), dim3(256), 0, stream,
                        rows, positions, half, table);
     return hipGetLastError();
+}
+
+const RopeTable &rope_inverse_table(int head_dim, float theta, int llama3, float factor, float low, float high,
+                                    float original_max) {
+    return rope_table(head_dim, theta, llama3, factor, low, high, original_max);
 }
 
 hipError_t launch_rope(const uint16_t *in, uint16_t *out, int tokens, int heads, int head_dim,

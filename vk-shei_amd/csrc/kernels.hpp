@@ -8,6 +8,8 @@
 
 #include <string>
 
+#include "common.hpp"
+
 namespace mslim {
 
 constexpr int kMaxBatch = 64;
@@ -110,6 +112,41 @@ struct RopeCosSin {
     const uint16_t *rows = nullptr;
     int64_t positions = 0;
 };
+// Inverse frequencies of the rotary pairs f = 0 .. head_dim/2 - 1 of one
+// launch, computed on the host with the same f32 operations as
+// rope_inverse_frequency (llm_rope, gpu_llm.cl:123-138) and the same
+// once-rounded f64 log and exp, so the kernels need no f64 log or exp per
+// lane.  Covers head_dim <= 2 * kRopeTable.  The host keeps the last one per
+// thread.
+constexpr int kRopeTable = 256;
+struct RopeTable {
+    float inv[kRopeTable];
+};
+const RopeTable &rope_inverse_table(int head_dim, float theta, int llama3, float factor, float low, float high,
+                                    float original_max);
+
+// c and s of pair f at `position`: BF16(cos(position * inv)), BF16(sin(...))
+// with the phase in f32 and the functions in f64.  No contraction: with it
+// the compiler may fold the f32 product into a double-precision FMA of the
+// inlined cos, which changes c and s at some positions.
+__device__ __forceinline__ void rope_trig(int64_t position, float inv, float &cs, float &sn) {
+#pragma clang fp contract(off)
+    const float phase = __fmul_rn((float)position, inv);
+    cs = round_bf16((float)cos((double)phase));
+    sn = round_bf16((float)sin((double)phase));
+}
+
+// The same from a RopeCosSin table where it covers the position.
+__device__ __forceinline__ void rope_cs(const RopeCosSin &t, int64_t position, int f, int half, float inv,
+                                        float &cs, float &sn) {
+    if (position >= 0 && position < t.positions) {
+        const uint16_t *row = t.rows + position * 2 * half;
+        cs = read_bf16(row[f]);
+        sn = read_bf16(row[half + f]);
+    } else {
+        rope_trig(position, inv, cs, sn);
+    }
+}
 hipError_t launch_rope_cossin(uint16_t *rows, int64_t positions, int head_dim, float theta, int llama3, float factor,
                               float low, float high, float original_max, hipStream_t stream);
 // Row t at position start + t, or positions[t] (device int32) when not null.
@@ -209,6 +246,24 @@ bool skinny_supported(int inner, int tokens, const void *x, const void *w0, cons
 bool skinny_norm_supported(int inner, int tokens, const void *norm_w);
 hipError_t launch_skinny_gemm(const SkinnyMatrix *m, int count, const uint16_t *x, int inner, int tokens,
                               hipStream_t stream, const uint16_t *norm_w = nullptr, float eps = 0.0f);
+// Q, K and V of a decode step with the RoPE and K/V append of
+// launch_rope_append in the epilogue (m[0..2] = Q, K, V; m[0].out receives
+// the rotated Q, K and V go into the pools), optionally after the RMSNorm;
+// bit-identical to the product (or RMSNorm + product) followed by
+// launch_rope_append.  When skinny_rope_supported.
+struct SkinnyRope {
+    const int32_t *positions, *page_table;
+    uint16_t *k_pool, *v_pool;
+    int pages_per_seq, shift, kv_heads, head_dim;
+    float theta;
+    int llama3;
+    float factor, low, high, original_max;
+    RopeCosSin cossin;
+};
+bool skinny_rope_supported(int inner, int tokens, int head_dim, const void *x, const void *wq, const void *wk,
+                           const void *wv, const void *norm_w);
+hipError_t launch_skinny_qkv_rope(const SkinnyMatrix *m, const uint16_t *x, int inner, int tokens,
+                                  const uint16_t *norm_w, float eps, const SkinnyRope &r, hipStream_t stream);
 hipError_t launch_skinny_gemm_add(const SkinnyMatrix &m, const uint16_t *resid, const uint16_t *x, int inner,
                                   int tokens, hipStream_t stream);
 // act_table: launch_swiglu_table's table (device, 128 KiB).

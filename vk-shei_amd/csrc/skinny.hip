@@ -37,6 +37,7 @@
 #include "kernels.hpp"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace mslim {
 
@@ -54,7 +55,8 @@ constexpr int kBlock = 32 * kUnroll;
 constexpr int kMaxSegments = 3;
 constexpr int kCus = 256;
 
-enum Epilogue { kPlain = 0, kAdd = 1, kSwiglu = 2 };
+// kQkvRope: Q, K and V with RoPE and the K/V append in the epilogue.
+enum Epilogue { kPlain = 0, kAdd = 1, kSwiglu = 2, kQkvRope = 3 };
 
 struct SkinnyArgs {
     const uint16_t *w[kMaxSegments];
@@ -70,7 +72,18 @@ struct SkinnyArgs {
     const uint16_t *act_table;  // swiglu: swiglu_act_bf16 of every BF16 gate value
     float eps;
     int inner, tokens;
+    // kQkvRope: segments Q, K, V; token t at positions[t] in page-table row t
+    const int32_t *positions, *page_table;
+    uint16_t *k_pool, *v_pool;
+    int pages_per_seq, shift, kv_heads, head_dim;
+    RopeCosSin cossin;
 };
+
+// The inverse-frequency table rides in the kernel arguments of the RoPE
+// variant only.
+struct NoRope {};
+template <int EPI>
+using RopeArg = typename std::conditional<EPI == kQkvRope, RopeTable, NoRope>::type;
 
 __device__ __forceinline__ bf16x8_t load8(const uint16_t *p) { return *reinterpret_cast<const bf16x8_t *>(p); }
 
@@ -91,7 +104,8 @@ __device__ __forceinline__ int stage_index(int row, int col) {
 }
 
 template <int EPI, bool XLDS, bool NORM, int WAVES, int DEPTH>
-__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(4))) void skinny_kernel(SkinnyArgs a) {
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(4))) void skinny_kernel(
+    SkinnyArgs a, RopeArg<EPI> rope) {
     // Partial slots per wavefront, MFMA steps per load batch (half a block
     // when two matrices stream, to fit two batches in flight in the register
     // budget) and batches per block.
@@ -118,10 +132,19 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(4)))
     // The tile's weights: lane l holds row r0 + l % 16, inputs 8 (l / 16) ..
     // +7 of each 32-input step; rows past the end re-read the last row and
     // are not written.
+    // With RoPE, a Q or K tile takes 8 rows of the first half of a head
+    // and their 8 rotate-half partners (rows 8 .. 15 of the tile), so each
+    // pair meets in lanes l and l + 32 of the output; which rows a tile
+    // reads changes nothing in how each output is summed.
     struct Tile {
         const uint16_t *wp, *up;
         uint16_t *out;
-        int rows, r0;
+        int rows, r0, seg;
+    };
+    auto rope_row = [&](int r0, int i) __attribute__((always_inline)) {
+        const int tph = a.head_dim / 16;  // tiles per head
+        const int tl = r0 / kTileRows;
+        return (tl / tph) * a.head_dim + (tl % tph) * 8 + (i < 8 ? i : a.head_dim / 2 + i - 8);
     };
     auto tile_of = [&](int tile) __attribute__((always_inline)) {
         int seg = 0;
@@ -129,8 +152,9 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(4)))
         if (a.segments > 2 && tile >= a.first_tile[2]) seg = 2;
         Tile t;
         t.rows = a.rows[seg];
+        t.seg = seg;
         t.r0 = (tile - a.first_tile[seg]) * kTileRows;
-        const int row = min(t.r0 + (lane & 15), t.rows - 1);
+        const int row = EPI == kQkvRope && seg < 2 ? rope_row(t.r0, lane & 15) : min(t.r0 + (lane & 15), t.rows - 1);
         t.wp = a.w[seg] + (int64_t)row * a.inner + kq;
         t.up = EPI == kSwiglu ? a.w_up + (int64_t)row * a.inner + kq : nullptr;
         t.out = a.out[seg];
@@ -185,6 +209,68 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(4)))
         return kb0 + (u / PB) * WAVES * kBlock + (u % PB) * 32 * UB;
     };
     const int kfirst = wave * kBlock;
+
+    // kQkvRope: the lane's token position, the pool row of kv head 0 at it
+    // (-1: nothing to append) and the c and s of its four output rows, loaded
+    // after the tile's k loop, behind the next tile's first weight batches,
+    // so that they arrive while the partial tiles are exchanged.
+    struct RopeIn {
+        int pos, row;
+        float cs[4], sn[4];
+    };
+    auto rope_fetch = [&](const Tile &cur) __attribute__((always_inline)) {
+        RopeIn in{};
+        in.row = -1;
+        if constexpr (EPI == kQkvRope) {
+            in.pos = a.positions[tok];
+            if (in.pos >= 0 && (int64_t)in.pos < ((int64_t)a.pages_per_seq << a.shift)) {
+                const int page = a.page_table[(int64_t)tok * a.pages_per_seq + (in.pos >> a.shift)];
+                in.row = ((page * a.kv_heads) << a.shift) + (in.pos & ((1 << a.shift) - 1));
+            }
+            if (cur.seg < 2) {
+                const int half = a.head_dim / 2;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int f = rope_row(cur.r0, 4 * (lane >> 4) + j) % a.head_dim % half;
+                    rope_cs(a.cossin, in.pos, f, half, rope.inv[f], in.cs[j], in.sn[j]);
+                }
+            }
+        }
+        return in;
+    };
+
+    // kQkvRope output (wave 0, live lanes): BF16 of each sum as the plain
+    // product writes it, then for Q and K the rotation of rope_append
+    // (x c + (-+partner) s, each product rounded, BF16 sum), Q to out[0] and
+    // K and V into the page pools at the token's position; positions outside
+    // the page table append nothing, as rope_append.
+    auto rope_epilogue = [&](const Tile &cur, const floatx4_t &sum, const RopeIn &in) __attribute__((always_inline)) {
+        if constexpr (EPI == kQkvRope) {
+            const int rp_row = in.row;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int i = 4 * (lane >> 4) + j;
+                const uint16_t y = write_bf16(sum[j]);
+                if (cur.seg == 2) {
+                    const int r = cur.r0 + i;
+                    if (rp_row >= 0 && r < cur.rows)
+                        a.v_pool[((int64_t)rp_row + ((int64_t)(r / a.head_dim) << a.shift)) * a.head_dim +
+                                 r % a.head_dim] = y;
+                    continue;
+                }
+                const uint16_t partner = (uint16_t)__shfl_xor((int)y, 32, 64);
+                const int r = rope_row(cur.r0, i);
+                const int head = r / a.head_dim, d = r % a.head_dim;
+                const float p = read_bf16(partner);
+                const float left = round_bf16(__fmul_rn(read_bf16(y), in.cs[j]));
+                const float right = round_bf16(__fmul_rn(i < 8 ? -p : p, in.sn[j]));
+                const uint16_t o = write_bf16(__fadd_rn(left, right));
+                if (cur.seg == 0) cur.out[(int64_t)tok * cur.rows + r] = o;
+                else if (rp_row >= 0)
+                    a.k_pool[((int64_t)rp_row + ((int64_t)head << a.shift)) * a.head_dim + d] = o;
+            }
+        }
+    };
 
     int tile = blockIdx.x;
     Batch ring[DEPTH];
@@ -303,6 +389,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(4)))
         }
     }
 
+
     while (true) {
 #pragma unroll
         for (int m = 0; m < NS; ++m) {
@@ -333,6 +420,8 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(4)))
             for (int d = 0; d < DEPTH; ++d)
                 if (k_of(kfirst, d) < a.inner) load_batch(ring[d], t, k_of(kfirst, d));
         }
+        RopeIn rin{};
+        if (EPI == kQkvRope && wave == 0 && live) rin = rope_fetch(cur);
         floatx4_t sum, sum_up;
 #pragma unroll
         for (int p = 0; p < (EPI == kSwiglu ? 2 : 1); ++p) {
@@ -347,7 +436,9 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(4)))
             }
             __syncthreads();  // the partials are read before they are written again
         }
-        if (wave == 0 && live) {
+        if constexpr (EPI == kQkvRope) {
+            if (wave == 0 && live) rope_epilogue(cur, sum, rin);
+        } else if (wave == 0 && live) {
             // D layout: lane l holds rows 4*(l/16) + j, token l%16.
             uint16_t *out = cur.out + (int64_t)tok * cur.rows;
 #pragma unroll
@@ -391,7 +482,7 @@ Shape skinny_shape(int epi, bool xlds, bool norm) {
 }
 
 template <int EPI, bool XLDS, bool NORM>
-hipError_t launch_with(SkinnyArgs &a, hipStream_t stream) {
+hipError_t launch_with(SkinnyArgs &a, hipStream_t stream, const RopeArg<EPI> &rope = {}) {
     int tiles = 0;
     for (int s = 0; s < a.segments; ++s) {
         a.first_tile[s] = tiles;
@@ -401,9 +492,9 @@ hipError_t launch_with(SkinnyArgs &a, hipStream_t stream) {
     const Shape sh = skinny_shape(EPI, XLDS, NORM);
     const unsigned grid = (unsigned)std::min(tiles, sh.per_cu * kCus);
     if constexpr (EPI == kSwiglu && XLDS && !NORM)
-        hipLaunchKernelGGL((skinny_kernel<EPI, XLDS, NORM, 8, 4>), dim3(grid), dim3(8 * 64), 0, stream, a);
+        hipLaunchKernelGGL((skinny_kernel<EPI, XLDS, NORM, 8, 4>), dim3(grid), dim3(8 * 64), 0, stream, a, rope);
     else
-        hipLaunchKernelGGL((skinny_kernel<EPI, XLDS, NORM, 8, 2>), dim3(grid), dim3(8 * 64), 0, stream, a);
+        hipLaunchKernelGGL((skinny_kernel<EPI, XLDS, NORM, 8, 2>), dim3(grid), dim3(8 * 64), 0, stream, a, rope);
     return hipGetLastError();
 }
 
@@ -445,6 +536,41 @@ hipError_t launch_skinny_gemm(const SkinnyMatrix *m, int count, const uint16_t *
     a.norm_w = norm_w;
     a.eps = eps;
     return launch<kPlain>(a, stream);
+}
+
+bool skinny_rope_supported(int inner, int tokens, int head_dim, const void *x, const void *wq, const void *wk,
+                           const void *wv, const void *norm_w) {
+    return skinny_supported(inner, tokens, x, wq, wk, wv) && tokens <= kStageTokens && inner <= kStageInner &&
+           aligned16(norm_w) && head_dim % 16 == 0 && head_dim >= 16 && head_dim <= 2 * kRopeTable;
+}
+
+hipError_t launch_skinny_qkv_rope(const SkinnyMatrix *m, const uint16_t *x, int inner, int tokens,
+                                  const uint16_t *norm_w, float eps, const SkinnyRope &r, hipStream_t stream) {
+    SkinnyArgs a{};
+    for (int s = 0; s < 3; ++s) {
+        a.w[s] = m[s].w;
+        a.out[s] = m[s].out;
+        a.rows[s] = m[s].rows;
+    }
+    a.segments = 3;
+    a.x = x;
+    a.inner = inner;
+    a.tokens = tokens;
+    a.norm_w = norm_w;
+    a.eps = eps;
+    a.positions = r.positions;
+    a.page_table = r.page_table;
+    a.k_pool = r.k_pool;
+    a.v_pool = r.v_pool;
+    a.pages_per_seq = r.pages_per_seq;
+    a.shift = r.shift;
+    a.kv_heads = r.kv_heads;
+    a.head_dim = r.head_dim;
+    a.cossin = r.cossin;
+    const RopeTable &table =
+        rope_inverse_table(r.head_dim, r.theta, r.llama3, r.factor, r.low, r.high, r.original_max);
+    if (!norm_w) return launch_with<kQkvRope, true, false>(a, stream, table);
+    return launch_with<kQkvRope, true, true>(a, stream, table);
 }
 
 hipError_t launch_skinny_gemm_add(const SkinnyMatrix &m, const uint16_t *resid, const uint16_t *x, int inner,

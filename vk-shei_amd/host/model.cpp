@@ -252,7 +252,6 @@ std::vector<Step> DecoderRunner::forward_batch(const std::vector<int32_t> &token
         std::lock_guard<std::mutex> lock(ctx_->mutex());
         void *h = ctx_->handle();
         const ModelSpec &s = spec_;
-        const int qd = s.q_heads * s.head_dim, kvd = s.kv_heads * s.head_dim;
         ctx_->check("upload token ids",
                     mslim_attn_buf_write(h, ids_, 0, reinterpret_cast<const uint8_t *>(tokens.data()), (size_t)b * 4));
         ctx_->check("upload positions", mslim_attn_buf_write(h, pos_, 0, reinterpret_cast<const uint8_t *>(pos.data()),
@@ -261,13 +260,12 @@ std::vector<Step> DecoderRunner::forward_batch(const std::vector<int32_t> &token
         for (int l = 0; l < s.layers; ++l) {
             const LayerWeights &w = w_.layers[l];
             injected_error(l);
-            ctx_->check("input norm + QKV projection",
-                        mslim_attn_rmsnorm_gemm_qkv(h, w.input_norm, s.rms_eps, w.q, w.k, w.v, x_, q_, k_, v_,
-                                                    s.hidden, qd, kvd, b));
-            ctx_->check("RoPE + K/V append",
-                        mslim_attn_rope_append(h, q_, k_, v_, qr_, k_pools_[l], v_pools_[l], table_, pages_per_seq_,
-                                               page_tokens_, b, pos_, s.q_heads, s.kv_heads, s.head_dim, s.rope_theta,
-                                               s.llama3, s.rope_factor, s.rope_low, s.rope_high, s.rope_original_max));
+            ctx_->check("input norm + QKV + RoPE + K/V append",
+                        mslim_attn_rmsnorm_qkv_rope_append(h, w.input_norm, s.rms_eps, w.q, w.k, w.v, x_, qr_,
+                                                           k_pools_[l], v_pools_[l], table_, pages_per_seq_,
+                                                           page_tokens_, b, pos_, s.hidden, s.q_heads, s.kv_heads,
+                                                           s.head_dim, s.rope_theta, s.llama3, s.rope_factor,
+                                                           s.rope_low, s.rope_high, s.rope_original_max));
             if (layout_ == KvLayout::Dense)
                 ctx_->check("dense attention",
                             mslim_attn_decode_dense(h, qr_, k_pools_[l], v_pools_[l], attn_, b, lens.data(), max_context_,

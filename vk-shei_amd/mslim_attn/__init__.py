@@ -95,6 +95,7 @@ EXPORTS = (
     "mslim_attn_rmsnorm_gemm_bf16",
     "mslim_attn_rmsnorm_gemm_qkv",
     "mslim_attn_rmsnorm_gemm_swiglu",
+    "mslim_attn_rmsnorm_qkv_rope_append",
     "mslim_attn_add",
     "mslim_attn_embed",
     "mslim_attn_argmax",
@@ -183,6 +184,8 @@ def library() -> C.CDLL:
         "mslim_attn_rmsnorm_gemm_bf16": (I, [P, P, F, P, P, P, I, I, I]),
         "mslim_attn_rmsnorm_gemm_qkv": (I, [P, P, F, P, P, P, P, P, P, P, I, I, I, I]),
         "mslim_attn_rmsnorm_gemm_swiglu": (I, [P, P, F, P, P, P, P, I, I, I]),
+        "mslim_attn_rmsnorm_qkv_rope_append": (I, [P, P, F, P, P, P, P, P, P, P, P, I, I, I, P, I, I, I, I, F, I, F,
+                                                   F, F, F]),
         "mslim_attn_add": (I, [P, P, P, P, SZ]),
         "mslim_attn_embed": (I, [P, P, I, I, P, I, P, P]),
         "mslim_attn_argmax": (I, [P, P, I, I, P]),
@@ -523,6 +526,17 @@ class Context:
         self._check("rmsnorm_gemm_swiglu", self._lib.mslim_attn_rmsnorm_gemm_swiglu(
             self._h, _ptr(norm_weight), eps, _ptr(gate_weight), _ptr(up_weight), _ptr(input_dev), _ptr(output),
             inner, rows, tokens))
+
+    def rmsnorm_qkv_rope_append(self, norm_weight, eps: float, q_weight, k_weight, v_weight, input_dev, q_out,
+                                k_pool, v_pool, page_table, pages_per_seq: int, page_tokens: int, batch: int,
+                                positions, inner: int, q_heads: int, kv_heads: int, head_dim: int, theta: float,
+                                llama3_scaling: bool = False, factor: float = 1.0, low_freq_factor: float = 1.0,
+                                high_freq_factor: float = 2.0, original_max_position: float = 1.0) -> None:
+        self._check("rmsnorm_qkv_rope_append", self._lib.mslim_attn_rmsnorm_qkv_rope_append(
+            self._h, _ptr(norm_weight), eps, _ptr(q_weight), _ptr(k_weight), _ptr(v_weight), _ptr(input_dev),
+            _ptr(q_out), _ptr(k_pool), _ptr(v_pool), _ptr(page_table), pages_per_seq, page_tokens, batch,
+            _ptr(positions), inner, q_heads, kv_heads, head_dim, theta, int(bool(llama3_scaling)), factor,
+            low_freq_factor, high_freq_factor, original_max_position))
 
     def add(self, a, b, out, n: int) -> None:
         self._check("add", self._lib.mslim_attn_add(self._h, _ptr(a), _ptr(b), _ptr(out), n))
