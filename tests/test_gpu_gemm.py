@@ -110,6 +110,32 @@ def test_decode_batch_product_within_bound(ctx, inner, rows, tokens):
     assert within_bound(host_bits(out), w, x, inner, rows, tokens)
 
 
+@pytest.mark.parametrize("inner", [4096, 8192, 14336, 4128])
+def test_decode_product_does_not_depend_on_the_batch(ctx, inner):
+    # A token's output is the same whichever batch it rides in: 8 tokens
+    # (token rows staged in LDS up to 4096 inputs) against the first 8 of 9
+    # (token rows read from L2 every k-step) and a 1-token call, bit for bit,
+    # plain and with the residual add
+    rng = np.random.default_rng(inner)
+    rows = 208
+    w, x = bf16(rng, rows * inner, 0.02), bf16(rng, 9 * inner)
+    resid = bf16(rng, 9 * rows, 2.0)
+    wd = dev_bits(w)
+    outs = {}
+    for t in (9, 8, 1):
+        out = torch.empty(t * rows, dtype=torch.int16, device="cuda")
+        add = torch.empty(t * rows, dtype=torch.int16, device="cuda")
+        ctx.gemm_bf16(wd, dev_bits(x[: t * inner]), out, inner, rows, t)
+        ctx.gemm_bf16_add(wd, dev_bits(x[: t * inner]), dev_bits(resid[: t * rows]), add, inner, rows, t)
+        outs[t] = (out, add)
+    torch.cuda.synchronize()
+    for i in range(2):
+        nine = host_bits(outs[9][i])
+        assert np.array_equal(host_bits(outs[8][i]), nine[: 8 * rows])
+        assert np.array_equal(host_bits(outs[1][i]), nine[:rows])
+    assert within_bound(host_bits(outs[9][0]), w, x, inner, rows, 9)
+
+
 def test_unaligned_inner_uses_library_path(ctx):
     rng = np.random.default_rng(9)
     inner, rows, tokens = 4104, 300, 4
