@@ -49,7 +49,12 @@
 extern "C" {
 #endif
 
-#define MSLIM_ATTN_MAX_BATCH 64 /* sequences per decode launch */
+/* Sequences per decode launch.  Launches of up to 64 sequences carry their
+ * launch tables in the kernel arguments; larger ones copy the tables (16
+ * bytes per sequence) host to device on the context stream before the
+ * kernel, so they cannot be recorded into a graph, and the allocation-free
+ * entry point takes at most 64. */
+#define MSLIM_ATTN_MAX_BATCH 4096
 
 /* ---- Context and errors -------------------------------------------------- */
 

@@ -130,7 +130,7 @@ def test_auto_split_invariants():
 
 def test_auto_split_rejects_bad_batches():
     from mslim_attn import MslimAttnError, auto_split
-    for lens, kvh in (([], 8), ([0], 8), ([5] * 65, 8), ([5], 0)):
+    for lens, kvh in (([], 8), ([0], 8), ([5] * 4097, 8), ([5], 0)):
         with pytest.raises(MslimAttnError, match="code=-1"):
             auto_split(lens, kvh)
 

@@ -246,6 +246,8 @@ def test_decode_rejects_bad_arguments(ctx):
             ctx.decode_dense(q, k, k, out, [64], 8, 8, 128, **kwargs)
     with pytest.raises(mslim_attn.MslimAttnError, match="seq_lens"):
         ctx.decode_dense(q, k, k, out, [0], 8, 8, 128)
+    with pytest.raises(mslim_attn.MslimAttnError, match="1..4096"):
+        ctx.decode_dense(q, k, k, out, [1] * 4097, 8, 8, 128, seq_stride_tokens=64)
     with pytest.raises(mslim_attn.MslimAttnError, match="geometry"):
         ctx.decode_dense(q, k, k, out, [64], 8, 3, 128)
     table = torch.zeros((1, 4), dtype=torch.int32, device="cuda")
@@ -451,3 +453,78 @@ def test_decode_option_rejects_unknown_values(ctx):
         ctx.set_option(mslim_attn.OPT_DECODE_MERGE, 2)
     with pytest.raises(mslim_attn.MslimAttnError, match="unknown context option"):
         ctx.set_option(99, 0)
+
+
+def _chunked(fn, batch, step):
+    """fn(lo, hi) for consecutive sequence ranges of at most `step`."""
+    for lo in range(0, batch, step):
+        fn(lo, min(batch, lo + step))
+
+
+def test_decode_batches_past_the_kernel_argument_tables(ctx):
+    # Launches of more than 64 sequences read their launch tables from a
+    # device copy made on the stream before the kernel.  Partitions are fixed
+    # by logical token index, so a sequence's output does not depend on the
+    # batch it rides in: 300 sequences in one launch equal the same sequences
+    # in launches of at most 64, bit for bit, dense and paged, under the fused
+    # and the separate merge; 100 single-partition sequences (800 partitions
+    # over 8 kv heads) take the list mode with the tables on the device.
+    # Six large launches are queued back to back, more than the context's
+    # ring of table buffers, before anything is read back.
+    gen = torch.Generator(device="cuda").manual_seed(4096)
+    rng = np.random.default_rng(4096)
+    qh, kvh, d, pt, split = 32, 8, 128, 16, 256
+    batch = 300
+    lens = [int(x) for x in rng.integers(1, 700, size=batch)]
+    lens[:100] = [int(x) for x in rng.integers(1, split + 1, size=100)]
+    stride = max(lens)
+    k = torch.randn((batch, stride, kvh, d), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    v = torch.randn((batch, stride, kvh, d), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    q = torch.randn((batch, qh, d), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    k_pool, v_pool, table_t, pps, _ = _paged_pool(ctx, k, v, lens, stride, pt, seed=77)
+
+    def dense(lo, hi, out):
+        ctx.decode_dense(q[lo:hi], k[lo:hi], v[lo:hi], out[lo:hi], lens[lo:hi], qh, kvh, d,
+                         seq_stride_tokens=stride, split_tokens=split)
+
+    def paged(lo, hi, out):
+        ctx.decode_paged(q[lo:hi], k_pool, v_pool, out[lo:hi], lens[lo:hi], table_t[lo:hi], pps, pt,
+                         qh, kvh, d, split_tokens=split)
+
+    def run():
+        outs = [torch.full_like(q, -1) for _ in range(6)]
+        dense(0, batch, outs[0])
+        paged(0, batch, outs[1])
+        dense(0, 100, outs[2])   # list mode, tables on the device
+        paged(0, 100, outs[3])
+        dense(64, batch, outs[4])
+        paged(64, batch, outs[5])
+        torch.cuda.synchronize()
+        return [from_torch(o).reshape(batch, -1) for o in outs]
+
+    fused, separate = _merge_modes(ctx, run)
+    small = [torch.full_like(q, -1) for _ in range(2)]
+    _chunked(lambda lo, hi: dense(lo, hi, small[0]), batch, 64)
+    _chunked(lambda lo, hi: paged(lo, hi, small[1]), batch, 50)
+    torch.cuda.synchronize()
+    want = from_torch(small[0]).reshape(batch, -1)
+    assert np.array_equal(from_torch(small[1]).reshape(batch, -1), want)
+    for outs in (fused, separate):
+        assert np.array_equal(outs[0], want) and np.array_equal(outs[1], want)
+        assert np.array_equal(outs[2][:100], want[:100]) and np.array_equal(outs[3][:100], want[:100])
+        assert np.array_equal(outs[4][64:], want[64:]) and np.array_equal(outs[5][64:], want[64:])
+    for b in (0, 99, 100, int(np.argmax(lens)), batch - 1):
+        t = lens[b]
+        ref = _oracle_decode(from_torch(q[b]), from_torch(k[b, :t]), from_torch(v[b, :t]), qh, kvh, d)
+        check_bf16(want[b], ref, TOL, "test_decode_batches_past_the_kernel_argument_tables")
+    # the library's own split for the whole batch: paged == dense, and parity
+    auto_d, auto_p = torch.empty_like(q), torch.empty_like(q)
+    ctx.decode_dense(q, k, v, auto_d, lens, qh, kvh, d, seq_stride_tokens=stride)
+    ctx.decode_paged(q, k_pool, v_pool, auto_p, lens, table_t, pps, pt, qh, kvh, d)
+    torch.cuda.synchronize()
+    assert torch.equal(auto_d, auto_p)
+    got = from_torch(auto_d).reshape(batch, -1)
+    for b in (3, int(np.argmax(lens))):
+        t = lens[b]
+        ref = _oracle_decode(from_torch(q[b]), from_torch(k[b, :t]), from_torch(v[b, :t]), qh, kvh, d)
+        check_bf16(got[b], ref, TOL, "decode of 300 sequences, automatic split")

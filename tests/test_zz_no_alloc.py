@@ -99,3 +99,13 @@ def test_noalloc_decode_rejects_partials_above_the_fixed_array(ctx):
     table = torch.zeros((64, pps), dtype=torch.int32, device="cuda")
     with pytest.raises(mslim_attn.MslimAttnError, match="16777216-byte scratch"):
         ctx.decode_paged_noalloc(q, pool, pool, out, lens, table, pps, pt, qh, kvh, d, split_tokens=64)
+
+
+def test_noalloc_decode_rejects_more_sequences_than_the_kernel_arguments_hold(ctx):
+    # Above 64 sequences the launch tables need a device copy, which the
+    # allocation-free entry point does not make; the host check refuses it.
+    qh, kvh, d, pt = 8, 8, 128, 16
+    q, k_pool, v_pool, table, pps = _pool([16] * 65, qh, kvh, d, pt, seed=65)
+    out = torch.empty_like(q)
+    with pytest.raises(mslim_attn.MslimAttnError, match="at most 64 sequences"):
+        ctx.decode_paged_noalloc(q, k_pool, v_pool, out, [16] * 65, table, pps, pt, qh, kvh, d, split_tokens=64)

@@ -54,6 +54,15 @@ struct Context {
     float rope_key[6] = {};    // head_dim, theta, llama3, factor, low, high
     float rope_key_max = 0.0f;  // original_max
     size_t workspace_bytes = 0;
+    // Decode launch tables beyond the kernel arguments: a ring of pinned
+    // host / device buffer pairs, each free again once its event completes.
+    static constexpr int kTableSlots = 4;
+    struct TableSlot {
+        void *host = nullptr, *device = nullptr;
+        size_t host_bytes = 0, device_bytes = 0;
+        hipEvent_t done = nullptr;
+    } table_slot[kTableSlots];
+    int table_next = 0;
     int *counters = nullptr;        // decode split counters, zero between launches
     size_t counter_bytes = 0;
     bool counters_dirty = false;    // a decode launch failed: clear before the next
@@ -88,6 +97,11 @@ struct Context {
         if (prefill_partial) (void)hipFree(prefill_partial);
         if (prefill_counters) (void)hipFree(prefill_counters);
         if (counters) (void)hipFree(counters);
+        for (TableSlot &t : table_slot) {
+            if (t.host) (void)hipHostFree(t.host);
+            if (t.device) (void)hipFree(t.device);
+            if (t.done) (void)hipEventDestroy(t.done);
+        }
         if (staging) (void)hipFree(staging);
         if (host_staging) (void)hipHostFree(host_staging);
         if (backend) (void)hipFree(backend);
@@ -150,10 +164,12 @@ struct Lock {
     int saved = -1;
 };
 
+static_assert(MSLIM_ATTN_MAX_BATCH == mslim::kMaxBatch, "decode batch limit of the C ABI and the launcher");
+
 // Argument checks and the split choice shared by every decode entry point.
 int decode_prepare(mslim::DecodeLaunch &l, const int32_t *seq_lens, int split_tokens) {
     if (l.batch < 1 || l.batch > MSLIM_ATTN_MAX_BATCH || !seq_lens)
-        return fail("decode batch must be 1..64 with host seq_lens");
+        return fail("decode batch must be 1..4096 with host seq_lens");
     if (!valid_geometry(l.q_heads, l.kv_heads, l.head_dim))
         return fail("decode geometry invalid (q_heads % kv_heads, head_dim multiple of 8 <= 256)");
     if (!l.q || !l.k || !l.v || !l.out) return fail("decode needs non-null q, k, v, out");
@@ -188,7 +204,7 @@ int decode_common(Context &c, mslim::DecodeLaunch &l, const int32_t *seq_lens, i
     decode_place_partials(l, c.workspace);
     // One split counter per (sequence, kv head); the kernel leaves them at
     // zero, so they are cleared only when the buffer is (re)allocated.
-    const size_t ctr_bytes = (size_t)MSLIM_ATTN_MAX_BATCH * l.kv_heads * sizeof(int);
+    const size_t ctr_bytes = (size_t)std::max(l.batch, mslim::kInlineBatch) * l.kv_heads * sizeof(int);
     if (c.counter_bytes < ctr_bytes) {
         void *mem = c.counters;
         if (int rc = grow_device(c, &mem, &c.counter_bytes, ctr_bytes, "hipMalloc decode split counters"))
@@ -205,6 +221,25 @@ int decode_common(Context &c, mslim::DecodeLaunch &l, const int32_t *seq_lens, i
     }
     l.counters = c.counters;
     l.separate_merge = c.separate_merge;
+    mslim::DecodeTables tables{};
+    if (const size_t bytes = mslim::decode_table_bytes(l)) {
+        hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+        if (int rc = check_hip(hipStreamIsCapturing(c.stream, &capture), "hipStreamIsCapturing")) return rc;
+        if (capture != hipStreamCaptureStatusNone)
+            return fail("decode of more than 64 sequences copies its launch tables host to device and "
+                        "cannot be recorded into a graph");
+        Context::TableSlot &t = c.table_slot[c.table_next];
+        c.table_next = (c.table_next + 1) % Context::kTableSlots;
+        // The slot's previous launch has read both buffers once this returns.
+        if (!t.done)
+            if (int rc = check_hip(hipEventCreateWithFlags(&t.done, hipEventDisableTiming), "hipEventCreate tables"))
+                return rc;
+        if (int rc = check_hip(hipEventSynchronize(t.done), "decode tables wait")) return rc;
+        if (int rc = grow_host(&t.host, &t.host_bytes, bytes, "hipHostMalloc decode tables")) return rc;
+        if (int rc = grow_device(c, &t.device, &t.device_bytes, bytes, "hipMalloc decode tables")) return rc;
+        tables = mslim::DecodeTables{t.host, t.device, bytes, t.done};
+        l.tables = &tables;
+    }
     const int rc = check_hip(mslim::launch_decode(l, c.stream), "decode attention launch");
     // A launch that failed may have left counts behind: clear them before
     // the next fused merge relies on them.
@@ -468,7 +503,7 @@ int mslim_attn_buf_write(void *ctx, void *buffer, size_t offset, const uint8_t *
 int mslim_attn_decode_auto_split(const int32_t *seq_lens, int batch, int kv_heads) {
     g_error.clear();
     if (!seq_lens || batch < 1 || batch > MSLIM_ATTN_MAX_BATCH || kv_heads < 1)
-        return fail("decode batch must be 1..64 with host seq_lens and kv_heads >= 1");
+        return fail("decode batch must be 1..4096 with host seq_lens and kv_heads >= 1");
     for (int i = 0; i < batch; ++i)
         if (seq_lens[i] < 1) return fail("decode seq_lens must be >= 1");
     return mslim::decode_auto_split_tokens(seq_lens, batch, kv_heads);
@@ -573,6 +608,9 @@ int mslim_attn_decode_paged_noalloc(void *ctx, const void *q, const void *k_pool
     // The merge runs as its own launch, so no counter has to start at zero.
     l.counters = nullptr;
     l.separate_merge = true;
+    if (mslim::decode_table_bytes(l))
+        return fail("allocation-free decode takes at most 64 sequences (launch tables in the kernel "
+                    "arguments); use mslim_attn_decode_paged");
     return check_hip(mslim::launch_decode(l, c.stream), "decode attention launch");
 }
 

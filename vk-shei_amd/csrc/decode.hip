@@ -55,9 +55,18 @@ constexpr int kWaves = 4;
 constexpr int kDepth = 2;
 constexpr int kTile = 32;
 // List mode: two lists per CU (two workgroups fit), at most kMaxListItems
-// partitions in all (the tables ride in the kernel arguments).
+// partitions in all.
 constexpr int kListBins = 512;
 constexpr int kMaxListItems = 896;
+
+// Launch tables.  32-bit words: seq_len[batch] | split_begin[batch + 1] |
+// full_begin[batch + 1]; 16-bit halves: last_order[batch] |
+// bin_start[list_bins + 1] | list[items].  Launches of up to kInlineBatch
+// sequences carry them in the kernel arguments (words / halves); larger ones
+// read a device copy made on the stream before the launch (ext_words /
+// ext_halves non-zero).  Either way the kernel reads them with scalar loads.
+constexpr int kInlineWords = 3 * kInlineBatch + 2;
+constexpr int kInlineHalves = (kInlineBatch + kListBins + 1 + kMaxListItems + 1) / 2 * 2;
 
 struct DeviceArgs {
     const uint16_t *q, *k, *v;
@@ -71,21 +80,52 @@ struct DeviceArgs {
     int batch, q_heads, kv_heads;
     int split_tokens;
     float scale_log2e;
-    int seq_len[kMaxBatch];
-    int split_begin[kMaxBatch + 1];
-    // Launch order of the partitions: every sequence's partitions but its
-    // last, in sequence order (full_begin: prefix counts), then the last
-    // partitions, longest first (last_order: sequence indices).
-    int full_begin[kMaxBatch + 1];
-    int16_t last_order[kMaxBatch];
     // List mode (list_bins > 0, the LIST kernel): workgroup w runs the
     // partitions list[i], bin_start[w] <= i < bin_start[w + 1], one after
     // another, each given by its launch index (what blockIdx.x is in the
     // one-partition-per-workgroup kernel).
     int list_bins;
-    uint16_t bin_start[kListBins + 1];
-    uint16_t list[kMaxListItems];
+    uint64_t ext_words, ext_halves;
+    // Launch order of the partitions: every sequence's partitions but its
+    // last, in sequence order (full_begin: prefix counts), then the last
+    // partitions, longest first (last_order: sequence indices).
+    int32_t words[kInlineWords];
+    uint16_t halves[kInlineHalves];
 };
+
+typedef const __attribute__((address_space(4))) uint32_t ConstantU32;
+
+// The launch tables as the kernel reads them (constant address space, so a
+// uniform index becomes a scalar load; halves are read as their aligned
+// dword).
+struct Tables {
+    ConstantU32 *w, *h;
+    int batch, bins;
+    __device__ int half(int i) const { return (int)((h[i >> 1] >> ((i & 1) * 16)) & 0xFFFFu); }
+    __device__ int seq_len(int b) const { return (int)w[b]; }
+    __device__ int split_begin(int b) const { return (int)w[batch + b]; }
+    __device__ int full_begin(int b) const { return (int)w[2 * batch + 1 + b]; }
+    __device__ int last_order(int i) const { return half(i); }
+    __device__ int bin_start(int i) const { return half(batch + i); }
+    __device__ int list(int i) const { return half(batch + bins + 1 + i); }
+};
+
+// Every kernel here takes the DeviceArgs as its first argument, at offset 0
+// of the kernel-argument segment.
+__device__ __forceinline__ Tables tables_of(const DeviceArgs &a) {
+    Tables t;
+    if (a.ext_words) {
+        t.w = reinterpret_cast<ConstantU32 *>(a.ext_words);
+        t.h = reinterpret_cast<ConstantU32 *>(a.ext_halves);
+    } else {
+        const auto base = (const __attribute__((address_space(4))) char *)__builtin_amdgcn_kernarg_segment_ptr();
+        t.w = reinterpret_cast<ConstantU32 *>(base + offsetof(DeviceArgs, words));
+        t.h = reinterpret_cast<ConstantU32 *>(base + offsetof(DeviceArgs, halves));
+    }
+    t.batch = a.batch;
+    t.bins = a.list_bins;
+    return t;
+}
 
 // Base of the 16-token block starting at logical token t0 (a multiple of 16).
 template <int D, bool PAGED>
@@ -193,6 +233,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void decode_kernel(DeviceArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int row16 = lane & 15;
     const int grp = lane >> 4;
+    const Tables tab = tables_of(a);
     // One partition, given by its launch index (kv head fastest).
     auto partition = [&](const int launch_index) __attribute__((always_inline)) {
     const int kvh = launch_index % a.kv_heads;
@@ -202,16 +243,23 @@ __global__ __launch_bounds__(64 * kWaves, 2) void decode_kernel(DeviceArgs a) {
     // once, the dispatcher hands the short ones to the CUs that free up.
     // The partition's logical index (split_begin[b] + split) is unchanged.
     int b = 0, split = 0;
-    const int full_total = a.full_begin[a.batch];
+    const int full_total = tab.full_begin(a.batch);
     if (sg < full_total) {
-        while (b + 1 < a.batch && a.full_begin[b + 1] <= sg) ++b;
-        split = sg - a.full_begin[b];
+        // the last sequence whose full partitions begin at or before sg
+        // (full_begin does not decrease and starts at 0)
+        int hi = a.batch - 1;
+        while (b < hi) {
+            const int mid = (b + hi + 1) >> 1;
+            if (tab.full_begin(mid) <= sg) b = mid;
+            else hi = mid - 1;
+        }
+        split = sg - tab.full_begin(b);
     } else {
-        b = a.last_order[sg - full_total];
-        split = a.split_begin[b + 1] - a.split_begin[b] - 1;
+        b = tab.last_order(sg - full_total);
+        split = tab.split_begin(b + 1) - tab.split_begin(b) - 1;
     }
-    const int nsplit = a.split_begin[b + 1] - a.split_begin[b];
-    const int seq_len = a.seq_len[b];
+    const int nsplit = tab.split_begin(b + 1) - tab.split_begin(b);
+    const int seq_len = tab.seq_len(b);
     const int begin = split * a.split_tokens;
     const int end = min(seq_len, begin + a.split_tokens);
     const int ntiles = (end - begin + kTile - 1) / kTile;
@@ -398,7 +446,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void decode_kernel(DeviceArgs a) {
     const bool final_write = nsplit == 1;
     // Partials are stored by logical partition index, the order the merge
     // reads them in, whatever the launch order.
-    const int64_t part = ((int64_t)(a.split_begin[b] + split) * a.kv_heads + kvh) * G;
+    const int64_t part = ((int64_t)(tab.split_begin(b) + split) * a.kv_heads + kvh) * G;
     for (int it = tid; it < ITEMS; it += 64 * kWaves) {
         const int g = it / (D / 4);
         const int d = (it % (D / 4)) * 4;
@@ -466,10 +514,10 @@ __global__ __launch_bounds__(64 * kWaves, 2) void decode_kernel(DeviceArgs a) {
     }
     };
     if constexpr (LIST) {
-        const int i0 = a.bin_start[blockIdx.x], i1 = a.bin_start[blockIdx.x + 1];
+        const int i0 = tab.bin_start(blockIdx.x), i1 = tab.bin_start(blockIdx.x + 1);
         for (int i = i0; i < i1; ++i) {
             if (i > i0) __syncthreads();  // the previous partition's LDS is free
-            partition(a.list[i]);
+            partition(tab.list(i));
         }
     } else {
         partition((int)blockIdx.x);
@@ -485,8 +533,9 @@ __global__ __launch_bounds__(64 * kWaves, 2) void decode_kernel(DeviceArgs a) {
 template <int D, int G>
 __device__ __forceinline__ void merge_splits(const DeviceArgs &a, int b, int kvh, int tid, int nthreads,
                                              bool coherent) {
-    const int nsplit = a.split_begin[b + 1] - a.split_begin[b];
-    const int s0 = a.split_begin[b];
+    const Tables tab = tables_of(a);
+    const int nsplit = tab.split_begin(b + 1) - tab.split_begin(b);
+    const int s0 = tab.split_begin(b);
     const float c = a.scale_log2e;
     const int qh0 = kvh * G;
     for (int it = tid; it < G * D / 4; it += nthreads) {
@@ -548,7 +597,8 @@ template <int D, int G>
 __global__ __launch_bounds__(256) void decode_merge_kernel(DeviceArgs a) {
     const int kvh = blockIdx.x % a.kv_heads;
     const int b = blockIdx.x / a.kv_heads;
-    if (a.split_begin[b + 1] - a.split_begin[b] <= 1) return;
+    const Tables tab = tables_of(a);
+    if (tab.split_begin(b + 1) - tab.split_begin(b) <= 1) return;
     merge_splits<D, G>(a, b, kvh, threadIdx.x, 256, false);
 }
 
@@ -564,7 +614,7 @@ __global__ __launch_bounds__(64) void decode_generic_kernel(DeviceArgs a, int D)
     const int qh = blockIdx.x % a.q_heads;
     const int group = a.q_heads / a.kv_heads;
     const int kvh = qh / group;
-    const int seq_len = a.seq_len[b];
+    const int seq_len = tables_of(a).seq_len(b);
     const float c = a.scale_log2e;
     const uint16_t *q = a.q + ((int64_t)b * a.q_heads + qh) * D;
     auto row_ptr = [&](const uint16_t *cache, int t) -> const uint16_t * {
@@ -788,17 +838,30 @@ int decode_auto_split_tokens(const int32_t *seq_lens, int batch, int kv_heads) {
 // allocation-free entry point plans too.
 constexpr int64_t kListItemCost = 256;
 
-void plan_lists(DeviceArgs &a, int total, const int32_t *seq_len) {
-    const int kvh = a.kv_heads;
+// Host view of the launch tables, in the layout of DeviceArgs::words and
+// DeviceArgs::halves (or of their device copy).
+struct TableWriter {
+    int32_t *w;
+    uint16_t *h;
+    int batch, bins;
+    int32_t &seq_len(int b) { return w[b]; }
+    int32_t &split_begin(int b) { return w[batch + b]; }
+    int32_t &full_begin(int b) { return w[2 * batch + 1 + b]; }
+    uint16_t &last_order(int i) { return h[i]; }
+    uint16_t &bin_start(int i) { return h[batch + i]; }
+    uint16_t &list(int i) { return h[batch + bins + 1 + i]; }
+};
+
+void plan_lists(TableWriter &t, int total, int kvh, int split_tokens) {
     const int items = total * kvh;
-    const int full = a.full_begin[a.batch];
+    const int full = t.full_begin(t.batch);
     std::pair<int, int> order[kMaxListItems];  // (tokens, launch index)
     for (int i = 0; i < items; ++i) {
         const int sg = i / kvh;
-        int tokens = a.split_tokens;
+        int tokens = split_tokens;
         if (sg >= full) {
-            const int b = a.last_order[sg - full];
-            tokens = seq_len[b] - (a.split_begin[b + 1] - a.split_begin[b] - 1) * a.split_tokens;
+            const int b = t.last_order(sg - full);
+            tokens = t.seq_len(b) - (t.split_begin(b + 1) - t.split_begin(b) - 1) * split_tokens;
         }
         order[i] = {tokens, i};
     }
@@ -822,13 +885,40 @@ void plan_lists(DeviceArgs &a, int total, const int32_t *seq_len) {
         std::push_heap(heap, heap + kListBins, later);
     }
     int cursor[kListBins];
-    a.bin_start[0] = 0;
+    t.bin_start(0) = 0;
     for (int w = 0; w < kListBins; ++w) {
-        cursor[w] = a.bin_start[w];
-        a.bin_start[w + 1] = (uint16_t)(a.bin_start[w] + count[w]);
+        cursor[w] = t.bin_start(w);
+        t.bin_start(w + 1) = (uint16_t)(t.bin_start(w) + count[w]);
     }
-    for (int i = 0; i < items; ++i) a.list[cursor[bin_of[i]]++] = (uint16_t)order[i].second;
-    a.list_bins = kListBins;
+    for (int i = 0; i < items; ++i) t.list(cursor[bin_of[i]]++) = (uint16_t)order[i].second;
+}
+
+// Layout of a launch's tables: partitions in all, list mode, and where they
+// go (the kernel arguments, or a device copy of word_bytes of words followed
+// by half_bytes of halves).
+struct TablePlan {
+    int total = 0;
+    bool lists = false;
+    bool inline_args = true;
+    size_t word_bytes = 0, half_bytes = 0;
+};
+
+TablePlan table_plan(const DecodeLaunch &l) {
+    TablePlan p;
+    for (int i = 0; i < l.batch; ++i) p.total += decode_splits(l.seq_len[i], l.split_tokens);
+    const int64_t items = (int64_t)p.total * l.kv_heads;
+    p.lists = decode_fast_path(l.head_dim, l.q_heads / l.kv_heads) && !l.separate_merge && items > kListBins &&
+              items <= kMaxListItems;
+    const int64_t halves = l.batch + (p.lists ? kListBins + 1 + items : 0);
+    p.inline_args = l.batch <= kInlineBatch && halves <= kInlineHalves;
+    p.word_bytes = ((size_t)(3 * l.batch + 2) * 4 + 255) & ~(size_t)255;
+    p.half_bytes = ((size_t)halves * 2 + 3) & ~(size_t)3;
+    return p;
+}
+
+size_t decode_table_bytes(const DecodeLaunch &l) {
+    const TablePlan p = table_plan(l);
+    return p.inline_args ? 0 : p.word_bytes + p.half_bytes;
 }
 
 bool decode_fast_path(int head_dim, int group) {
@@ -836,54 +926,12 @@ bool decode_fast_path(int head_dim, int group) {
            (group == 1 || group == 2 || group == 4 || group == 8 || group == 16);
 }
 
-hipError_t launch_decode(const DecodeLaunch &l, hipStream_t stream) {
-    DeviceArgs a{};
-    a.q = l.q; a.k = l.k; a.v = l.v; a.out = l.out;
-    a.partial_ml = l.partial_ml; a.partial_acc = l.partial_acc;
-    a.counters = l.counters;
-    a.page_table = l.page_table;
-    a.seq_stride_tokens = l.seq_stride_tokens;
-    a.pages_per_seq = l.pages_per_seq;
-    a.page_shift = 0;
-    if (l.paged) {
-        while ((1 << a.page_shift) < l.page_tokens) ++a.page_shift;
-    }
-    a.batch = l.batch; a.q_heads = l.q_heads; a.kv_heads = l.kv_heads;
-    a.split_tokens = l.split_tokens;
-    a.scale_log2e = l.scale * kLog2e;
-    int total = 0;
-    bool merge = false;
-    int64_t kv_tokens = 0;
-    for (int i = 0; i < l.batch; ++i) {
-        kv_tokens += l.seq_len[i];
-        a.seq_len[i] = l.seq_len[i];
-        a.split_begin[i] = total;
-        const int n = decode_splits(l.seq_len[i], l.split_tokens);
-        merge |= n > 1;
-        total += n;
-    }
-    a.split_begin[l.batch] = total;
-    int full = 0;
-    for (int i = 0; i < l.batch; ++i) {
-        a.full_begin[i] = full;
-        full += a.split_begin[i + 1] - a.split_begin[i] - 1;
-        a.last_order[i] = (int16_t)i;
-    }
-    a.full_begin[l.batch] = full;
-    auto last_len = [&](int i) {
-        return l.seq_len[i] - (a.split_begin[i + 1] - a.split_begin[i] - 1) * l.split_tokens;
-    };
-    // Longest last partition first, ties in sequence order; no allocation
-    // (std::stable_sort may take a temporary buffer from the heap).
-    std::sort(a.last_order, a.last_order + l.batch, [&](int16_t x, int16_t y) {
-        const int lx = last_len(x), ly = last_len(y);
-        return lx != ly ? lx > ly : x < y;
-    });
+namespace {
+
+hipError_t launch_kernels(const DeviceArgs &a, const DecodeLaunch &l, int total, bool merge, int64_t kv_tokens,
+                          hipStream_t stream) {
     const int group = l.q_heads / l.kv_heads;
     const bool nt = kv_tokens * l.kv_heads * l.head_dim * 2 * 2 >= kNonTemporalBytes;
-    const int64_t items = (int64_t)total * l.kv_heads;
-    if (decode_fast_path(l.head_dim, group) && !l.separate_merge && items > kListBins && items <= kMaxListItems)
-        plan_lists(a, total, l.seq_len);
     if (!decode_fast_path(l.head_dim, group)) {
         const dim3 grid((unsigned)(l.batch * l.q_heads));
         if (l.paged)
@@ -907,6 +955,76 @@ hipError_t launch_decode(const DecodeLaunch &l, hipStream_t stream) {
     MSLIM_DECODE_CASE(64, 1)
 #undef MSLIM_DECODE_CASE
     return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+hipError_t launch_decode(const DecodeLaunch &l, hipStream_t stream) {
+    DeviceArgs a{};
+    a.q = l.q; a.k = l.k; a.v = l.v; a.out = l.out;
+    a.partial_ml = l.partial_ml; a.partial_acc = l.partial_acc;
+    a.counters = l.counters;
+    a.page_table = l.page_table;
+    a.seq_stride_tokens = l.seq_stride_tokens;
+    a.pages_per_seq = l.pages_per_seq;
+    a.page_shift = 0;
+    if (l.paged) {
+        while ((1 << a.page_shift) < l.page_tokens) ++a.page_shift;
+    }
+    a.batch = l.batch; a.q_heads = l.q_heads; a.kv_heads = l.kv_heads;
+    a.split_tokens = l.split_tokens;
+    a.scale_log2e = l.scale * kLog2e;
+    const TablePlan plan = table_plan(l);
+    TableWriter t{a.words, a.halves, l.batch, plan.lists ? kListBins : 0};
+    if (!plan.inline_args) {
+        if (!l.tables || l.tables->bytes < plan.word_bytes + plan.half_bytes) return hipErrorInvalidValue;
+        t.w = static_cast<int32_t *>(l.tables->host);
+        t.h = reinterpret_cast<uint16_t *>(static_cast<char *>(l.tables->host) + plan.word_bytes);
+    }
+    int total = 0;
+    bool merge = false;
+    int64_t kv_tokens = 0;
+    for (int i = 0; i < l.batch; ++i) {
+        kv_tokens += l.seq_len[i];
+        t.seq_len(i) = l.seq_len[i];
+        t.split_begin(i) = total;
+        const int n = decode_splits(l.seq_len[i], l.split_tokens);
+        merge |= n > 1;
+        total += n;
+    }
+    t.split_begin(l.batch) = total;
+    int full = 0;
+    for (int i = 0; i < l.batch; ++i) {
+        t.full_begin(i) = full;
+        full += t.split_begin(i + 1) - t.split_begin(i) - 1;
+        t.last_order(i) = (uint16_t)i;
+    }
+    t.full_begin(l.batch) = full;
+    auto last_len = [&](int i) {
+        return l.seq_len[i] - (t.split_begin(i + 1) - t.split_begin(i) - 1) * l.split_tokens;
+    };
+    // Longest last partition first, ties in sequence order; no allocation
+    // (std::stable_sort may take a temporary buffer from the heap).
+    std::sort(t.h, t.h + l.batch, [&](uint16_t x, uint16_t y) {
+        const int lx = last_len(x), ly = last_len(y);
+        return lx != ly ? lx > ly : x < y;
+    });
+    if (plan.lists) {
+        plan_lists(t, total, l.kv_heads, l.split_tokens);
+        a.list_bins = kListBins;
+    }
+    if (!plan.inline_args) {
+        const hipError_t err = hipMemcpyAsync(l.tables->device, l.tables->host, plan.word_bytes + plan.half_bytes,
+                                              hipMemcpyHostToDevice, stream);
+        if (err != hipSuccess) return err;
+        a.ext_words = (uint64_t)reinterpret_cast<uintptr_t>(l.tables->device);
+        a.ext_halves = a.ext_words + plan.word_bytes;
+    }
+    const hipError_t err = launch_kernels(a, l, total, merge, kv_tokens, stream);
+    // The host and device copies of the tables are free again once the
+    // launches are done.
+    if (err == hipSuccess && !plan.inline_args) return hipEventRecord(l.tables->done, stream);
+    return err;
 }
 
 }  // namespace mslim

@@ -12,7 +12,22 @@
 
 namespace mslim {
 
-constexpr int kMaxBatch = 64;
+// Sequences per decode launch.  Launches of up to kInlineBatch sequences
+// carry their launch tables in the kernel arguments; larger ones copy them to
+// the device on the stream first (DecodeTables).
+constexpr int kMaxBatch = 4096;
+constexpr int kInlineBatch = 64;
+
+// A pinned host buffer and a device buffer of `bytes` each for the launch
+// tables of a decode launch that does not carry them in its arguments, and
+// the event recorded after the launches that read them: the caller waits for
+// it before reusing the buffers.
+struct DecodeTables {
+    void *host;
+    void *device;
+    size_t bytes;
+    hipEvent_t done;
+};
 
 struct DecodeLaunch {
     const uint16_t *q;
@@ -30,12 +45,14 @@ struct DecodeLaunch {
     float scale;
     int split_tokens;           // multiple of 64
     int seq_len[kMaxBatch];
-    int split_begin[kMaxBatch + 1];
     bool paged;
     // false: the last split workgroup of each (sequence, kv head) merges the
     // partials (counters needed); true: a merge launch follows the decode
     // launch (counters unused).  Both give the same bits.
     bool separate_merge;
+    // Launches whose tables do not fit the kernel arguments
+    // (decode_table_bytes > 0) need these buffers.
+    const DecodeTables *tables;
 };
 
 // Number of split partitions of a sequence of `tokens` tokens.
@@ -49,6 +66,9 @@ int decode_auto_split_tokens(const int32_t *seq_lens, int batch, int kv_heads);
 // True when the MFMA fast path covers this geometry.
 bool decode_fast_path(int head_dim, int group);
 hipError_t launch_decode(const DecodeLaunch &a, hipStream_t stream);
+// Bytes of the device copy of a launch's tables (0: they fit the kernel
+// arguments).  Needs seq_len, split_tokens, the geometry and separate_merge.
+size_t decode_table_bytes(const DecodeLaunch &l);
 // Split-partial bytes a decode launch of this shape needs.
 size_t decode_partial_bytes(const DecodeLaunch &l);
 // A file-scope device array of kDecodeStaticBytes that the allocation-free

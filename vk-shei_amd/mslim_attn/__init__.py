@@ -20,7 +20,7 @@ from typing import Optional, Sequence
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmslim_attn.so")
 
-MAX_BATCH = 64
+MAX_BATCH = 4096  # MSLIM_ATTN_MAX_BATCH; launches above 64 sequences copy their tables to the device
 OPT_DECODE_MERGE = 1                        # mslim_attn_ctx_set_option options
 DECODE_MERGE_FUSED, DECODE_MERGE_SEPARATE = 0, 1
 OPT_PREFILL_SPLIT = 2
