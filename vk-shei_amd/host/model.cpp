@@ -40,7 +40,7 @@ DecoderRunner::DecoderRunner(std::shared_ptr<NativeContext> ctx, ModelSpec spec,
     for (const auto &l : w_.layers)
         ensure(l.input_norm && l.q && l.k && l.v && l.o && l.post_norm && l.gate && l.up && l.down,
                "every layer needs all nine weight tensors");
-    ensure(max_batch_ >= 1 && max_batch_ <= MSLIM_ATTN_MAX_BATCH, "max_batch must be 1..=64");
+    ensure(max_batch_ >= 1 && max_batch_ <= kMaxSlots, "max_batch must be 1..=64");
     ensure(chunk_tokens_ >= 1 && chunk_tokens_ <= 512, "prefill chunk must be 1..=512 tokens");
     ensure(max_context_ >= 1 && max_context_ <= (1 << 24), "max_context must be 1..=16777216 tokens");
     ensure(layout_ == KvLayout::Paged || layout_ == KvLayout::Dense, "unknown K/V layout");

@@ -73,6 +73,10 @@ struct ColdReport {
     double last_restore_seconds = 0.0;
 };
 
+// Sequence slots per runner: every decode step's launch tables then travel in
+// the kernel arguments (no host-to-device copy inside a step).
+constexpr int kMaxSlots = 64;
+
 class DecoderRunner {
 public:
     static constexpr int kPageTokens = 16;
