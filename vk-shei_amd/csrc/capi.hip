@@ -866,6 +866,14 @@ int mslim_attn_rope(void *ctx, const void *input, void *output, int tokens, int 
     const mslim::RopeCosSin table = rope_cossin(c, head_dim, theta, llama3_scaling, factor, low_freq_factor,
                                                 high_freq_factor, original_max_position,
                                                 (int64_t)start_position + tokens);
+    // The Q + K kernel with no K rows: the same bits, several rows per
+    // workgroup.
+    if (mslim::rope_qk_supported(head_dim, input, output, input, output) && heads * head_dim <= 32768)
+        return check_hip(mslim::launch_rope_qk(static_cast<const uint16_t *>(input), static_cast<uint16_t *>(output),
+                                               nullptr, nullptr, tokens, heads, 0, head_dim, start_position, theta,
+                                               llama3_scaling, factor, low_freq_factor, high_freq_factor,
+                                               original_max_position, table, c.stream),
+                         "RoPE launch");
     return check_hip(mslim::launch_rope(static_cast<const uint16_t *>(input),
                                         static_cast<uint16_t *>(output), tokens, heads, head_dim,
                                         start_position, nullptr, theta, llama3_scaling, factor,
