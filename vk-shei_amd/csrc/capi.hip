@@ -1019,22 +1019,13 @@ int mslim_attn_pages_append(void *ctx, void *k_pool, void *v_pool, const int32_t
                      "page append launch");
 }
 
-int mslim_attn_rope_append(void *ctx, const void *q, const void *k, const void *v, void *q_out, void *k_pool,
-                           void *v_pool, const int32_t *page_table, int pages_per_seq, int page_tokens, int batch,
-                           const int32_t *positions, int q_heads, int kv_heads, int head_dim, float theta,
-                           int llama3_scaling, float factor, float low_freq_factor, float high_freq_factor,
-                           float original_max_position) {
-    g_error.clear();
-    if (!ctx || !q || !k || !v || !q_out || !k_pool || !v_pool || !page_table || !positions || batch < 1 ||
-        pages_per_seq < 1 || q_heads < 1 || kv_heads < 1 || head_dim < 8 || head_dim % 8 || head_dim > 512 ||
-        !is_pow2(page_tokens) || page_tokens > (1 << 20) || !(theta > 0.0f) || !std::isfinite(theta))
-        return fail("invalid RoPE append arguments");
-    if (q_out == q) return fail("RoPE output must not alias its input");
-    if (llama3_scaling && (!(factor > 0.0f) || !(high_freq_factor > low_freq_factor) ||
-                           !(low_freq_factor > 0.0f) || !(original_max_position > 0.0f)))
-        return fail("invalid llama3 RoPE scaling parameters");
-    Context &c = *ctx_of(ctx);
-    Lock lock(c);
+// RoPE of Q and K and the append of K and V on a context already locked,
+// arguments checked.
+static int rope_append_locked(Context &c, const void *q, const void *k, const void *v, void *q_out, void *k_pool,
+                              void *v_pool, const int32_t *page_table, int pages_per_seq, int page_tokens, int batch,
+                              const int32_t *positions, int q_heads, int kv_heads, int head_dim, float theta,
+                              int llama3_scaling, float factor, float low_freq_factor, float high_freq_factor,
+                              float original_max_position) {
     mslim::RopeAppendArgs a{};
     a.q = static_cast<const uint16_t *>(q);
     a.k = static_cast<const uint16_t *>(k);
@@ -1061,6 +1052,27 @@ int mslim_attn_rope_append(void *ctx, const void *q, const void *k, const void *
     a.cossin = rope_cossin(c, head_dim, theta, llama3_scaling, factor, low_freq_factor, high_freq_factor,
                            original_max_position, (int64_t)pages_per_seq << a.shift);
     return check_hip(mslim::launch_rope_append(a, c.stream), "RoPE append launch");
+}
+
+int mslim_attn_rope_append(void *ctx, const void *q, const void *k, const void *v, void *q_out, void *k_pool,
+                           void *v_pool, const int32_t *page_table, int pages_per_seq, int page_tokens, int batch,
+                           const int32_t *positions, int q_heads, int kv_heads, int head_dim, float theta,
+                           int llama3_scaling, float factor, float low_freq_factor, float high_freq_factor,
+                           float original_max_position) {
+    g_error.clear();
+    if (!ctx || !q || !k || !v || !q_out || !k_pool || !v_pool || !page_table || !positions || batch < 1 ||
+        pages_per_seq < 1 || q_heads < 1 || kv_heads < 1 || head_dim < 8 || head_dim % 8 || head_dim > 512 ||
+        !is_pow2(page_tokens) || page_tokens > (1 << 20) || !(theta > 0.0f) || !std::isfinite(theta))
+        return fail("invalid RoPE append arguments");
+    if (q_out == q) return fail("RoPE output must not alias its input");
+    if (llama3_scaling && (!(factor > 0.0f) || !(high_freq_factor > low_freq_factor) ||
+                           !(low_freq_factor > 0.0f) || !(original_max_position > 0.0f)))
+        return fail("invalid llama3 RoPE scaling parameters");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    return rope_append_locked(c, q, k, v, q_out, k_pool, v_pool, page_table, pages_per_seq, page_tokens, batch,
+                              positions, q_heads, kv_heads, head_dim, theta, llama3_scaling, factor, low_freq_factor,
+                              high_freq_factor, original_max_position);
 }
 
 int mslim_attn_pages_gather(void *ctx, const void *pool, const int32_t *page_table, int page_tokens,
@@ -1460,17 +1472,10 @@ int mslim_attn_rmsnorm_gemm_bf16(void *ctx, const void *norm_weight, float epsil
     return project(c, weight, x, output, inner, rows, tokens);
 }
 
-int mslim_attn_rmsnorm_gemm_qkv(void *ctx, const void *norm_weight, float epsilon, const void *q_weight,
-                                const void *k_weight, const void *v_weight, const void *input, void *q_out,
-                                void *k_out, void *v_out, int inner, int q_rows, int kv_rows, int tokens) {
-    g_error.clear();
-    if (!gemm_args_ok(ctx, q_weight, input, q_out, inner, q_rows, tokens) ||
-        !gemm_args_ok(ctx, k_weight, input, k_out, inner, kv_rows, tokens) ||
-        !gemm_args_ok(ctx, v_weight, input, v_out, inner, kv_rows, tokens) || !norm_args_ok(norm_weight, epsilon))
-        return fail("invalid RMSNorm + BF16 matrix arguments");
-    if (q_out == input || k_out == input || v_out == input) return fail("GEMM output must not alias its inputs");
-    Context &c = *ctx_of(ctx);
-    Lock lock(c);
+// RMSNorm + QKV on a context already locked, arguments checked.
+static int rmsnorm_gemm_qkv_locked(Context &c, const void *norm_weight, float epsilon, const void *q_weight,
+                                   const void *k_weight, const void *v_weight, const void *input, void *q_out,
+                                   void *k_out, void *v_out, int inner, int q_rows, int kv_rows, int tokens) {
     const mslim::SkinnyMatrix m[3] = {
         {static_cast<const uint16_t *>(q_weight), static_cast<uint16_t *>(q_out), q_rows},
         {static_cast<const uint16_t *>(k_weight), static_cast<uint16_t *>(k_out), kv_rows},
@@ -1495,6 +1500,21 @@ int mslim_attn_rmsnorm_gemm_qkv(void *ctx, const void *norm_weight, float epsilo
                      "projection launch")
                ? 404
                : 0;
+}
+
+int mslim_attn_rmsnorm_gemm_qkv(void *ctx, const void *norm_weight, float epsilon, const void *q_weight,
+                                const void *k_weight, const void *v_weight, const void *input, void *q_out,
+                                void *k_out, void *v_out, int inner, int q_rows, int kv_rows, int tokens) {
+    g_error.clear();
+    if (!gemm_args_ok(ctx, q_weight, input, q_out, inner, q_rows, tokens) ||
+        !gemm_args_ok(ctx, k_weight, input, k_out, inner, kv_rows, tokens) ||
+        !gemm_args_ok(ctx, v_weight, input, v_out, inner, kv_rows, tokens) || !norm_args_ok(norm_weight, epsilon))
+        return fail("invalid RMSNorm + BF16 matrix arguments");
+    if (q_out == input || k_out == input || v_out == input) return fail("GEMM output must not alias its inputs");
+    Context &c = *ctx_of(ctx);
+    Lock lock(c);
+    return rmsnorm_gemm_qkv_locked(c, norm_weight, epsilon, q_weight, k_weight, v_weight, input, q_out, k_out, v_out,
+                                   inner, q_rows, kv_rows, tokens);
 }
 
 int mslim_attn_rmsnorm_gemm_swiglu(void *ctx, const void *norm_weight, float epsilon, const void *gate_weight,
@@ -1544,22 +1564,22 @@ int mslim_attn_rmsnorm_qkv_rope_append(void *ctx, const void *norm_weight, float
                                        int kv_heads, int head_dim, float theta, int llama3_scaling, float factor,
                                        float low_freq_factor, float high_freq_factor, float original_max_position) {
     g_error.clear();
-    const int q_rows = q_heads * head_dim, kv_rows = kv_heads * head_dim;
     if (!ctx || !norm_args_ok(norm_weight, epsilon) || !q_weight || !k_weight || !v_weight || !input || !q_out ||
         !k_pool || !v_pool || !page_table || !positions || batch < 1 || batch > 512 || inner < 1 ||
         inner > 32768 || pages_per_seq < 1 || q_heads < 1 || kv_heads < 1 || head_dim < 8 || head_dim % 8 ||
-        head_dim > 512 || !is_pow2(page_tokens) || page_tokens > (1 << 20) || !(theta > 0.0f) ||
-        !std::isfinite(theta))
+        head_dim > 512 || (int64_t)q_heads * head_dim > 500000 || (int64_t)kv_heads * head_dim > 500000 ||
+        !is_pow2(page_tokens) || page_tokens > (1 << 20) || !(theta > 0.0f) || !std::isfinite(theta))
         return fail("invalid RMSNorm + QKV + RoPE append arguments");
+    const int q_rows = q_heads * head_dim, kv_rows = kv_heads * head_dim;
     if (llama3_scaling && (!(factor > 0.0f) || !(high_freq_factor > low_freq_factor) ||
                            !(low_freq_factor > 0.0f) || !(original_max_position > 0.0f)))
         return fail("invalid llama3 RoPE scaling parameters");
     if (q_out == input || q_out == k_pool || q_out == v_pool) return fail("Q output must not alias the inputs or pools");
     Context &c = *ctx_of(ctx);
+    Lock lock(c);
     int shift = 0;
     while ((1 << shift) < page_tokens) ++shift;
     if (mslim::skinny_rope_supported(inner, batch, head_dim, input, q_weight, k_weight, v_weight, norm_weight)) {
-        Lock lock(c);
         mslim::SkinnyRope r{};
         r.positions = positions;
         r.page_table = page_table;
@@ -1588,21 +1608,19 @@ int mslim_attn_rmsnorm_qkv_rope_append(void *ctx, const void *norm_weight, float
                    ? 404
                    : 0;
     }
-    // Other shapes: the two calls, Q, K and V through a context buffer.
-    uint16_t *rows = nullptr;
-    {
-        Lock lock(c);
-        const size_t bytes = (size_t)batch * (q_rows + 2 * (size_t)kv_rows) * 2;
-        if (grow_device(c, &c.qkv_rows, &c.qkv_rows_bytes, bytes, "hipMalloc QKV rows")) return 400;
-        rows = static_cast<uint16_t *>(c.qkv_rows);
-    }
-    uint16_t *q = rows, *k = rows + (size_t)batch * q_rows, *v = k + (size_t)batch * kv_rows;
-    if (int rc = mslim_attn_rmsnorm_gemm_qkv(ctx, norm_weight, epsilon, q_weight, k_weight, v_weight, input, q, k, v,
-                                             inner, q_rows, kv_rows, batch))
+    // Other shapes: the two operations, Q, K and V through a context buffer,
+    // under the one lock (another call on the context may not regrow the
+    // buffer in between).
+    const size_t bytes = (size_t)batch * (q_rows + 2 * (size_t)kv_rows) * 2;
+    if (grow_device(c, &c.qkv_rows, &c.qkv_rows_bytes, bytes, "hipMalloc QKV rows")) return 400;
+    uint16_t *q = static_cast<uint16_t *>(c.qkv_rows);
+    uint16_t *k = q + (size_t)batch * q_rows, *v = k + (size_t)batch * kv_rows;
+    if (int rc = rmsnorm_gemm_qkv_locked(c, norm_weight, epsilon, q_weight, k_weight, v_weight, input, q, k, v, inner,
+                                         q_rows, kv_rows, batch))
         return rc;
-    return mslim_attn_rope_append(ctx, q, k, v, q_out, k_pool, v_pool, page_table, pages_per_seq, page_tokens, batch,
-                                  positions, q_heads, kv_heads, head_dim, theta, llama3_scaling, factor,
-                                  low_freq_factor, high_freq_factor, original_max_position);
+    return rope_append_locked(c, q, k, v, q_out, k_pool, v_pool, page_table, pages_per_seq, page_tokens, batch,
+                              positions, q_heads, kv_heads, head_dim, theta, llama3_scaling, factor, low_freq_factor,
+                              high_freq_factor, original_max_position);
 }
 
 }  // extern "C"

@@ -38,12 +38,10 @@ namespace mslim {
 
 namespace {
 
-#ifndef PROJ_BK
-#define PROJ_BK 64
-#define PROJ_ST 3
-#endif
 constexpr int kBM = 128;   // weight rows per workgroup tile
-constexpr int kKAlign = PROJ_BK;  // inner must be a multiple of this for the tiled kernel
+constexpr int kBK = 64;    // inputs per k-step
+constexpr int kStages = 3; // LDS ring stages
+constexpr int kKAlign = kBK;  // inner must be a multiple of this for the tiled kernel
 constexpr int kXcds = 8;
 constexpr int kMaxSeg = 3;
 
@@ -477,18 +475,18 @@ hipError_t launch(ProjArgs &a, hipStream_t stream) {
     for (int s = 0; s < a.segments; ++s) a.out_base[s + 1] = a.out_base[s] + (int64_t)a.rows[s] * a.tokens;
     for (int s = a.segments + 1; s <= kMaxSeg; ++s) a.out_base[s] = a.out_base[a.segments];
     const bool wide = (a.ksplit > 1 || m_tiles * ((a.tokens + 127) / 128) >= 192) &&
-                      proj_lds_bytes(64, PROJ_BK, PROJ_ST, EPI) <= 163840;
+                      proj_lds_bytes(64, kBK, kStages, EPI) <= 163840;
     const int bn = wide ? 128 : 64;
     a.n_tiles = (a.tokens + bn - 1) / bn;
     const int64_t tiles = m_tiles * a.n_tiles * a.ksplit;
     const unsigned grid = (unsigned)(((tiles + kXcds - 1) / kXcds) * kXcds);
-    if constexpr (proj_lds_bytes(64, PROJ_BK, PROJ_ST, EPI) <= 163840) {
+    if constexpr (proj_lds_bytes(64, kBK, kStages, EPI) <= 163840) {
         if (wide) {
-            hipLaunchKernelGGL((proj_kernel<64, PROJ_BK, PROJ_ST, EPI>), dim3(grid), dim3(256), 0, stream, a);
+            hipLaunchKernelGGL((proj_kernel<64, kBK, kStages, EPI>), dim3(grid), dim3(256), 0, stream, a);
             return hipGetLastError();
         }
     }
-    hipLaunchKernelGGL((proj_kernel<32, PROJ_BK, PROJ_ST, EPI>), dim3(grid), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((proj_kernel<32, kBK, kStages, EPI>), dim3(grid), dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 
