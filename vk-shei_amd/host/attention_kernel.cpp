@@ -101,8 +101,8 @@ void AttentionKernelConfig::validate() const {
 }
 
 void AttentionKernelConfig::check_snapshot(const json::Value *recorded) const {
-    // Legacy snapshots predate tiled kernels and therefore belong to
-    // reference mode.
+    // A snapshot without an attention record was taken before tiled kernels
+    // existed: it compares as the default (reference) configuration.
     const AttentionKernelConfig r = recorded ? from_value(*recorded) : AttentionKernelConfig{};
     r.validate();
     ensure(*this == r, "snapshot attention numeric configuration mismatch");

@@ -531,9 +531,9 @@ void ColdStore::write_record(const uint8_t *const *parts, const size_t *lens, in
 
 PageMeta ColdStore::commit(PageMeta meta, const uint8_t *const *parts, const size_t *lens, int nparts,
                            bool durable) {
-    // cold_store.rs:367-389: the store ends at the last committed record; a
-    // torn tail left by an earlier failed append is cut first, and a failed
-    // append rolls the file back again.
+    // cold_store.rs:367-389: a record is written at the end of the committed
+    // records (bytes an earlier failed append left there are cut off first);
+    // if this write fails, the file is cut back to that same offset.
     const uint64_t record_offset = committed_end();
     if (file_len(fd_) != record_offset && ftruncate(fd_, (off_t)record_offset) != 0)
         io_error("truncate " + path_, errno);
@@ -598,13 +598,17 @@ void ColdStore::rebuild_catalogue() {
     try {
         while (offset < len) {
             const uint64_t remaining = len - offset;
-            if (remaining < kHeaderLen) break;  // torn uncommitted tail
+            // Too short for a header: a write stopped before any record
+            // could commit, so the file's store ends here.
+            if (remaining < kHeaderLen) break;
             uint8_t header[kHeaderLen];
             read_exact_at(fd_, offset, header, kHeaderLen);
             PageMeta m = parse_header(header, offset);
             const uint64_t record_len =
                 kHeaderLen + (uint64_t)m.geometry.tokens * 16 + m.key_len + m.value_len + kFooterLen;
-            if (record_len > remaining) break;  // footer cannot exist: never committed
+            // The header promises more bytes than the file holds, so the
+            // footer of this record was never written: not committed either.
+            if (record_len > remaining) break;
             uint8_t footer[kFooterLen];
             read_exact_at(fd_, offset + record_len - kFooterLen, footer, kFooterLen);
             if (std::memcmp(footer, kFooterMagic, 8) != 0) invalid("invalid KV commit footer");
@@ -623,8 +627,9 @@ void ColdStore::rebuild_catalogue() {
     if (structural) std::rethrow_exception(structural);
     for (const PageMeta &m : found) committed_bytes_ += m.record_len;
     pages_ = std::move(found);
-    // Only bytes after the last commit footer are discarded; a read-only
-    // store never modifies the file.
+    // Recovery cuts the file to the end of its last complete record, so the
+    // next append lands where a later open finds it; a store opened read-only
+    // leaves the file untouched and simply stops reading at that point.
     if (offset < len && !read_only_) {
         if (ftruncate(fd_, (off_t)offset) != 0) io_error("truncate " + path_, errno);
         if (fdatasync(fd_) != 0) io_error("sync " + path_, errno);

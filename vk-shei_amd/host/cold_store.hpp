@@ -86,8 +86,9 @@ struct PageMeta {
     uint64_t record_len = 0;
 };
 
-// cold_store.rs:63-68: a complete record assembled away from the store; its
-// offsets are relative to the record until it is appended.
+// cold_store.rs:63-68: one record's bytes built outside the store (on any
+// thread); the offsets in its metadata count from the record's first byte
+// until append places it in the file.
 struct PreparedPage {
     PageMeta meta;
     std::vector<uint8_t> record;
@@ -188,7 +189,8 @@ public:
     void audit() const;
 
     // Test hook (cold_store.rs:116-119, fail_append_after_bytes): the next
-    // append writes only this many bytes and then fails, as a full disk would.
+    // append writes that many bytes of its record, then reports an I/O error
+    // (a short write that leaves a partial record in the file).
     void fail_next_append_after(size_t bytes) { fail_append_after_bytes_ = bytes; }
     bool hot_contains(uint64_t page_id) const { return hot_.count(page_id) != 0; }
 

@@ -39,7 +39,8 @@ private:
     std::string message_;
 };
 
-// portable.rs:60-175: owned immutable little-endian tensor bits.
+// portable.rs:60-175: a tensor's bytes (little-endian) with its dtype and
+// shape; the bytes are copied in and never change.
 class RawTensor {
 public:
     static RawTensor from_le_bytes(FloatFormat dtype, std::vector<size_t> shape, std::vector<uint8_t> bytes);
@@ -82,7 +83,8 @@ public:
     bool is_empty() const { return frames_.empty(); }
     size_t payload_bytes() const;
     const std::vector<std::pair<RawTensor, RawTensor>> &frames() const { return frames_; }
-    // Logical digest of dtype, shapes and bytes ("mslim-portable-exact-kv-v1").
+    // SHA-256 over the domain string "mslim-portable-exact-kv-v1", then the
+    // dtype, the shapes and the bytes of the stored K/V.
     std::string digest_sha256() const;
     std::vector<float> decode(const AttentionBackend &backend, const std::vector<float> &query) const;
 

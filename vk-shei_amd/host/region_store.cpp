@@ -263,8 +263,8 @@ void RegionStore::append_batch(size_t layer, size_t position, const std::vector<
     ensure(pages_[layer].size() == position, "GPU LOD append needs sequential tokens");
     const size_t kvh = geometry_.kv_heads;
     const size_t row_bytes = geometry_.head_dim * 2;
-    // Every value, and each layer-zero key, is validated before any page is
-    // committed.
+    // All checks run first (each value row, and the keys of layer 0), so a
+    // rejected batch changes no page.
     std::vector<double> maxima = value_abs_max_[layer];
     for (size_t i = 0; i < count; ++i) {
         const uint8_t *k = keys.data() + i * token_bytes;
