@@ -214,6 +214,65 @@ def test_rmsnorm_qkv_rope_append_equals_the_two_calls(ctx, batch, inner, d, qh, 
     assert torch.equal(k_a, k_b) and torch.equal(v_a, v_b)
 
 
+def test_fused_append_fallback_from_several_threads(ctx):
+    # Batches above 8 rows take the fused call's fallback, which runs its two
+    # operations through one context row buffer.  Four host threads with
+    # batches of 9, 12, 16 and 24 rows (each new size regrows that buffer)
+    # call it on one context at the same time; every result equals the same
+    # call made alone.
+    import threading
+    rng = np.random.default_rng(4242)
+    inner, d, qh, kvh, pt = 256, 64, 4, 2, 16
+    pps = 96 // pt
+    nw = to_torch(normal_bf16(rng, (inner,), 0.5))
+    wq, wk, wv = (to_torch(normal_bf16(rng, (h * d, inner), 0.05)) for h in (qh, kvh, kvh))
+    cases = []
+    for batch in (9, 12, 16, 24):
+        table = _dev_i32(rng.permutation(batch * pps).astype(np.int32).reshape(batch, pps))
+        positions = _dev_i32([int(p) for p in rng.integers(0, 96, size=batch)])
+        x = to_torch(normal_bf16(rng, (batch, inner), 3.0))
+        pools = to_torch(normal_bf16(rng, (2, batch * pps, kvh, pt, d)))
+        cases.append((batch, table, positions, x, pools))
+
+    def call(case, q_out, k_pool, v_pool):
+        batch, table, positions, x, _ = case
+        ctx.rmsnorm_qkv_rope_append(nw, 1e-5, wq, wk, wv, x, q_out, k_pool, v_pool, table, pps, pt, batch,
+                                    positions, inner, qh, kvh, d, 500000.0)
+
+    want = []
+    for case in cases:
+        q_out = torch.empty((case[0], qh * d), dtype=torch.int16, device="cuda")
+        kv = case[4].clone()
+        call(case, q_out, kv[0], kv[1])
+        torch.cuda.synchronize()
+        want.append((q_out, kv))
+    got = [[] for _ in cases]
+    errors = []
+
+    def worker(i):
+        try:
+            for _ in range(12):
+                q_out = torch.empty((cases[i][0], qh * d), dtype=torch.int16, device="cuda")
+                kv = cases[i][4].clone()
+                call(cases[i], q_out, kv[0], kv[1])
+                got[i].append((q_out, kv))
+        except Exception as e:  # reported below, after every thread has ended
+            errors.append(repr(e))
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(len(cases))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    torch.cuda.synchronize()
+    assert not errors, errors
+    for i, runs in enumerate(got):
+        assert len(runs) == 12
+        for q_out, kv in runs:
+            assert torch.equal(q_out, want[i][0]), cases[i][0]
+            assert torch.equal(kv, want[i][1]), cases[i][0]
+
+
 def test_rope_append_rejects_head_dim_above_512(ctx):
     # the fused step takes its inverse frequencies from a 256-pair table
     from mslim_attn import MslimAttnError
