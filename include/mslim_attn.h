@@ -321,7 +321,7 @@ int mslim_attn_rope(void *ctx, const void *input, void *output, int tokens, int 
  * rotates the two with two llm_prefill_rope launches, gpu_llm.cl:412-456).
  * One launch shares each row's cos/sin between the Q and K heads when
  * head_dim is a multiple of 16 (at most 512), the rows are 16-byte aligned
- * and (q_heads + kv_heads) * head_dim <= 32768; otherwise two. */
+ * and (q_heads + kv_heads) * head_dim <= 16384; otherwise two. */
 int mslim_attn_rope_qk(void *ctx, const void *q, void *q_out, const void *k, void *k_out, int tokens,
                        int q_heads, int kv_heads, int head_dim, int start_position, float theta,
                        int llama3_scaling, float factor, float low_freq_factor, float high_freq_factor,

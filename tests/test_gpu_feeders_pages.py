@@ -45,13 +45,16 @@ def test_rope_bit_exact(ctx, llama3, start):
 
 
 @pytest.mark.parametrize("tokens,qh,kvh,d,start,llama3", [
-    (2048, 32, 8, 128, 0, False),     # cfg2's prompt: six rows per workgroup
+    (2048, 32, 8, 128, 0, False),     # cfg2's prompt: three rows per workgroup
     (13, 32, 8, 128, 4090, True),     # a ragged last workgroup
-    (9, 64, 8, 128, 7, False),        # three rows per workgroup
+    (9, 64, 8, 128, 7, False),        # one row per workgroup
     (7, 4, 2, 64, 123, False),
     (3, 2, 1, 512, 32760, True),      # the whole 256-pair table
     (4, 8, 8, 256, 1, False),
     (5, 4, 4, 72, 9, False),          # head_dim % 16 != 0: two separate launches
+    (3, 96, 32, 128, 40, False),      # 16,384 elements per row: the most one launch takes
+    (3, 160, 32, 128, 40, True),      # 24,576: two separate launches
+    (2, 224, 32, 128, 5, False),      # 32,768
 ])
 def test_rope_qk_bit_exact(ctx, tokens, qh, kvh, d, start, llama3):
     # one launch for Q and K gives mslim_attn_rope's bits on each
@@ -66,6 +69,20 @@ def test_rope_qk_bit_exact(ctx, tokens, qh, kvh, d, start, llama3):
                                                                       int(llama3), *params))
     assert np.array_equal(from_torch(ko).reshape(-1), oracle.rope_gpu(kb, tokens, kvh, d, start, 500000.0,
                                                                       int(llama3), *params))
+
+
+@pytest.mark.parametrize("heads", [128, 129, 256])
+def test_rope_many_heads_bit_exact(ctx, heads):
+    # mslim_attn_rope on rows of up to 128 heads x 128 runs the Q + K kernel
+    # with no K rows; wider rows the per-token kernel; both give the oracle's
+    # bits
+    tokens, d, start = 3, 128, 1000
+    rng = np.random.default_rng(heads)
+    xb = normal_bf16(rng, (tokens, heads, d))
+    out = torch.empty((tokens, heads, d), dtype=torch.int16, device="cuda")
+    ctx.rope(to_torch(xb), out, tokens, heads, d, start, 500000.0)
+    torch.cuda.synchronize()
+    assert np.array_equal(from_torch(out).reshape(-1), oracle.rope_gpu(xb, tokens, heads, d, start, 500000.0))
 
 
 @pytest.mark.parametrize("llama3", [False, True])

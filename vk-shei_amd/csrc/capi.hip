@@ -868,7 +868,7 @@ int mslim_attn_rope(void *ctx, const void *input, void *output, int tokens, int 
                                                 (int64_t)start_position + tokens);
     // The Q + K kernel with no K rows: the same bits, several rows per
     // workgroup.
-    if (mslim::rope_qk_supported(head_dim, input, output, input, output) && heads * head_dim <= 32768)
+    if (mslim::rope_qk_supported(head_dim, heads, input, output, input, output))
         return check_hip(mslim::launch_rope_qk(static_cast<const uint16_t *>(input), static_cast<uint16_t *>(output),
                                                nullptr, nullptr, tokens, heads, 0, head_dim, start_position, theta,
                                                llama3_scaling, factor, low_freq_factor, high_freq_factor,
@@ -901,7 +901,7 @@ int mslim_attn_rope_qk(void *ctx, const void *q, void *q_out, const void *k, voi
     const mslim::RopeCosSin table = rope_cossin(c, head_dim, theta, llama3_scaling, factor, low_freq_factor,
                                                 high_freq_factor, original_max_position,
                                                 (int64_t)start_position + tokens);
-    if (mslim::rope_qk_supported(head_dim, q, q_out, k, k_out) && (q_heads + kv_heads) * head_dim <= 32768)
+    if (mslim::rope_qk_supported(head_dim, q_heads + kv_heads, q, q_out, k, k_out))
         return check_hip(mslim::launch_rope_qk(qi, qo, ki, ko, tokens, q_heads, kv_heads, head_dim, start_position,
                                                theta, llama3_scaling, factor, low_freq_factor, high_freq_factor,
                                                original_max_position, table, c.stream),

@@ -589,8 +589,11 @@ hipError_t launch_rope(const uint16_t *in, uint16_t *out, int tokens, int heads,
     return hipGetLastError();
 }
 
-bool rope_qk_supported(int head_dim, const void *q, const void *q_out, const void *k, const void *k_out) {
-    return head_dim % 16 == 0 && head_dim <= 2 * kRopeTable &&
+bool rope_qk_supported(int head_dim, int heads, const void *q, const void *q_out, const void *k, const void *k_out) {
+    // a row's pair units (8 rotate-half pairs each) must fit one workgroup's
+    // kRopePairsPerLane x 256 lanes
+    return head_dim % 16 == 0 && head_dim <= 2 * kRopeTable && heads >= 1 &&
+           (int64_t)heads * (head_dim / 16) <= kRopePairsPerLane * 256 &&
            ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(q_out) | reinterpret_cast<uintptr_t>(k) |
              reinterpret_cast<uintptr_t>(k_out)) & 15) == 0;
 }

@@ -176,9 +176,9 @@ hipError_t launch_rope(const uint16_t *in, uint16_t *out, int tokens, int heads,
 // RoPE of a prompt chunk's Q ([tokens][q_heads][head_dim]) and K
 // ([tokens][kv_heads][head_dim]) rows at positions start + t in one launch,
 // bit-identical to launch_rope on each; when rope_qk_supported (head_dim a
-// multiple of 16, at most 512; 16-byte aligned rows) and (q_heads +
-// kv_heads) * head_dim <= 32768.
-bool rope_qk_supported(int head_dim, const void *q, const void *q_out, const void *k, const void *k_out);
+// multiple of 16, at most 512; heads = q_heads + kv_heads with heads *
+// head_dim <= 16384; 16-byte aligned rows).
+bool rope_qk_supported(int head_dim, int heads, const void *q, const void *q_out, const void *k, const void *k_out);
 hipError_t launch_rope_qk(const uint16_t *q, uint16_t *q_out, const uint16_t *k, uint16_t *k_out, int tokens,
                           int q_heads, int kv_heads, int head_dim, int start, float theta, int llama3, float factor,
                           float low, float high, float original_max, RopeCosSin cossin, hipStream_t stream);
