@@ -18,6 +18,7 @@
 #include <thread>
 
 #include "../csrc/sha256.hpp"
+#include "parallel.hpp"
 
 namespace mslim {
 namespace cold {
@@ -76,40 +77,6 @@ void fnv1a64_two(const uint8_t *b, size_t n, uint64_t &first, uint64_t &second) 
     second = y;
 }
 
-// Run fn(i) for i in [0, n) on up to `threads` threads; the exception of the
-// smallest failing index is rethrown, so a parallel check reports the same
-// first failure as a sequential one.
-template <class F>
-void parallel_indices(size_t n, size_t threads, F fn) {
-    std::atomic<size_t> next{0};
-    std::mutex m;
-    size_t failed = SIZE_MAX;
-    std::exception_ptr error;
-    auto worker = [&] {
-        for (size_t i = next++; i < n; i = next++) {
-            try {
-                fn(i);
-            } catch (...) {
-                std::lock_guard<std::mutex> g(m);
-                if (i < failed) {
-                    failed = i;
-                    error = std::current_exception();
-                }
-            }
-        }
-    };
-    threads = std::max<size_t>(1, std::min(threads, n));
-    std::vector<std::thread> pool;
-    for (size_t t = 1; t < threads; ++t) pool.emplace_back(worker);
-    worker();
-    for (auto &t : pool) t.join();
-    if (error) std::rethrow_exception(error);
-}
-
-size_t verify_threads() {
-    const unsigned hw = std::thread::hardware_concurrency();
-    return std::min<size_t>(16, hw ? hw : 1);
-}
 
 uint64_t checksum_many(std::initializer_list<Span> parts) {
     uint64_t s = kFnvOffset;
@@ -409,7 +376,7 @@ void ColdStore::audit_mapped() {
     if (map == MAP_FAILED) io_error("mmap " + path_, errno);
     const uint8_t *bytes = static_cast<const uint8_t *>(map);
     try {
-        parallel_indices(pages_.size(), verify_threads(),
+        parallel_indices(pages_.size(), host_worker_threads(),
                          [&](size_t i) { verify_mapped_record(bytes, len, pages_[i]); });
     } catch (...) {
         munmap(map, (size_t)len);
@@ -420,7 +387,7 @@ void ColdStore::audit_mapped() {
 }
 
 void ColdStore::audit() const {
-    parallel_indices(pages_.size(), verify_threads(), [&](size_t i) { read_and_verify(fd_, pages_[i]); });
+    parallel_indices(pages_.size(), host_worker_threads(), [&](size_t i) { read_and_verify(fd_, pages_[i]); });
 }
 
 // ---- append ------------------------------------------------------------------
@@ -623,7 +590,7 @@ void ColdStore::rebuild_catalogue() {
     } catch (const ColdStoreError &) {
         structural = std::current_exception();
     }
-    parallel_indices(found.size(), verify_threads(), [&](size_t i) { read_and_verify(fd_, found[i]); });
+    parallel_indices(found.size(), host_worker_threads(), [&](size_t i) { read_and_verify(fd_, found[i]); });
     if (structural) std::rethrow_exception(structural);
     for (const PageMeta &m : found) committed_bytes_ += m.record_len;
     pages_ = std::move(found);
@@ -681,7 +648,7 @@ void ColdStore::for_each_verified(const std::vector<uint64_t> &ids,
     std::vector<const PageMeta *> metas;
     metas.reserve(ids.size());
     for (uint64_t id : ids) metas.push_back(&page_meta(id));
-    parallel_indices(ids.size(), verify_threads(), [&](size_t i) { fn(i, read_and_verify(fd_, *metas[i])); });
+    parallel_indices(ids.size(), host_worker_threads(), [&](size_t i) { fn(i, read_and_verify(fd_, *metas[i])); });
     for (const PageMeta *m : metas) {
         ++misses_;
         ++reads_;

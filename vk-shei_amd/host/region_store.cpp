@@ -14,41 +14,9 @@
 #include <thread>
 
 #include "../csrc/sha256.hpp"
+#include "parallel.hpp"
 
 namespace mslim {
-namespace {
-
-// fn(i) for i in [0, n) on up to 16 threads; the exception of the smallest
-// failing index is rethrown.
-template <class F>
-void parallel_for(size_t n, F fn) {
-    const unsigned hw = std::thread::hardware_concurrency();
-    const size_t threads = std::max<size_t>(1, std::min<size_t>({n, 16, hw ? hw : 1}));
-    std::atomic<size_t> next{0};
-    std::mutex m;
-    size_t failed = SIZE_MAX;
-    std::exception_ptr error;
-    auto worker = [&] {
-        for (size_t i = next++; i < n; i = next++) {
-            try {
-                fn(i);
-            } catch (...) {
-                std::lock_guard<std::mutex> g(m);
-                if (i < failed) {
-                    failed = i;
-                    error = std::current_exception();
-                }
-            }
-        }
-    };
-    std::vector<std::thread> pool;
-    for (size_t t = 1; t < threads; ++t) pool.emplace_back(worker);
-    worker();
-    for (auto &t : pool) t.join();
-    if (error) std::rethrow_exception(error);
-}
-
-}  // namespace
 
 namespace region {
 
@@ -538,7 +506,7 @@ void RegionStore::seal_device_layers(DeviceStaging &st, size_t position, size_t 
         std::vector<cold::PreparedPage> prepared;
         if (host_frames) {
             prepared.resize(records);
-            parallel_for(records, [&](size_t i) {
+            parallel_indices(records, host_worker_threads(), [&](size_t i) {
                 cold::PageGeometry pg;
                 pg.layer = descs[i].layer;
                 pg.token_start = descs[i].token_start;
