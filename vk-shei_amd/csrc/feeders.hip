@@ -280,11 +280,11 @@ __global__ __launch_bounds__(256) void rope_token_kernel(const uint16_t *in, uin
 // the table does not reach), shared by Q and K.  Each output is
 // rope_element's value for its position, bit-identical to rope_token_kernel
 // on Q and on K.
-// head_dim % 16 == 0 and 16-byte aligned rows.
-// Four pairs per lane (three cfg2 rows per workgroup, 683 workgroups)
-// measured 9.05 us at cfg2 against 11.2 us for eight (342 workgroups).
+// head_dim % 16 == 0 and 16-byte aligned rows.  PAIRS pair units per lane
+// (each unit 8 rotate-half pairs); the launcher picks it (rope_qk_shape).
 constexpr int kRopeRows = 8;
-constexpr int kRopePairsPerLane = 4;
+constexpr int kRopePairsPerLane = 4;  // the most a launch uses: its capacity
+template <int PAIRS>
 __global__ __launch_bounds__(256) void rope_qk_kernel(const uint16_t *q, uint16_t *q_out, const uint16_t *k,
                                                       uint16_t *k_out, int tokens, int rows_per_group,
                                                       int q_heads, int kv_heads, int head_dim, int start,
@@ -296,9 +296,9 @@ __global__ __launch_bounds__(256) void rope_qk_kernel(const uint16_t *q, uint16_
     const int row0 = blockIdx.x * rows_per_group;
     const int rows = min(rows_per_group, tokens - row0);
     const int work = rows * units;
-    uint4 x[kRopePairsPerLane], p[kRopePairsPerLane];
+    uint4 x[PAIRS], p[PAIRS];
 #pragma unroll
-    for (int j = 0; j < kRopePairsPerLane; ++j) {
+    for (int j = 0; j < PAIRS; ++j) {
         const int i = min((int)threadIdx.x + j * 256, work - 1);
         const int r = i / units, u = i % units, head = u / hchunks, c = (u % hchunks) * 8;
         const uint16_t *src = head < q_heads ? q + ((int64_t)(row0 + r) * q_heads + head) * head_dim
@@ -321,7 +321,7 @@ __global__ __launch_bounds__(256) void rope_qk_kernel(const uint16_t *q, uint16_
     }
     __syncthreads();
 #pragma unroll
-    for (int j = 0; j < kRopePairsPerLane; ++j) {
+    for (int j = 0; j < PAIRS; ++j) {
         const int i = (int)threadIdx.x + j * 256;
         if (i >= work) break;
         const int r = i / units, u = i % units, head = u / hchunks, c = (u % hchunks) * 8;
@@ -603,11 +603,26 @@ hipError_t launch_rope_qk(const uint16_t *q, uint16_t *q_out, const uint16_t *k,
                           float low, float high, float original_max, RopeCosSin cossin, hipStream_t stream) {
     const RopeTable &table = rope_table(head_dim, theta, llama3, factor, low, high, original_max);
     const int units = (q_heads + kv_heads) * (head_dim / 16);
-    // rows per workgroup: as many as kRopePairsPerLane pairs per lane cover
-    const int rows = std::max(1, std::min(kRopeRows, kRopePairsPerLane * 256 / units));
     if (units > kRopePairsPerLane * 256) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(rope_qk_kernel, dim3((unsigned)((tokens + rows - 1) / rows)), dim3(256), 0, stream, q, q_out,
-                       k, k_out, tokens, rows, q_heads, kv_heads, head_dim, start, table, cossin);
+    // About 1,024 workgroups: rows per workgroup from the token count, then
+    // the fewest pair units per lane (2 to 4) that hold those rows.  Measured
+    // (us; 2 / 3 / 4 pairs per lane): 2,048 rows of 32 + 8 heads of 128 8.83 /
+    // 8.37 / 8.91; 512 rows after 3,584 tokens 4.21 / 4.58 / 4.97; 8,192 rows
+    // of 64 + 8 heads (one row per workgroup either way) - / 51.3 / 53.2.
+    const int want = std::max(1, std::min(kRopeRows, tokens / 1024));
+    const int pairs = std::max(2, std::min(kRopePairsPerLane, (want * units + 255) / 256));
+    const int rows = std::max(1, std::min(kRopeRows, pairs * 256 / units));
+    const int needed = std::max(2, (rows * units + 255) / 256);  // the same rows with fewer pairs
+    const dim3 grid((unsigned)((tokens + rows - 1) / rows));
+    if (needed <= 2)
+        hipLaunchKernelGGL(rope_qk_kernel<2>, grid, dim3(256), 0, stream, q, q_out, k, k_out, tokens, rows, q_heads,
+                           kv_heads, head_dim, start, table, cossin);
+    else if (needed == 3)
+        hipLaunchKernelGGL(rope_qk_kernel<3>, grid, dim3(256), 0, stream, q, q_out, k, k_out, tokens, rows, q_heads,
+                           kv_heads, head_dim, start, table, cossin);
+    else
+        hipLaunchKernelGGL(rope_qk_kernel<4>, grid, dim3(256), 0, stream, q, q_out, k, k_out, tokens, rows, q_heads,
+                           kv_heads, head_dim, start, table, cossin);
     return hipGetLastError();
 }
 
