@@ -378,6 +378,43 @@ __global__ __launch_bounds__(256) void proj_merge_kernel(ProjArgs a) {
     const int64_t n = a.out_base[a.segments];
     const int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
     if (i0 >= n) return;
+    // Four outputs of one segment with 16-byte partials and 8-byte outputs
+    // (and residual): one vector access each; otherwise element by element.
+    // The arithmetic per element is the same either way.
+    const int seg0 = (a.segments > 2 && i0 >= a.out_base[2]) ? 2 : (a.segments > 1 && i0 >= a.out_base[1]) ? 1 : 0;
+    const int64_t li0 = i0 - a.out_base[seg0];
+    const bool vec = i0 + 3 < a.out_base[seg0 + 1] && (li0 & 3) == 0 &&
+                     ((reinterpret_cast<uintptr_t>(a.partial) | reinterpret_cast<uintptr_t>(a.out[seg0]) |
+                       (EPI == kAdd ? reinterpret_cast<uintptr_t>(a.resid) : 0)) & 15) == 0;
+    if (vec) {
+        float4 v = *reinterpret_cast<const float4 *>(a.partial + i0);
+        float4 vu = EPI == kSwiglu ? *reinterpret_cast<const float4 *>(a.partial + n + i0) : float4{};
+        for (int s = 1; s < a.ksplit; ++s) {
+            const float4 w = *reinterpret_cast<const float4 *>(a.partial + (int64_t)s * NA * n + i0);
+            v = float4{__fadd_rn(v.x, w.x), __fadd_rn(v.y, w.y), __fadd_rn(v.z, w.z), __fadd_rn(v.w, w.w)};
+            if (EPI == kSwiglu) {
+                const float4 wu = *reinterpret_cast<const float4 *>(a.partial + ((int64_t)s * NA + 1) * n + i0);
+                vu = float4{__fadd_rn(vu.x, wu.x), __fadd_rn(vu.y, wu.y), __fadd_rn(vu.z, wu.z), __fadd_rn(vu.w, wu.w)};
+            }
+        }
+        const float vs[4] = {v.x, v.y, v.z, v.w}, us[4] = {vu.x, vu.y, vu.z, vu.w};
+        uint16_t rs[4] = {0, 0, 0, 0};
+        if (EPI == kAdd) {
+            const uint2 r = *reinterpret_cast<const uint2 *>(a.resid + li0);
+            rs[0] = (uint16_t)r.x; rs[1] = (uint16_t)(r.x >> 16); rs[2] = (uint16_t)r.y; rs[3] = (uint16_t)(r.y >> 16);
+        }
+        uint16_t ys[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            uint16_t y = write_bf16(vs[e]);
+            if (EPI == kSwiglu) y = swiglu_mul_bf16(a.act_table[y], write_bf16(us[e]));
+            if (EPI == kAdd) y = write_bf16(__fadd_rn(read_bf16(rs[e]), read_bf16(y)));
+            ys[e] = y;
+        }
+        *reinterpret_cast<uint2 *>(a.out[seg0] + li0) =
+            uint2{(uint32_t)ys[0] | ((uint32_t)ys[1] << 16), (uint32_t)ys[2] | ((uint32_t)ys[3] << 16)};
+        return;
+    }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const int64_t i = i0 + e;
