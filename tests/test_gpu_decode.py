@@ -528,3 +528,34 @@ def test_decode_batches_past_the_kernel_argument_tables(ctx):
         t = lens[b]
         ref = _oracle_decode(from_torch(q[b]), from_torch(k[b, :t]), from_torch(v[b, :t]), qh, kvh, d)
         check_bf16(got[b], ref, TOL, "decode of 300 sequences, automatic split")
+
+
+def test_decode_at_the_batch_limit(ctx):
+    # MSLIM_ATTN_MAX_BATCH (4,096) sequences of 1 to 40 tokens: dense ==
+    # paged, both equal to the same sequences in launches of 64, and sampled
+    # sequences against the oracle; one more sequence is refused.
+    import mslim_attn
+    batch, qh, kvh, d, pt, split = mslim_attn.MAX_BATCH, 8, 4, 64, 16, 64
+    gen = torch.Generator(device="cuda").manual_seed(4096)
+    rng = np.random.default_rng(4097)
+    lens = [int(x) for x in rng.integers(1, 41, size=batch)]
+    stride = max(lens)
+    k = torch.randn((batch, stride, kvh, d), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    v = torch.randn((batch, stride, kvh, d), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    q = torch.randn((batch, qh, d), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    k_pool, v_pool, table_t, pps, _ = _paged_pool(ctx, k, v, lens, stride, pt, seed=41)
+    dense, paged, small = (torch.full_like(q, -1) for _ in range(3))
+    ctx.decode_dense(q, k, v, dense, lens, qh, kvh, d, seq_stride_tokens=stride, split_tokens=split)
+    ctx.decode_paged(q, k_pool, v_pool, paged, lens, table_t, pps, pt, qh, kvh, d, split_tokens=split)
+    _chunked(lambda lo, hi: ctx.decode_dense(q[lo:hi], k[lo:hi], v[lo:hi], small[lo:hi], lens[lo:hi], qh, kvh, d,
+                                             seq_stride_tokens=stride, split_tokens=split), batch, 64)
+    torch.cuda.synchronize()
+    assert torch.equal(dense, paged) and torch.equal(dense, small)
+    got = from_torch(dense).reshape(batch, -1)
+    for b in (0, 1, 2047, int(np.argmax(lens)), batch - 1):
+        t = lens[b]
+        ref = _oracle_decode(from_torch(q[b]), from_torch(k[b, :t]), from_torch(v[b, :t]), qh, kvh, d)
+        check_bf16(got[b], ref, TOL, "test_decode_at_the_batch_limit")
+    over = torch.empty((batch + 1, qh, d), dtype=torch.int16, device="cuda")
+    with pytest.raises(mslim_attn.MslimAttnError, match="1..4096"):
+        ctx.decode_dense(over, k, k, over.clone(), [1] * (batch + 1), qh, kvh, d, seq_stride_tokens=stride)
