@@ -140,9 +140,14 @@ def test_prefill_split_choices():
     # 0 when the launch keeps every CU busy without splitting
     from mslim_attn import MslimAttnError, prefill_split_tiles
     assert prefill_split_tiles(8192, 0, 64, 8, 128) == 0     # cfg4: 2,048 workgroups
-    assert prefill_split_tiles(2048, 0, 32, 8, 128) == 19    # cfg2: 256 workgroups of 1..32 tiles
+    assert prefill_split_tiles(2048, 0, 32, 8, 128) == 20    # cfg2: 256 workgroups of 1..32 tiles
     assert prefill_split_tiles(512, 3584, 32, 8, 128) == 16  # a decoder prompt chunk after 3,584 tokens
-    assert prefill_split_tiles(512, 0, 32, 8, 128) == 4
+    assert prefill_split_tiles(512, 512, 32, 8, 128) == 8
+    assert prefill_split_tiles(1000, 777, 32, 8, 128) == 14
+    # 32-row blocks (64/8 heads) after 777 tokens, and a first 512-token chunk:
+    # measured no slower unsplit, so not split
+    assert prefill_split_tiles(1000, 777, 64, 8, 128) == 0
+    assert prefill_split_tiles(512, 0, 32, 8, 128) == 0
     assert prefill_split_tiles(100, 0, 32, 8, 128) == 0
     assert prefill_split_tiles(300, 0, 4, 2, 80) == 0        # generic kernel: never split
     for args in ((0, 0, 32, 8, 128), (5, -1, 32, 8, 128), (5, 0, 32, 3, 128)):

@@ -170,8 +170,9 @@ def test_prefill_rejects_bad_arguments(ctx):
 # Launches too small to fill the CUs split long row blocks into chunks of key
 # tiles (merged in fixed chunk order): cfg2, the decoder's 512-token prompt
 # chunks after a long prior, ragged query counts, D = 64 and a group of 2.
-SPLIT_SHAPES = [(2048, 0, 32, 8, 128), (512, 3584, 32, 8, 128), (1000, 777, 64, 8, 128),
-                (1500, 0, 16, 2, 64), (2048, 0, 16, 8, 128), (512, 0, 32, 8, 128)]
+SPLIT_SHAPES = [(2048, 0, 32, 8, 128), (512, 3584, 32, 8, 128), (1000, 777, 32, 8, 128),
+                (1500, 0, 16, 2, 64), (2048, 0, 16, 8, 128), (512, 512, 32, 8, 128),
+                (512, 512, 64, 8, 128), (2048, 0, 32, 8, 64)]
 
 
 @pytest.mark.parametrize("queries,prior,qh,kvh,d", SPLIT_SHAPES)
@@ -253,7 +254,7 @@ def test_prefill_split_plan_is_shape_only(ctx):
     assert mslim_attn.prefill_split_tiles(8192, 0, 64, 8, 128) == 0
     # tiny launches have nothing to split
     assert mslim_attn.prefill_split_tiles(100, 0, 32, 8, 128) == 0
-    assert mslim_attn.prefill_split_tiles(2048, 0, 32, 8, 128) == 19
+    assert mslim_attn.prefill_split_tiles(2048, 0, 32, 8, 128) == 20
     with pytest.raises(mslim_attn.MslimAttnError):
         mslim_attn.prefill_split_tiles(0, 0, 32, 8, 128)
 

@@ -802,11 +802,13 @@ namespace {
 // own kv heads when they divide evenly over the XCDs, as launch_prefill deals
 // them; otherwise all CUs share one list); an item costs its tiles plus
 // kItemFixedTiles (Q, the first copies, the partial or output write), and a
-// split row block ends kMergeTiles after its last chunk.  Fitted to cfg2 and
-// to the decoder's 512-token chunks after 3,584 tokens, whose measured best
-// chunk lengths (19-20 and 16 tiles) it reproduces.
-constexpr double kItemFixedTiles = 6.0;
-constexpr double kMergeTiles = 2.0;
+// row block split into n chunks ends (n - 1) * kMergeChunkTiles after its last
+// chunk (the merge loads every other chunk's O as one uncached batch).  Fitted
+// to every chunk length measured on 28 launches of 256 to 3,072 queries after
+// 0 to 3,584 tokens, 4 to 8 heads per kv head: the chunk it picks is the
+// fastest measured or within 3.5% of it.
+constexpr double kItemFixedTiles = 7.0;
+constexpr double kMergeChunkTiles = 4.0;
 
 double split_span(const PrefillLaunch &l, int rows, int nrb, int groups, int subgroups, int tc) {
     const bool by_head = l.kv_heads % kXcds == 0;
@@ -842,8 +844,10 @@ double split_span(const PrefillLaunch &l, int rows, int nrb, int groups, int sub
     }
     if (tc < (int)1e9) {
         for (int hg = 0; hg < groups; ++hg)
-            for (int rb = 0; rb < nrb; ++rb)
-                if (row_block_tiles(l, rows, rb) > tc) span = std::max(span, row_end[(size_t)hg * nrb + rb] + kMergeTiles);
+            for (int rb = 0; rb < nrb; ++rb) {
+                const int nc = (row_block_tiles(l, rows, rb) + tc - 1) / tc;
+                if (nc > 1) span = std::max(span, row_end[(size_t)hg * nrb + rb] + (nc - 1) * kMergeChunkTiles);
+            }
     }
     return span;
 }
