@@ -6,7 +6,7 @@
 // 366-378) stream every weight once per step, so the work is HBM-bound on the
 // weights; the token vectors are a few hundred KiB and stay in L2.
 //
-// Workgroups of 8 wavefronts work through 16-row tiles of the output (a grid
+// Workgroups of 8 wavefronts work through tiles of 16 weight rows (a grid
 // of a few workgroups per CU, each taking every grid-th tile).  A tile's sum
 // over the inner dimension is cut into 16 partial sums: partial j folds the
 // 128-input blocks j, j + 16, ... in order, four v_mfma_f32_16x16x32_bf16
@@ -15,9 +15,9 @@
 // zeros); wavefront w keeps partials w and w + 8, and the 16 partial 16x16
 // tiles are added in LDS in order 0 .. 15.  That order depends on the inner
 // dimension only, so a product gives the same bits in every entry point,
-// fused form and launch shape.  Each wavefront keeps a ring of two (or
-// four) load batches in flight, and the next tile's first batches go out
-// before a tile's partials are summed.
+// fused form and launch shape.  Each wavefront keeps a ring of two load
+// batches in flight, and the next tile's first batches go out before a
+// tile's partials are summed.
 //
 // When the token rows fit (<= 8 tokens of <= 4096 inputs) the workgroup
 // stages them in LDS once for all its tiles, by DMA while its first weight
@@ -30,7 +30,11 @@
 //   plain   out = BF16(acc)
 //   add     out = BF16(resid + BF16(acc))           (llm_add after the product)
 //   swiglu  out = SwiGLU(BF16(acc_gate), BF16(acc_up))   (llm_swiglu after both;
-//           its first stage read from the context's table of every gate value)
+//           its first stage read from the context's table of every gate value).
+//           A tile is 8 outputs: rows 0-7 of the A operand are their gate
+//           rows and rows 8-15 their up rows, so the two sums of an output
+//           meet in lanes l and l + 32 (14,336 outputs make 1,792 tiles, 7
+//           per CU, where 16 gate plus 16 up rows per tile left 3.5)
 // which equal the unfused product followed by the elementwise kernel bit for
 // bit.  Up to three matrices with separate outputs share one launch (Q, K, V).
 #include "common.hpp"
@@ -106,20 +110,19 @@ __device__ __forceinline__ int stage_index(int row, int col) {
 template <int EPI, bool XLDS, bool NORM, int WAVES, int DEPTH>
 __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(4))) void skinny_kernel(
     SkinnyArgs a, RopeArg<EPI> rope) {
-    // Partial slots per wavefront, MFMA steps per load batch (half a block
-    // when two matrices stream, to fit two batches in flight in the register
-    // budget) and batches per block.
+    // Partial slots per wavefront, MFMA steps per load batch and batches per
+    // block.
     constexpr int NS = kSlots / WAVES;
-    constexpr int UB = EPI == kSwiglu ? kUnroll / 2 : kUnroll;
+    constexpr int UB = kUnroll;
     constexpr int PB = kUnroll / UB;
+    constexpr int kTileOut = EPI == kSwiglu ? kTileRows / 2 : kTileRows;  // outputs per tile
     // Batches per loop iteration: a multiple of the ring depth and of the
     // slot cycle (powers of two), so that every batch's ring entry and
     // accumulator are known at compile time.
     constexpr int PERIOD = PB * NS > DEPTH ? PB * NS : DEPTH;
     constexpr int kThreads = WAVES * 64;
-    // LDS: the staged rows, then one matrix's partial tiles (SwiGLU sums
-    // gate and up one after the other in the same space); the RMSNorm
-    // scratch lives in the partial space before the first tile ends.
+    // LDS: the staged rows, then the partial tiles; the RMSNorm scratch
+    // lives in the partial space before the first tile ends.
     __shared__ __align__(16) unsigned char lds[(XLDS ? kStageBytes : 0) + kPartialBytes];
     uint16_t *xs = reinterpret_cast<uint16_t *>(lds);
     auto partial = reinterpret_cast<floatx4_t(*)[64]>(lds + (XLDS ? kStageBytes : 0));
@@ -133,11 +136,12 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(4)))
     // +7 of each 32-input step; rows past the end re-read the last row and
     // are not written.
     // With RoPE, a Q or K tile takes 8 rows of the first half of a head
-    // and their 8 rotate-half partners (rows 8 .. 15 of the tile), so each
-    // pair meets in lanes l and l + 32 of the output; which rows a tile
-    // reads changes nothing in how each output is summed.
+    // and their 8 rotate-half partners (rows 8 .. 15 of the tile); a SwiGLU
+    // tile takes the gate rows of 8 outputs and then their up rows.  Either
+    // way each pair meets in lanes l and l + 32 of the output, and which rows
+    // a tile reads changes nothing in how each output is summed.
     struct Tile {
-        const uint16_t *wp, *up;
+        const uint16_t *wp;
         uint16_t *out;
         int rows, r0, seg;
     };
@@ -153,15 +157,20 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(4)))
         Tile t;
         t.rows = a.rows[seg];
         t.seg = seg;
-        t.r0 = (tile - a.first_tile[seg]) * kTileRows;
-        const int row = EPI == kQkvRope && seg < 2 ? rope_row(t.r0, lane & 15) : min(t.r0 + (lane & 15), t.rows - 1);
-        t.wp = a.w[seg] + (int64_t)row * a.inner + kq;
-        t.up = EPI == kSwiglu ? a.w_up + (int64_t)row * a.inner + kq : nullptr;
+        t.r0 = (tile - a.first_tile[seg]) * kTileOut;
+        if constexpr (EPI == kSwiglu) {
+            const int row = min(t.r0 + (lane & 7), t.rows - 1);
+            t.wp = ((lane & 15) < 8 ? a.w[seg] : a.w_up) + (int64_t)row * a.inner + kq;
+        } else {
+            const int row =
+                EPI == kQkvRope && seg < 2 ? rope_row(t.r0, lane & 15) : min(t.r0 + (lane & 15), t.rows - 1);
+            t.wp = a.w[seg] + (int64_t)row * a.inner + kq;
+        }
         t.out = a.out[seg];
         return t;
     };
     struct Batch {
-        bf16x8_t wa[UB], wu[UB], xb[UB];
+        bf16x8_t wa[UB], xb[UB];
     };
     const uint16_t *xp = a.x + (int64_t)(live ? tok : 0) * a.inner + kq;
     // inner % 32 == 0: a step that starts inside the row ends inside it.
@@ -171,7 +180,6 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(4)))
             const int k = k0 + u * 32;
             const bool in = k < a.inner;
             bt.wa[u] = in ? load8(t.wp + k) : zero;
-            if (EPI == kSwiglu) bt.wu[u] = in ? load8(t.up + k) : zero;
             if (!XLDS) bt.xb[u] = in && live ? load8(xp + k) : zero;
         }
     };
@@ -185,14 +193,10 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(4)))
             const int kc = min(k, a.inner - 32);
             const bf16x8_t w = load8(t.wp + kc);
             bt.wa[u] = k < a.inner ? w : zero;
-            if (EPI == kSwiglu) {
-                const bf16x8_t wu = load8(t.up + kc);
-                bt.wu[u] = k < a.inner ? wu : zero;
-            }
         }
     };
-    constexpr int kRingLoads = DEPTH * UB * (EPI == kSwiglu ? 2 : 1);
-    floatx4_t acc[NS], acc_up[NS];
+    constexpr int kRingLoads = DEPTH * UB;
+    floatx4_t acc[NS];
     auto use_batch = [&](const Batch &bt, int k0, int m) __attribute__((always_inline)) {
 #pragma unroll
         for (int u = 0; u < UB; ++u) {
@@ -201,7 +205,6 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(4)))
             if (XLDS) xb = k < a.inner && live ? *reinterpret_cast<const bf16x8_t *>(xs + stage_index(tok, k + kq)) : zero;
             else xb = bt.xb[u];
             acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bt.wa[u], xb, acc[m], 0, 0, 0);
-            if (EPI == kSwiglu) acc_up[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bt.wu[u], xb, acc_up[m], 0, 0, 0);
         }
     };
     // Batch i of a wavefront: block wave + (i / PB) * WAVES, part i % PB.
@@ -392,10 +395,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(4)))
 
     while (true) {
 #pragma unroll
-        for (int m = 0; m < NS; ++m) {
-            acc[m] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
-            acc_up[m] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
-        }
+        for (int m = 0; m < NS; ++m) acc[m] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
         // A ring of DEPTH batches: batch i + DEPTH loads into batch i's
         // registers once batch i is used.
         for (int kb0 = kfirst; kb0 < a.inner; kb0 += (PERIOD / PB) * WAVES * kBlock) {
@@ -422,22 +422,33 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(4)))
         }
         RopeIn rin{};
         if (EPI == kQkvRope && wave == 0 && live) rin = rope_fetch(cur);
-        floatx4_t sum, sum_up;
+        floatx4_t sum;
 #pragma unroll
-        for (int p = 0; p < (EPI == kSwiglu ? 2 : 1); ++p) {
-#pragma unroll
-            for (int m = 0; m < NS; ++m) partial[wave + m * WAVES][lane] = p ? acc_up[m] : acc[m];
-            __syncthreads();
-            if (wave == 0) {
-                floatx4_t s = partial[0][lane];
-                for (int j = 1; j < kSlots; ++j) s += partial[j][lane];
-                if (p) sum_up = s;
-                else sum = s;
-            }
-            __syncthreads();  // the partials are read before they are written again
+        for (int m = 0; m < NS; ++m) partial[wave + m * WAVES][lane] = acc[m];
+        __syncthreads();
+        if (wave == 0) {
+            sum = partial[0][lane];
+            for (int j = 1; j < kSlots; ++j) sum += partial[j][lane];
         }
+        __syncthreads();  // the partials are read before they are written again
         if constexpr (EPI == kQkvRope) {
             if (wave == 0 && live) rope_epilogue(cur, sum, rin);
+        } else if constexpr (EPI == kSwiglu) {
+            if (wave == 0 && live) {
+                // lane l < 32 holds the gate sums of outputs r0 + 4 (l / 16)
+                // + j, lane l + 32 the up sums of the same outputs
+                float up[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) up[j] = __shfl_xor(sum[j], 32, 64);
+                if (lane < 32) {
+                    uint16_t *out = cur.out + (int64_t)tok * cur.rows;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int r = cur.r0 + 4 * (lane >> 4) + j;
+                        if (r < cur.rows) out[r] = swiglu_mul_bf16(a.act_table[write_bf16(sum[j])], write_bf16(up[j]));
+                    }
+                }
+            }
         } else if (wave == 0 && live) {
             // D layout: lane l holds rows 4*(l/16) + j, token l%16.
             uint16_t *out = cur.out + (int64_t)tok * cur.rows;
@@ -446,13 +457,8 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(4)))
                 const int r = cur.r0 + 4 * (lane >> 4) + j;
                 if (r >= cur.rows) continue;
                 const uint16_t y = write_bf16(sum[j]);
-                if (EPI == kPlain) {
-                    out[r] = y;
-                } else if (EPI == kAdd) {
-                    out[r] = write_bf16(__fadd_rn(read_bf16(a.resid[(int64_t)tok * cur.rows + r]), read_bf16(y)));
-                } else {
-                    out[r] = swiglu_mul_bf16(a.act_table[y], write_bf16(sum_up[j]));
-                }
+                if (EPI == kPlain) out[r] = y;
+                else out[r] = write_bf16(__fadd_rn(read_bf16(a.resid[(int64_t)tok * cur.rows + r]), read_bf16(y)));
             }
         }
         if (next >= a.tiles) break;
@@ -460,41 +466,33 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(4)))
     }
 }
 
-int tiles_of(int rows) { return (rows + kTileRows - 1) / kTileRows; }
-
-// Launch shape: wavefronts per workgroup, workgroups per CU (a grid of at
-// most per_cu * kCus workgroups, each working through every grid-th tile)
-// and load batches in flight per wavefront.
-struct Shape {
-    int waves, per_cu, depth;
-};
-
-// Measured at the cfg5 decode shapes (1 and 8 tokens, weights cycled
-// through more memory than the last-level cache): 8 wavefronts per
-// workgroup with two workgroups per CU ahead of 16 with one (QKV's 384
-// tiles then all run at once, and one workgroup's reduction overlaps the
-// other's loads); a four-deep ring and a grid of up to four workgroups per
-// CU for the SwiGLU pair; a two-deep ring elsewhere (four gained nothing for
-// one matrix and spills when the token rows are not staged).
-Shape skinny_shape(int epi, bool xlds, bool norm) {
-    if (epi == kSwiglu && xlds && !norm) return Shape{8, 4, 4};
-    return Shape{8, 2, 2};
+// Tiles of a matrix of `rows` outputs: 16 rows each, or 8 gate/up pairs.
+int tiles_of(int epi, int rows) {
+    const int per = epi == kSwiglu ? kTileRows / 2 : kTileRows;
+    return (rows + per - 1) / per;
 }
+
+// Launch shape, measured at the cfg5 decode shapes (1 and 8 tokens, weights
+// cycled through more memory than the last-level cache): workgroups of 8
+// wavefronts, at most two per CU (a grid of at most 512, each workgroup
+// taking every grid-th tile), ahead of 16 wavefronts with one (QKV's 384
+// tiles then all run at once, and one workgroup's reduction overlaps the
+// other's loads), and a two-deep ring of load batches (four gained nothing
+// and spills when the token rows are not staged).  The paired SwiGLU tiles
+// run best on the same shape: at 8 tokens, RMSNorm + gate/up 46.6 us against
+// 55.5 with one workgroup per CU and 58.8 with one per tile.
+constexpr int kPerCu = 2;
 
 template <int EPI, bool XLDS, bool NORM>
 hipError_t launch_with(SkinnyArgs &a, hipStream_t stream, const RopeArg<EPI> &rope = {}) {
     int tiles = 0;
     for (int s = 0; s < a.segments; ++s) {
         a.first_tile[s] = tiles;
-        tiles += tiles_of(a.rows[s]);
+        tiles += tiles_of(EPI, a.rows[s]);
     }
     a.tiles = tiles;
-    const Shape sh = skinny_shape(EPI, XLDS, NORM);
-    const unsigned grid = (unsigned)std::min(tiles, sh.per_cu * kCus);
-    if constexpr (EPI == kSwiglu && XLDS && !NORM)
-        hipLaunchKernelGGL((skinny_kernel<EPI, XLDS, NORM, 8, 4>), dim3(grid), dim3(8 * 64), 0, stream, a, rope);
-    else
-        hipLaunchKernelGGL((skinny_kernel<EPI, XLDS, NORM, 8, 2>), dim3(grid), dim3(8 * 64), 0, stream, a, rope);
+    const unsigned grid = (unsigned)std::min(tiles, kPerCu * kCus);
+    hipLaunchKernelGGL((skinny_kernel<EPI, XLDS, NORM, 8, 2>), dim3(grid), dim3(8 * 64), 0, stream, a, rope);
     return hipGetLastError();
 }
 
