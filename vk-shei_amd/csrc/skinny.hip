@@ -15,9 +15,9 @@
 // zeros); wavefront w keeps partials w and w + 8, and the 16 partial 16x16
 // tiles are added in LDS in order 0 .. 15.  That order depends on the inner
 // dimension only, so a product gives the same bits in every entry point,
-// fused form and launch shape.  Each wavefront keeps a ring of two load
-// batches in flight, and the next tile's first batches go out before a
-// tile's partials are summed.
+// fused form and launch shape.  Each wavefront keeps a ring of two (or
+// four) load batches in flight, and the next tile's first batches go out
+// before a tile's partials are summed.
 //
 // When the token rows fit (<= 8 tokens of <= 4096 inputs) the workgroup
 // stages them in LDS once for all its tiles, by DMA while its first weight
@@ -479,8 +479,10 @@ int tiles_of(int epi, int rows) {
 // tiles then all run at once, and one workgroup's reduction overlaps the
 // other's loads), and a two-deep ring of load batches (four gained nothing
 // and spills when the token rows are not staged).  The paired SwiGLU tiles
-// run best on the same shape: at 8 tokens, RMSNorm + gate/up 46.6 us against
-// 55.5 with one workgroup per CU and 58.8 with one per tile.
+// run best on the same grid (at 8 tokens, RMSNorm + gate/up 46.1 us against
+// 49.1 with four workgroups per CU, 55.5 with one and 58.8 with one per
+// tile), with a four-deep ring when the token rows are staged (45.2 against
+// 46.1 us; the same at 1 token and without the RMSNorm).
 constexpr int kPerCu = 2;
 
 template <int EPI, bool XLDS, bool NORM>
@@ -492,7 +494,10 @@ hipError_t launch_with(SkinnyArgs &a, hipStream_t stream, const RopeArg<EPI> &ro
     }
     a.tiles = tiles;
     const unsigned grid = (unsigned)std::min(tiles, kPerCu * kCus);
-    hipLaunchKernelGGL((skinny_kernel<EPI, XLDS, NORM, 8, 2>), dim3(grid), dim3(8 * 64), 0, stream, a, rope);
+    if constexpr (EPI == kSwiglu && XLDS)
+        hipLaunchKernelGGL((skinny_kernel<EPI, XLDS, NORM, 8, 4>), dim3(grid), dim3(8 * 64), 0, stream, a, rope);
+    else
+        hipLaunchKernelGGL((skinny_kernel<EPI, XLDS, NORM, 8, 2>), dim3(grid), dim3(8 * 64), 0, stream, a, rope);
     return hipGetLastError();
 }
 
