@@ -194,6 +194,34 @@ def test_fused_projections_equal_unfused(ctx, tokens, inner):
     assert within_bound(host_bits(down_prod), wd_bits, x_bits, inner, qr, min(tokens, 8))
 
 
+@pytest.mark.parametrize("inter", [1, 13, 100, 1000])
+@pytest.mark.parametrize("tokens,inner", [(1, 4096), (8, 4096), (5, 96), (12, 4096), (8, 6144)])
+def test_swiglu_tiles_of_any_row_count(ctx, tokens, inner, inter):
+    # a decode SwiGLU tile is 8 outputs (their gate rows, then their up rows,
+    # in one MFMA operand): row counts that leave a partial last tile, token
+    # rows staged in LDS (<= 8 of <= 4096) or read per step (12 tokens, inner
+    # 6144), against the two plain products and mslim_attn_swiglu, and with
+    # the RMSNorm fused against mslim_attn_rmsnorm first
+    rng = np.random.default_rng(inter * 131 + tokens * 7 + inner)
+    x = dev_bits(bf16(rng, tokens * inner, 2.0))
+    nw = dev_bits(bf16(rng, inner, 0.5))
+    wg, wu = dev_bits(bf16(rng, inter * inner, 0.05)), dev_bits(bf16(rng, inter * inner, 0.05))
+    empty = lambda n: torch.empty(n, dtype=torch.int16, device="cuda")  # noqa: E731
+    act, g, u, act2 = empty(tokens * inter), empty(tokens * inter), empty(tokens * inter), empty(tokens * inter)
+    ctx.gemm_swiglu(wg, wu, x, act, inner, inter, tokens)
+    ctx.gemm_bf16(wg, x, g, inner, inter, tokens)
+    ctx.gemm_bf16(wu, x, u, inner, inter, tokens)
+    ctx.swiglu(g, u, act2, tokens * inter)
+    normed, fused, unfused = empty(tokens * inner), empty(tokens * inter), empty(tokens * inter)
+    ctx.rmsnorm(x, nw, normed, tokens, inner, 1e-5)
+    ctx.gemm_swiglu(wg, wu, normed, unfused, inner, inter, tokens)
+    ctx.rmsnorm_gemm_swiglu(nw, 1e-5, wg, wu, x, fused, inner, inter, tokens)
+    torch.cuda.synchronize()
+    assert torch.equal(act, act2)
+    assert torch.equal(fused, unfused)
+    assert within_bound(host_bits(g), host_bits(wg), host_bits(x), inner, inter, min(tokens, 8))
+
+
 @pytest.mark.parametrize("tokens,inner", [(1, 4096), (8, 4096), (3, 96), (9, 4096), (4, 4104), (40, 512),
                                           (2, 8192)])
 def test_rmsnorm_fused_projections_equal_unfused(ctx, tokens, inner):
