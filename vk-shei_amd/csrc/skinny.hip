@@ -275,9 +275,28 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(4)))
         }
     };
 
+    // kAdd: wave 0's residual values of a tile (lane l: token l % 16, rows
+    // r0 + 4 (l / 16) + j) are loaded before the tile's first weight batches,
+    // so their latency passes under the k loop instead of after the fold;
+    // being older than every batch, they change none of the waits for the
+    // batches.  A tile reads only its own rows, so out == resid is safe.
+    uint16_t res_next[4] = {}, res_cur[4] = {};
+    auto resid_fetch = [&](const Tile &tt) __attribute__((always_inline)) {
+        if constexpr (EPI == kAdd) {
+            if (wave == 0 && live) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int r = tt.r0 + 4 * (lane >> 4) + j;
+                    if (r < tt.rows) res_next[j] = a.resid[(int64_t)tok * tt.rows + r];
+                }
+            }
+        }
+    };
+
     int tile = blockIdx.x;
     Batch ring[DEPTH];
     Tile t = tile_of(tile);
+    resid_fetch(t);
     if constexpr (!XLDS) {
 #pragma unroll
         for (int d = 0; d < DEPTH; ++d)
@@ -413,9 +432,12 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(4)))
         // The next tile's first batches go out before this tile's partials
         // are summed.
         const Tile cur = t;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) res_cur[j] = res_next[j];
         const int next = tile + (int)gridDim.x;
         if (next < a.tiles) {
             t = tile_of(next);
+            resid_fetch(t);
 #pragma unroll
             for (int d = 0; d < DEPTH; ++d)
                 if (k_of(kfirst, d) < a.inner) load_batch(ring[d], t, k_of(kfirst, d));
@@ -458,7 +480,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(4)))
                 if (r >= cur.rows) continue;
                 const uint16_t y = write_bf16(sum[j]);
                 if (EPI == kPlain) out[r] = y;
-                else out[r] = write_bf16(__fadd_rn(read_bf16(a.resid[(int64_t)tok * cur.rows + r]), read_bf16(y)));
+                else out[r] = write_bf16(__fadd_rn(read_bf16(res_cur[j]), read_bf16(y)));
             }
         }
         if (next >= a.tiles) break;
