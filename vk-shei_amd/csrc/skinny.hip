@@ -349,20 +349,30 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(4)))
                 const int r = grp + rr * kGroups;
                 s[rr] = 0.0f;
                 if (r < a.tokens) {
-                    // eight reads ahead of their FMAs, in element order;
-                    // reads past the row's end stay inside its LDS row and
-                    // add exact zeros (the sum is never -0)
-#pragma unroll
-                    for (int j0 = 0; j0 < kStageInner / 128; j0 += 8) {
+                    // Element g + 128 k of the row sits 128 k elements after
+                    // element g (the swizzle permutes chunks within groups
+                    // of 64 elements), so one base address with immediate
+                    // offsets serves every read.  Eight reads go ahead of
+                    // their FMAs, in element order; elements past the row's
+                    // end would add exact zeros (the sum is never -0) and
+                    // are left out.
+                    const uint16_t *rowp = xs + stage_index(r, g);
+                    const int steps = a.inner / 128;
+                    int k = 0;
+                    for (; k + 8 <= steps; k += 8) {
                         float e[8];
 #pragma unroll
-                        for (int j = 0; j < 8; ++j) {
-                            const int i = g + 128 * (j0 + j);
-                            const float v = read_bf16(xs[stage_index(r, i)]);
-                            e[j] = i < a.inner ? v : 0.0f;
-                        }
+                        for (int j = 0; j < 8; ++j) e[j] = read_bf16(rowp[128 * (k + j)]);
 #pragma unroll
                         for (int j = 0; j < 8; ++j) s[rr] = __fmaf_rn(e[j], e[j], s[rr]);
+                    }
+                    for (; k < steps; ++k) {
+                        const float v = read_bf16(rowp[128 * k]);
+                        s[rr] = __fmaf_rn(v, v, s[rr]);
+                    }
+                    if (g + 128 * steps < a.inner) {
+                        const float v = read_bf16(rowp[128 * steps]);
+                        s[rr] = __fmaf_rn(v, v, s[rr]);
                     }
                     if (g >= 64) norm_part[r * 64 + g - 64] = s[rr];
                 }
