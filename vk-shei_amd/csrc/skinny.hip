@@ -126,10 +126,16 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(4)))
     __shared__ __align__(16) unsigned char lds[(XLDS ? kStageBytes : 0) + kPartialBytes];
     uint16_t *xs = reinterpret_cast<uint16_t *>(lds);
     auto partial = reinterpret_cast<floatx4_t(*)[64]>(lds + (XLDS ? kStageBytes : 0));
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // wave is uniform: the k range of a batch and its bounds tests are
+    // scalar, so a step's B read is branched on, not masked lane by lane
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int kq = (lane >> 4) * 8;
     const int tok = lane & 15;
     const bool live = tok < a.tokens;
+    // Column j of an MFMA result depends on column j of B only, and the
+    // columns of tokens past the batch are never written: their lanes read a
+    // staged row that exists (whatever it holds) instead of being masked.
+    const int xrow = min(tok, kStageTokens - 1);
     const bf16x8_t zero = {};
 
     // The tile's weights: lane l holds row r0 + l % 16, inputs 8 (l / 16) ..
@@ -202,7 +208,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(4)))
         for (int u = 0; u < UB; ++u) {
             const int k = k0 + u * 32;
             bf16x8_t xb;
-            if (XLDS) xb = k < a.inner && live ? *reinterpret_cast<const bf16x8_t *>(xs + stage_index(tok, k + kq)) : zero;
+            if (XLDS) xb = k < a.inner ? *reinterpret_cast<const bf16x8_t *>(xs + stage_index(xrow, k + kq)) : zero;
             else xb = bt.xb[u];
             acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bt.wa[u], xb, acc[m], 0, 0, 0);
         }
@@ -312,15 +318,14 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(4)))
         // (row & 7).
         const int chunks = a.inner / 8;
         const uint32_t xs_lds = lds_offset(xs);
-        const int uwave = __builtin_amdgcn_readfirstlane(wave);
-        for (int j = uwave; j < a.tokens * (kStageInner / 8 / 64); j += WAVES) {
+        for (int j = wave; j < a.tokens * (kStageInner / 8 / 64); j += WAVES) {
             const int r = j >> 3;
             const int c = ((j & 7) * 64 + lane) ^ (r & 7);
             if (c < chunks) dma16_async(a.x, (uint32_t)(r * a.inner + c * 8) * 2u, xs_lds + (uint32_t)j * 1024u);
         }
         if constexpr (NORM) {
             // the RMSNorm weights into the partial space, after its scratch
-            for (int j = uwave; j * 64 < chunks; j += WAVES)
+            for (int j = wave; j * 64 < chunks; j += WAVES)
                 if (j * 64 + lane < chunks)
                     dma16_async(a.norm_w, (uint32_t)(j * 64 + lane) * 16u,
                                 lds_offset(partial) + kNormWeightOffset + (uint32_t)j * 1024u);
